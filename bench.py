@@ -1,0 +1,228 @@
+#!/usr/bin/env python
+"""Fused latent flash-decode benchmark on one MI355X.
+
+Workload (the headline configuration): one Llama-3.1-8B-shaped attention layer, 32 Q / 8 KV heads,
+head_dim 128, batch 32, every row at context 8192 (cur_pos 8191), M-LRD r_k = r_v = 64, bf16 latent
+caches, V absorbed into wo. One step = one decode call of one layer. Latents are drawn as
+sqrt(sigma_j) * z with sigma the singular values of a per-head SVD of random N(0, 0.02) k/v
+projections (the distribution of x @ VT^T for N(0, 1) hidden states); u_k comes from the same SVD;
+q = x W_q^T rotated at position 8191 with Llama-3 RoPE (theta 5e5, factor 8). Steps rotate over
+--layers distinct layer caches (8 x 537 MB by default) so the 256 MB MALL cannot hold the working set.
+
+Prints one JSON line: µs per layer-step (value), tokens/s of the attention op over a 32-layer decode,
+the roofline of the fused kernel on latent bytes (HIP events on the launch stream), the stock bf16
+full-KV flash-decode at the same shape, and the oracle's fp32 CPU decode on a bounded sample.
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO / "tt-cadlab_amd", REPO):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import torch  # noqa: E402
+
+HD, NQ, NKV, HIDDEN = 128, 32, 8, 4096
+THETA = 500000.0
+LLAMA3 = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+N_LAYERS_MODEL = 32
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--layers", type=int, default=8, help="distinct layer caches rotated over the steps")
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--ctx", type=int, default=8192)
+    ap.add_argument("--rank-k", type=int, default=64)
+    ap.add_argument("--rank-v", type=int, default=64)
+    ap.add_argument("--no-stock", action="store_true", help="skip the full-KV comparator")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-rows", type=int, default=2, help="batch rows of the CPU baseline sample")
+    ap.add_argument("--traffic", default=str(REPO / "profiles" / "palu_decode_b32_ctx8192_r64_traffic.txt"),
+                    help="rocprofv3 --pmc summary holding the measured HBM bytes per launch")
+    return ap.parse_args()
+
+
+def svd_sigma(W, n_heads, rank):
+    from palu_tt import compress
+    U, VT = compress.svd_per_head(W, n_heads, rank)
+    return U, VT, VT.pow(2).sum(-1)                          # row j of VT_h has norm^2 = sigma_j
+
+
+def build_workload(a, dev):
+    from palu_tt import convert, fused
+    g = torch.Generator().manual_seed(0)
+    Wq = torch.randn(HIDDEN, HIDDEN, generator=g) * 0.02
+    Wk = torch.randn(NKV * HD, HIDDEN, generator=g) * 0.02
+    Wv = torch.randn(NKV * HD, HIDDEN, generator=g) * 0.02
+    Uk, _, sig_k = svd_sigma(Wk, NKV, a.rank_k)
+    _, _, sig_v = svd_sigma(Wv, NKV, a.rank_v)
+    u_k = torch.stack([convert.reverse_permute(Uk[h], 1, HD, a.rank_k).T for h in range(NKV)])
+    w_rot = fused.w_rot_from_u_k(u_k)[None].to(dev, torch.bfloat16).contiguous()
+    cos, sin = fused.cos_sin_tables(HD, a.ctx, THETA, LLAMA3)
+    cs = fused.cs_table(cos, sin, a.ctx)[None, None].to(dev).contiguous()
+    x = torch.randn(a.batch, HIDDEN, generator=g)
+    q = (x @ convert.reverse_permute(Wq, NQ, HIDDEN, HIDDEN).T).view(a.batch, NQ, HD)
+    q = fused.apply_rope_meta(q, cos[a.ctx - 1], sin[a.ctx - 1])
+    q = q[None].to(dev, torch.bfloat16).contiguous()
+    gd = torch.Generator(device=dev).manual_seed(1)
+    sk = sig_k.sqrt().to(dev)[None, :, None, :]
+    sv = sig_v.sqrt().to(dev)[None, :, None, :]
+    layers = []
+    for _ in range(a.layers):
+        k = (torch.randn(a.batch, NKV, a.ctx, a.rank_k, device=dev, generator=gd) * sk).to(torch.bfloat16)
+        v = (torch.randn(a.batch, NKV, a.ctx, a.rank_v, device=dev, generator=gd) * sv).to(torch.bfloat16)
+        layers.append((k, v))
+    cur = torch.full((a.batch,), a.ctx - 1, dtype=torch.int32, device=dev)
+    return dict(q=q, w_rot=w_rot, cs=cs, layers=layers, cur=cur, u_k=u_k, cos=cos, sin=sin)
+
+
+def time_calls(fn, n_layers, steps, warmup):
+    """Warm up, then time exactly `steps` calls bracketed by synchronize; returns (wall ms/step, mean
+    kernel ms from per-call HIP events on the launch stream, all per-call ms)."""
+    for i in range(warmup):
+        fn(i % n_layers)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        fn(i % n_layers)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    per = [s.elapsed_time(e) for s, e in ev]
+    return wall, statistics.mean(per), per
+
+
+def read_traffic(path):
+    p = Path(path)
+    if not p.exists():
+        return None
+    for ln in p.read_text().splitlines():
+        if ln.startswith("traffic_bytes_per_launch:"):
+            return float(ln.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(a, wl):
+    from oracle import palu_oracle as ref
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rows = max(1, min(a.cpu_rows, a.batch))
+    k, v = wl["layers"][0]
+    kc, vc = k[:rows].float().cpu(), v[:rows].float().cpu()
+    qc = wl["q"][:, :rows].float().cpu()
+    u_k = wl["w_rot"][0, :, :, :HD].float().cpu()
+    cur = torch.full((rows,), a.ctx - 1)
+    run = lambda: ref.reference_decode(qc, kc, u_k, vc, cur, wl["cos"], wl["sin"], HD ** -0.5)
+    run()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    per_layer_us = statistics.median(ts) * 1e6 * (a.batch / rows)
+    return {"value": round(per_layer_us, 1), "unit": "us/layer", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle reference_decode (fp32 torch) on {rows} of {a.batch} batch rows of the same workload, "
+                      f"median of 3 after 1 warm-up, scaled x{a.batch / rows:g} to the full batch; "
+                      f"min {min(ts) * 1e6 * a.batch / rows:.0f} us/layer"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU: the fused decode holds all 32 Q / "
+                                   "8 KV heads of a layer on one MI355X and uses no collectives; "
+                                   "re-run with --gpus 1"}))
+        sys.exit(2)
+    from palu_tt import fused
+    dev = torch.device("cuda:0")
+    wl = build_workload(a, dev)
+    B, S, rk, rv = a.batch, a.ctx, a.rank_k, a.rank_v
+    out = torch.empty(1, B, NQ, rv, dtype=torch.bfloat16, device=dev)
+    ws_bytes = fused._native.load().palu_decode_workspace_bytes(B, NKV, S, rv)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+
+    def fused_step(l):
+        k, v = wl["layers"][l]
+        fused.palu_sdpa_decode(wl["q"], k, wl["w_rot"], wl["cs"], v, rv, wl["cur"], scale=HD ** -0.5, out=out,
+                               workspace=ws)
+
+    wall_ms, kern_ms, per = time_calls(fused_step, a.layers, a.steps, a.warmup)
+    lat_bytes = B * NKV * S * (rk + rv) * 2
+    flops = 2 * B * NKV * S * rk * HD + 2 * B * NQ * S * HD + 2 * B * NQ * S * rv
+    achieved = lat_bytes / (kern_ms * 1e-3) / 1e9
+    res = {
+        "metric": "fused latent decode us/layer + HBM TB/s frac (B=32, ctx 8K, r=64, 1 GPU)",
+        "value": round(wall_ms * 1e3, 2),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded: SVD-spectrum latents, random-init projections)",
+        "config": {"workload": "M-LRD fused latent flash-decode, one Llama-3.1-8B attention layer", "batch": B,
+                   "ctx": S, "cur_pos": S - 1, "n_q": NQ, "n_kv": NKV, "head_dim": HD, "rank_k": rk, "rank_v": rv,
+                   "latent_dtype": "bf16", "absorbed_v": True, "layer_caches_rotated": a.layers,
+                   "rope": "llama3 theta 5e5 factor 8"},
+        "kernel_us": round(kern_ms * 1e3, 2),
+        "kernel_us_min": round(min(per) * 1e3, 2),
+        "tokens_per_s": round(B / (N_LAYERS_MODEL * wall_ms * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": read_traffic(a.traffic),
+                     "algorithmic_bytes": lat_bytes},
+        "mfma": {"achieved_tflops": round(flops / (kern_ms * 1e-3) / 1e12, 2), "peak_tflops": BF16_PEAK_TFLOPS,
+                 "frac": round(flops / (kern_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4), "flops": flops},
+    }
+    if not a.no_stock:
+        wl_layers = wl.pop("layers")       # free the latent caches before the full-KV ones
+        del wl_layers
+        torch.cuda.empty_cache()
+        n_stock = max(1, min(a.layers, 4))
+        gd = torch.Generator(device=dev).manual_seed(2)
+        kv = [(torch.randn(B, NKV, S, HD, device=dev, generator=gd).to(torch.bfloat16),
+               torch.randn(B, NKV, S, HD, device=dev, generator=gd).to(torch.bfloat16)) for _ in range(n_stock)]
+        out_s = torch.empty(1, B, NQ, HD, dtype=torch.bfloat16, device=dev)
+        ws_s = torch.empty(max(fused._native.load().palu_decode_workspace_bytes(B, NKV, S, HD), 1),
+                           dtype=torch.uint8, device=dev)
+
+        def stock_step(l):
+            fused.flash_decode(wl["q"], kv[l][0], kv[l][1], wl["cur"], scale=HD ** -0.5, out=out_s, workspace=ws_s)
+
+        s_wall, s_kern, _ = time_calls(stock_step, n_stock, max(a.steps // 2, 1), max(a.warmup // 2, 1))
+        s_bytes = B * NKV * S * HD * 2 * 2
+        res["stock_full_kv"] = {"us_per_layer": round(s_wall * 1e3, 2), "kernel_us": round(s_kern * 1e3, 2),
+                                "achieved_GBps": round(s_bytes / (s_kern * 1e-3) / 1e9, 1),
+                                "frac": round(s_bytes / (s_kern * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                                "bytes": s_bytes, "layer_caches_rotated": n_stock}
+        res["speedup_vs_stock"] = round(s_wall / wall_ms, 3)
+        del kv
+        wl["layers"] = None
+    if not a.no_cpu:
+        if wl.get("layers") is None:
+            gd = torch.Generator(device=dev).manual_seed(1)
+            wl["layers"] = build_workload(argparse.Namespace(**{**vars(a), "layers": 1}), dev)["layers"]
+        res["cpu_baseline"] = cpu_baseline(a, wl)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,103 @@
+/* C-ABI of the MI355X Palu fused latent flash-decode library (libpalu_mi355x.so).
+ *
+ * Every entry point takes raw device pointers, plain integer shapes and a hipStream_t, enqueues its
+ * kernels on that stream and returns without synchronising. No entry point allocates device memory:
+ * split-K partials go to a caller-provided workspace whose size palu_decode_workspace_bytes reports.
+ * Tensors are dense row-major in the shapes given below; bf16 tensors must be 16-byte aligned.
+ *
+ * Return value: PALU_OK, or an error code with a message for palu_last_error() (thread-local, valid
+ * until the next call on the same thread). Envelope messages carry the substrings the reference op's
+ * own validation uses ("r_k", "cs_tab", "w_rot", "optional together", "Phase 1", "rot_mode must be",
+ * "heads_per_group", "u_v", "head_dim_v", "heads_per_core", "KV head count", "grouped latents").
+ */
+#ifndef PALU_MI355X_H
+#define PALU_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PALU_ABI_VERSION 1
+
+#define PALU_OK 0
+#define PALU_EINVAL 1       /* arguments outside the op's envelope */
+#define PALU_EUNSUPPORTED 2 /* inside the reference envelope but not built in this library */
+#define PALU_EHIP 3         /* HIP runtime error while launching */
+
+#define PALU_DTYPE_F32 0
+#define PALU_DTYPE_BF16 1
+
+#define PALU_ROT_LEGACY 0
+#define PALU_ROT_PACK 1
+#define PALU_ROT_DST 2
+
+typedef struct ihipStream_t* palu_stream_t; /* the same handle as hipStream_t */
+
+/* Message of the last failed call on this thread ("" after a successful one). */
+const char* palu_last_error(void);
+
+/* PALU_ABI_VERSION of the loaded library. */
+int palu_abi_version(void);
+
+/* Bytes of fp32 workspace palu_sdpa_decode / palu_flash_decode need for these shapes (0 when the
+ * sequence is not split across workgroups). head_dim_v is the output width of the call. */
+size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_dim_v);
+
+/* Fused latent flash-decode. Replaces ttnn.transformer.palu_sdpa_decode, the op PaluAttention's decode
+ * branch calls (palu_tt/attention.py:632-639; interface in
+ * docs/superpowers/specs/2026-09-10-palu-tt-stage2-design.md:47-81 and, for u_v / heads_per_core,
+ * docs/superpowers/specs/2026-09-12-palu-tt-stage2b-design.md:80-139; fp32 semantics
+ * palu_tt/fused.py:82-107).
+ *
+ *   q        [B, n_q, 128] bf16      query, already rotated at its own position (cur_pos[b])
+ *   k_latent [B, n_groups, S, r_k]   bf16 K latent cache
+ *   w_rot    [n_kv, r_k, 256] bf16   [u_k | u_k T] per KV head, u_k in Meta head order
+ *   cs_tab   [cs_rows, 256]          [cos | sin] per position, Meta-interleaved; fp32 or bf16
+ *   v_latent [B, n_groups, S, r_v]   bf16 V latent cache (absorbed V: attended over directly)
+ *   cur_pos  [B] int32 (device)      inclusive last valid position of each row
+ *   out      [B, n_q, head_dim_v]    fp32 or bf16
+ *   rot_step, trans_mat              the reference's Phase 2 constants; optional together. They are
+ *                                    validated as the reference does and otherwise unused: this kernel
+ *                                    always rotates chunk-relative from cs_tab.
+ *   u_v      [n_kv, r_v, 128] bf16   in-kernel V rebuild for grouped latents (not built yet: returns
+ *                                    PALU_EUNSUPPORTED)
+ *   scale                            softmax scale (the reference passes head_dim^-0.5)
+ *   heads_per_core, rot_mode, table_mcast, k_chunk
+ *                                    the reference's Tensix work-split switches; validated, and
+ *                                    otherwise without effect on MI355X (k_chunk 0 = default)
+ * Head h of q attends KV head h / (n_q / n_kv); KV head j reads latent group j / (n_kv / n_groups).
+ */
+int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab, const void* v_latent,
+                     int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step, const void* trans_mat,
+                     const void* u_v, float scale, int heads_per_core, int rot_mode, int table_mcast, int k_chunk,
+                     int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width,
+                     int cs_rows, int cs_cols, int cs_dtype, int out_dtype, void* workspace, size_t workspace_bytes,
+                     palu_stream_t stream);
+
+/* Stock flash-decode over full, already-rotated K and a V cache of width head_dim_v. Replaces
+ * ttnn.transformer.scaled_dot_product_attention_decode (head_dim_v == 128) and
+ * ttnn.transformer.flash_multi_latent_attention_decode (head_dim_v == r_v), the two ops the reference's
+ * non-fused decode path calls (palu_tt/attention.py:703-706; tests/test_palu_sdpa_device.py:58-65,
+ * 238-241). It is also the full-KV comparator for the fused op.
+ *   q [B, n_q, 128] bf16, k [B, n_kv, S, 128] bf16, v [B, n_kv, S, head_dim_v] bf16,
+ *   cur_pos [B] int32 (device), out [B, n_q, head_dim_v] fp32 or bf16. */
+int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t* cur_pos, void* out, float scale,
+                      int batch, int n_q, int n_kv, int seq_len, int head_dim_v, int out_dtype, void* workspace,
+                      size_t workspace_bytes, palu_stream_t stream);
+
+/* Latent append: cache[b, g, update_idxs[b], :] = new_rows[b, g, :] for every row whose index lies in
+ * [0, seq_len) (other rows are skipped). Replaces ttnn.experimental.paged_update_cache on the latent
+ * caches (palu_tt/attention.py:622-623).
+ *   cache [B, n_groups, S, width] bf16, new_rows [B, n_groups, width] bf16, update_idxs [B] int32
+ *   (device), width a multiple of 8. */
+int palu_latent_append(void* cache, const void* new_rows, const int32_t* update_idxs, int batch, int n_groups,
+                       int seq_len, int width, palu_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PALU_MI355X_H */

@@ -1,0 +1,193 @@
+"""GPU parity of the fused latent flash-decode, the stock decode and the latent append against the oracle.
+
+Bar (north star): max |out - oracle| <= 2e-2 and cosine >= 0.9999 on attention outputs, oracle in fp32
+on the same bf16-rounded inputs and the same cos/sin table. Cases follow the reference's op tests
+(tests/test_palu_sdpa_device.py): positions 0, 127, 128 and S-1 among the rows, batch 1 and 32, the
+reference's 16 Q / 4 KV shape and the Llama-3.1-8B 32 Q / 8 KV shape, every latent width the library
+builds, sequence splits merged across workgroups, and bf16 tables.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import palu_oracle as ref
+from palu_tt import fused
+
+pytestmark = pytest.mark.gpu
+
+HD = 128
+THETA = 500000.0
+LLAMA3 = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+MAX_ABS = 2e-2
+COS = 0.9999
+
+
+def _bf(t):
+    return t.to(torch.bfloat16).float()
+
+
+def _inputs(B, S, r_k, r_v, nh=32, nkv=8, seed=0, scaling=LLAMA3):
+    g = torch.Generator().manual_seed(seed)
+    q = _bf(torch.randn(1, B, nh, HD, generator=g))
+    k_lat = _bf(torch.randn(B, nkv, S, r_k, generator=g))
+    u_k = _bf(torch.randn(nkv, r_k, HD, generator=g) / r_k ** 0.5)
+    v = _bf(torch.randn(B, nkv, S, r_v, generator=g))
+    pos = torch.randint(0, S, (B,), generator=g)
+    pos[0] = S - 1
+    if B >= 4:
+        pos[1], pos[2], pos[3] = 0, 127, min(128, S - 1)
+    cos, sin = ref.cos_sin_tables(HD, S, THETA, scaling)
+    return q, k_lat, u_k, v, pos, cos, sin
+
+
+def _run_fused(dev, q, k_lat, u_k, v, pos, cos, sin, S, out_dtype=torch.float32, cs_dtype=torch.float32, **kw):
+    w_rot = ref.w_rot_from_u_k(u_k)[None]
+    cs = ref.cs_table(cos, sin, S)[None, None].to(cs_dtype)
+    out = fused.palu_sdpa_decode(
+        q.to(dev, torch.bfloat16), k_lat.to(dev, torch.bfloat16), w_rot.to(dev, torch.bfloat16), cs.to(dev),
+        v.to(dev, torch.bfloat16), v.shape[-1], pos.to(dev, torch.int32), scale=HD ** -0.5, out_dtype=out_dtype, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu()
+
+
+def _check(out, exp, max_abs=MAX_ABS, cos=COS):
+    assert out.shape == exp.shape
+    assert torch.isfinite(out).all()
+    ma, cs = ref.max_abs(out, exp), ref.cosine(out, exp)
+    assert ma <= max_abs and cs >= cos, f"max_abs {ma:.3e} (bar {max_abs}), cosine {cs:.6f} (bar {cos})"
+
+
+@pytest.mark.parametrize("r_k,r_v", [(32, 32), (32, 64), (64, 64), (64, 32), (96, 64), (128, 64), (64, 128),
+                                     (32, 128), (96, 96), (128, 128)])
+def test_fused_matches_oracle_batch4(gpu, r_k, r_v):
+    args = _inputs(4, 1024, r_k, r_v)
+    exp = ref.reference_decode(*args, HD ** -0.5)
+    _check(_run_fused(gpu, *args, 1024), exp)
+
+
+@pytest.mark.parametrize("B,S", [(1, 1024), (32, 256), (1, 8192), (2, 4096), (3, 300), (5, 33)])
+def test_fused_batch_and_length_envelope(gpu, B, S):
+    """Batch 1 (many splits merged across workgroups), batch 32, a length that is not a multiple of the
+    32-position block, and a cache shorter than the 128-position rotation chunk."""
+    args = _inputs(B, S, 64, 64)
+    exp = ref.reference_decode(*args, HD ** -0.5)
+    _check(_run_fused(gpu, *args, S), exp)
+
+
+def test_fused_reference_head_shape(gpu):
+    """The reference op tests' shape: 16 Q / 4 KV heads per chip, batch 32, 1024 positions."""
+    args = _inputs(32, 1024, 64, 64, nh=16, nkv=4)
+    exp = ref.reference_decode(*args, HD ** -0.5)
+    _check(_run_fused(gpu, *args, 1024), exp)
+
+
+def test_fused_without_rope_scaling_and_bf16_output(gpu):
+    args = _inputs(8, 2048, 64, 64, scaling=None)
+    exp = ref.reference_decode(*args, HD ** -0.5)
+    out = _run_fused(gpu, *args, 2048, out_dtype=torch.bfloat16)
+    _check(out, exp)
+
+
+def test_fused_bf16_table(gpu):
+    """bf16 [cos | sin] as the reference's device tables are stored; oracle on the same rounded table.
+    Chunk-relative rotation composes two rounded angles, so the bar is the reference's PCC 0.99 op bar
+    plus a looser cosine."""
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(8, 2048, 64, 64)
+    cos_b, sin_b = _bf(cos), _bf(sin)
+    exp = ref.reference_decode(q, k_lat, u_k, v, pos, cos_b, sin_b, HD ** -0.5)
+    out = _run_fused(gpu, q, k_lat, u_k, v, pos, cos_b, sin_b, 2048, cs_dtype=torch.bfloat16)
+    assert ref.pcc(out, exp) >= 0.99
+    _check(out, exp, max_abs=5e-2, cos=0.999)
+
+
+def test_phase2_switches_do_not_change_the_result(gpu):
+    """rot_step/trans_mat (Phase 2), rot_mode and table_mcast select Tensix schedules in the reference;
+    the MI355X kernel has one schedule, so every combination must give the bit-identical output."""
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(4, 1024, 64, 64)
+    dev = gpu
+    base = _run_fused(dev, q, k_lat, u_k, v, pos, cos, sin, 1024)
+    p2 = dict(rot_step=fused.rot_step_table(cos, sin, 512)[None, None].to(dev),
+              trans_mat=fused.trans_mat_tile().to(dev, torch.bfloat16))
+    for kw in (p2, dict(p2, rot_mode="legacy", table_mcast=False), dict(rot_mode="pack"),
+               dict(program_config=fused.SDPAProgramConfig(k_chunk_size=128))):
+        assert torch.equal(base, _run_fused(dev, q, k_lat, u_k, v, pos, cos, sin, 1024, **kw))
+
+
+def test_fused_headline_shape_full_size(gpu):
+    """B=32, 32 Q / 8 KV, every row at context 8192, r_k = r_v = 64 (the headline workload), against
+    the oracle at full size."""
+    B, S = 32, 8192
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(B, S, 64, 64)
+    pos[:] = S - 1
+    exp = ref.reference_decode(q, k_lat, u_k, v, pos, cos, sin, HD ** -0.5)
+    _check(_run_fused(gpu, q, k_lat, u_k, v, pos, cos, sin, S), exp)
+
+
+@pytest.mark.parametrize("B,S,dv", [(4, 1024, 128), (32, 512, 128), (1, 8192, 128), (4, 1024, 64), (3, 300, 32)])
+def test_stock_flash_decode_matches_oracle(gpu, B, S, dv):
+    g = torch.Generator().manual_seed(1)
+    q = _bf(torch.randn(1, B, 32, HD, generator=g))
+    k = _bf(torch.randn(B, 8, S, HD, generator=g))
+    v = _bf(torch.randn(B, 8, S, dv, generator=g))
+    pos = torch.randint(0, S, (B,), generator=g)
+    pos[0] = S - 1
+    exp = ref.full_kv_decode(q, k, v, pos, HD ** -0.5)
+    out = fused.flash_decode(q.to(gpu, torch.bfloat16), k.to(gpu, torch.bfloat16), v.to(gpu, torch.bfloat16),
+                             pos.to(gpu, torch.int32), scale=HD ** -0.5, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _check(out.cpu(), exp)
+
+
+def test_fused_equals_stock_on_host_rebuilt_k(gpu):
+    """The reference's second check (test_palu_sdpa_device.py:58-65): the stock op on host-rebuilt,
+    host-rotated K must agree with the fused op."""
+    B, S = 8, 1024
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(B, S, 64, 64)
+    K = torch.einsum("bhsr,hrd->bhsd", k_lat, u_k)
+    K = _bf(ref.meta_rotate(K, cos[None, None, :S], sin[None, None, :S])).contiguous()
+    stock = fused.flash_decode(q.to(gpu, torch.bfloat16), K.to(gpu, torch.bfloat16), v.to(gpu, torch.bfloat16),
+                               pos.to(gpu, torch.int32), scale=HD ** -0.5, out_dtype=torch.float32).cpu()
+    out = _run_fused(gpu, q, k_lat, u_k, v, pos, cos, sin, S)
+    assert ref.pcc(stock, out) >= 0.9995
+    _check(out, stock)
+
+
+def test_latent_append_writes_rows_at_positions(gpu):
+    B, G, S, r = 5, 8, 64, 64
+    cache = torch.randn(B, G, S, r).to(torch.bfloat16)
+    rows = torch.randn(1, B, G, r).to(torch.bfloat16)
+    idx = torch.tensor([0, 63, 17, -1, 64], dtype=torch.int32)   # -1 and 64 are outside: skipped
+    exp = cache.clone()
+    for b in range(B):
+        if 0 <= idx[b] < S:
+            exp[b, :, idx[b]] = rows[0, b]
+    d = cache.to(gpu)
+    fused.paged_update_cache(d, rows.to(gpu), idx.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(d.cpu(), exp)
+
+
+def test_fused_reads_appended_rows(gpu):
+    """Append the decode step's latent rows, then decode: the new position must be attended."""
+    B, S = 4, 256
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(B, S, 64, 64)
+    pos[:] = torch.tensor([10, 255, 127, 128])
+    new_k = _bf(torch.randn(1, B, 8, 64))
+    new_v = _bf(torch.randn(1, B, 8, 64))
+    k_full, v_full = k_lat.clone(), v.clone()
+    for b in range(B):
+        k_full[b, :, pos[b]] = new_k[0, b]
+        v_full[b, :, pos[b]] = new_v[0, b]
+    exp = ref.reference_decode(q, k_full, u_k, v_full, pos, cos, sin, HD ** -0.5)
+    dk, dv = k_lat.to(gpu, torch.bfloat16), v.to(gpu, torch.bfloat16)
+    dpos = pos.to(gpu, torch.int32)
+    fused.paged_update_cache(dk, new_k.to(gpu, torch.bfloat16), dpos)
+    fused.paged_update_cache(dv, new_v.to(gpu, torch.bfloat16), dpos)
+    w_rot = ref.w_rot_from_u_k(u_k)[None].to(gpu, torch.bfloat16)
+    cs = ref.cs_table(cos, sin, S)[None, None].to(gpu)
+    out = fused.palu_sdpa_decode(q.to(gpu, torch.bfloat16), dk, w_rot, cs, dv, 64, dpos, scale=HD ** -0.5,
+                                 out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _check(out.cpu(), exp)

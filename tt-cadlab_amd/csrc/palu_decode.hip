@@ -1,0 +1,687 @@
+// Palu fused latent flash-decode for MI355X (gfx950): HIP kernels and their C-ABI.
+//
+// One work item is one (batch row b, KV head h). Per position p <= cur_pos[b] the item's key is
+// rebuilt from its latent row, K[p] = RoPE_p(lat_k[p] @ u_k[h]), and the GQA group of query heads
+// that share KV head h runs an online-softmax flash-decode over those keys. With the absorbed-V
+// layout the value rows are the V latent itself, so the output is [B, n_q, r_v] in latent space
+// (the up-projection lives in wo_fused). Semantics follow the reference op
+// ttnn.transformer.palu_sdpa_decode (docs/superpowers/specs/2026-09-10-palu-tt-stage2-design.md:47-81,
+// fp32 model palu_tt/fused.py:82-107).
+//
+// Kernel shape (all MFMA work is v_mfma_f32_16x16x32_bf16, bf16 in / fp32 accumulate):
+//   * A workgroup owns one item and one split of its sequence; its NW waves each own a contiguous
+//     slice of that split, so a wave streams its latent rows straight from HBM into registers with
+//     16-byte loads, one block of 32 positions at a time, prefetching the next block.
+//   * K is rebuilt transposed, K^T[d][p] = u_k^T[d][:] . lat[p][:]: the accumulator layout then gives
+//     every lane one position and 4 consecutive head dims per 16-dim tile, so each RoPE pair
+//     (Meta-interleaved dims 2f, 2f+1) sits in one lane and the rotation is plain VALU work on the
+//     fp32 accumulators.
+//   * RoPE is applied chunk-relative: K rows are rotated by their offset t inside a 128-position
+//     chunk (angle table resident in LDS, laid out in lane order), and the query is rotated back by
+//     the chunk base once per chunk, q~ = R_{-s0} q. Rotations in one plane commute, so
+//     q~ . R_t k = q . R_{s0+t} k, the score of the reference.
+//   * The rebuilt K tile is reused in registers as the A operand of the QK MFMA; the head dim is
+//     contracted in a permuted order that the query operand mirrors, so no lane shuffles are needed.
+//   * Scores come out with one head per lane column. The online softmax runs in the exp2 domain
+//     (scale * log2 e folded into q~) with a lazily refreshed running max, and the probabilities feed
+//     the PV MFMA directly as its B operand.
+//   * The V rows are brought into the PV A-operand layout (8 consecutive positions of one latent
+//     column per lane) by an MFMA against an identity tile: exact in bf16, and it keeps the
+//     transpose on the matrix core instead of LDS or VALU.
+//   * The waves of a workgroup merge their (O, m, l) partials in LDS; several splits of one item are
+//     merged by a second small kernel through a caller-provided workspace.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdarg.h>
+#include <string.h>
+
+#include "../../include/palu_mi355x.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int HD = 128;     // head dim
+constexpr int BLK = 32;     // positions per inner block (two 16-position MFMA tiles)
+constexpr int CH = 128;     // rotation chunk: q~ is re-based every CH positions
+constexpr float NEG_INF = -__builtin_huge_valf();
+constexpr float LAZY_RESCALE_LOG2 = 8.0f;  // running max is refreshed when a score exceeds it by > 2^8
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float to_f(float x) { return x; }
+__device__ __forceinline__ float to_f(__bf16 x) { return (float)x; }
+
+__device__ __forceinline__ void store_out(float* p, float v) { *p = v; }
+__device__ __forceinline__ void store_out(__bf16* p, float v) { *p = (__bf16)v; }
+
+__device__ __forceinline__ bf16x8 pack8(f32x4 lo, f32x4 hi) {
+  bf16x8 r;
+  r[0] = (__bf16)lo[0]; r[1] = (__bf16)lo[1]; r[2] = (__bf16)lo[2]; r[3] = (__bf16)lo[3];
+  r[4] = (__bf16)hi[0]; r[5] = (__bf16)hi[1]; r[6] = (__bf16)hi[2]; r[7] = (__bf16)hi[3];
+  return r;
+}
+
+__device__ __forceinline__ float wave_max_xor48(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  x = fmaxf(x, __shfl_xor(x, 32, 64));
+  return x;
+}
+__device__ __forceinline__ float wave_sum_xor48(float x) {
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+struct DecodeArgs {
+  const __bf16* q;        // [B, n_q, HD], already rotated at its own position
+  const __bf16* k;        // latent [B, n_groups, S, RK]   or full rotated K [B, n_kv, S, HD]
+  const __bf16* v;        // latent [B, n_groups, S, RV]   or full V [B, n_kv, S, RV]
+  const __bf16* w_rot;    // [n_kv, RK, 2*HD]; columns 0..HD-1 are u_k (Meta head order)
+  const void* cs;         // [cs_rows, 2*HD]: [cos | sin], Meta-interleaved, fp32 or bf16
+  const int32_t* cur_pos; // [B], inclusive last valid position
+  void* out;              // [B, n_q, RV]
+  float* ws;              // [items, n_splits, 16, RV + 2] split partials (n_splits > 1)
+  size_t ws_bytes;
+  long long k_sb, k_sg;   // element strides of k: batch, group (row stride is RK / HD)
+  long long v_sb, v_sg;
+  int B, n_q, n_kv, rep, hpg, S, cs_rows;
+  int split_len;          // positions per workgroup split, a multiple of NW * CH
+  int n_splits;
+  float qscale;           // softmax scale * log2(e)
+};
+
+// Lane-ordered rotation table entry for (block, tile, 16-dim row tile, lane):
+// {cos f, sin f, cos f+1, sin f+1} at chunk offset t, f = 8*rt + 2*(lane/16).
+__device__ __forceinline__ int rtab_index(int blk, int c, int rt, int lane) {
+  return ((blk * 2 + c) * 8 + rt) * 64 + lane;
+}
+
+template <int RK, int RV, bool KFULL, int NW>
+struct Smem {
+  static constexpr bool UK_LDS = !KFULL && RK > 64;
+  static constexpr int UKT_STRIDE = RK + 8;                    // bf16 elements; +16 B kills bank conflicts
+  static constexpr int RTAB_BYTES = KFULL ? 0 : CH * 32 * 16;  // float4 per (t, f pair)
+  static constexpr int UKT_BYTES = KFULL ? 0 : HD * UKT_STRIDE * 2;
+  static constexpr int MERGE_BYTES = NW * 16 * (RV + 2) * 4;
+  static constexpr int MAIN_BYTES = RTAB_BYTES + UKT_BYTES;
+  static constexpr int BYTES = MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES;
+};
+
+template <int RK, int RV, bool KFULL, int NW, typename TabT, typename OutT>
+__global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a) {
+  static_assert(RK % 32 == 0 && RK <= 128, "RK");
+  static_assert(RV % 32 == 0 && RV <= 128, "RV");
+  static_assert(!KFULL || RK == HD, "full K has the head dim");
+  constexpr int KB = RK / 32;   // 32-wide contraction blocks of the K operand
+  constexpr int VB = RV / 32;   // 32-wide blocks of a V row
+  constexpr int VT = RV / 16;   // 16-wide V tiles = PV M-tiles
+  using SM = Smem<RK, RV, KFULL, NW>;
+
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  float4* rtab = reinterpret_cast<float4*>(smem);
+  __bf16* ukT = reinterpret_cast<__bf16*>(smem + SM::RTAB_BYTES);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int item = blockIdx.y, split = blockIdx.x;
+  const int b = item / a.n_kv, kvh = item - b * a.n_kv;
+  const int grp = KFULL ? kvh : kvh / a.hpg;
+
+  int len = a.cur_pos[b] + 1;
+  len = len < 0 ? 0 : (len > a.S ? a.S : len);
+  const int s_lo = split * a.split_len;
+  const int s_hi = min(len, s_lo + a.split_len);
+  const int Lw = a.split_len / NW;
+  const int w_lo = s_lo + w * Lw;
+  const int w_hi = min(s_hi, w_lo + Lw);
+
+  // ---- prologue: chunk-relative angle table and u_k^T in LDS ------------------------------------
+  if constexpr (!KFULL) {
+    const TabT* cs = static_cast<const TabT*>(a.cs);
+    for (int e = tid; e < CH * 32; e += NW * 64) {
+      const int l = e & 63, rt = (e >> 6) & 7, c = (e >> 9) & 1, blk = e >> 10;
+      const int nn = l & 15, gg = l >> 4;
+      const int t = blk * BLK + 8 * (nn >> 2) + 4 * c + (nn & 3);
+      const int col = 16 * rt + 4 * gg;  // = 2f for f = 8*rt + 2*gg
+      float4 v = make_float4(1.f, 0.f, 1.f, 0.f);
+      if (t < a.cs_rows) {
+        const TabT* row = cs + (long long)t * (2 * HD);
+        v = make_float4(to_f(row[col]), to_f(row[HD + col]), to_f(row[col + 2]), to_f(row[HD + col + 2]));
+      }
+      rtab[e] = v;
+    }
+    const __bf16* uk = a.w_rot + (long long)kvh * RK * (2 * HD);
+    for (int e = tid; e < RK * (HD / 8); e += NW * 64) {
+      const int r = e / (HD / 8), d0 = (e % (HD / 8)) * 8;
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(uk + (long long)r * (2 * HD) + d0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ukT[(d0 + i) * SM::UKT_STRIDE + r] = v[i];
+    }
+    __syncthreads();
+  }
+
+  // u_k^T as the A operand of the rebuild: row d = 16*rt + n, ranks 32*kb + 8*g + 0..7.
+  bf16x8 ukA[SM::UK_LDS ? 1 : 8][SM::UK_LDS ? 1 : KB];
+  if constexpr (!KFULL && !SM::UK_LDS) {
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+        ukA[rt][kb] = *reinterpret_cast<const bf16x8*>(ukT + (16 * rt + n) * SM::UKT_STRIDE + 32 * kb + 8 * g);
+  }
+
+  // Identity B operands that move one 16-column slice of a 32-wide V block into the PV layout.
+  bf16x8 idB[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) idB[par][j] = (8 * g + j == 16 * par + n) ? (__bf16)1.0f : (__bf16)0.0f;
+
+  f32x4 O[VT];
+#pragma unroll
+  for (int i = 0; i < VT; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = NEG_INF, l_run = 0.f;
+  bf16x8 qB[4];
+
+  const bool qvalid = n < a.rep;
+  const __bf16* qrow = a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + (qvalid ? n : 0)) * HD;
+  const __bf16* kbase = a.k + b * a.k_sb + grp * a.k_sg;
+  const __bf16* vbase = a.v + b * a.v_sb + grp * a.v_sg;
+
+  // Query operand. Latent mode: q~ = R_{-s0} q * qscale with the head dim contracted in the order
+  // d(kb, g, j) = 16*(2*kb + j/4) + 4*g + j%4, which is the order the rebuilt K^T tile has in
+  // registers. Full-K mode: q * qscale in natural order d = 32*kb + 8*g + j.
+  auto make_q = [&](int s0) {
+    if constexpr (KFULL) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        bf16x8 v = *reinterpret_cast<const bf16x8*>(qrow + 32 * kb + 8 * g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qB[kb][j] = (__bf16)(qvalid ? (float)v[j] * a.qscale : 0.f);
+      }
+    } else {
+      const TabT* row = static_cast<const TabT*>(a.cs) + (long long)s0 * (2 * HD);
+#pragma unroll
+      for (int rt = 0; rt < 8; ++rt) {
+        const int col = 16 * rt + 4 * g;
+        const bf16x4 x = *reinterpret_cast<const bf16x4*>(qrow + col);
+        const float c0 = to_f(row[col]), sn0 = to_f(row[HD + col]);
+        const float c1 = to_f(row[col + 2]), sn1 = to_f(row[HD + col + 2]);
+        const float x0 = (float)x[0], x1 = (float)x[1], x2 = (float)x[2], x3 = (float)x[3];
+        const float s = qvalid ? a.qscale : 0.f;
+        const int kb = rt >> 1, j0 = 4 * (rt & 1);
+        qB[kb][j0 + 0] = (__bf16)((x0 * c0 + x1 * sn0) * s);
+        qB[kb][j0 + 1] = (__bf16)((x1 * c0 - x0 * sn0) * s);
+        qB[kb][j0 + 2] = (__bf16)((x2 * c1 + x3 * sn1) * s);
+        qB[kb][j0 + 3] = (__bf16)((x3 * c1 - x2 * sn1) * s);
+      }
+    }
+  };
+
+  // Latent / K / V rows of one block. Lane row n of tile c is position base + 8*(n/4) + 4*c + n%4;
+  // rows past the cache end are clamped (their scores are masked).
+  auto load_blk = [&](int base, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[2][VB]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      int p = base + 8 * (n >> 2) + 4 * c + (n & 3);
+      p = p < a.S ? p : a.S - 1;
+      const __bf16* kr = kbase + (long long)p * RK + 8 * g;
+      const __bf16* vr = vbase + (long long)p * RV + 8 * g;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) kd[c][kb] = *reinterpret_cast<const bf16x8*>(kr + 32 * kb);
+#pragma unroll
+      for (int vb = 0; vb < VB; ++vb) vd[c][vb] = *reinterpret_cast<const bf16x8*>(vr + 32 * vb);
+    }
+  };
+
+  int q_s0 = -1;
+  // One block of 32 positions on the buffers (kc, vc), with the next block prefetched into (kn, vn).
+  auto step = [&](int base, bf16x8 (&kc)[2][KB], bf16x8 (&vc)[2][VB], bf16x8 (&kn)[2][KB],
+                  bf16x8 (&vn)[2][VB]) __attribute__((always_inline)) {
+    if (base + BLK < w_hi) load_blk(base + BLK, kn, vn);
+
+    const int s0 = base & ~(CH - 1);
+    if (s0 != q_s0) { make_q(s0); q_s0 = s0; }
+    const int blk = (base - s0) / BLK;
+
+    f32x4 sc[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (KFULL) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) s = mfma16(kc[c][kb], qB[kb], s);
+      } else {
+        f32x4 acc[8];
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt) {
+          acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+            bf16x8 ua;
+            if constexpr (SM::UK_LDS)
+              ua = *reinterpret_cast<const bf16x8*>(ukT + (16 * rt + n) * SM::UKT_STRIDE + 32 * kb + 8 * g);
+            else
+              ua = ukA[rt][kb];
+            acc[rt] = mfma16(ua, kc[c][kb], acc[rt]);
+          }
+        }
+        // RoPE by the chunk offset of this lane's position: (x0, x1) -> (x0 c - x1 s, x1 c + x0 s).
+#pragma unroll
+        for (int rt = 0; rt < 8; ++rt) {
+          const float4 t = rtab[rtab_index(blk, c, rt, lane)];
+          const float x0 = acc[rt][0], x1 = acc[rt][1], x2 = acc[rt][2], x3 = acc[rt][3];
+          acc[rt][0] = x0 * t.x - x1 * t.y;
+          acc[rt][1] = x1 * t.x + x0 * t.y;
+          acc[rt][2] = x2 * t.z - x3 * t.w;
+          acc[rt][3] = x3 * t.z + x2 * t.w;
+        }
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) s = mfma16(pack8(acc[2 * kb], acc[2 * kb + 1]), qB[kb], s);
+      }
+      sc[c] = s;
+    }
+
+    // Causal / range mask: score register i of tile c is position base + 8*g + 4*c + i.
+    const bool partial = base + BLK > w_hi;
+    if (partial) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (base + 8 * g + 4 * c + i >= w_hi) sc[c][i] = NEG_INF;
+    }
+
+    // Online softmax, exp2 domain; lanes n, n+16, n+32, n+48 hold query head n.
+    float bm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    bm = wave_max_xor48(bm);
+    if (__any(bm > m_run + LAZY_RESCALE_LOG2)) {
+      const float mn = fmaxf(m_run, bm);
+      const float alpha = (m_run == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(m_run - mn);
+#pragma unroll
+      for (int i = 0; i < VT; ++i) O[i] *= alpha;
+      l_run *= alpha;
+      m_run = mn;
+    }
+    const float mref = (m_run == NEG_INF) ? 0.f : m_run;
+    f32x4 p[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[c][i] = __builtin_amdgcn_exp2f(sc[c][i] - mref);
+    l_run += (p[0][0] + p[0][1]) + (p[0][2] + p[0][3]) + (p[1][0] + p[1][1]) + (p[1][2] + p[1][3]);
+    const bf16x8 pB = pack8(p[0], p[1]);
+
+    // V rows into the PV A layout (identity MFMA), masked rows zeroed, then O^T += V^T P^T.
+#pragma unroll
+    for (int mt = 0; mt < VT; ++mt) {
+      f32x4 x0 = mfma16(vc[0][mt >> 1], idB[mt & 1], f32x4{0.f, 0.f, 0.f, 0.f});
+      f32x4 x1 = mfma16(vc[1][mt >> 1], idB[mt & 1], f32x4{0.f, 0.f, 0.f, 0.f});
+      if (partial) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (base + 8 * g + i >= w_hi) x0[i] = 0.f;
+          if (base + 8 * g + 4 + i >= w_hi) x1[i] = 0.f;
+        }
+      }
+      O[mt] = mfma16(pack8(x0, x1), pB, O[mt]);
+    }
+  };
+
+  bf16x8 kl[2][KB], vl[2][VB], kln[2][KB], vln[2][VB];
+  int base = w_lo;
+  if (base < w_hi) load_blk(base, kl, vl);
+  while (base < w_hi) {
+    step(base, kl, vl, kln, vln);
+    base += BLK;
+    if (base >= w_hi) break;
+    step(base, kln, vln, kl, vl);
+    base += BLK;
+  }
+
+  // ---- merge the NW wave partials of this workgroup ---------------------------------------------
+  l_run = wave_sum_xor48(l_run);
+  __syncthreads();  // the merge buffer overlays the angle table
+  float* mbuf = reinterpret_cast<float*>(smem);
+  if (n < a.rep) {
+    float* row = mbuf + (w * 16 + n) * (RV + 2);
+    if (g == 0) { row[RV] = m_run; row[RV + 1] = l_run; }
+#pragma unroll
+    for (int mt = 0; mt < VT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) row[16 * mt + 4 * g + i] = O[mt][i];
+  }
+  __syncthreads();
+  for (int e = tid; e < a.rep * RV; e += NW * 64) {
+    const int h = e / RV, r = e - h * RV;
+    float M = NEG_INF;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mbuf[(ww * 16 + h) * (RV + 2) + RV]);
+    float L = 0.f, acc = 0.f;
+    if (M != NEG_INF) {
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) {
+        const float* row = mbuf + (ww * 16 + h) * (RV + 2);
+        const float f = __builtin_amdgcn_exp2f(row[RV] - M);
+        L += row[RV + 1] * f;
+        acc += row[r] * f;
+      }
+    }
+    if (a.n_splits == 1) {
+      OutT* o = static_cast<OutT*>(a.out) + ((long long)b * a.n_q + (long long)kvh * a.rep + h) * RV + r;
+      store_out(o, L > 0.f ? acc / L : 0.f);
+    } else {
+      float* wrow = a.ws + (((long long)item * a.n_splits + split) * 16 + h) * (RV + 2);
+      wrow[r] = acc;
+      if (r == 0) { wrow[RV] = M; wrow[RV + 1] = L; }
+    }
+  }
+}
+
+// Merge the split partials of every item: out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+template <int RV, typename OutT>
+__global__ __launch_bounds__(256) void palu_merge_kernel(const float* ws, void* out, int n_splits, int rep,
+                                                         int n_q, int n_kv) {
+  const int item = blockIdx.x;
+  const int b = item / n_kv, kvh = item - b * n_kv;
+  for (int e = threadIdx.x; e < rep * RV; e += blockDim.x) {
+    const int h = e / RV, r = e - h * RV;
+    float M = NEG_INF;
+    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ws[(((long long)item * n_splits + s) * 16 + h) * (RV + 2) + RV]);
+    float L = 0.f, acc = 0.f;
+    if (M != NEG_INF) {
+      for (int s = 0; s < n_splits; ++s) {
+        const float* row = ws + (((long long)item * n_splits + s) * 16 + h) * (RV + 2);
+        const float f = __builtin_amdgcn_exp2f(row[RV] - M);
+        L += row[RV + 1] * f;
+        acc += row[r] * f;
+      }
+    }
+    OutT* o = static_cast<OutT*>(out) + ((long long)b * n_q + (long long)kvh * rep + h) * RV + r;
+    store_out(o, L > 0.f ? acc / L : 0.f);
+  }
+}
+
+// Latent append: cache[b, g, idx[b], :] = rows[b, g, :] (16-byte vector copies).
+__global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const __bf16* rows, const int32_t* idx,
+                                                          int B, int G, int S, int width) {
+  const int vec = width / 8;
+  const long long total = (long long)B * G * vec;
+  for (long long e = blockIdx.x * (long long)blockDim.x + threadIdx.x; e < total; e += (long long)gridDim.x * blockDim.x) {
+    const int v = (int)(e % vec);
+    const long long bg = e / vec;
+    const int b = (int)(bg / G);
+    const int p = idx[b];
+    if (p < 0 || p >= S) continue;
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(rows + bg * width + 8 * v);
+    *reinterpret_cast<bf16x8*>(cache + (bg * S + p) * width + 8 * v) = x;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Host side: launch configuration, validation, error reporting.
+
+thread_local char g_err[1024] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+// Waves per workgroup: 8 (two per SIMD) where the kernel fits 256 registers, else 4 (one per SIMD,
+// which lets the compiler use the full 512-entry register file instead of spilling).
+template <int RK, int RV, bool KFULL>
+constexpr int pick_nw() {
+  if (KFULL) return RV <= 96 ? 8 : 4;
+  return ((RK <= 32 && RV <= 96) || (RK == 64 && RV <= 64)) ? 8 : 4;
+}
+constexpr int MIN_NW = 4;
+constexpr int TARGET_WGS = 256;  // one workgroup per CU at full occupancy of the chip
+
+struct Plan {
+  int n_splits, split_len;
+};
+
+Plan plan_splits(int items, int S, int nw) {
+  // Positions per wave: about TARGET_WGS workgroups over the whole job, at least one rotation
+  // chunk per wave.
+  const long long total = (long long)items * S;
+  long long lw = (total + (long long)TARGET_WGS * nw - 1) / ((long long)TARGET_WGS * nw);
+  lw = ((lw + CH - 1) / CH) * CH;
+  if (lw < CH) lw = CH;
+  int split_len = (int)(lw * nw);
+  const int n_splits = (S + split_len - 1) / split_len;
+  if (n_splits == 1) {
+    // one split per item: shrink the per-wave slice so the waves of a short cache stay balanced
+    long long per_wave = ((long long)S + nw - 1) / nw;
+    per_wave = ((per_wave + CH - 1) / CH) * CH;
+    split_len = (int)(per_wave * nw);
+  }
+  return Plan{n_splits, split_len};
+}
+
+size_t ws_bytes(int items, int n_splits, int rv) {
+  return n_splits <= 1 ? 0 : (size_t)items * n_splits * 16 * (rv + 2) * sizeof(float);
+}
+
+template <int RK, int RV, bool KFULL, typename TabT, typename OutT>
+int launch(const DecodeArgs& a0, hipStream_t stream) {
+  constexpr int NW = pick_nw<RK, RV, KFULL>();
+  DecodeArgs a = a0;
+  const int items = a.B * a.n_kv;
+  const Plan p = plan_splits(items, a.S, NW);
+  a.split_len = p.split_len;
+  a.n_splits = p.n_splits;
+  const size_t need = ws_bytes(items, p.n_splits, RV);
+  if (need > 0 && (a.ws == nullptr || a.ws_bytes < need))
+    return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_decode_workspace_bytes), got %zu", need, a.ws_bytes);
+  using SM = Smem<RK, RV, KFULL, NW>;
+  auto kern = palu_decode_kernel<RK, RV, KFULL, NW, TabT, OutT>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, SM::BYTES);
+    if (e != hipSuccess) return fail(PALU_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(a.n_splits, items), dim3(NW * 64), SM::BYTES, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PALU_EHIP, "decode kernel launch: %s", hipGetErrorString(e));
+  if (a.n_splits > 1) {
+    hipLaunchKernelGGL((palu_merge_kernel<RV, OutT>), dim3(items), dim3(256), 0, stream, a.ws, a.out, a.n_splits,
+                       a.rep, a.n_q, a.n_kv);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(PALU_EHIP, "merge kernel launch: %s", hipGetErrorString(e));
+  }
+  return PALU_OK;
+}
+
+template <int RK, bool KFULL, typename TabT, typename OutT>
+int dispatch_rv(const DecodeArgs& a, int rv, hipStream_t s) {
+  switch (rv) {
+    case 32: return launch<RK, 32, KFULL, TabT, OutT>(a, s);
+    case 64: return launch<RK, 64, KFULL, TabT, OutT>(a, s);
+    case 96: return launch<RK, 96, KFULL, TabT, OutT>(a, s);
+    case 128: return launch<RK, 128, KFULL, TabT, OutT>(a, s);
+  }
+  return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128", rv);
+}
+
+template <typename TabT, typename OutT>
+int dispatch_latent(const DecodeArgs& a, int rk, int rv, hipStream_t s) {
+  switch (rk) {
+    case 32: return dispatch_rv<32, false, TabT, OutT>(a, rv, s);
+    case 64: return dispatch_rv<64, false, TabT, OutT>(a, rv, s);
+    case 96: return dispatch_rv<96, false, TabT, OutT>(a, rv, s);
+    case 128: return dispatch_rv<128, false, TabT, OutT>(a, rv, s);
+  }
+  return fail(PALU_EUNSUPPORTED, "r_k %d: this build rebuilds K from latents of width 32, 64, 96 or 128", rk);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------------------
+extern "C" {
+
+const char* palu_last_error(void) { return g_err; }
+
+int palu_abi_version(void) { return PALU_ABI_VERSION; }
+
+size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_dim_v) {
+  if (batch <= 0 || n_kv <= 0 || seq_len <= 0 || head_dim_v <= 0) return 0;
+  // The narrowest workgroup splits the most, so its plan bounds every kernel variant.
+  Plan p = plan_splits(batch * n_kv, seq_len, MIN_NW);
+  return ws_bytes(batch * n_kv, p.n_splits, head_dim_v);
+}
+
+int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab, const void* v_latent,
+                     int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step, const void* trans_mat,
+                     const void* u_v, float scale, int heads_per_core, int rot_mode, int table_mcast, int k_chunk,
+                     int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width,
+                     int cs_rows, int cs_cols, int cs_dtype, int out_dtype, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
+  g_err[0] = 0;
+  (void)table_mcast;
+  if (!q || !k_latent || !w_rot || !cs_tab || !v_latent || !cur_pos || !out)
+    return fail(PALU_EINVAL, "palu_sdpa_decode: a required tensor pointer is null");
+  if (rot_mode < 0 || rot_mode > 2) return fail(PALU_EINVAL, "rot_mode must be 'legacy', 'pack' or 'dst'");
+  if ((rot_step == nullptr) != (trans_mat == nullptr))
+    return fail(PALU_EINVAL, "rot_step and trans_mat are optional together: pass both (Phase 2) or neither (Phase 1)");
+  if (rot_step == nullptr && k_chunk > 128)
+    return fail(PALU_EINVAL, "Phase 1 streams the angle table per chunk and needs k_chunk_size <= 128, got %d", k_chunk);
+  if (k_chunk < 0 || (k_chunk > 0 && (k_chunk % 32 != 0 || (k_chunk & (k_chunk - 1)) != 0)))
+    return fail(PALU_EINVAL, "k_chunk_size must be 0 or a power of two multiple of 32, got %d", k_chunk);
+  if (batch <= 0 || n_q <= 0 || n_kv <= 0 || n_groups <= 0 || seq_len <= 0)
+    return fail(PALU_EINVAL, "palu_sdpa_decode: batch, head counts and seq_len must be positive");
+  if (r_k <= 0 || r_k % 32 != 0 || r_k > 512)
+    return fail(PALU_EINVAL, "r_k must be a multiple of 32 in 32..512 (the latent width of k_latent), got %d", r_k);
+  if (r_v <= 0 || r_v % 32 != 0 || r_v > 512)
+    return fail(PALU_EINVAL, "r_v must be a multiple of 32 in 32..512 (the latent width of v_latent), got %d", r_v);
+  if (n_kv % n_groups != 0)
+    return fail(PALU_EINVAL, "heads_per_group: %d latent heads do not divide the %d KV heads of w_rot", n_groups, n_kv);
+  const int hpg = n_kv / n_groups;
+  if (w_rot_width != 2 * HD)
+    return fail(PALU_EINVAL, "w_rot must be [1, n_kv, r_k, %d] = [u_k | u_k T], got last dim %d", 2 * HD, w_rot_width);
+  if (cs_cols != 2 * HD) return fail(PALU_EINVAL, "cs_tab must be [1, 1, S, %d] = [cos | sin], got last dim %d", 2 * HD, cs_cols);
+  if (cs_rows < seq_len)
+    return fail(PALU_EINVAL, "cs_tab has %d rows but the latent cache has %d positions", cs_rows, seq_len);
+  if (n_q % n_kv != 0 || n_q / n_kv > 16)
+    return fail(PALU_EINVAL, "KV head count %d must divide the %d query heads with at most 16 query heads per KV head", n_kv, n_q);
+  if (heads_per_core > 1) {
+    if (heads_per_core > n_kv)
+      return fail(PALU_EINVAL, "heads_per_core %d exceeds the KV head count %d", heads_per_core, n_kv);
+    if (hpg == 1) return fail(PALU_EINVAL, "heads_per_core > 1 shares a latent between heads and needs grouped latents");
+    if (hpg % heads_per_core != 0)
+      return fail(PALU_EINVAL, "heads_per_core %d must divide heads_per_group %d", heads_per_core, hpg);
+  }
+  if (u_v != nullptr) {
+    if (head_dim_v != HD) return fail(PALU_EINVAL, "head_dim_v must be %d when u_v rebuilds V in-kernel, got %d", HD, head_dim_v);
+    return fail(PALU_EUNSUPPORTED, "u_v (in-kernel V rebuild, grouped latents) is not built in this library yet");
+  }
+  if (hpg != 1) return fail(PALU_EINVAL, "grouped V latent (heads_per_group %d) needs u_v", hpg);
+  if (head_dim_v != r_v)
+    return fail(PALU_EINVAL, "head_dim_v %d must equal the V latent width %d on the absorbed-V path", head_dim_v, r_v);
+  if (cs_dtype != PALU_DTYPE_F32 && cs_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "cs_tab dtype must be fp32 or bf16");
+  if (out_dtype != PALU_DTYPE_F32 && out_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "output dtype must be fp32 or bf16");
+  if (!aligned16(q) || !aligned16(k_latent) || !aligned16(v_latent) || !aligned16(w_rot))
+    return fail(PALU_EINVAL, "q, k_latent, v_latent and w_rot must be 16-byte aligned");
+
+  const int items = batch * n_kv;
+  if ((long long)items > 65535) return fail(PALU_EUNSUPPORTED, "batch * n_kv = %d exceeds the grid limit", items);
+
+  DecodeArgs a;
+  a.q = static_cast<const __bf16*>(q);
+  a.k = static_cast<const __bf16*>(k_latent);
+  a.v = static_cast<const __bf16*>(v_latent);
+  a.w_rot = static_cast<const __bf16*>(w_rot);
+  a.cs = cs_tab;
+  a.cur_pos = cur_pos;
+  a.out = out;
+  a.ws = static_cast<float*>(workspace);
+  a.ws_bytes = workspace_bytes;
+  a.k_sg = (long long)seq_len * r_k;
+  a.k_sb = a.k_sg * n_groups;
+  a.v_sg = (long long)seq_len * r_v;
+  a.v_sb = a.v_sg * n_groups;
+  a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = hpg; a.S = seq_len; a.cs_rows = cs_rows;
+  a.qscale = scale * 1.4426950408889634f;
+
+  if (cs_dtype == PALU_DTYPE_F32) {
+    return out_dtype == PALU_DTYPE_F32 ? dispatch_latent<float, float>(a, r_k, r_v, stream)
+                                       : dispatch_latent<float, __bf16>(a, r_k, r_v, stream);
+  }
+  return out_dtype == PALU_DTYPE_F32 ? dispatch_latent<__bf16, float>(a, r_k, r_v, stream)
+                                     : dispatch_latent<__bf16, __bf16>(a, r_k, r_v, stream);
+}
+
+int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t* cur_pos, void* out, float scale,
+                      int batch, int n_q, int n_kv, int seq_len, int head_dim_v, int out_dtype, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream) {
+  g_err[0] = 0;
+  if (!q || !k || !v || !cur_pos || !out) return fail(PALU_EINVAL, "palu_flash_decode: a required tensor pointer is null");
+  if (batch <= 0 || n_q <= 0 || n_kv <= 0 || seq_len <= 0)
+    return fail(PALU_EINVAL, "palu_flash_decode: batch, head counts and seq_len must be positive");
+  if (n_q % n_kv != 0 || n_q / n_kv > 16)
+    return fail(PALU_EINVAL, "KV head count %d must divide the %d query heads with at most 16 query heads per KV head", n_kv, n_q);
+  if (out_dtype != PALU_DTYPE_F32 && out_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "output dtype must be fp32 or bf16");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return fail(PALU_EINVAL, "q, k and v must be 16-byte aligned");
+  const int items = batch * n_kv;
+  if ((long long)items > 65535) return fail(PALU_EUNSUPPORTED, "batch * n_kv = %d exceeds the grid limit", items);
+
+  DecodeArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = static_cast<const __bf16*>(q);
+  a.k = static_cast<const __bf16*>(k);
+  a.v = static_cast<const __bf16*>(v);
+  a.cur_pos = cur_pos;
+  a.out = out;
+  a.ws = static_cast<float*>(workspace);
+  a.ws_bytes = workspace_bytes;
+  a.k_sg = (long long)seq_len * HD;
+  a.k_sb = a.k_sg * n_kv;
+  a.v_sg = (long long)seq_len * head_dim_v;
+  a.v_sb = a.v_sg * n_kv;
+  a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = 1; a.S = seq_len; a.cs_rows = 0;
+  a.qscale = scale * 1.4426950408889634f;
+  const bool f32o = out_dtype == PALU_DTYPE_F32;
+  switch (head_dim_v) {
+    case 32: return f32o ? launch<HD, 32, true, float, float>(a, stream) : launch<HD, 32, true, float, __bf16>(a, stream);
+    case 64: return f32o ? launch<HD, 64, true, float, float>(a, stream) : launch<HD, 64, true, float, __bf16>(a, stream);
+    case 96: return f32o ? launch<HD, 96, true, float, float>(a, stream) : launch<HD, 96, true, float, __bf16>(a, stream);
+    case 128: return f32o ? launch<HD, 128, true, float, float>(a, stream) : launch<HD, 128, true, float, __bf16>(a, stream);
+  }
+  return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128", head_dim_v);
+}
+
+int palu_latent_append(void* cache, const void* new_rows, const int32_t* update_idxs, int batch, int n_groups,
+                       int seq_len, int width, hipStream_t stream) {
+  g_err[0] = 0;
+  if (!cache || !new_rows || !update_idxs) return fail(PALU_EINVAL, "palu_latent_append: a required pointer is null");
+  if (batch <= 0 || n_groups <= 0 || seq_len <= 0 || width <= 0 || width % 8 != 0)
+    return fail(PALU_EINVAL, "palu_latent_append: width must be a positive multiple of 8, got %d", width);
+  if (!aligned16(cache) || !aligned16(new_rows)) return fail(PALU_EINVAL, "palu_latent_append: 16-byte alignment required");
+  const long long total = (long long)batch * n_groups * (width / 8);
+  int blocks = (int)((total + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(palu_append_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<__bf16*>(cache),
+                     static_cast<const __bf16*>(new_rows), update_idxs, batch, n_groups, seq_len, width);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PALU_EHIP, "append kernel launch: %s", hipGetErrorString(e));
+  return PALU_OK;
+}
+
+}  // extern "C"

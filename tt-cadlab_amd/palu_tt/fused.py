@@ -1,0 +1,307 @@
+"""Host side of the fused latent flash-decode: the tables the kernel reads and the op entry points.
+
+Mirrors the reference module palu_tt/fused.py (table builders, fused.py:36-79) and the op it calls,
+ttnn.transformer.palu_sdpa_decode (call site palu_tt/attention.py:632-639; interface
+docs/superpowers/specs/2026-09-10-palu-tt-stage2-design.md:47-81). The op runs as hand-written HIP on
+MI355X through libpalu_mi355x.so; this module only validates, shapes and launches.
+
+Layouts (all torch tensors on the GPU unless noted):
+  q        [1, B, n_q, 128] bf16, rotated at its own position
+  k_latent [B, n_groups, S, r_k] bf16, v_latent [B, n_groups, S, r_v] bf16
+  w_rot    [1, n_kv, r_k, 256] bf16 = [u_k | u_k T]
+  cs_tab   [1, 1, >= S, 256] fp32 (or bf16) = [cos | sin], Meta-interleaved
+  cur_pos  [B] int32, inclusive last valid position per row
+The output is [1, B, n_q, head_dim_v]: head_dim_v == r_v for the absorbed-V path.
+
+The reference's Tensix switches (rot_step/trans_mat selecting Phase 2, rot_mode, table_mcast,
+heads_per_core, program_config chunk) are accepted and validated with the reference's messages. The
+MI355X kernel has one schedule: K rows are rotated by their offset inside a 128-position chunk from
+an LDS-resident table and the query is rotated back by the chunk base, which is the reference's Phase 2
+identity (fused.py:1-24) with a fixed chunk; results do not depend on those switches.
+"""
+import math
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from palu_tt import _native
+
+MAX_CHUNK = 512          # the reference's cap on the static K chunk (ttnn sdpa_decode)
+HEAD_DIM = 128
+ROT_MODES = {"legacy": 0, "pack": 1, "dst": 2}
+
+
+# ------------------------------------------------------------------------------------------------
+# Tables (palu_tt/fused.py:36-79)
+
+def rope_transformation_matrix(head_dim: int) -> torch.Tensor:
+    """[hd, hd] pair rotation: x @ T maps every adjacent pair (x0, x1) to (-x1, x0)."""
+    idx = torch.arange(0, head_dim, 2)
+    T = torch.zeros(head_dim, head_dim)
+    T[idx, idx + 1] = 1.0
+    T[idx + 1, idx] = -1.0
+    return T
+
+
+def trans_mat_tile() -> torch.Tensor:
+    """[1, 1, 32, 32]: the pair rotation on one 32-column tile (reference Phase 2 input)."""
+    return rope_transformation_matrix(32)[None, None]
+
+
+def w_rot_from_u_k(u_k: torch.Tensor) -> torch.Tensor:
+    """u_k [n_kv, r_k, hd] -> [n_kv, r_k, 2*hd] = [u_k | u_k @ T]."""
+    return torch.cat([u_k, u_k @ rope_transformation_matrix(u_k.shape[-1]).to(u_k)], dim=-1)
+
+
+def chunk_size(seq_len: int) -> int:
+    """Largest power of two dividing seq_len, capped at MAX_CHUNK (the reference's static chunk rule)."""
+    assert seq_len > 0, f"chunk_size requires seq_len > 0, got {seq_len}"
+    return min(MAX_CHUNK, seq_len & -seq_len)
+
+
+def _rope_field(rope_scaling, name, default=None):
+    if rope_scaling is None:
+        return default
+    if isinstance(rope_scaling, dict):
+        return rope_scaling.get(name, default)
+    return getattr(rope_scaling, name, default)
+
+
+def rope_frequencies(head_dim: int, theta: float, rope_scaling=None) -> torch.Tensor:
+    """fp32 [hd/2] RoPE frequencies; llama3 scaling (factor, low/high frequency factors, original
+    context) when rope_scaling carries a factor, e.g. Llama-3.1's factor 8, 1, 4, 8192."""
+    base = 1.0 / (theta ** (torch.arange(0, head_dim, 2).float() / head_dim))
+    factor = _rope_field(rope_scaling, "factor")
+    if factor is None:
+        return base
+    low = float(_rope_field(rope_scaling, "low_freq_factor", 1.0))
+    high = float(_rope_field(rope_scaling, "high_freq_factor", 4.0))
+    orig = float(_rope_field(rope_scaling, "original_max_position_embeddings", 8192))
+    wavelen = 2 * math.pi / base
+    slow = torch.where(wavelen > orig / low, base / factor, base)
+    smooth = (orig / wavelen - low) / (high - low)
+    blended = (1 - smooth) * slow / factor + smooth * slow
+    middle = ~(wavelen < orig / high) & ~(wavelen > orig / low)
+    return torch.where(middle, blended, slow).float()
+
+
+def cos_sin_tables(head_dim: int, seq_len: int, theta: float, rope_scaling=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Meta-interleaved fp32 cos, sin, each [seq_len + MAX_CHUNK + 1, head_dim] (the extra rows hold the
+    step constants): columns 2i and 2i+1 carry angle fp32(t * f_i)."""
+    n = seq_len + MAX_CHUNK + 1
+    ang = torch.outer(torch.arange(n, dtype=torch.float32), rope_frequencies(head_dim, theta, rope_scaling))
+    return (torch.repeat_interleave(ang.cos(), 2, dim=1).contiguous(),
+            torch.repeat_interleave(ang.sin(), 2, dim=1).contiguous())
+
+
+def cs_table(cos: torch.Tensor, sin: torch.Tensor, seq_len: int) -> torch.Tensor:
+    """[seq_len, 2*hd] = [cos | sin] for positions 0..seq_len-1."""
+    return torch.cat([cos[:seq_len], sin[:seq_len]], dim=-1)
+
+
+def rot_step_table(cos: torch.Tensor, sin: torch.Tensor, chunk: int) -> torch.Tensor:
+    """[32, 2*hd] fp32: [cos(chunk f) | sin(chunk f)] on every row (the reference's Phase 2 step)."""
+    return torch.cat([cos[chunk], sin[chunk]]).expand(32, -1).contiguous().float()
+
+
+def apply_rope_meta(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x * cos + (x @ T) * sin over the last dim (Meta-interleaved pairs), cos/sin broadcastable to x:
+    the rotation the reference applies to q with rotary_embedding_llama before the fused op."""
+    x2 = x.float().unflatten(-1, (-1, 2))
+    c, s = cos.float()[..., 0::2], sin.float()[..., 0::2]
+    y0 = x2[..., 0] * c - x2[..., 1] * s
+    y1 = x2[..., 1] * c + x2[..., 0] * s
+    return torch.stack((y0, y1), dim=-1).flatten(-2)
+
+
+# ------------------------------------------------------------------------------------------------
+# Program config stand-ins (the reference passes ttnn.SDPAProgramConfig / compute kernel configs)
+
+@dataclass
+class SDPAProgramConfig:
+    compute_with_storage_grid_size: Tuple[int, int] = (8, 8)
+    q_chunk_size: int = 0
+    k_chunk_size: int = 0
+    exp_approx_mode: bool = False
+
+
+def _k_chunk(program_config) -> int:
+    if program_config is None:
+        return 0
+    return int(getattr(program_config, "k_chunk_size", 0) or 0)
+
+
+def _grid_cores(program_config) -> Optional[int]:
+    grid = getattr(program_config, "compute_with_storage_grid_size", None) if program_config is not None else None
+    if grid is None:
+        return None
+    gx, gy = (grid.x, grid.y) if hasattr(grid, "x") else tuple(grid)
+    return int(gx) * int(gy)
+
+
+# ------------------------------------------------------------------------------------------------
+# Op entry points
+
+_DTYPES = {torch.float32: _native.DTYPE_F32, torch.bfloat16: _native.DTYPE_BF16}
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _as_dev(t: torch.Tensor, name: str, dtype=None, device=None) -> torch.Tensor:
+    _require(isinstance(t, torch.Tensor), f"{name} must be a torch.Tensor")
+    _require(t.is_cuda, f"{name} must live on the GPU (got {t.device})")
+    if device is not None:
+        _require(t.device == device, f"{name} is on {t.device}, expected {device}")
+    if dtype is not None:
+        _require(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+    _require(t.is_contiguous(), f"{name} must be contiguous")
+    return t
+
+
+def _workspace(batch: int, n_kv: int, seq_len: int, width: int, device, workspace):
+    need = _native.load().palu_decode_workspace_bytes(batch, n_kv, seq_len, width)
+    if need == 0:
+        return None, 0
+    if workspace is not None:
+        _require(workspace.is_cuda and workspace.numel() * workspace.element_size() >= need,
+                 f"workspace must hold {need} bytes on the GPU")
+        return workspace, workspace.numel() * workspace.element_size()
+    return torch.empty(need, dtype=torch.uint8, device=device), need
+
+
+def _cur_pos(cur_pos_tensor: torch.Tensor, batch: int, device) -> torch.Tensor:
+    _require(isinstance(cur_pos_tensor, torch.Tensor), "cur_pos_tensor must be a torch.Tensor")
+    cp = cur_pos_tensor.reshape(-1)
+    _require(cp.numel() == batch, f"cur_pos_tensor has {cp.numel()} entries for batch {batch}")
+    if cp.device != device or cp.dtype != torch.int32:
+        cp = cp.to(device=device, dtype=torch.int32)
+    return cp.contiguous()
+
+
+def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_tensor, *, rot_step=None,
+                     trans_mat=None, u_v=None, scale=None, heads_per_core=None, rot_mode="dst", table_mcast=True,
+                     program_config=None, compute_kernel_config=None, memory_config=None,
+                     out_dtype=torch.bfloat16, out=None, workspace=None) -> torch.Tensor:
+    """Fused latent flash-decode (ttnn.transformer.palu_sdpa_decode). Returns [1, B, n_q, head_dim_v].
+
+    For every p <= cur_pos[b]: K[p] = RoPE_p(k_latent[p] @ u_k) with u_k = w_rot[..., :128], then
+    softmax(q K^T * scale) over the attended rows of v_latent (absorbed V). Query head h reads KV head
+    h // (n_q // n_kv); KV head j reads latent group j // (n_kv // n_groups).
+
+    compute_kernel_config and memory_config are accepted for call compatibility and unused (the kernel
+    always accumulates in fp32; the output is a fresh tensor unless ``out`` is given).
+    """
+    del compute_kernel_config, memory_config
+    _require(isinstance(q, torch.Tensor) and q.dim() == 4 and q.shape[0] == 1 and q.shape[3] == HEAD_DIM,
+             f"q must be [1, B, n_q, {HEAD_DIM}], got {tuple(getattr(q, 'shape', ()))}")
+    dev = q.device
+    _as_dev(q, "q", torch.bfloat16)
+    _require(k_latent.dim() == 4, f"k_latent must be [B, n_groups, S, r_k], got {tuple(k_latent.shape)}")
+    _require(v_latent.dim() == 4, f"v_latent must be [B, n_groups, S, r_v], got {tuple(v_latent.shape)}")
+    _as_dev(k_latent, "k_latent", torch.bfloat16, dev)
+    _as_dev(v_latent, "v_latent", torch.bfloat16, dev)
+    B, n_groups, S, r_k = k_latent.shape
+    _require(tuple(v_latent.shape[:3]) == (B, n_groups, S),
+             f"v_latent {tuple(v_latent.shape)} does not match k_latent {tuple(k_latent.shape)} in [B, n_groups, S]")
+    r_v = v_latent.shape[3]
+    _require(q.shape[1] == B, f"q has batch {q.shape[1]} but the latent caches have {B}")
+    n_q = q.shape[2]
+    w = w_rot.reshape(-1, *w_rot.shape[-2:]) if w_rot.dim() >= 3 else w_rot
+    _require(w.dim() == 3 and (w_rot.dim() == 3 or w_rot.shape[0] == 1),
+             f"w_rot must be [1, n_kv, r_k, 256], got {tuple(w_rot.shape)}")
+    _as_dev(w, "w_rot", torch.bfloat16, dev)
+    n_kv, w_rank, w_width = w.shape
+    _require(w_rank == r_k, f"w_rot rank {w_rank} != k_latent width r_k {r_k}")
+    cs = cs_tab.reshape(-1, cs_tab.shape[-1])
+    _require(cs_tab.dim() in (2, 4), f"cs_tab must be [1, 1, S, 256], got {tuple(cs_tab.shape)}")
+    _require(cs.dtype in (torch.float32, torch.bfloat16), f"cs_tab must be fp32 or bf16, got {cs.dtype}")
+    _as_dev(cs, "cs_tab", None, dev)
+    rot = ROT_MODES.get(rot_mode, -1) if isinstance(rot_mode, str) else -1
+    if rot < 0:
+        raise RuntimeError(f"rot_mode must be 'legacy', 'pack' or 'dst', got {rot_mode!r}")
+    if heads_per_core is not None and int(heads_per_core) > 1 and program_config is not None:
+        cores = _grid_cores(program_config)
+        hpg = n_kv // n_groups if n_groups and n_kv % n_groups == 0 else 1
+        if cores is not None and hpg > 1 and int(heads_per_core) <= n_kv and hpg % int(heads_per_core) == 0:
+            items = B * (n_kv // int(heads_per_core))
+            _require(items <= cores, f"heads_per_core={heads_per_core} needs {items} cores for {B} rows of "
+                                     f"{n_kv // int(heads_per_core)} head groups, only {cores} available")
+    if out_dtype not in _DTYPES:
+        raise RuntimeError(f"out_dtype must be torch.float32 or torch.bfloat16, got {out_dtype}")
+    cp = _cur_pos(cur_pos_tensor, B, dev)
+    rs = None if rot_step is None else _as_dev(rot_step.float().contiguous(), "rot_step", torch.float32, dev)
+    tm = None if trans_mat is None else _as_dev(trans_mat.contiguous(), "trans_mat", None, dev)
+    uv = None if u_v is None else _as_dev(u_v.reshape(-1, *u_v.shape[-2:]).contiguous(), "u_v", torch.bfloat16, dev)
+    width = int(head_dim_v)
+    if out is None:
+        out = torch.empty(1, B, n_q, width, dtype=out_dtype, device=dev)
+    else:
+        _as_dev(out, "out", out_dtype, dev)
+        _require(tuple(out.shape) == (1, B, n_q, width), f"out must be [1, {B}, {n_q}, {width}]")
+    ws, ws_bytes = _workspace(B, n_kv, S, max(width, 1), dev, workspace)
+    lib = _native.load()
+    _native.check(lib.palu_sdpa_decode(
+        _native.ptr(q), _native.ptr(k_latent), _native.ptr(w), _native.ptr(cs), _native.ptr(v_latent), width,
+        _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv),
+        float(HEAD_DIM ** -0.5 if scale is None else scale), int(heads_per_core or 0), rot, int(bool(table_mcast)),
+        _k_chunk(program_config), B, n_q, n_kv, n_groups, S, r_k, r_v, w_width, cs.shape[0], cs.shape[1],
+        _DTYPES[cs.dtype], _DTYPES[out_dtype], _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
+    return out
+
+
+def flash_decode(q, k, v, cur_pos_tensor, *, scale=None, head_dim_v=None, out_dtype=torch.bfloat16, out=None,
+                 workspace=None) -> torch.Tensor:
+    """Stock flash-decode over full rotated K [B, n_kv, S, 128] and V [B, n_kv, S, head_dim_v]: the
+    MI355X counterpart of ttnn.transformer.scaled_dot_product_attention_decode (head_dim_v 128) and
+    flash_multi_latent_attention_decode (head_dim_v = V width). Returns [1, B, n_q, head_dim_v]."""
+    _require(isinstance(q, torch.Tensor) and q.dim() == 4 and q.shape[0] == 1 and q.shape[3] == HEAD_DIM,
+             f"q must be [1, B, n_q, {HEAD_DIM}]")
+    dev = q.device
+    _as_dev(q, "q", torch.bfloat16)
+    _as_dev(k, "k", torch.bfloat16, dev)
+    _as_dev(v, "v", torch.bfloat16, dev)
+    B, n_kv, S, hd = k.shape
+    _require(hd == HEAD_DIM, f"k must be [B, n_kv, S, {HEAD_DIM}], got {tuple(k.shape)}")
+    _require(tuple(v.shape[:3]) == (B, n_kv, S), f"v {tuple(v.shape)} does not match k {tuple(k.shape)}")
+    width = int(v.shape[3] if head_dim_v is None else head_dim_v)
+    _require(width == v.shape[3], f"head_dim_v {width} != V width {v.shape[3]}")
+    n_q = q.shape[2]
+    if out_dtype not in _DTYPES:
+        raise RuntimeError(f"out_dtype must be torch.float32 or torch.bfloat16, got {out_dtype}")
+    cp = _cur_pos(cur_pos_tensor, B, dev)
+    if out is None:
+        out = torch.empty(1, B, n_q, width, dtype=out_dtype, device=dev)
+    ws, ws_bytes = _workspace(B, n_kv, S, width, dev, workspace)
+    lib = _native.load()
+    _native.check(lib.palu_flash_decode(
+        _native.ptr(q), _native.ptr(k), _native.ptr(v), _native.ptr(cp), _native.ptr(out),
+        float(HEAD_DIM ** -0.5 if scale is None else scale), B, n_q, n_kv, S, width, _DTYPES[out_dtype],
+        _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
+    return out
+
+
+def scaled_dot_product_attention_decode(q, k, v, cur_pos_tensor, scale=None, **_):
+    """Name-compatible alias of the stock decode op (full K and V, head_dim_v = 128)."""
+    return flash_decode(q, k, v, cur_pos_tensor, scale=scale)
+
+
+def flash_multi_latent_attention_decode(q, k, v, head_dim_v, cur_pos_tensor, scale=None, **_):
+    """Name-compatible alias of the MLA decode op (full rotated K, V of width head_dim_v)."""
+    return flash_decode(q, k, v, cur_pos_tensor, scale=scale, head_dim_v=head_dim_v)
+
+
+def paged_update_cache(cache: torch.Tensor, new_rows: torch.Tensor, update_idxs_tensor: torch.Tensor) -> None:
+    """Latent append (ttnn.experimental.paged_update_cache on a latent cache, attention.py:622-623):
+    cache[b, g, update_idxs[b], :] = new_rows[..., b, g, :] for every b with 0 <= idx < S."""
+    _as_dev(cache, "cache", torch.bfloat16)
+    B, G, S, width = cache.shape
+    rows = new_rows.reshape(B, G, width)
+    _as_dev(rows, "new_rows", torch.bfloat16, cache.device)
+    cp = _cur_pos(update_idxs_tensor, B, cache.device)
+    lib = _native.load()
+    _native.check(lib.palu_latent_append(_native.ptr(cache), _native.ptr(rows), _native.ptr(cp), B, G, S, width,
+                                         _native.stream_handle(cache.device)))
