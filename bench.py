@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--ctx", type=int, default=8192)
     ap.add_argument("--rank-k", type=int, default=64)
     ap.add_argument("--rank-v", type=int, default=64)
+    ap.add_argument("--layout", choices=("tiled", "rows"), default="tiled",
+                    help="latent / KV cache layout: tiled (LatentCache, the fast path) or row-major [B, G, S, r]")
     ap.add_argument("--no-stock", action="store_true", help="skip the full-KV comparator")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=2, help="batch rows of the CPU baseline sample")
@@ -60,6 +62,11 @@ def svd_sigma(W, n_heads, rank):
     from palu_tt import compress
     U, VT = compress.svd_per_head(W, n_heads, rank)
     return U, VT, VT.pow(2).sum(-1)                          # row j of VT_h has norm^2 = sigma_j
+
+
+def as_layout(t, layout):
+    from palu_tt.cache import LatentCache
+    return LatentCache.from_rows(t) if layout == "tiled" else t
 
 
 def build_workload(a, dev):
@@ -85,7 +92,7 @@ def build_workload(a, dev):
     for _ in range(a.layers):
         k = (torch.randn(a.batch, NKV, a.ctx, a.rank_k, device=dev, generator=gd) * sk).to(torch.bfloat16)
         v = (torch.randn(a.batch, NKV, a.ctx, a.rank_v, device=dev, generator=gd) * sv).to(torch.bfloat16)
-        layers.append((k, v))
+        layers.append((as_layout(k, a.layout), as_layout(v, a.layout)))
     cur = torch.full((a.batch,), a.ctx - 1, dtype=torch.int32, device=dev)
     return dict(q=q, w_rot=w_rot, cs=cs, layers=layers, cur=cur, u_k=u_k, cos=cos, sin=sin)
 
@@ -124,6 +131,8 @@ def cpu_baseline(a, wl):
     torch.set_num_threads(cores)
     rows = max(1, min(a.cpu_rows, a.batch))
     k, v = wl["layers"][0]
+    if not isinstance(k, torch.Tensor):
+        k, v = k.to_rows(), v.to_rows()
     kc, vc = k[:rows].float().cpu(), v[:rows].float().cpu()
     qc = wl["q"][:, :rows].float().cpu()
     u_k = wl["w_rot"][0, :, :, :HD].float().cpu()
@@ -181,7 +190,8 @@ def main():
         "data": "synthetic (seeded: SVD-spectrum latents, random-init projections)",
         "config": {"workload": "M-LRD fused latent flash-decode, one Llama-3.1-8B attention layer", "batch": B,
                    "ctx": S, "cur_pos": S - 1, "n_q": NQ, "n_kv": NKV, "head_dim": HD, "rank_k": rk, "rank_v": rv,
-                   "latent_dtype": "bf16", "absorbed_v": True, "layer_caches_rotated": a.layers,
+                   "latent_dtype": "bf16", "absorbed_v": True, "cache_layout": a.layout,
+                   "layer_caches_rotated": a.layers,
                    "rope": "llama3 theta 5e5 factor 8"},
         "kernel_us": round(kern_ms * 1e3, 2),
         "kernel_us_min": round(min(per) * 1e3, 2),
@@ -198,8 +208,9 @@ def main():
         torch.cuda.empty_cache()
         n_stock = max(1, min(a.layers, 4))
         gd = torch.Generator(device=dev).manual_seed(2)
-        kv = [(torch.randn(B, NKV, S, HD, device=dev, generator=gd).to(torch.bfloat16),
-               torch.randn(B, NKV, S, HD, device=dev, generator=gd).to(torch.bfloat16)) for _ in range(n_stock)]
+        kv = [(as_layout(torch.randn(B, NKV, S, HD, device=dev, generator=gd).to(torch.bfloat16), a.layout),
+               as_layout(torch.randn(B, NKV, S, HD, device=dev, generator=gd).to(torch.bfloat16), a.layout))
+              for _ in range(n_stock)]
         out_s = torch.empty(1, B, NQ, HD, dtype=torch.bfloat16, device=dev)
         ws_s = torch.empty(max(fused._native.load().palu_decode_workspace_bytes(B, NKV, S, HD), 1),
                            dtype=torch.uint8, device=dev)
@@ -212,7 +223,7 @@ def main():
         res["stock_full_kv"] = {"us_per_layer": round(s_wall * 1e3, 2), "kernel_us": round(s_kern * 1e3, 2),
                                 "achieved_GBps": round(s_bytes / (s_kern * 1e-3) / 1e9, 1),
                                 "frac": round(s_bytes / (s_kern * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                                "bytes": s_bytes, "layer_caches_rotated": n_stock}
+                                "bytes": s_bytes, "layer_caches_rotated": n_stock, "cache_layout": a.layout}
         res["speedup_vs_stock"] = round(s_wall / wall_ms, 3)
         del kv
         wl["layers"] = None

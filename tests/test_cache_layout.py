@@ -1,0 +1,38 @@
+"""Tiled latent-cache layout: round trip and the slot -> (position, width index) mapping the kernel reads."""
+import pytest
+import torch
+
+from palu_tt.cache import LatentCache, rows_to_tiled, tiled_to_rows
+
+
+@pytest.mark.parametrize("S,r", [(32, 32), (64, 64), (256, 96), (96, 128)])
+def test_round_trip_is_exact(S, r):
+    rows = torch.randn(2, 3, S, r).to(torch.bfloat16)
+    tiled = rows_to_tiled(rows)
+    assert tiled.shape == (2, 3, S // 32, 2 * r // 32, 64, 8)
+    assert torch.equal(tiled_to_rows(tiled), rows)
+
+
+def test_slot_mapping_matches_the_documented_operand_order():
+    """Tile (c, kb), slot l = 16*g + n holds r-index 32*kb + 8*g + j of position 32*blk + 8*(n//4) + 4*c + n%4."""
+    S, r = 64, 64
+    pos = torch.arange(S)[:, None].expand(S, r)
+    col = torch.arange(r)[None, :].expand(S, r)
+    code = (pos * 1000 + col).float()[None, None]          # exact in fp32
+    tiled = rows_to_tiled(code)
+    for blk in range(S // 32):
+        for c in range(2):
+            for kb in range(r // 32):
+                for l in range(64):
+                    g, n = divmod(l, 16)
+                    p = 32 * blk + 8 * (n // 4) + 4 * c + n % 4
+                    for j in range(8):
+                        assert tiled[0, 0, blk, c * (r // 32) + kb, l, j] == p * 1000 + 32 * kb + 8 * g + j
+
+
+def test_latent_cache_reports_logical_shape():
+    lc = LatentCache.zeros(2, 8, 128, 64, device="cpu")
+    assert lc.shape == (2, 8, 128, 64) and lc.dtype == torch.bfloat16
+    assert lc.nbytes() == 2 * 8 * 128 * 64 * 2
+    rows = torch.randn(2, 8, 128, 64).to(torch.bfloat16)
+    assert torch.equal(LatentCache.from_rows(rows).to_rows(), rows)

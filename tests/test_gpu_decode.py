@@ -191,3 +191,63 @@ def test_fused_reads_appended_rows(gpu):
                                  out_dtype=torch.float32)
     torch.cuda.synchronize()
     _check(out.cpu(), exp)
+
+
+# ---------------- tiled HBM layout (LatentCache) ----------------
+
+from palu_tt.cache import LatentCache  # noqa: E402
+
+
+@pytest.mark.parametrize("B,S,r_k,r_v", [(4, 1024, 64, 64), (1, 8192, 64, 64), (3, 320, 32, 128), (2, 2048, 128, 96),
+                                         (32, 256, 96, 32)])
+def test_tiled_layout_is_bit_identical_to_rows(gpu, B, S, r_k, r_v):
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(B, S, r_k, r_v)
+    rows_out = _run_fused(gpu, q, k_lat, u_k, v, pos, cos, sin, S)
+    w_rot = ref.w_rot_from_u_k(u_k)[None].to(gpu, torch.bfloat16)
+    cs = ref.cs_table(cos, sin, S)[None, None].to(gpu)
+    kc = LatentCache.from_rows(k_lat.to(gpu, torch.bfloat16))
+    vc = LatentCache.from_rows(v.to(gpu, torch.bfloat16))
+    out = fused.palu_sdpa_decode(q.to(gpu, torch.bfloat16), kc, w_rot, cs, vc, r_v, pos.to(gpu, torch.int32),
+                                 scale=HD ** -0.5, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), rows_out)
+    _check(out.cpu(), ref.reference_decode(q, k_lat, u_k, v, pos, cos, sin, HD ** -0.5))
+
+
+def test_tiled_append_then_decode(gpu):
+    B, S = 4, 256
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(B, S, 64, 64)
+    pos[:] = torch.tensor([10, 255, 127, 128])
+    new_k = _bf(torch.randn(1, B, 8, 64))
+    new_v = _bf(torch.randn(1, B, 8, 64))
+    kc = LatentCache.from_rows(k_lat.to(gpu, torch.bfloat16))
+    vc = LatentCache.from_rows(v.to(gpu, torch.bfloat16))
+    dpos = pos.to(gpu, torch.int32)
+    fused.paged_update_cache(kc, new_k.to(gpu, torch.bfloat16), dpos)
+    fused.paged_update_cache(vc, new_v.to(gpu, torch.bfloat16), dpos)
+    k_full, v_full = k_lat.clone(), v.clone()
+    for b in range(B):
+        k_full[b, :, pos[b]] = new_k[0, b]
+        v_full[b, :, pos[b]] = new_v[0, b]
+    torch.cuda.synchronize()
+    assert torch.equal(kc.to_rows().float().cpu(), k_full) and torch.equal(vc.to_rows().float().cpu(), v_full)
+    w_rot = ref.w_rot_from_u_k(u_k)[None].to(gpu, torch.bfloat16)
+    cs = ref.cs_table(cos, sin, S)[None, None].to(gpu)
+    out = fused.palu_sdpa_decode(q.to(gpu, torch.bfloat16), kc, w_rot, cs, vc, 64, dpos, scale=HD ** -0.5,
+                                 out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _check(out.cpu(), ref.reference_decode(q, k_full, u_k, v_full, pos, cos, sin, HD ** -0.5))
+
+
+@pytest.mark.parametrize("B,S,dv", [(4, 1024, 128), (1, 8192, 128), (3, 320, 64)])
+def test_stock_tiled_is_bit_identical_to_rows(gpu, B, S, dv):
+    g = torch.Generator().manual_seed(3)
+    q = _bf(torch.randn(1, B, 32, HD, generator=g)).to(gpu, torch.bfloat16)
+    k = _bf(torch.randn(B, 8, S, HD, generator=g)).to(gpu, torch.bfloat16)
+    v = _bf(torch.randn(B, 8, S, dv, generator=g)).to(gpu, torch.bfloat16)
+    pos = torch.randint(0, S, (B,), generator=g).to(gpu, torch.int32)
+    a = fused.flash_decode(q, k, v, pos, scale=HD ** -0.5, out_dtype=torch.float32)
+    b = fused.flash_decode(q, LatentCache.from_rows(k), LatentCache.from_rows(v), pos, scale=HD ** -0.5,
+                           out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(a.cpu(), b.cpu())

@@ -12,6 +12,11 @@
 //   * A workgroup owns one item and one split of its sequence; its NW waves each own a contiguous
 //     slice of that split, so a wave streams its latent rows straight from HBM into registers with
 //     16-byte loads, one block of 32 positions at a time, prefetching the next block.
+//   * Two cache layouts. ROWS is the reference's logical [B, G, S, r] row-major tensor. TILED stores
+//     every 32-position block as (2 * r / 32) tiles of 1 KB already in MFMA operand order (tile (c, kb),
+//     slot l = 16*g + n holds ranks 32*kb + 8*g .. +7 of position 8*(n/4) + 4*c + n%4 of the block), so
+//     each wave load instruction is one contiguous 1 KB and is issued nontemporal (the stream is read
+//     once per decode step).
 //   * K is rebuilt transposed, K^T[d][p] = u_k^T[d][:] . lat[p][:]: the accumulator layout then gives
 //     every lane one position and 4 consecutive head dims per 16-dim tile, so each RoPE pair
 //     (Meta-interleaved dims 2f, 2f+1) sits in one lane and the rotation is plain VALU work on the
@@ -115,7 +120,17 @@ struct Smem {
   static constexpr int BYTES = MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES;
 };
 
-template <int RK, int RV, bool KFULL, int NW, typename TabT, typename OutT>
+template <typename T>
+__device__ __forceinline__ float4 load4f(const T* p);
+template <>
+__device__ __forceinline__ float4 load4f<float>(const float* p) { return *reinterpret_cast<const float4*>(p); }
+template <>
+__device__ __forceinline__ float4 load4f<__bf16>(const __bf16* p) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+  return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+}
+
+template <int RK, int RV, bool KFULL, bool TILED, int NW, typename TabT, typename OutT>
 __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a) {
   static_assert(RK % 32 == 0 && RK <= 128, "RK");
   static_assert(RV % 32 == 0 && RV <= 128, "RV");
@@ -144,6 +159,43 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   const int w_lo = s_lo + w * Lw;
   const int w_hi = min(s_hi, w_lo + Lw);
 
+  const __bf16* kbase = a.k + b * a.k_sb + grp * a.k_sg;
+  const __bf16* vbase = a.v + b * a.v_sb + grp * a.v_sg;
+
+  // Latent / K / V rows of one block into registers. Lane row n of tile c is position
+  // base + 8*(n/4) + 4*c + n%4; ROWS clamps rows past the cache end (their scores are masked).
+  auto load_blk = [&](int base, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[2][VB]) {
+    if constexpr (TILED) {
+      const __bf16* kt = kbase + (long long)(base >> 5) * (32 * RK) + lane * 8;
+      const __bf16* vt = vbase + (long long)(base >> 5) * (32 * RV) + lane * 8;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+          kd[c][kb] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(kt + (c * KB + kb) * 512));
+#pragma unroll
+        for (int vb = 0; vb < VB; ++vb)
+          vd[c][vb] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(vt + (c * VB + vb) * 512));
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        int p = base + 8 * (n >> 2) + 4 * c + (n & 3);
+        p = p < a.S ? p : a.S - 1;
+        const __bf16* kr = kbase + (long long)p * RK + 8 * g;
+        const __bf16* vr = vbase + (long long)p * RV + 8 * g;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) kd[c][kb] = *reinterpret_cast<const bf16x8*>(kr + 32 * kb);
+#pragma unroll
+        for (int vb = 0; vb < VB; ++vb) vd[c][vb] = *reinterpret_cast<const bf16x8*>(vr + 32 * vb);
+      }
+    }
+  };
+
+  // The first block's loads go out before the prologue so its HBM latency overlaps the table build.
+  bf16x8 kl[2][KB], vl[2][VB], kln[2][KB], vln[2][VB];
+  if (w_lo < w_hi) load_blk(w_lo, kl, vl);
+
   // ---- prologue: chunk-relative angle table and u_k^T in LDS ------------------------------------
   if constexpr (!KFULL) {
     const TabT* cs = static_cast<const TabT*>(a.cs);
@@ -155,13 +207,14 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       float4 v = make_float4(1.f, 0.f, 1.f, 0.f);
       if (t < a.cs_rows) {
         const TabT* row = cs + (long long)t * (2 * HD);
-        v = make_float4(to_f(row[col]), to_f(row[HD + col]), to_f(row[col + 2]), to_f(row[HD + col + 2]));
+        const float4 cv = load4f(row + col), sv = load4f(row + HD + col);  // {c_f, c_f, c_f+1, c_f+1}
+        v = make_float4(cv.x, sv.x, cv.z, sv.z);
       }
       rtab[e] = v;
     }
     const __bf16* uk = a.w_rot + (long long)kvh * RK * (2 * HD);
     for (int e = tid; e < RK * (HD / 8); e += NW * 64) {
-      const int r = e / (HD / 8), d0 = (e % (HD / 8)) * 8;
+      const int r = e % RK, d0 = (e / RK) * 8;  // consecutive lanes: consecutive ranks, one column block
       const bf16x8 v = *reinterpret_cast<const bf16x8*>(uk + (long long)r * (2 * HD) + d0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) ukT[(d0 + i) * SM::UKT_STRIDE + r] = v[i];
@@ -194,8 +247,6 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
 
   const bool qvalid = n < a.rep;
   const __bf16* qrow = a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + (qvalid ? n : 0)) * HD;
-  const __bf16* kbase = a.k + b * a.k_sb + grp * a.k_sg;
-  const __bf16* vbase = a.v + b * a.v_sb + grp * a.v_sg;
 
   // Query operand. Latent mode: q~ = R_{-s0} q * qscale with the head dim contracted in the order
   // d(kb, g, j) = 16*(2*kb + j/4) + 4*g + j%4, which is the order the rebuilt K^T tile has in
@@ -214,8 +265,8 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       for (int rt = 0; rt < 8; ++rt) {
         const int col = 16 * rt + 4 * g;
         const bf16x4 x = *reinterpret_cast<const bf16x4*>(qrow + col);
-        const float c0 = to_f(row[col]), sn0 = to_f(row[HD + col]);
-        const float c1 = to_f(row[col + 2]), sn1 = to_f(row[HD + col + 2]);
+        const float4 cv = load4f(row + col), sv = load4f(row + HD + col);
+        const float c0 = cv.x, sn0 = sv.x, c1 = cv.z, sn1 = sv.z;
         const float x0 = (float)x[0], x1 = (float)x[1], x2 = (float)x[2], x3 = (float)x[3];
         const float s = qvalid ? a.qscale : 0.f;
         const int kb = rt >> 1, j0 = 4 * (rt & 1);
@@ -224,22 +275,6 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
         qB[kb][j0 + 2] = (__bf16)((x2 * c1 + x3 * sn1) * s);
         qB[kb][j0 + 3] = (__bf16)((x3 * c1 - x2 * sn1) * s);
       }
-    }
-  };
-
-  // Latent / K / V rows of one block. Lane row n of tile c is position base + 8*(n/4) + 4*c + n%4;
-  // rows past the cache end are clamped (their scores are masked).
-  auto load_blk = [&](int base, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[2][VB]) {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      int p = base + 8 * (n >> 2) + 4 * c + (n & 3);
-      p = p < a.S ? p : a.S - 1;
-      const __bf16* kr = kbase + (long long)p * RK + 8 * g;
-      const __bf16* vr = vbase + (long long)p * RV + 8 * g;
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) kd[c][kb] = *reinterpret_cast<const bf16x8*>(kr + 32 * kb);
-#pragma unroll
-      for (int vb = 0; vb < VB; ++vb) vd[c][vb] = *reinterpret_cast<const bf16x8*>(vr + 32 * vb);
     }
   };
 
@@ -338,9 +373,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     }
   };
 
-  bf16x8 kl[2][KB], vl[2][VB], kln[2][KB], vln[2][VB];
   int base = w_lo;
-  if (base < w_hi) load_blk(base, kl, vl);
   while (base < w_hi) {
     step(base, kl, vl, kln, vln);
     base += BLK;
@@ -412,7 +445,15 @@ __global__ __launch_bounds__(256) void palu_merge_kernel(const float* ws, void* 
   }
 }
 
-// Latent append: cache[b, g, idx[b], :] = rows[b, g, :] (16-byte vector copies).
+// Offset (elements) of rank k of position p inside one (b, g) stream of a TILED cache of width R.
+__device__ __forceinline__ long long tiled_offset(int p, int k, int R) {
+  const int t = p & 31, c = (t >> 2) & 1, nn = ((t >> 3) << 2) | (t & 3);
+  const int kb = k >> 5, gg = (k >> 3) & 3;
+  return (long long)(p >> 5) * (32 * R) + ((c * (R >> 5) + kb) * 64 + 16 * gg + nn) * 8 + (k & 7);
+}
+
+// Latent append: cache[b, g, idx[b], :] = rows[b, g, :], one 16-byte vector (8 ranks) per thread.
+template <bool TILED>
 __global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const __bf16* rows, const int32_t* idx,
                                                           int B, int G, int S, int width) {
   const int vec = width / 8;
@@ -424,7 +465,8 @@ __global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const _
     const int p = idx[b];
     if (p < 0 || p >= S) continue;
     const bf16x8 x = *reinterpret_cast<const bf16x8*>(rows + bg * width + 8 * v);
-    *reinterpret_cast<bf16x8*>(cache + (bg * S + p) * width + 8 * v) = x;
+    const long long off = TILED ? bg * S * width + tiled_offset(p, 8 * v, width) : (bg * S + p) * width + 8 * v;
+    *reinterpret_cast<bf16x8*>(cache + off) = x;
   }
 }
 
@@ -477,7 +519,7 @@ size_t ws_bytes(int items, int n_splits, int rv) {
   return n_splits <= 1 ? 0 : (size_t)items * n_splits * 16 * (rv + 2) * sizeof(float);
 }
 
-template <int RK, int RV, bool KFULL, typename TabT, typename OutT>
+template <int RK, int RV, bool KFULL, bool TILED, typename TabT, typename OutT>
 int launch(const DecodeArgs& a0, hipStream_t stream) {
   constexpr int NW = pick_nw<RK, RV, KFULL>();
   DecodeArgs a = a0;
@@ -489,7 +531,7 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
   if (need > 0 && (a.ws == nullptr || a.ws_bytes < need))
     return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_decode_workspace_bytes), got %zu", need, a.ws_bytes);
   using SM = Smem<RK, RV, KFULL, NW>;
-  auto kern = palu_decode_kernel<RK, RV, KFULL, NW, TabT, OutT>;
+  auto kern = palu_decode_kernel<RK, RV, KFULL, TILED, NW, TabT, OutT>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, SM::BYTES);
@@ -508,29 +550,56 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
   return PALU_OK;
 }
 
-template <int RK, bool KFULL, typename TabT, typename OutT>
+template <int RK, bool KFULL, bool TILED, typename TabT, typename OutT>
 int dispatch_rv(const DecodeArgs& a, int rv, hipStream_t s) {
   switch (rv) {
-    case 32: return launch<RK, 32, KFULL, TabT, OutT>(a, s);
-    case 64: return launch<RK, 64, KFULL, TabT, OutT>(a, s);
-    case 96: return launch<RK, 96, KFULL, TabT, OutT>(a, s);
-    case 128: return launch<RK, 128, KFULL, TabT, OutT>(a, s);
+    case 32: return launch<RK, 32, KFULL, TILED, TabT, OutT>(a, s);
+    case 64: return launch<RK, 64, KFULL, TILED, TabT, OutT>(a, s);
+    case 96: return launch<RK, 96, KFULL, TILED, TabT, OutT>(a, s);
+    case 128: return launch<RK, 128, KFULL, TILED, TabT, OutT>(a, s);
   }
   return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128", rv);
 }
 
-template <typename TabT, typename OutT>
+template <bool TILED, typename TabT, typename OutT>
 int dispatch_latent(const DecodeArgs& a, int rk, int rv, hipStream_t s) {
   switch (rk) {
-    case 32: return dispatch_rv<32, false, TabT, OutT>(a, rv, s);
-    case 64: return dispatch_rv<64, false, TabT, OutT>(a, rv, s);
-    case 96: return dispatch_rv<96, false, TabT, OutT>(a, rv, s);
-    case 128: return dispatch_rv<128, false, TabT, OutT>(a, rv, s);
+    case 32: return dispatch_rv<32, false, TILED, TabT, OutT>(a, rv, s);
+    case 64: return dispatch_rv<64, false, TILED, TabT, OutT>(a, rv, s);
+    case 96: return dispatch_rv<96, false, TILED, TabT, OutT>(a, rv, s);
+    case 128: return dispatch_rv<128, false, TILED, TabT, OutT>(a, rv, s);
   }
   return fail(PALU_EUNSUPPORTED, "r_k %d: this build rebuilds K from latents of width 32, 64, 96 or 128", rk);
 }
 
+template <typename TabT, typename OutT>
+int dispatch_layout(const DecodeArgs& a, int layout, int rk, int rv, hipStream_t s) {
+  return layout == PALU_LAYOUT_TILED ? dispatch_latent<true, TabT, OutT>(a, rk, rv, s)
+                                     : dispatch_latent<false, TabT, OutT>(a, rk, rv, s);
+}
+
+template <bool TILED>
+int dispatch_full(const DecodeArgs& a, int dv, bool f32o, hipStream_t s) {
+  using B16 = __bf16;
+  switch (dv) {
+    case 32: return f32o ? launch<HD, 32, true, TILED, float, float>(a, s) : launch<HD, 32, true, TILED, float, B16>(a, s);
+    case 64: return f32o ? launch<HD, 64, true, TILED, float, float>(a, s) : launch<HD, 64, true, TILED, float, B16>(a, s);
+    case 96: return f32o ? launch<HD, 96, true, TILED, float, float>(a, s) : launch<HD, 96, true, TILED, float, B16>(a, s);
+    case 128: return f32o ? launch<HD, 128, true, TILED, float, float>(a, s) : launch<HD, 128, true, TILED, float, B16>(a, s);
+  }
+  return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128", dv);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_layout(int layout, int seq_len, const char* who) {
+  if (layout != PALU_LAYOUT_ROWS && layout != PALU_LAYOUT_TILED)
+    return fail(PALU_EINVAL, "%s: cache layout must be PALU_LAYOUT_ROWS or PALU_LAYOUT_TILED, got %d", who, layout);
+  if (layout == PALU_LAYOUT_TILED && seq_len % 32 != 0)
+    return fail(PALU_EINVAL, "%s: a tiled cache holds whole 32-position blocks; seq_len %d is not a multiple of 32", who,
+                seq_len);
+  return PALU_OK;
+}
 
 }  // namespace
 
@@ -552,8 +621,8 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
                      int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step, const void* trans_mat,
                      const void* u_v, float scale, int heads_per_core, int rot_mode, int table_mcast, int k_chunk,
                      int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width,
-                     int cs_rows, int cs_cols, int cs_dtype, int out_dtype, void* workspace, size_t workspace_bytes,
-                     hipStream_t stream) {
+                     int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, void* workspace,
+                     size_t workspace_bytes, hipStream_t stream) {
   g_err[0] = 0;
   (void)table_mcast;
   if (!q || !k_latent || !w_rot || !cs_tab || !v_latent || !cur_pos || !out)
@@ -597,13 +666,15 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
     return fail(PALU_EINVAL, "head_dim_v %d must equal the V latent width %d on the absorbed-V path", head_dim_v, r_v);
   if (cs_dtype != PALU_DTYPE_F32 && cs_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "cs_tab dtype must be fp32 or bf16");
   if (out_dtype != PALU_DTYPE_F32 && out_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "output dtype must be fp32 or bf16");
-  if (!aligned16(q) || !aligned16(k_latent) || !aligned16(v_latent) || !aligned16(w_rot))
-    return fail(PALU_EINVAL, "q, k_latent, v_latent and w_rot must be 16-byte aligned");
+  if (int rc = check_layout(cache_layout, seq_len, "palu_sdpa_decode")) return rc;
+  if (!aligned16(q) || !aligned16(k_latent) || !aligned16(v_latent) || !aligned16(w_rot) || !aligned16(cs_tab))
+    return fail(PALU_EINVAL, "q, k_latent, v_latent, w_rot and cs_tab must be 16-byte aligned");
 
   const int items = batch * n_kv;
   if ((long long)items > 65535) return fail(PALU_EUNSUPPORTED, "batch * n_kv = %d exceeds the grid limit", items);
 
   DecodeArgs a;
+  memset(&a, 0, sizeof(a));
   a.q = static_cast<const __bf16*>(q);
   a.k = static_cast<const __bf16*>(k_latent);
   a.v = static_cast<const __bf16*>(v_latent);
@@ -621,16 +692,16 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
   a.qscale = scale * 1.4426950408889634f;
 
   if (cs_dtype == PALU_DTYPE_F32) {
-    return out_dtype == PALU_DTYPE_F32 ? dispatch_latent<float, float>(a, r_k, r_v, stream)
-                                       : dispatch_latent<float, __bf16>(a, r_k, r_v, stream);
+    return out_dtype == PALU_DTYPE_F32 ? dispatch_layout<float, float>(a, cache_layout, r_k, r_v, stream)
+                                       : dispatch_layout<float, __bf16>(a, cache_layout, r_k, r_v, stream);
   }
-  return out_dtype == PALU_DTYPE_F32 ? dispatch_latent<__bf16, float>(a, r_k, r_v, stream)
-                                     : dispatch_latent<__bf16, __bf16>(a, r_k, r_v, stream);
+  return out_dtype == PALU_DTYPE_F32 ? dispatch_layout<__bf16, float>(a, cache_layout, r_k, r_v, stream)
+                                     : dispatch_layout<__bf16, __bf16>(a, cache_layout, r_k, r_v, stream);
 }
 
 int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t* cur_pos, void* out, float scale,
-                      int batch, int n_q, int n_kv, int seq_len, int head_dim_v, int out_dtype, void* workspace,
-                      size_t workspace_bytes, hipStream_t stream) {
+                      int batch, int n_q, int n_kv, int seq_len, int head_dim_v, int out_dtype, int cache_layout,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
   g_err[0] = 0;
   if (!q || !k || !v || !cur_pos || !out) return fail(PALU_EINVAL, "palu_flash_decode: a required tensor pointer is null");
   if (batch <= 0 || n_q <= 0 || n_kv <= 0 || seq_len <= 0)
@@ -638,6 +709,7 @@ int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t
   if (n_q % n_kv != 0 || n_q / n_kv > 16)
     return fail(PALU_EINVAL, "KV head count %d must divide the %d query heads with at most 16 query heads per KV head", n_kv, n_q);
   if (out_dtype != PALU_DTYPE_F32 && out_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "output dtype must be fp32 or bf16");
+  if (int rc = check_layout(cache_layout, seq_len, "palu_flash_decode")) return rc;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return fail(PALU_EINVAL, "q, k and v must be 16-byte aligned");
   const int items = batch * n_kv;
   if ((long long)items > 65535) return fail(PALU_EUNSUPPORTED, "batch * n_kv = %d exceeds the grid limit", items);
@@ -658,27 +730,29 @@ int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t
   a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = 1; a.S = seq_len; a.cs_rows = 0;
   a.qscale = scale * 1.4426950408889634f;
   const bool f32o = out_dtype == PALU_DTYPE_F32;
-  switch (head_dim_v) {
-    case 32: return f32o ? launch<HD, 32, true, float, float>(a, stream) : launch<HD, 32, true, float, __bf16>(a, stream);
-    case 64: return f32o ? launch<HD, 64, true, float, float>(a, stream) : launch<HD, 64, true, float, __bf16>(a, stream);
-    case 96: return f32o ? launch<HD, 96, true, float, float>(a, stream) : launch<HD, 96, true, float, __bf16>(a, stream);
-    case 128: return f32o ? launch<HD, 128, true, float, float>(a, stream) : launch<HD, 128, true, float, __bf16>(a, stream);
-  }
-  return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128", head_dim_v);
+  return cache_layout == PALU_LAYOUT_TILED ? dispatch_full<true>(a, head_dim_v, f32o, stream)
+                                           : dispatch_full<false>(a, head_dim_v, f32o, stream);
 }
 
 int palu_latent_append(void* cache, const void* new_rows, const int32_t* update_idxs, int batch, int n_groups,
-                       int seq_len, int width, hipStream_t stream) {
+                       int seq_len, int width, int cache_layout, hipStream_t stream) {
   g_err[0] = 0;
   if (!cache || !new_rows || !update_idxs) return fail(PALU_EINVAL, "palu_latent_append: a required pointer is null");
   if (batch <= 0 || n_groups <= 0 || seq_len <= 0 || width <= 0 || width % 8 != 0)
     return fail(PALU_EINVAL, "palu_latent_append: width must be a positive multiple of 8, got %d", width);
+  if (int rc = check_layout(cache_layout, seq_len, "palu_latent_append")) return rc;
+  if (cache_layout == PALU_LAYOUT_TILED && width % 32 != 0)
+    return fail(PALU_EINVAL, "palu_latent_append: a tiled cache row is a multiple of 32 wide, got %d", width);
   if (!aligned16(cache) || !aligned16(new_rows)) return fail(PALU_EINVAL, "palu_latent_append: 16-byte alignment required");
   const long long total = (long long)batch * n_groups * (width / 8);
   int blocks = (int)((total + 255) / 256);
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(palu_append_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<__bf16*>(cache),
-                     static_cast<const __bf16*>(new_rows), update_idxs, batch, n_groups, seq_len, width);
+  if (cache_layout == PALU_LAYOUT_TILED)
+    hipLaunchKernelGGL(palu_append_kernel<true>, dim3(blocks), dim3(256), 0, stream, static_cast<__bf16*>(cache),
+                       static_cast<const __bf16*>(new_rows), update_idxs, batch, n_groups, seq_len, width);
+  else
+    hipLaunchKernelGGL(palu_append_kernel<false>, dim3(blocks), dim3(256), 0, stream, static_cast<__bf16*>(cache),
+                       static_cast<const __bf16*>(new_rows), update_idxs, batch, n_groups, seq_len, width);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "append kernel launch: %s", hipGetErrorString(e));
   return PALU_OK;

@@ -12,6 +12,8 @@ Layouts (all torch tensors on the GPU unless noted):
   cs_tab   [1, 1, >= S, 256] fp32 (or bf16) = [cos | sin], Meta-interleaved
   cur_pos  [B] int32, inclusive last valid position per row
 The output is [1, B, n_q, head_dim_v]: head_dim_v == r_v for the absorbed-V path.
+Either cache may instead be a ``palu_tt.cache.LatentCache`` (same logical shape, tiled HBM layout, the
+fast path); both caches of one call use the same layout.
 
 The reference's Tensix switches (rot_step/trans_mat selecting Phase 2, rot_mode, table_mcast,
 heads_per_core, program_config chunk) are accepted and validated with the reference's messages. The
@@ -26,6 +28,7 @@ from typing import Optional, Tuple
 import torch
 
 from palu_tt import _native
+from palu_tt.cache import LatentCache
 
 MAX_CHUNK = 512          # the reference's cap on the static K chunk (ttnn sdpa_decode)
 HEAD_DIM = 128
@@ -162,6 +165,16 @@ def _as_dev(t: torch.Tensor, name: str, dtype=None, device=None) -> torch.Tensor
     return t
 
 
+def _cache_arg(t, name: str, device):
+    """(storage tensor, logical shape, layout id) of a row-major tensor or a LatentCache."""
+    if isinstance(t, LatentCache):
+        _as_dev(t.data, name, torch.bfloat16, device)
+        return t.data, tuple(t.shape), _native.LAYOUT_TILED
+    _require(isinstance(t, torch.Tensor) and t.dim() == 4, f"{name} must be [B, n_groups, S, width] or a LatentCache")
+    _as_dev(t, name, torch.bfloat16, device)
+    return t, tuple(t.shape), _native.LAYOUT_ROWS
+
+
 def _workspace(batch: int, n_kv: int, seq_len: int, width: int, device, workspace):
     need = _native.load().palu_decode_workspace_bytes(batch, n_kv, seq_len, width)
     if need == 0:
@@ -200,14 +213,13 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
              f"q must be [1, B, n_q, {HEAD_DIM}], got {tuple(getattr(q, 'shape', ()))}")
     dev = q.device
     _as_dev(q, "q", torch.bfloat16)
-    _require(k_latent.dim() == 4, f"k_latent must be [B, n_groups, S, r_k], got {tuple(k_latent.shape)}")
-    _require(v_latent.dim() == 4, f"v_latent must be [B, n_groups, S, r_v], got {tuple(v_latent.shape)}")
-    _as_dev(k_latent, "k_latent", torch.bfloat16, dev)
-    _as_dev(v_latent, "v_latent", torch.bfloat16, dev)
-    B, n_groups, S, r_k = k_latent.shape
-    _require(tuple(v_latent.shape[:3]) == (B, n_groups, S),
-             f"v_latent {tuple(v_latent.shape)} does not match k_latent {tuple(k_latent.shape)} in [B, n_groups, S]")
-    r_v = v_latent.shape[3]
+    k_store, k_shape, layout = _cache_arg(k_latent, "k_latent", dev)
+    v_store, v_shape, v_layout = _cache_arg(v_latent, "v_latent", dev)
+    _require(layout == v_layout, "k_latent and v_latent must use the same cache layout")
+    B, n_groups, S, r_k = k_shape
+    _require(tuple(v_shape[:3]) == (B, n_groups, S),
+             f"v_latent {v_shape} does not match k_latent {k_shape} in [B, n_groups, S]")
+    r_v = v_shape[3]
     _require(q.shape[1] == B, f"q has batch {q.shape[1]} but the latent caches have {B}")
     n_q = q.shape[2]
     w = w_rot.reshape(-1, *w_rot.shape[-2:]) if w_rot.dim() >= 3 else w_rot
@@ -245,11 +257,11 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
     ws, ws_bytes = _workspace(B, n_kv, S, max(width, 1), dev, workspace)
     lib = _native.load()
     _native.check(lib.palu_sdpa_decode(
-        _native.ptr(q), _native.ptr(k_latent), _native.ptr(w), _native.ptr(cs), _native.ptr(v_latent), width,
+        _native.ptr(q), _native.ptr(k_store), _native.ptr(w), _native.ptr(cs), _native.ptr(v_store), width,
         _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv),
         float(HEAD_DIM ** -0.5 if scale is None else scale), int(heads_per_core or 0), rot, int(bool(table_mcast)),
         _k_chunk(program_config), B, n_q, n_kv, n_groups, S, r_k, r_v, w_width, cs.shape[0], cs.shape[1],
-        _DTYPES[cs.dtype], _DTYPES[out_dtype], _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
+        _DTYPES[cs.dtype], _DTYPES[out_dtype], layout, _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
     return out
 
 
@@ -262,13 +274,14 @@ def flash_decode(q, k, v, cur_pos_tensor, *, scale=None, head_dim_v=None, out_dt
              f"q must be [1, B, n_q, {HEAD_DIM}]")
     dev = q.device
     _as_dev(q, "q", torch.bfloat16)
-    _as_dev(k, "k", torch.bfloat16, dev)
-    _as_dev(v, "v", torch.bfloat16, dev)
-    B, n_kv, S, hd = k.shape
-    _require(hd == HEAD_DIM, f"k must be [B, n_kv, S, {HEAD_DIM}], got {tuple(k.shape)}")
-    _require(tuple(v.shape[:3]) == (B, n_kv, S), f"v {tuple(v.shape)} does not match k {tuple(k.shape)}")
-    width = int(v.shape[3] if head_dim_v is None else head_dim_v)
-    _require(width == v.shape[3], f"head_dim_v {width} != V width {v.shape[3]}")
+    k_store, k_shape, layout = _cache_arg(k, "k", dev)
+    v_store, v_shape, v_layout = _cache_arg(v, "v", dev)
+    _require(layout == v_layout, "k and v must use the same cache layout")
+    B, n_kv, S, hd = k_shape
+    _require(hd == HEAD_DIM, f"k must be [B, n_kv, S, {HEAD_DIM}], got {k_shape}")
+    _require(tuple(v_shape[:3]) == (B, n_kv, S), f"v {v_shape} does not match k {k_shape}")
+    width = int(v_shape[3] if head_dim_v is None else head_dim_v)
+    _require(width == v_shape[3], f"head_dim_v {width} != V width {v_shape[3]}")
     n_q = q.shape[2]
     if out_dtype not in _DTYPES:
         raise RuntimeError(f"out_dtype must be torch.float32 or torch.bfloat16, got {out_dtype}")
@@ -278,8 +291,8 @@ def flash_decode(q, k, v, cur_pos_tensor, *, scale=None, head_dim_v=None, out_dt
     ws, ws_bytes = _workspace(B, n_kv, S, width, dev, workspace)
     lib = _native.load()
     _native.check(lib.palu_flash_decode(
-        _native.ptr(q), _native.ptr(k), _native.ptr(v), _native.ptr(cp), _native.ptr(out),
-        float(HEAD_DIM ** -0.5 if scale is None else scale), B, n_q, n_kv, S, width, _DTYPES[out_dtype],
+        _native.ptr(q), _native.ptr(k_store), _native.ptr(v_store), _native.ptr(cp), _native.ptr(out),
+        float(HEAD_DIM ** -0.5 if scale is None else scale), B, n_q, n_kv, S, width, _DTYPES[out_dtype], layout,
         _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
     return out
 
@@ -294,14 +307,15 @@ def flash_multi_latent_attention_decode(q, k, v, head_dim_v, cur_pos_tensor, sca
     return flash_decode(q, k, v, cur_pos_tensor, scale=scale, head_dim_v=head_dim_v)
 
 
-def paged_update_cache(cache: torch.Tensor, new_rows: torch.Tensor, update_idxs_tensor: torch.Tensor) -> None:
+def paged_update_cache(cache, new_rows: torch.Tensor, update_idxs_tensor: torch.Tensor) -> None:
     """Latent append (ttnn.experimental.paged_update_cache on a latent cache, attention.py:622-623):
-    cache[b, g, update_idxs[b], :] = new_rows[..., b, g, :] for every b with 0 <= idx < S."""
-    _as_dev(cache, "cache", torch.bfloat16)
-    B, G, S, width = cache.shape
+    cache[b, g, update_idxs[b], :] = new_rows[..., b, g, :] for every b with 0 <= idx < S. ``cache`` is a
+    [B, G, S, width] bf16 tensor or a LatentCache."""
+    dev = cache.device
+    store, (B, G, S, width), layout = _cache_arg(cache, "cache", dev)
     rows = new_rows.reshape(B, G, width)
-    _as_dev(rows, "new_rows", torch.bfloat16, cache.device)
-    cp = _cur_pos(update_idxs_tensor, B, cache.device)
+    _as_dev(rows, "new_rows", torch.bfloat16, dev)
+    cp = _cur_pos(update_idxs_tensor, B, dev)
     lib = _native.load()
-    _native.check(lib.palu_latent_append(_native.ptr(cache), _native.ptr(rows), _native.ptr(cp), B, G, S, width,
-                                         _native.stream_handle(cache.device)))
+    _native.check(lib.palu_latent_append(_native.ptr(store), _native.ptr(rows), _native.ptr(cp), B, G, S, width, layout,
+                                         _native.stream_handle(dev)))
