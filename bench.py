@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--rank-v", type=int, default=64)
     ap.add_argument("--layout", choices=("tiled", "rows"), default="tiled",
                     help="latent / KV cache layout: tiled (LatentCache, the fast path) or row-major [B, G, S, r]")
+    ap.add_argument("--deterministic", action="store_true",
+                    help="fixed block order inside each workgroup (bit-reproducible) instead of a shared counter")
     ap.add_argument("--no-stock", action="store_true", help="skip the full-KV comparator")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=2, help="batch rows of the CPU baseline sample")
@@ -64,9 +66,9 @@ def svd_sigma(W, n_heads, rank):
     return U, VT, VT.pow(2).sum(-1)                          # row j of VT_h has norm^2 = sigma_j
 
 
-def as_layout(t, layout):
+def as_layout(t, layout, role):
     from palu_tt.cache import LatentCache
-    return LatentCache.from_rows(t) if layout == "tiled" else t
+    return LatentCache.from_rows(t, role) if layout == "tiled" else t
 
 
 def build_workload(a, dev):
@@ -92,7 +94,7 @@ def build_workload(a, dev):
     for _ in range(a.layers):
         k = (torch.randn(a.batch, NKV, a.ctx, a.rank_k, device=dev, generator=gd) * sk).to(torch.bfloat16)
         v = (torch.randn(a.batch, NKV, a.ctx, a.rank_v, device=dev, generator=gd) * sv).to(torch.bfloat16)
-        layers.append((as_layout(k, a.layout), as_layout(v, a.layout)))
+        layers.append((as_layout(k, a.layout, "k"), as_layout(v, a.layout, "v")))
     cur = torch.full((a.batch,), a.ctx - 1, dtype=torch.int32, device=dev)
     return dict(q=q, w_rot=w_rot, cs=cs, layers=layers, cur=cur, u_k=u_k, cos=cos, sin=sin)
 
@@ -169,7 +171,7 @@ def main():
     def fused_step(l):
         k, v = wl["layers"][l]
         fused.palu_sdpa_decode(wl["q"], k, wl["w_rot"], wl["cs"], v, rv, wl["cur"], scale=HD ** -0.5, out=out,
-                               workspace=ws)
+                               workspace=ws, deterministic=a.deterministic)
 
     wall_ms, kern_ms, per = time_calls(fused_step, a.layers, a.steps, a.warmup)
     lat_bytes = B * NKV * S * (rk + rv) * 2
@@ -192,7 +194,7 @@ def main():
                    "ctx": S, "cur_pos": S - 1, "n_q": NQ, "n_kv": NKV, "head_dim": HD, "rank_k": rk, "rank_v": rv,
                    "latent_dtype": "bf16", "absorbed_v": True, "cache_layout": a.layout,
                    "layer_caches_rotated": a.layers,
-                   "rope": "llama3 theta 5e5 factor 8"},
+                   "rope": "llama3 theta 5e5 factor 8", "deterministic": a.deterministic},
         "kernel_us": round(kern_ms * 1e3, 2),
         "kernel_us_min": round(min(per) * 1e3, 2),
         "tokens_per_s": round(B / (N_LAYERS_MODEL * wall_ms * 1e-3), 1),
@@ -208,15 +210,16 @@ def main():
         torch.cuda.empty_cache()
         n_stock = max(1, min(a.layers, 4))
         gd = torch.Generator(device=dev).manual_seed(2)
-        kv = [(as_layout(torch.randn(B, NKV, S, HD, device=dev, generator=gd).to(torch.bfloat16), a.layout),
-               as_layout(torch.randn(B, NKV, S, HD, device=dev, generator=gd).to(torch.bfloat16), a.layout))
+        kv = [(as_layout(torch.randn(B, NKV, S, HD, device=dev, generator=gd).to(torch.bfloat16), a.layout, "k"),
+               as_layout(torch.randn(B, NKV, S, HD, device=dev, generator=gd).to(torch.bfloat16), a.layout, "v"))
               for _ in range(n_stock)]
         out_s = torch.empty(1, B, NQ, HD, dtype=torch.bfloat16, device=dev)
         ws_s = torch.empty(max(fused._native.load().palu_decode_workspace_bytes(B, NKV, S, HD), 1),
                            dtype=torch.uint8, device=dev)
 
         def stock_step(l):
-            fused.flash_decode(wl["q"], kv[l][0], kv[l][1], wl["cur"], scale=HD ** -0.5, out=out_s, workspace=ws_s)
+            fused.flash_decode(wl["q"], kv[l][0], kv[l][1], wl["cur"], scale=HD ** -0.5, out=out_s, workspace=ws_s,
+                               deterministic=a.deterministic)
 
         s_wall, s_kern, _ = time_calls(stock_step, n_stock, max(a.steps // 2, 1), max(a.warmup // 2, 1))
         s_bytes = B * NKV * S * HD * 2 * 2

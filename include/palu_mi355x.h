@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define PALU_ABI_VERSION 2
+#define PALU_ABI_VERSION 4
 
 #define PALU_OK 0
 #define PALU_EINVAL 1       /* arguments outside the op's envelope */
@@ -30,12 +30,18 @@ extern "C" {
 #define PALU_DTYPE_F32 0
 #define PALU_DTYPE_BF16 1
 
-/* Cache layouts. ROWS: the reference's logical [B, G, S, width] row-major tensor. TILED: the same
- * bytes reordered so each 32-position block is (2 * width / 32) tiles of 1 KB in MFMA operand order:
- * tile (c, kb) holds, in slot l = 16*g + n, the 8 values width-index 32*kb + 8*g .. +7 of block position
- * 8*(n/4) + 4*c + n%4 (g < 4, n < 16, c < 2). S must be a multiple of 32 for TILED. */
+/* Cache layouts. ROWS: the reference's logical [B, G, S, width] row-major tensor. The tiled layouts
+ * hold the same values with every 32-position block stored as (width / 16) tiles of 1 KB (64 slots of
+ * 8 bf16) in the operand order of the kernel's MFMAs (g < 4, n < 16, c < 2):
+ *   K-tile order (K latents, full K): tile c * (width/32) + kb, slot 16*g + n holds width-index
+ *     32*kb + 8*g .. +7 of block position 8*(n/4) + 4*c + n%4;
+ *   V-tile order (V latents, full V): tile mt, slot 16*g + m holds block positions 8*g .. 8*g+7 of
+ *     width-index 16*mt + m.
+ * A decode call with PALU_LAYOUT_TILED reads K caches in K-tile order and V caches in V-tile order;
+ * the append call names the order of the cache it writes. S must be a multiple of 32 when tiled. */
 #define PALU_LAYOUT_ROWS 0
-#define PALU_LAYOUT_TILED 1
+#define PALU_LAYOUT_TILED 1   /* decode: K-tile K, V-tile V; append: K-tile order */
+#define PALU_LAYOUT_TILED_V 2 /* append: V-tile order */
 
 #define PALU_ROT_LEGACY 0
 #define PALU_ROT_PACK 1
@@ -67,6 +73,11 @@ size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_di
  *   cur_pos  [B] int32 (device)      inclusive last valid position of each row
  *   out      [B, n_q, head_dim_v]    fp32 or bf16
  *   cache_layout                     PALU_LAYOUT_ROWS or PALU_LAYOUT_TILED for both latent caches
+ *   deterministic                    0: the waves of a workgroup take 32-position blocks from a shared
+ *                                    counter (fastest; which wave sums which block varies, so results
+ *                                    differ between calls at the bf16 rounding of the probabilities);
+ *                                    1: fixed block order, bit-reproducible
+ *   seq_len                          at most 65536
  *   rot_step, trans_mat              the reference's Phase 2 constants; optional together. They are
  *                                    validated as the reference does and otherwise unused: this kernel
  *                                    always rotates chunk-relative from cs_tab.
@@ -82,8 +93,8 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
                      int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step, const void* trans_mat,
                      const void* u_v, float scale, int heads_per_core, int rot_mode, int table_mcast, int k_chunk,
                      int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width,
-                     int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, void* workspace,
-                     size_t workspace_bytes, palu_stream_t stream);
+                     int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
+                     void* workspace, size_t workspace_bytes, palu_stream_t stream);
 
 /* Stock flash-decode over full, already-rotated K and a V cache of width head_dim_v. Replaces
  * ttnn.transformer.scaled_dot_product_attention_decode (head_dim_v == 128) and
@@ -91,16 +102,18 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
  * non-fused decode path calls (palu_tt/attention.py:703-706; tests/test_palu_sdpa_device.py:58-65,
  * 238-241). It is also the full-KV comparator for the fused op.
  *   q [B, n_q, 128] bf16, k [B, n_kv, S, 128] bf16, v [B, n_kv, S, head_dim_v] bf16,
- *   cur_pos [B] int32 (device), out [B, n_q, head_dim_v] fp32 or bf16; cache_layout as above for K and V. */
+ *   cur_pos [B] int32 (device), out [B, n_q, head_dim_v] fp32 or bf16; cache_layout and deterministic
+ *   as for palu_sdpa_decode. */
 int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t* cur_pos, void* out, float scale,
                       int batch, int n_q, int n_kv, int seq_len, int head_dim_v, int out_dtype, int cache_layout,
-                      void* workspace, size_t workspace_bytes, palu_stream_t stream);
+                      int deterministic, void* workspace, size_t workspace_bytes, palu_stream_t stream);
 
 /* Latent append: cache[b, g, update_idxs[b], :] = new_rows[b, g, :] for every row whose index lies in
  * [0, seq_len) (other rows are skipped). Replaces ttnn.experimental.paged_update_cache on the latent
  * caches (palu_tt/attention.py:622-623).
  *   cache [B, n_groups, S, width] bf16, new_rows [B, n_groups, width] bf16, update_idxs [B] int32
- *   (device), width a multiple of 8 (of 32 for a TILED cache). */
+ *   (device), width a multiple of 8 (of 32 for a tiled cache); cache_layout PALU_LAYOUT_ROWS,
+ *   PALU_LAYOUT_TILED (a K cache) or PALU_LAYOUT_TILED_V (a V cache). */
 int palu_latent_append(void* cache, const void* new_rows, const int32_t* update_idxs, int batch, int n_groups,
                        int seq_len, int width, int cache_layout, palu_stream_t stream);
 

@@ -5,12 +5,13 @@ import torch
 from palu_tt.cache import LatentCache, rows_to_tiled, tiled_to_rows
 
 
+@pytest.mark.parametrize("role", ["k", "v"])
 @pytest.mark.parametrize("S,r", [(32, 32), (64, 64), (256, 96), (96, 128)])
-def test_round_trip_is_exact(S, r):
+def test_round_trip_is_exact(S, r, role):
     rows = torch.randn(2, 3, S, r).to(torch.bfloat16)
-    tiled = rows_to_tiled(rows)
-    assert tiled.shape == (2, 3, S // 32, 2 * r // 32, 64, 8)
-    assert torch.equal(tiled_to_rows(tiled), rows)
+    tiled = rows_to_tiled(rows, role)
+    assert tiled.shape == (2, 3, S // 32, r // 16, 64, 8)
+    assert torch.equal(tiled_to_rows(tiled, role), rows)
 
 
 def test_slot_mapping_matches_the_documented_operand_order():
@@ -19,7 +20,7 @@ def test_slot_mapping_matches_the_documented_operand_order():
     pos = torch.arange(S)[:, None].expand(S, r)
     col = torch.arange(r)[None, :].expand(S, r)
     code = (pos * 1000 + col).float()[None, None]          # exact in fp32
-    tiled = rows_to_tiled(code)
+    tiled = rows_to_tiled(code, "k")
     for blk in range(S // 32):
         for c in range(2):
             for kb in range(r // 32):
@@ -30,9 +31,24 @@ def test_slot_mapping_matches_the_documented_operand_order():
                         assert tiled[0, 0, blk, c * (r // 32) + kb, l, j] == p * 1000 + 32 * kb + 8 * g + j
 
 
+def test_v_slot_mapping_matches_the_documented_operand_order():
+    """V order: tile mt, slot l = 16*g + m holds positions 32*blk + 8*g + j (j < 8) of r-index 16*mt + m."""
+    S, r = 64, 64
+    pos = torch.arange(S)[:, None].expand(S, r)
+    col = torch.arange(r)[None, :].expand(S, r)
+    tiled = rows_to_tiled((pos * 1000 + col).float()[None, None], "v")
+    for blk in range(S // 32):
+        for mt in range(r // 16):
+            for l in range(64):
+                g, m = divmod(l, 16)
+                for j in range(8):
+                    assert tiled[0, 0, blk, mt, l, j] == (32 * blk + 8 * g + j) * 1000 + 16 * mt + m
+
+
 def test_latent_cache_reports_logical_shape():
-    lc = LatentCache.zeros(2, 8, 128, 64, device="cpu")
-    assert lc.shape == (2, 8, 128, 64) and lc.dtype == torch.bfloat16
+    lc = LatentCache.zeros(2, 8, 128, 64, device="cpu", role="v")
+    assert lc.shape == (2, 8, 128, 64) and lc.dtype == torch.bfloat16 and lc.role == "v"
     assert lc.nbytes() == 2 * 8 * 128 * 64 * 2
     rows = torch.randn(2, 8, 128, 64).to(torch.bfloat16)
-    assert torch.equal(LatentCache.from_rows(rows).to_rows(), rows)
+    for role in ("k", "v"):
+        assert torch.equal(LatentCache.from_rows(rows, role).to_rows(), rows)

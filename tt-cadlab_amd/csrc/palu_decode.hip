@@ -42,6 +42,7 @@
 #include <stdio.h>
 #include <stdarg.h>
 #include <string.h>
+#include <type_traits>
 
 #include "../../include/palu_mi355x.h"
 
@@ -52,8 +53,7 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int HD = 128;     // head dim
-constexpr int BLK = 32;     // positions per inner block (two 16-position MFMA tiles)
-constexpr int CH = 128;     // rotation chunk: q~ is re-based every CH positions
+constexpr int BLK = 32;     // positions per block: two 16-position MFMA tiles, also the rotation chunk
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LAZY_RESCALE_LOG2 = 8.0f;  // running max is refreshed when a score exceeds it by > 2^8
 
@@ -98,26 +98,39 @@ struct DecodeArgs {
   long long k_sb, k_sg;   // element strides of k: batch, group (row stride is RK / HD)
   long long v_sb, v_sg;
   int B, n_q, n_kv, rep, hpg, S, cs_rows;
-  int split_len;          // positions per workgroup split, a multiple of NW * CH
+  int split_len;          // positions per workgroup split, a multiple of BLK
   int n_splits;
+  int deterministic;      // 1: wave w takes blocks w, w + NW, ... (reproducible); 0: blocks from a counter
   float qscale;           // softmax scale * log2(e)
 };
 
-// Lane-ordered rotation table entry for (block, tile, 16-dim row tile, lane):
-// {cos f, sin f, cos f+1, sin f+1} at chunk offset t, f = 8*rt + 2*(lane/16).
-__device__ __forceinline__ int rtab_index(int blk, int c, int rt, int lane) {
-  return ((blk * 2 + c) * 8 + rt) * 64 + lane;
-}
-
+// LDS map of one workgroup (latent mode; full-K mode keeps only the merge buffer and the counter):
+//   rtab  block-relative K rotation, float4 {cos f, sin f, cos f+1, sin f+1} per (tile, 16-dim row
+//         tile, lane), i.e. exactly the operand order of the rebuilt K^T accumulators   16 KB
+//   ukT   u_k^T, rows padded by 16 bytes (bank spread)                               HD x (RK + 8) bf16
+//   qx    per wave, the rotated query regrouped into its MFMA operand layout         NW x 4 KB
+//   tl    (cos, sin) of angle 32*Lo*f, Lo < 32: the low part of a block base          [32][64] float2
+//   ctr   the block counter
+//   th    (cos, sin) of angle 1024*H*f, H < ceil(S / 1024): the high part             [nH][64] float2
+//   kc    staging of rows 0..31 of cs_tab ([t][f] float2) while rtab is built, overlaying qx
+// The wave-merge buffer of the epilogue overlays the front.
 template <int RK, int RV, bool KFULL, int NW>
 struct Smem {
-  static constexpr bool UK_LDS = !KFULL && RK > 64;
-  static constexpr int UKT_STRIDE = RK + 8;                    // bf16 elements; +16 B kills bank conflicts
-  static constexpr int RTAB_BYTES = KFULL ? 0 : CH * 32 * 16;  // float4 per (t, f pair)
+  static constexpr int UKT_STRIDE = RK + 8;
+  static constexpr int RTAB_BYTES = KFULL ? 0 : 2 * 8 * 64 * 16;
   static constexpr int UKT_BYTES = KFULL ? 0 : HD * UKT_STRIDE * 2;
+  static constexpr int QX_WAVE_BYTES = 16 * 4 * 8 * 4 * 2;   // [head 16][g 4][row tile 8][4 dims] bf16
+  static constexpr int QX_BYTES = KFULL ? 0 : NW * QX_WAVE_BYTES;
+  static constexpr int TL_BYTES = KFULL ? 0 : 32 * 64 * 8;
+  static constexpr int UKT_OFFSET = RTAB_BYTES;
+  static constexpr int QX_OFFSET = UKT_OFFSET + UKT_BYTES;
+  static constexpr int TL_OFFSET = QX_OFFSET + QX_BYTES;
+  static constexpr int MAIN_BYTES = TL_OFFSET + TL_BYTES;
   static constexpr int MERGE_BYTES = NW * 16 * (RV + 2) * 4;
-  static constexpr int MAIN_BYTES = RTAB_BYTES + UKT_BYTES;
-  static constexpr int BYTES = MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES;
+  static constexpr int CTR_OFFSET = ((MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES) + 15) & ~15;
+  static constexpr int TH_OFFSET = CTR_OFFSET + 16;
+  static_assert(KFULL || QX_BYTES >= 32 * 64 * 8, "the cs_tab staging rows overlay qx");
+  static int bytes(int S) { return TH_OFFSET + (KFULL ? 0 : ((S + 1023) / 1024) * 64 * 8); }
 };
 
 template <typename T>
@@ -142,7 +155,11 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
   float4* rtab = reinterpret_cast<float4*>(smem);
-  __bf16* ukT = reinterpret_cast<__bf16*>(smem + SM::RTAB_BYTES);
+  __bf16* ukT = reinterpret_cast<__bf16*>(smem + SM::UKT_OFFSET);
+  float2* tl = reinterpret_cast<float2*>(smem + SM::TL_OFFSET);
+  float2* th = reinterpret_cast<float2*>(smem + SM::TH_OFFSET);
+  float2* kc = reinterpret_cast<float2*>(smem + SM::QX_OFFSET);
+  int* ctr = reinterpret_cast<int*>(smem + SM::CTR_OFFSET);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
@@ -150,33 +167,36 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   const int item = blockIdx.y, split = blockIdx.x;
   const int b = item / a.n_kv, kvh = item - b * a.n_kv;
   const int grp = KFULL ? kvh : kvh / a.hpg;
+  __bf16* qx = reinterpret_cast<__bf16*>(smem + SM::QX_OFFSET + w * SM::QX_WAVE_BYTES);
 
   int len = a.cur_pos[b] + 1;
   len = len < 0 ? 0 : (len > a.S ? a.S : len);
   const int s_lo = split * a.split_len;
   const int s_hi = min(len, s_lo + a.split_len);
-  const int Lw = a.split_len / NW;
-  const int w_lo = s_lo + w * Lw;
-  const int w_hi = min(s_hi, w_lo + Lw);
+  const int nblk = s_hi > s_lo ? (s_hi - s_lo + BLK - 1) / BLK : 0;
 
   const __bf16* kbase = a.k + b * a.k_sb + grp * a.k_sg;
   const __bf16* vbase = a.v + b * a.v_sb + grp * a.v_sg;
 
-  // Latent / K / V rows of one block into registers. Lane row n of tile c is position
-  // base + 8*(n/4) + 4*c + n%4; ROWS clamps rows past the cache end (their scores are masked).
-  auto load_blk = [&](int base, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[2][VB]) {
+  // One block's K (latent or full) and V rows into registers.
+  //   K, both layouts: register kd[c][kb] of lane (n, g) = width-index 32*kb + 8*g .. +7 of block
+  //     position 8*(n/4) + 4*c + n%4 (the B operand of the rebuild, or the A operand of QK).
+  //   V, TILED: register vd[mt] of lane (m = n, g) = block positions 8*g .. 8*g+7 of V column 16*mt + m,
+  //     which is directly the A operand of O^T += V^T P^T.
+  //   V, ROWS: register vd[c*VB + vb] holds the row pieces like K; an identity MFMA regroups them.
+  // ROWS clamps rows past the cache end (their scores and values are masked).
+  auto load_blk = [&](int base, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[VT]) {
     if constexpr (TILED) {
       const __bf16* kt = kbase + (long long)(base >> 5) * (32 * RK) + lane * 8;
       const __bf16* vt = vbase + (long long)(base >> 5) * (32 * RV) + lane * 8;
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
           kd[c][kb] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(kt + (c * KB + kb) * 512));
 #pragma unroll
-        for (int vb = 0; vb < VB; ++vb)
-          vd[c][vb] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(vt + (c * VB + vb) * 512));
-      }
+      for (int mt = 0; mt < VT; ++mt)
+        vd[mt] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(vt + mt * 512));
     } else {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -187,44 +207,94 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) kd[c][kb] = *reinterpret_cast<const bf16x8*>(kr + 32 * kb);
 #pragma unroll
-        for (int vb = 0; vb < VB; ++vb) vd[c][vb] = *reinterpret_cast<const bf16x8*>(vr + 32 * vb);
+        for (int vb = 0; vb < VB; ++vb) vd[c * VB + vb] = *reinterpret_cast<const bf16x8*>(vr + 32 * vb);
       }
     }
   };
 
-  // The first block's loads go out before the prologue so its HBM latency overlaps the table build.
-  bf16x8 kl[2][KB], vl[2][VB], kln[2][KB], vln[2][VB];
-  if (w_lo < w_hi) load_blk(w_lo, kl, vl);
+  // Blocks are handed out from an LDS counter so that the waves of a workgroup finish together
+  // (which wave sums which blocks then depends on timing, and each wave rounds its probabilities to
+  // bf16 against its own running max, so calls differ at that rounding level); wave w starts on block
+  // w. The deterministic schedule gives wave w every NW-th block.
+  if (tid == 0) *ctr = NW;
+  bf16x8 kl[2][KB], vl[VT], kln[2][KB], vln[VT];
 
-  // ---- prologue: chunk-relative angle table and u_k^T in LDS ------------------------------------
+  // ---- prologue ----------------------------------------------------------------------------------
+  // Latent mode: the angle tables and u_k^T go to LDS. The tables come from whole rows of cs_tab, one
+  // coalesced row per wave load (rows t < 32 for K, 32*Lo and 1024*H for the query); these (L2) loads
+  // are issued before the first latent block's (HBM) loads, so waiting on them does not wait on HBM.
   if constexpr (!KFULL) {
     const TabT* cs = static_cast<const TabT*>(a.cs);
-    for (int e = tid; e < CH * 32; e += NW * 64) {
-      const int l = e & 63, rt = (e >> 6) & 7, c = (e >> 9) & 1, blk = e >> 10;
-      const int nn = l & 15, gg = l >> 4;
-      const int t = blk * BLK + 8 * (nn >> 2) + 4 * c + (nn & 3);
-      const int col = 16 * rt + 4 * gg;  // = 2f for f = 8*rt + 2*gg
-      float4 v = make_float4(1.f, 0.f, 1.f, 0.f);
-      if (t < a.cs_rows) {
-        const TabT* row = cs + (long long)t * (2 * HD);
-        const float4 cv = load4f(row + col), sv = load4f(row + HD + col);  // {c_f, c_f, c_f+1, c_f+1}
-        v = make_float4(cv.x, sv.x, cv.z, sv.z);
-      }
-      rtab[e] = v;
-    }
-    const __bf16* uk = a.w_rot + (long long)kvh * RK * (2 * HD);
-    for (int e = tid; e < RK * (HD / 8); e += NW * 64) {
-      const int r = e % RK, d0 = (e / RK) * 8;  // consecutive lanes: consecutive ranks, one column block
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(uk + (long long)r * (2 * HD) + d0);
+    const int n_hi = (a.S + 1023) / 1024;
+    const int n_rows = 64 + n_hi;               // 32 K rows, 32 low-base rows, n_hi high-base rows
+    constexpr int RPW = (64 + 64 + NW - 1) / NW;  // rows per wave, enough for S <= 65536
+    float4 rowv[RPW];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ukT[(d0 + i) * SM::UKT_STRIDE + r] = v[i];
+    for (int i = 0; i < RPW; ++i) {
+      const int r = w + i * NW;
+      int t = r < 32 ? r : (r < 64 ? 32 * (r - 32) : 1024 * (r - 64));
+      t = (r < n_rows && t < a.cs_rows) ? t : 0;
+      rowv[i] = load4f(cs + (long long)t * (2 * HD) + 4 * lane);   // lane < 32: cos, else sin
+    }
+    constexpr int UPT = (RK * (HD / 8) + NW * 64 - 1) / (NW * 64);
+    bf16x8 ukv[UPT];
+    const __bf16* ukp = a.w_rot + (long long)kvh * RK * (2 * HD);
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int e = tid + i * NW * 64;   // consecutive lanes: consecutive ranks, one 8-column block
+      if (e < RK * (HD / 8)) ukv[i] = *reinterpret_cast<const bf16x8*>(ukp + (long long)(e % RK) * (2 * HD) + (e / RK) * 8);
+    }
+    if (w < nblk) load_blk(s_lo + w * BLK, kl, vl);
+    // rows -> [row][f] (cos, sin); lane l < 32 holds cos of f = 2l, 2l+1, lane l >= 32 the sines
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int r = w + i * NW;
+      if (r < n_rows) {
+        int t = r < 32 ? r : (r < 64 ? 32 * (r - 32) : 1024 * (r - 64));
+        const bool ok = t < a.cs_rows;
+        float2* dst = r < 32 ? kc + r * 64 : (r < 64 ? tl + (r - 32) * 64 : th + (r - 64) * 64);
+        const int f = 2 * (lane & 31);
+        float* d0 = reinterpret_cast<float*>(dst + f) + (lane >> 5);
+        d0[0] = ok ? rowv[i].x : (lane < 32 ? 1.f : 0.f);
+        d0[2] = ok ? rowv[i].z : (lane < 32 ? 1.f : 0.f);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      const int e = tid + i * NW * 64;
+      if (e < RK * (HD / 8)) {
+        const int r = e % RK, d0 = (e / RK) * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ukT[(d0 + j) * SM::UKT_STRIDE + r] = ukv[i][j];
+      }
     }
     __syncthreads();
+    // K rotation table in lane order from the staged rows 0..31
+    for (int e = tid; e < 2 * 8 * 64; e += NW * 64) {
+      const int l = e & 63, rt = (e >> 6) & 7, c = e >> 9;
+      const int nn = l & 15, gg = l >> 4;
+      const int t = 8 * (nn >> 2) + 4 * c + (nn & 3);
+      const int f = 8 * rt + 2 * gg;
+      const float2 x = kc[t * 64 + f], y = kc[t * 64 + f + 1];
+      rtab[e] = make_float4(x.x, x.y, y.x, y.y);
+    }
+  } else {
+    if (w < nblk) load_blk(s_lo + w * BLK, kl, vl);
+  }
+  __syncthreads();
+
+  // Query rows of heads >= rep stay zero in the wave's regroup area, so every lane reads its operand.
+  if constexpr (!KFULL) {
+#pragma unroll
+    for (int i = 0; i < SM::QX_WAVE_BYTES / (64 * 16); ++i)
+      reinterpret_cast<float4*>(qx)[i * 64 + lane] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 
-  // u_k^T as the A operand of the rebuild: row d = 16*rt + n, ranks 32*kb + 8*g + 0..7.
-  bf16x8 ukA[SM::UK_LDS ? 1 : 8][SM::UK_LDS ? 1 : KB];
-  if constexpr (!KFULL && !SM::UK_LDS) {
+  // u_k^T as the A operand of the rebuild: row d = 16*rt + n, ranks 32*kb + 8*g + 0..7. Above
+  // r_k = 64 it stays in LDS and is read per use.
+  constexpr bool UK_LDS = !KFULL && RK > 64;
+  bf16x8 ukA[UK_LDS ? 1 : 8][UK_LDS ? 1 : KB];
+  if constexpr (!KFULL && !UK_LDS) {
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt)
 #pragma unroll
@@ -232,12 +302,14 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
         ukA[rt][kb] = *reinterpret_cast<const bf16x8*>(ukT + (16 * rt + n) * SM::UKT_STRIDE + 32 * kb + 8 * g);
   }
 
-  // Identity B operands that move one 16-column slice of a 32-wide V block into the PV layout.
-  bf16x8 idB[2];
+  // ROWS: identity B operands that move one 16-column slice of a 32-wide V block into the PV layout.
+  bf16x8 idB[TILED ? 1 : 2];
+  if constexpr (!TILED) {
 #pragma unroll
-  for (int par = 0; par < 2; ++par)
+    for (int par = 0; par < 2; ++par)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) idB[par][j] = (8 * g + j == 16 * par + n) ? (__bf16)1.0f : (__bf16)0.0f;
+      for (int j = 0; j < 8; ++j) idB[par][j] = (8 * g + j == 16 * par + n) ? (__bf16)1.0f : (__bf16)0.0f;
+  }
 
   f32x4 O[VT];
 #pragma unroll
@@ -245,48 +317,85 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   float m_run = NEG_INF, l_run = 0.f;
   bf16x8 qB[4];
 
-  const bool qvalid = n < a.rep;
-  const __bf16* qrow = a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + (qvalid ? n : 0)) * HD;
-
-  // Query operand. Latent mode: q~ = R_{-s0} q * qscale with the head dim contracted in the order
-  // d(kb, g, j) = 16*(2*kb + j/4) + 4*g + j%4, which is the order the rebuilt K^T tile has in
-  // registers. Full-K mode: q * qscale in natural order d = 32*kb + 8*g + j.
-  auto make_q = [&](int s0) {
-    if constexpr (KFULL) {
+  // Query. Full-K mode: q * qscale once, head dim in natural order d = 32*kb + 8*g + j. Latent mode:
+  // q~ = R_{-base} q * qscale per block. The rotation is spread over all 64 lanes (lane l owns query
+  // head l/16 (+4, +8, +12 while < rep) and head dims 8*(l%16) .. +7, i.e. 4 frequency pairs), then
+  // regrouped through the wave's LDS area into the operand order d(kb, g, j) =
+  // 16*(2*kb + j/4) + 4*g + j%4 that the rebuilt K^T tile has in registers.
+  const int qf = lane & 15;                 // dims 8*qf .. 8*qf + 7
+  constexpr int QSLOTS = 4;                 // up to 16 query heads per KV head
+  const __bf16* qbase = a.q + ((long long)b * a.n_q + (long long)kvh * a.rep) * HD + 8 * qf;
+  if constexpr (KFULL) {
+    const bool qvalid = n < a.rep;
+    const __bf16* qrow = a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + (qvalid ? n : 0)) * HD;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        bf16x8 v = *reinterpret_cast<const bf16x8*>(qrow + 32 * kb + 8 * g);
+    for (int kb = 0; kb < 4; ++kb) {
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(qrow + 32 * kb + 8 * g);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qB[kb][j] = (__bf16)(qvalid ? (float)v[j] * a.qscale : 0.f);
-      }
-    } else {
-      const TabT* row = static_cast<const TabT*>(a.cs) + (long long)s0 * (2 * HD);
+      for (int j = 0; j < 8; ++j) qB[kb][j] = (__bf16)(qvalid ? (float)v[j] * a.qscale : 0.f);
+    }
+  }
+  auto make_q = [&](int base) {
+    // angle of the block base 32*J, J = 32*H + Lo: (cos, sin) by angle addition of th[H] and tl[Lo]
+    const int J = base >> 5;
+    const float4* lo4 = reinterpret_cast<const float4*>(tl + (J & 31) * 64 + 4 * qf);
+    const float4* hi4 = reinterpret_cast<const float4*>(th + (J >> 5) * 64 + 4 * qf);
+    const float4 l01 = lo4[0], l23 = lo4[1], h01 = hi4[0], h23 = hi4[1];
+    const float lc[4] = {l01.x, l01.z, l23.x, l23.z}, ls[4] = {l01.y, l01.w, l23.y, l23.w};
+    const float hc[4] = {h01.x, h01.z, h23.x, h23.z}, hs[4] = {h01.y, h01.w, h23.y, h23.w};
+    const float qsc = a.qscale;
+    float cf[4], sf[4];
 #pragma unroll
-      for (int rt = 0; rt < 8; ++rt) {
-        const int col = 16 * rt + 4 * g;
-        const bf16x4 x = *reinterpret_cast<const bf16x4*>(qrow + col);
-        const float4 cv = load4f(row + col), sv = load4f(row + HD + col);
-        const float c0 = cv.x, sn0 = sv.x, c1 = cv.z, sn1 = sv.z;
-        const float x0 = (float)x[0], x1 = (float)x[1], x2 = (float)x[2], x3 = (float)x[3];
-        const float s = qvalid ? a.qscale : 0.f;
-        const int kb = rt >> 1, j0 = 4 * (rt & 1);
-        qB[kb][j0 + 0] = (__bf16)((x0 * c0 + x1 * sn0) * s);
-        qB[kb][j0 + 1] = (__bf16)((x1 * c0 - x0 * sn0) * s);
-        qB[kb][j0 + 2] = (__bf16)((x2 * c1 + x3 * sn1) * s);
-        qB[kb][j0 + 3] = (__bf16)((x3 * c1 - x2 * sn1) * s);
+    for (int p = 0; p < 4; ++p) {
+      cf[p] = (hc[p] * lc[p] - hs[p] * ls[p]) * qsc;
+      sf[p] = (hs[p] * lc[p] + hc[p] * ls[p]) * qsc;
+    }
+    const int rt = qf >> 1, g0 = 2 * (qf & 1);
+#pragma unroll
+    for (int k = 0; k < QSLOTS; ++k) {
+      const int h = g + 4 * k;
+      if (h < a.rep) {
+        const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qbase + h * HD);
+        bf16x4 y0, y1;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const float x0 = (float)qv[2 * p], x1 = (float)qv[2 * p + 1];
+          const float r0 = x0 * cf[p] + x1 * sf[p], r1 = x1 * cf[p] - x0 * sf[p];  // R_{-base}
+          if (p < 2) { y0[2 * p] = (__bf16)r0; y0[2 * p + 1] = (__bf16)r1; }
+          else { y1[2 * p - 4] = (__bf16)r0; y1[2 * p - 3] = (__bf16)r1; }
+        }
+        // dims 16*rt + 4*g0 + 0..3 and 16*rt + 4*(g0+1) + 0..3 of head h
+        *reinterpret_cast<bf16x4*>(qx + ((h * 4 + g0) * 8 + rt) * 4) = y0;
+        *reinterpret_cast<bf16x4*>(qx + ((h * 4 + g0 + 1) * 8 + rt) * 4) = y1;
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) qB[kb] = *reinterpret_cast<const bf16x8*>(qx + ((n * 4 + g) * 8 + 2 * kb) * 4);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   };
 
-  int q_s0 = -1;
-  // One block of 32 positions on the buffers (kc, vc), with the next block prefetched into (kn, vn).
-  auto step = [&](int base, bf16x8 (&kc)[2][KB], bf16x8 (&vc)[2][VB], bf16x8 (&kn)[2][KB],
-                  bf16x8 (&vn)[2][VB]) __attribute__((always_inline)) {
-    if (base + BLK < w_hi) load_blk(base + BLK, kn, vn);
+  // One block of 32 positions on the buffers (kc, vc); the next block is claimed and its loads are
+  // issued into (kn, vn) first. Returns the next block index. Only the last block of a range can be
+  // partial; it runs the masked variant (PARTIAL), every other block carries no masking work.
+  auto step = [&](auto partial_tag, int blk, bf16x8 (&kc)[2][KB], bf16x8 (&vc)[VT], bf16x8 (&kn)[2][KB],
+                  bf16x8 (&vn)[VT]) __attribute__((always_inline)) -> int {
+    constexpr bool PARTIAL = decltype(partial_tag)::value;
+    int nxt = nblk;                       // a partial block is the last one: nothing follows it
+    if constexpr (!PARTIAL) {
+      nxt = blk + NW;
+      if (!a.deterministic) {
+        if (lane == 0) nxt = atomicAdd(ctr, 1);
+        nxt = __shfl(nxt, 0, 64);
+      }
+      if (nxt < nblk) load_blk(s_lo + nxt * BLK, kn, vn);
+    }
 
-    const int s0 = base & ~(CH - 1);
-    if (s0 != q_s0) { make_q(s0); q_s0 = s0; }
-    const int blk = (base - s0) / BLK;
+    const int base = s_lo + blk * BLK;
+    if constexpr (!KFULL) make_q(base);
 
     f32x4 sc[2];
 #pragma unroll
@@ -298,22 +407,23 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       } else {
         f32x4 acc[8];
 #pragma unroll
-        for (int rt = 0; rt < 8; ++rt) {
-          acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int rt = 0; rt < 8; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) {
+        for (int kb = 0; kb < KB; ++kb) {       // independent MFMAs back to back
+#pragma unroll
+          for (int rt = 0; rt < 8; ++rt) {
             bf16x8 ua;
-            if constexpr (SM::UK_LDS)
+            if constexpr (UK_LDS)
               ua = *reinterpret_cast<const bf16x8*>(ukT + (16 * rt + n) * SM::UKT_STRIDE + 32 * kb + 8 * g);
             else
               ua = ukA[rt][kb];
             acc[rt] = mfma16(ua, kc[c][kb], acc[rt]);
           }
         }
-        // RoPE by the chunk offset of this lane's position: (x0, x1) -> (x0 c - x1 s, x1 c + x0 s).
+        // RoPE by the block offset of this lane's position: (x0, x1) -> (x0 c - x1 s, x1 c + x0 s).
 #pragma unroll
         for (int rt = 0; rt < 8; ++rt) {
-          const float4 t = rtab[rtab_index(blk, c, rt, lane)];
+          const float4 t = rtab[(c * 8 + rt) * 64 + lane];
           const float x0 = acc[rt][0], x1 = acc[rt][1], x2 = acc[rt][2], x3 = acc[rt][3];
           acc[rt][0] = x0 * t.x - x1 * t.y;
           acc[rt][1] = x1 * t.x + x0 * t.y;
@@ -327,13 +437,12 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     }
 
     // Causal / range mask: score register i of tile c is position base + 8*g + 4*c + i.
-    const bool partial = base + BLK > w_hi;
-    if (partial) {
+    if constexpr (PARTIAL) {
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (base + 8 * g + 4 * c + i >= w_hi) sc[c][i] = NEG_INF;
+          if (base + 8 * g + 4 * c + i >= s_hi) sc[c][i] = NEG_INF;
     }
 
     // Online softmax, exp2 domain; lanes n, n+16, n+32, n+48 hold query head n.
@@ -357,34 +466,59 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     l_run += (p[0][0] + p[0][1]) + (p[0][2] + p[0][3]) + (p[1][0] + p[1][1]) + (p[1][2] + p[1][3]);
     const bf16x8 pB = pack8(p[0], p[1]);
 
-    // V rows into the PV A layout (identity MFMA), masked rows zeroed, then O^T += V^T P^T.
+    // O^T += V^T P^T. Masked positions are zeroed in V too (their cache rows may hold anything).
 #pragma unroll
     for (int mt = 0; mt < VT; ++mt) {
-      f32x4 x0 = mfma16(vc[0][mt >> 1], idB[mt & 1], f32x4{0.f, 0.f, 0.f, 0.f});
-      f32x4 x1 = mfma16(vc[1][mt >> 1], idB[mt & 1], f32x4{0.f, 0.f, 0.f, 0.f});
-      if (partial) {
+      bf16x8 vA;
+      if constexpr (TILED) {
+        vA = vc[mt];
+        if constexpr (PARTIAL) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (base + 8 * g + i >= w_hi) x0[i] = 0.f;
-          if (base + 8 * g + 4 + i >= w_hi) x1[i] = 0.f;
+          for (int j = 0; j < 8; ++j)
+            if (base + 8 * g + j >= s_hi) vA[j] = (__bf16)0.0f;
         }
+      } else {
+        f32x4 x0 = mfma16(vc[mt >> 1], idB[mt & 1], f32x4{0.f, 0.f, 0.f, 0.f});
+        f32x4 x1 = mfma16(vc[VB + (mt >> 1)], idB[mt & 1], f32x4{0.f, 0.f, 0.f, 0.f});
+        if constexpr (PARTIAL) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (base + 8 * g + i >= s_hi) x0[i] = 0.f;
+            if (base + 8 * g + 4 + i >= s_hi) x1[i] = 0.f;
+          }
+        }
+        vA = pack8(x0, x1);
       }
-      O[mt] = mfma16(pack8(x0, x1), pB, O[mt]);
+      O[mt] = mfma16(vA, pB, O[mt]);
     }
+    return nxt;
   };
 
-  int base = w_lo;
-  while (base < w_hi) {
-    step(base, kl, vl, kln, vln);
-    base += BLK;
-    if (base >= w_hi) break;
-    step(base, kln, vln, kl, vl);
-    base += BLK;
+  const std::integral_constant<bool, false> full_blk;
+  const std::integral_constant<bool, true> partial_blk;
+  const int nfull = (s_hi - s_lo) % BLK != 0 ? nblk - 1 : nblk;
+  int blk = w;
+  bool in_second = false;            // the next block's rows sit in (kln, vln)
+  while (blk < nfull) {
+    blk = step(full_blk, blk, kl, vl, kln, vln);
+    if (blk >= nfull) { in_second = true; break; }
+    blk = step(full_blk, blk, kln, vln, kl, vl);
+  }
+  if (blk < nblk) {                  // the partial last block, already loaded
+    if (in_second) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) kl[c][kb] = kln[c][kb];
+#pragma unroll
+      for (int mt = 0; mt < VT; ++mt) vl[mt] = vln[mt];
+    }
+    step(partial_blk, blk, kl, vl, kln, vln);
   }
 
   // ---- merge the NW wave partials of this workgroup ---------------------------------------------
   l_run = wave_sum_xor48(l_run);
-  __syncthreads();  // the merge buffer overlays the angle table
+  __syncthreads();  // the merge buffer overlays the tables
   float* mbuf = reinterpret_cast<float*>(smem);
   if (n < a.rep) {
     float* row = mbuf + (w * 16 + n) * (RV + 2);
@@ -445,15 +579,21 @@ __global__ __launch_bounds__(256) void palu_merge_kernel(const float* ws, void* 
   }
 }
 
-// Offset (elements) of rank k of position p inside one (b, g) stream of a TILED cache of width R.
-__device__ __forceinline__ long long tiled_offset(int p, int k, int R) {
+// Offset (elements) of width-index k of position p inside one (b, g) stream of width R, K-tile order.
+__device__ __forceinline__ long long tiled_k_offset(int p, int k, int R) {
   const int t = p & 31, c = (t >> 2) & 1, nn = ((t >> 3) << 2) | (t & 3);
   const int kb = k >> 5, gg = (k >> 3) & 3;
   return (long long)(p >> 5) * (32 * R) + ((c * (R >> 5) + kb) * 64 + 16 * gg + nn) * 8 + (k & 7);
 }
 
-// Latent append: cache[b, g, idx[b], :] = rows[b, g, :], one 16-byte vector (8 ranks) per thread.
-template <bool TILED>
+// V-tile order: tile mt = k / 16, slot 16 * (t / 8) + k % 16, element t % 8 (t = p % 32).
+__device__ __forceinline__ long long tiled_v_offset(int p, int k, int R) {
+  const int t = p & 31;
+  return (long long)(p >> 5) * (32 * R) + ((k >> 4) * 64 + 16 * (t >> 3) + (k & 15)) * 8 + (t & 7);
+}
+
+// Latent append: cache[b, g, idx[b], :] = rows[b, g, :]; each thread moves 8 consecutive values.
+template <int LAYOUT>
 __global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const __bf16* rows, const int32_t* idx,
                                                           int B, int G, int S, int width) {
   const int vec = width / 8;
@@ -465,8 +605,16 @@ __global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const _
     const int p = idx[b];
     if (p < 0 || p >= S) continue;
     const bf16x8 x = *reinterpret_cast<const bf16x8*>(rows + bg * width + 8 * v);
-    const long long off = TILED ? bg * S * width + tiled_offset(p, 8 * v, width) : (bg * S + p) * width + 8 * v;
-    *reinterpret_cast<bf16x8*>(cache + off) = x;
+    __bf16* stream = cache + bg * S * width;
+    if constexpr (LAYOUT == PALU_LAYOUT_ROWS) {
+      *reinterpret_cast<bf16x8*>(stream + (long long)p * width + 8 * v) = x;
+    } else if constexpr (LAYOUT == PALU_LAYOUT_TILED) {
+      *reinterpret_cast<bf16x8*>(stream + tiled_k_offset(p, 8 * v, width)) = x;
+    } else {
+      const long long o = tiled_v_offset(p, 8 * v, width);   // 8 slots 16 bytes apart
+#pragma unroll
+      for (int j = 0; j < 8; ++j) stream[o + 8 * j] = x[j];
+    }
   }
 }
 
@@ -485,10 +633,10 @@ int fail(int code, const char* fmt, ...) {
 
 // Waves per workgroup: 8 (two per SIMD) where the kernel fits 256 registers, else 4 (one per SIMD,
 // which lets the compiler use the full 512-entry register file instead of spilling).
-template <int RK, int RV, bool KFULL>
+template <int RK, int RV, bool KFULL, bool TILED>
 constexpr int pick_nw() {
-  if (KFULL) return RV <= 96 ? 8 : 4;
-  return ((RK <= 32 && RV <= 96) || (RK == 64 && RV <= 64)) ? 8 : 4;
+  if (KFULL) return RV <= 64 ? 8 : 4;
+  return (RK + RV <= 96 || (TILED && RK == 64 && RV == 64)) ? 8 : 4;   // measured register fits
 }
 constexpr int MIN_NW = 4;
 constexpr int TARGET_WGS = 256;  // one workgroup per CU at full occupancy of the chip
@@ -498,21 +646,15 @@ struct Plan {
 };
 
 Plan plan_splits(int items, int S, int nw) {
-  // Positions per wave: about TARGET_WGS workgroups over the whole job, at least one rotation
-  // chunk per wave.
+  // Positions per workgroup: about TARGET_WGS workgroups over the whole job, in whole blocks for
+  // every wave; a sequence is split across workgroups only when its items alone cannot fill the chip.
   const long long total = (long long)items * S;
-  long long lw = (total + (long long)TARGET_WGS * nw - 1) / ((long long)TARGET_WGS * nw);
-  lw = ((lw + CH - 1) / CH) * CH;
-  if (lw < CH) lw = CH;
-  int split_len = (int)(lw * nw);
-  const int n_splits = (S + split_len - 1) / split_len;
-  if (n_splits == 1) {
-    // one split per item: shrink the per-wave slice so the waves of a short cache stay balanced
-    long long per_wave = ((long long)S + nw - 1) / nw;
-    per_wave = ((per_wave + CH - 1) / CH) * CH;
-    split_len = (int)(per_wave * nw);
-  }
-  return Plan{n_splits, split_len};
+  const long long unit = (long long)BLK * nw;
+  long long per_wg = (total + TARGET_WGS - 1) / TARGET_WGS;
+  per_wg = ((per_wg + unit - 1) / unit) * unit;
+  const long long whole = (((long long)S + BLK - 1) / BLK) * BLK;
+  if (per_wg > whole) per_wg = whole;
+  return Plan{(int)((S + per_wg - 1) / per_wg), (int)per_wg};
 }
 
 size_t ws_bytes(int items, int n_splits, int rv) {
@@ -521,7 +663,7 @@ size_t ws_bytes(int items, int n_splits, int rv) {
 
 template <int RK, int RV, bool KFULL, bool TILED, typename TabT, typename OutT>
 int launch(const DecodeArgs& a0, hipStream_t stream) {
-  constexpr int NW = pick_nw<RK, RV, KFULL>();
+  constexpr int NW = pick_nw<RK, RV, KFULL, TILED>();
   DecodeArgs a = a0;
   const int items = a.B * a.n_kv;
   const Plan p = plan_splits(items, a.S, NW);
@@ -532,13 +674,15 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
     return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_decode_workspace_bytes), got %zu", need, a.ws_bytes);
   using SM = Smem<RK, RV, KFULL, NW>;
   auto kern = palu_decode_kernel<RK, RV, KFULL, TILED, NW, TabT, OutT>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, SM::BYTES);
+  const int lds = SM::bytes(a.S);
+  if (lds > 160 * 1024) return fail(PALU_EUNSUPPORTED, "seq_len %d needs %d bytes of LDS (max 163840)", a.S, lds);
+  static int attr_set = 0;
+  if (attr_set < lds) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return fail(PALU_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-    attr_set = true;
+    attr_set = lds;
   }
-  hipLaunchKernelGGL(kern, dim3(a.n_splits, items), dim3(NW * 64), SM::BYTES, stream, a);
+  hipLaunchKernelGGL(kern, dim3(a.n_splits, items), dim3(NW * 64), lds, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "decode kernel launch: %s", hipGetErrorString(e));
   if (a.n_splits > 1) {
@@ -621,8 +765,8 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
                      int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step, const void* trans_mat,
                      const void* u_v, float scale, int heads_per_core, int rot_mode, int table_mcast, int k_chunk,
                      int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width,
-                     int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, void* workspace,
-                     size_t workspace_bytes, hipStream_t stream) {
+                     int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
   g_err[0] = 0;
   (void)table_mcast;
   if (!q || !k_latent || !w_rot || !cs_tab || !v_latent || !cur_pos || !out)
@@ -648,6 +792,8 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
   if (cs_cols != 2 * HD) return fail(PALU_EINVAL, "cs_tab must be [1, 1, S, %d] = [cos | sin], got last dim %d", 2 * HD, cs_cols);
   if (cs_rows < seq_len)
     return fail(PALU_EINVAL, "cs_tab has %d rows but the latent cache has %d positions", cs_rows, seq_len);
+  if (seq_len > 65536)
+    return fail(PALU_EUNSUPPORTED, "seq_len %d: this build's block-angle tables cover 65536 positions", seq_len);
   if (n_q % n_kv != 0 || n_q / n_kv > 16)
     return fail(PALU_EINVAL, "KV head count %d must divide the %d query heads with at most 16 query heads per KV head", n_kv, n_q);
   if (heads_per_core > 1) {
@@ -689,6 +835,7 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
   a.v_sg = (long long)seq_len * r_v;
   a.v_sb = a.v_sg * n_groups;
   a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = hpg; a.S = seq_len; a.cs_rows = cs_rows;
+  a.deterministic = deterministic ? 1 : 0;
   a.qscale = scale * 1.4426950408889634f;
 
   if (cs_dtype == PALU_DTYPE_F32) {
@@ -701,7 +848,7 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
 
 int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t* cur_pos, void* out, float scale,
                       int batch, int n_q, int n_kv, int seq_len, int head_dim_v, int out_dtype, int cache_layout,
-                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                      int deterministic, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   g_err[0] = 0;
   if (!q || !k || !v || !cur_pos || !out) return fail(PALU_EINVAL, "palu_flash_decode: a required tensor pointer is null");
   if (batch <= 0 || n_q <= 0 || n_kv <= 0 || seq_len <= 0)
@@ -728,6 +875,7 @@ int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t
   a.v_sg = (long long)seq_len * head_dim_v;
   a.v_sb = a.v_sg * n_kv;
   a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = 1; a.S = seq_len; a.cs_rows = 0;
+  a.deterministic = deterministic ? 1 : 0;
   a.qscale = scale * 1.4426950408889634f;
   const bool f32o = out_dtype == PALU_DTYPE_F32;
   return cache_layout == PALU_LAYOUT_TILED ? dispatch_full<true>(a, head_dim_v, f32o, stream)
@@ -740,19 +888,26 @@ int palu_latent_append(void* cache, const void* new_rows, const int32_t* update_
   if (!cache || !new_rows || !update_idxs) return fail(PALU_EINVAL, "palu_latent_append: a required pointer is null");
   if (batch <= 0 || n_groups <= 0 || seq_len <= 0 || width <= 0 || width % 8 != 0)
     return fail(PALU_EINVAL, "palu_latent_append: width must be a positive multiple of 8, got %d", width);
-  if (int rc = check_layout(cache_layout, seq_len, "palu_latent_append")) return rc;
-  if (cache_layout == PALU_LAYOUT_TILED && width % 32 != 0)
+  if (int rc = check_layout(cache_layout == PALU_LAYOUT_TILED_V ? PALU_LAYOUT_TILED : cache_layout, seq_len,
+                            "palu_latent_append"))
+    return rc;
+  if (cache_layout != PALU_LAYOUT_ROWS && width % 32 != 0)
     return fail(PALU_EINVAL, "palu_latent_append: a tiled cache row is a multiple of 32 wide, got %d", width);
   if (!aligned16(cache) || !aligned16(new_rows)) return fail(PALU_EINVAL, "palu_latent_append: 16-byte alignment required");
   const long long total = (long long)batch * n_groups * (width / 8);
   int blocks = (int)((total + 255) / 256);
   if (blocks > 4096) blocks = 4096;
+  auto* c = static_cast<__bf16*>(cache);
+  auto* r = static_cast<const __bf16*>(new_rows);
   if (cache_layout == PALU_LAYOUT_TILED)
-    hipLaunchKernelGGL(palu_append_kernel<true>, dim3(blocks), dim3(256), 0, stream, static_cast<__bf16*>(cache),
-                       static_cast<const __bf16*>(new_rows), update_idxs, batch, n_groups, seq_len, width);
+    hipLaunchKernelGGL(palu_append_kernel<PALU_LAYOUT_TILED>, dim3(blocks), dim3(256), 0, stream, c, r, update_idxs,
+                       batch, n_groups, seq_len, width);
+  else if (cache_layout == PALU_LAYOUT_TILED_V)
+    hipLaunchKernelGGL(palu_append_kernel<PALU_LAYOUT_TILED_V>, dim3(blocks), dim3(256), 0, stream, c, r, update_idxs,
+                       batch, n_groups, seq_len, width);
   else
-    hipLaunchKernelGGL(palu_append_kernel<false>, dim3(blocks), dim3(256), 0, stream, static_cast<__bf16*>(cache),
-                       static_cast<const __bf16*>(new_rows), update_idxs, batch, n_groups, seq_len, width);
+    hipLaunchKernelGGL(palu_append_kernel<PALU_LAYOUT_ROWS>, dim3(blocks), dim3(256), 0, stream, c, r, update_idxs,
+                       batch, n_groups, seq_len, width);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "append kernel launch: %s", hipGetErrorString(e));
   return PALU_OK;

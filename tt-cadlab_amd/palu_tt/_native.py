@@ -14,8 +14,8 @@ from palu_tt._build import library_path
 
 PALU_OK, PALU_EINVAL, PALU_EUNSUPPORTED, PALU_EHIP = 0, 1, 2, 3
 DTYPE_F32, DTYPE_BF16 = 0, 1
-ABI_VERSION = 2
-LAYOUT_ROWS, LAYOUT_TILED = 0, 1
+ABI_VERSION = 4
+LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_TILED_V = 0, 1, 2
 
 _vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 
@@ -24,8 +24,8 @@ _SIGNATURES = {
     "palu_abi_version": (_i, []),
     "palu_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "palu_sdpa_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i,
-                              _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
-    "palu_flash_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+                              _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "palu_flash_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "palu_latent_append": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
 }
 EXPORTED = tuple(_SIGNATURES)

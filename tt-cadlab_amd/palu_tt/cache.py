@@ -3,12 +3,17 @@
 The reference keeps each latent cache as a [B, n_groups, max_seq, r] device tensor
 (palu_tt/attention.py:274-283) and appends one row per decode step with paged_update_cache
 (attention.py:622-623). ``LatentCache`` holds the same logical tensor in the layout the fused decode
-streams fastest: every 32-position block is (2 * r / 32) tiles of 1 KB, each tile already in the
-operand order of the kernel's MFMAs, so a wave reads one contiguous KB per load instruction.
+streams fastest: every 32-position block is r / 16 tiles of 1 KB, each tile already in the operand
+order of the kernel's MFMAs, so a wave reads one contiguous KB per load instruction and feeds it to
+the matrix cores without any regrouping. The order depends on the cache's role:
 
-Tile (c, kb) of block blk, slot l = 16*g + n (g < 4, n < 16), holds the 8 values r-index 32*kb + 8*g
-.. +7 of position 32*blk + 8*(n//4) + 4*c + n%4. The storage tensor is [B, G, S/32, 2*r/32, 64, 8]
-bf16; ``from_rows`` / ``to_rows`` convert to and from the logical row-major tensor.
+  K caches ("k"): tile c * (r/32) + kb, slot l = 16*g + n (g < 4, n < 16) holds r-index 32*kb + 8*g
+    .. +7 of block position 8*(n//4) + 4*c + n%4 (the operand of the K rebuild);
+  V caches ("v"): tile mt, slot l = 16*g + m holds block positions 8*g .. 8*g + 7 of r-index 16*mt + m
+    (the operand of the probability-times-V product).
+
+The storage tensor is [B, G, S/32, r/16, 64, 8] bf16; ``from_rows`` / ``to_rows`` convert to and from
+the logical row-major tensor.
 """
 from dataclasses import dataclass
 from typing import Tuple
@@ -18,43 +23,59 @@ import torch
 BLOCK = 32
 
 
-def rows_to_tiled(rows: torch.Tensor) -> torch.Tensor:
-    """[B, G, S, r] -> tiled storage [B, G, S/32, 2*r/32, 64, 8] (same dtype, new contiguous tensor)."""
+ROLES = ("k", "v")
+
+
+def rows_to_tiled(rows: torch.Tensor, role: str = "k") -> torch.Tensor:
+    """[B, G, S, r] -> tiled storage [B, G, S/32, r/16, 64, 8] in the role's tile order."""
     B, G, S, r = rows.shape
+    assert role in ROLES, f"role must be 'k' or 'v', got {role!r}"
     assert S % BLOCK == 0 and r % 32 == 0, f"tiled layout needs S % 32 == 0 and r % 32 == 0, got S={S}, r={r}"
-    # position 32*blk + 8*tb + 4*c + i, r-index 32*kb + 8*g + j  ->  [blk][c][kb][g][tb][i][j]
-    x = rows.reshape(B, G, S // BLOCK, 4, 2, 4, r // 32, 4, 8)
-    x = x.permute(0, 1, 2, 4, 6, 7, 3, 5, 8)
-    return x.reshape(B, G, S // BLOCK, 2 * r // 32, 64, 8).contiguous()
+    if role == "k":
+        # position 32*blk + 8*tb + 4*c + i, r-index 32*kb + 8*g + j  ->  [blk][c][kb][g][tb][i][j]
+        x = rows.reshape(B, G, S // BLOCK, 4, 2, 4, r // 32, 4, 8).permute(0, 1, 2, 4, 6, 7, 3, 5, 8)
+    else:
+        # position 32*blk + 8*g + j, r-index 16*mt + m  ->  [blk][mt][g][m][j]
+        x = rows.reshape(B, G, S // BLOCK, 4, 8, r // 16, 16).permute(0, 1, 2, 5, 3, 6, 4)
+    return x.reshape(B, G, S // BLOCK, r // 16, 64, 8).contiguous()
 
 
-def tiled_to_rows(tiled: torch.Tensor) -> torch.Tensor:
+def tiled_to_rows(tiled: torch.Tensor, role: str = "k") -> torch.Tensor:
     """Inverse of rows_to_tiled."""
     B, G, nblk, ntile, _, _ = tiled.shape
     r = ntile * 16
-    x = tiled.reshape(B, G, nblk, 2, r // 32, 4, 4, 4, 8)          # [blk][c][kb][g][tb][i][j]
-    x = x.permute(0, 1, 2, 6, 3, 7, 4, 5, 8)                      # [blk][tb][c][i][kb][g][j]
+    if role == "k":
+        x = tiled.reshape(B, G, nblk, 2, r // 32, 4, 4, 4, 8)     # [blk][c][kb][g][tb][i][j]
+        x = x.permute(0, 1, 2, 6, 3, 7, 4, 5, 8)                 # [blk][tb][c][i][kb][g][j]
+    else:
+        x = tiled.reshape(B, G, nblk, r // 16, 4, 16, 8)         # [blk][mt][g][m][j]
+        x = x.permute(0, 1, 2, 4, 6, 3, 5)                       # [blk][g][j][mt][m]
     return x.reshape(B, G, nblk * BLOCK, r).contiguous()
 
 
 @dataclass
 class LatentCache:
-    """A latent cache of logical shape [B, n_groups, max_seq, width] in the tiled layout."""
+    """A K ("k") or V ("v") cache of logical shape [B, n_groups, max_seq, width] in the tiled layout."""
     data: torch.Tensor
+    role: str = "k"
+
+    def __post_init__(self):
+        assert self.role in ROLES, f"role must be 'k' or 'v', got {self.role!r}"
 
     @staticmethod
-    def zeros(batch: int, n_groups: int, max_seq: int, width: int, device, dtype=torch.bfloat16) -> "LatentCache":
+    def zeros(batch: int, n_groups: int, max_seq: int, width: int, device, role: str = "k",
+              dtype=torch.bfloat16) -> "LatentCache":
         assert max_seq % BLOCK == 0, f"max_seq must be a multiple of {BLOCK}, got {max_seq}"
         assert width % 32 == 0, f"width must be a multiple of 32, got {width}"
-        return LatentCache(torch.zeros(batch, n_groups, max_seq // BLOCK, 2 * width // 32, 64, 8, dtype=dtype,
-                                       device=device))
+        return LatentCache(torch.zeros(batch, n_groups, max_seq // BLOCK, width // 16, 64, 8, dtype=dtype,
+                                       device=device), role)
 
     @staticmethod
-    def from_rows(rows: torch.Tensor) -> "LatentCache":
-        return LatentCache(rows_to_tiled(rows))
+    def from_rows(rows: torch.Tensor, role: str = "k") -> "LatentCache":
+        return LatentCache(rows_to_tiled(rows, role), role)
 
     def to_rows(self) -> torch.Tensor:
-        return tiled_to_rows(self.data)
+        return tiled_to_rows(self.data, self.role)
 
     @property
     def shape(self) -> Tuple[int, int, int, int]:

@@ -165,11 +165,15 @@ def _as_dev(t: torch.Tensor, name: str, dtype=None, device=None) -> torch.Tensor
     return t
 
 
-def _cache_arg(t, name: str, device):
-    """(storage tensor, logical shape, layout id) of a row-major tensor or a LatentCache."""
+def _cache_arg(t, name: str, device, role: Optional[str] = None):
+    """(storage tensor, logical shape, layout id) of a row-major tensor or a LatentCache; a tiled cache
+    passed where the op reads K (role "k") or V (role "v") must be stored in that role's tile order."""
     if isinstance(t, LatentCache):
         _as_dev(t.data, name, torch.bfloat16, device)
-        return t.data, tuple(t.shape), _native.LAYOUT_TILED
+        _require(role is None or t.role == role,
+                 f"{name} is a LatentCache in {t.role!r} tile order; this argument reads a {role!r} cache")
+        layout = _native.LAYOUT_TILED if t.role == "k" else _native.LAYOUT_TILED_V
+        return t.data, tuple(t.shape), (_native.LAYOUT_TILED if role is not None else layout)
     _require(isinstance(t, torch.Tensor) and t.dim() == 4, f"{name} must be [B, n_groups, S, width] or a LatentCache")
     _as_dev(t, name, torch.bfloat16, device)
     return t, tuple(t.shape), _native.LAYOUT_ROWS
@@ -198,7 +202,7 @@ def _cur_pos(cur_pos_tensor: torch.Tensor, batch: int, device) -> torch.Tensor:
 def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_tensor, *, rot_step=None,
                      trans_mat=None, u_v=None, scale=None, heads_per_core=None, rot_mode="dst", table_mcast=True,
                      program_config=None, compute_kernel_config=None, memory_config=None,
-                     out_dtype=torch.bfloat16, out=None, workspace=None) -> torch.Tensor:
+                     out_dtype=torch.bfloat16, out=None, workspace=None, deterministic=False) -> torch.Tensor:
     """Fused latent flash-decode (ttnn.transformer.palu_sdpa_decode). Returns [1, B, n_q, head_dim_v].
 
     For every p <= cur_pos[b]: K[p] = RoPE_p(k_latent[p] @ u_k) with u_k = w_rot[..., :128], then
@@ -207,14 +211,17 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
 
     compute_kernel_config and memory_config are accepted for call compatibility and unused (the kernel
     always accumulates in fp32; the output is a fresh tensor unless ``out`` is given).
+    deterministic=True fixes which wave of a workgroup sums which 32-position block, so repeated calls
+    are bit-identical; the default hands blocks out from a counter (faster; calls differ at the bf16
+    rounding of the softmax probabilities, well inside the parity tolerance).
     """
     del compute_kernel_config, memory_config
     _require(isinstance(q, torch.Tensor) and q.dim() == 4 and q.shape[0] == 1 and q.shape[3] == HEAD_DIM,
              f"q must be [1, B, n_q, {HEAD_DIM}], got {tuple(getattr(q, 'shape', ()))}")
     dev = q.device
     _as_dev(q, "q", torch.bfloat16)
-    k_store, k_shape, layout = _cache_arg(k_latent, "k_latent", dev)
-    v_store, v_shape, v_layout = _cache_arg(v_latent, "v_latent", dev)
+    k_store, k_shape, layout = _cache_arg(k_latent, "k_latent", dev, "k")
+    v_store, v_shape, v_layout = _cache_arg(v_latent, "v_latent", dev, "v")
     _require(layout == v_layout, "k_latent and v_latent must use the same cache layout")
     B, n_groups, S, r_k = k_shape
     _require(tuple(v_shape[:3]) == (B, n_groups, S),
@@ -261,12 +268,13 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
         _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv),
         float(HEAD_DIM ** -0.5 if scale is None else scale), int(heads_per_core or 0), rot, int(bool(table_mcast)),
         _k_chunk(program_config), B, n_q, n_kv, n_groups, S, r_k, r_v, w_width, cs.shape[0], cs.shape[1],
-        _DTYPES[cs.dtype], _DTYPES[out_dtype], layout, _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
+        _DTYPES[cs.dtype], _DTYPES[out_dtype], layout, int(bool(deterministic)), _native.ptr(ws), ws_bytes,
+        _native.stream_handle(dev)))
     return out
 
 
 def flash_decode(q, k, v, cur_pos_tensor, *, scale=None, head_dim_v=None, out_dtype=torch.bfloat16, out=None,
-                 workspace=None) -> torch.Tensor:
+                 workspace=None, deterministic=False) -> torch.Tensor:
     """Stock flash-decode over full rotated K [B, n_kv, S, 128] and V [B, n_kv, S, head_dim_v]: the
     MI355X counterpart of ttnn.transformer.scaled_dot_product_attention_decode (head_dim_v 128) and
     flash_multi_latent_attention_decode (head_dim_v = V width). Returns [1, B, n_q, head_dim_v]."""
@@ -274,8 +282,8 @@ def flash_decode(q, k, v, cur_pos_tensor, *, scale=None, head_dim_v=None, out_dt
              f"q must be [1, B, n_q, {HEAD_DIM}]")
     dev = q.device
     _as_dev(q, "q", torch.bfloat16)
-    k_store, k_shape, layout = _cache_arg(k, "k", dev)
-    v_store, v_shape, v_layout = _cache_arg(v, "v", dev)
+    k_store, k_shape, layout = _cache_arg(k, "k", dev, "k")
+    v_store, v_shape, v_layout = _cache_arg(v, "v", dev, "v")
     _require(layout == v_layout, "k and v must use the same cache layout")
     B, n_kv, S, hd = k_shape
     _require(hd == HEAD_DIM, f"k must be [B, n_kv, S, {HEAD_DIM}], got {k_shape}")
@@ -293,7 +301,7 @@ def flash_decode(q, k, v, cur_pos_tensor, *, scale=None, head_dim_v=None, out_dt
     _native.check(lib.palu_flash_decode(
         _native.ptr(q), _native.ptr(k_store), _native.ptr(v_store), _native.ptr(cp), _native.ptr(out),
         float(HEAD_DIM ** -0.5 if scale is None else scale), B, n_q, n_kv, S, width, _DTYPES[out_dtype], layout,
-        _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
+        int(bool(deterministic)), _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
     return out
 
 
