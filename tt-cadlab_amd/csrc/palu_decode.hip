@@ -110,6 +110,8 @@ struct DecodeArgs {
 //   ukT   u_k^T, rows padded by 16 bytes (bank spread)                               HD x (RK + 8) bf16
 //   qx    per wave, the rotated query regrouped into its MFMA operand layout         NW x 4 KB
 //   tl    (cos, sin) of angle 32*Lo*f, Lo < 32: the low part of a block base          [32][64] float2
+//   qs    the item's query rows (zero rows past rep), so the block loop issues no global load
+//         besides the latent prefetch                                                 [16][128] bf16
 //   ctr   the block counter
 //   th    (cos, sin) of angle 1024*H*f, H < ceil(S / 1024): the high part             [nH][64] float2
 //   kc    staging of rows 0..31 of cs_tab ([t][f] float2) while rtab is built, overlaying qx
@@ -122,10 +124,12 @@ struct Smem {
   static constexpr int QX_WAVE_BYTES = 16 * 4 * 8 * 4 * 2;   // [head 16][g 4][row tile 8][4 dims] bf16
   static constexpr int QX_BYTES = KFULL ? 0 : NW * QX_WAVE_BYTES;
   static constexpr int TL_BYTES = KFULL ? 0 : 32 * 64 * 8;
+  static constexpr int QS_BYTES = KFULL ? 0 : 16 * HD * 2;
   static constexpr int UKT_OFFSET = RTAB_BYTES;
   static constexpr int QX_OFFSET = UKT_OFFSET + UKT_BYTES;
   static constexpr int TL_OFFSET = QX_OFFSET + QX_BYTES;
-  static constexpr int MAIN_BYTES = TL_OFFSET + TL_BYTES;
+  static constexpr int QS_OFFSET = TL_OFFSET + TL_BYTES;
+  static constexpr int MAIN_BYTES = QS_OFFSET + QS_BYTES;
   static constexpr int MERGE_BYTES = NW * 16 * (RV + 2) * 4;
   static constexpr int CTR_OFFSET = ((MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES) + 15) & ~15;
   static constexpr int TH_OFFSET = CTR_OFFSET + 16;
@@ -159,10 +163,12 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   float2* tl = reinterpret_cast<float2*>(smem + SM::TL_OFFSET);
   float2* th = reinterpret_cast<float2*>(smem + SM::TH_OFFSET);
   float2* kc = reinterpret_cast<float2*>(smem + SM::QX_OFFSET);
+  __bf16* qs_lds = reinterpret_cast<__bf16*>(smem + SM::QS_OFFSET);
   int* ctr = reinterpret_cast<int*>(smem + SM::CTR_OFFSET);
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, held in a scalar register
   const int n = lane & 15, g = lane >> 4;
   const int item = blockIdx.y, split = blockIdx.x;
   const int b = item / a.n_kv, kvh = item - b * a.n_kv;
@@ -184,11 +190,15 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   //   V, TILED: register vd[mt] of lane (m = n, g) = block positions 8*g .. 8*g+7 of V column 16*mt + m,
   //     which is directly the A operand of O^T += V^T P^T.
   //   V, ROWS: register vd[c*VB + vb] holds the row pieces like K; an identity MFMA regroups them.
-  // ROWS clamps rows past the cache end (their scores and values are masked).
-  auto load_blk = [&](int base, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[VT]) {
+  // ROWS clamps rows past the cache end (their scores and values are masked). A load that is not live
+  // (past the wave's last block) still issues the same instructions, at the block given, with every
+  // lane on the block's first bytes (TILED), so the number of loads in flight is the same on every
+  // path; its data is never used.
+  auto load_blk = [&](int base, bool live, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[VT]) {
     if constexpr (TILED) {
-      const __bf16* kt = kbase + (long long)(base >> 5) * (32 * RK) + lane * 8;
-      const __bf16* vt = vbase + (long long)(base >> 5) * (32 * RV) + lane * 8;
+      const int lo = live ? lane * 8 : 0;
+      const __bf16* kt = kbase + (long long)(base >> 5) * (32 * RK) + lo;
+      const __bf16* vt = vbase + (long long)(base >> 5) * (32 * RV) + lo;
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -212,10 +222,13 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     }
   };
 
-  // Blocks are handed out from an LDS counter so that the waves of a workgroup finish together
-  // (which wave sums which blocks then depends on timing, and each wave rounds its probabilities to
-  // bf16 against its own running max, so calls differ at that rounding level); wave w starts on block
-  // w. The deterministic schedule gives wave w every NW-th block.
+  // Work is handed out in pairs of full blocks (pair p = blocks 2p, 2p + 1) from an LDS counter, so
+  // that the waves of a workgroup finish together (which wave sums which blocks then depends on
+  // timing, and each wave rounds its probabilities to bf16 against its own running max, so calls
+  // differ at that rounding level); wave w starts on pair w. The deterministic schedule gives wave w
+  // every NW-th pair. A partial last block is taken by wave NW - 1 after its pairs.
+  const int nfull = (s_hi - s_lo) / BLK;
+  const int npairs = (nfull + 1) >> 1;
   if (tid == 0) *ctr = NW;
   bf16x8 kl[2][KB], vl[VT], kln[2][KB], vln[VT];
 
@@ -244,7 +257,13 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       const int e = tid + i * NW * 64;   // consecutive lanes: consecutive ranks, one 8-column block
       if (e < RK * (HD / 8)) ukv[i] = *reinterpret_cast<const bf16x8*>(ukp + (long long)(e % RK) * (2 * HD) + (e / RK) * 8);
     }
-    if (w < nblk) load_blk(s_lo + w * BLK, kl, vl);
+    // query rows: 16 heads x 256 B, 16 bytes per thread for the first 256 threads
+    bf16x8 qrow = bf16x8{};
+    const int qh = tid >> 4, qc = (tid & 15) * 8;
+    if (tid < 16 * (HD / 8) && qh < a.rep)
+      qrow = *reinterpret_cast<const bf16x8*>(a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + qh) * HD + qc);
+    if (w < npairs) load_blk(s_lo + 2 * w * BLK, true, kl, vl);
+    if (tid < 16 * (HD / 8)) *reinterpret_cast<bf16x8*>(qs_lds + qh * HD + qc) = qrow;
     // rows -> [row][f] (cos, sin); lane l < 32 holds cos of f = 2l, 2l+1, lane l >= 32 the sines
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
@@ -279,7 +298,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       rtab[e] = make_float4(x.x, x.y, y.x, y.y);
     }
   } else {
-    if (w < nblk) load_blk(s_lo + w * BLK, kl, vl);
+    if (w < npairs) load_blk(s_lo + 2 * w * BLK, true, kl, vl);
   }
   __syncthreads();
 
@@ -324,7 +343,6 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   // 16*(2*kb + j/4) + 4*g + j%4 that the rebuilt K^T tile has in registers.
   const int qf = lane & 15;                 // dims 8*qf .. 8*qf + 7
   constexpr int QSLOTS = 4;                 // up to 16 query heads per KV head
-  const __bf16* qbase = a.q + ((long long)b * a.n_q + (long long)kvh * a.rep) * HD + 8 * qf;
   if constexpr (KFULL) {
     const bool qvalid = n < a.rep;
     const __bf16* qrow = a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + (qvalid ? n : 0)) * HD;
@@ -355,7 +373,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     for (int k = 0; k < QSLOTS; ++k) {
       const int h = g + 4 * k;
       if (h < a.rep) {
-        const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qbase + h * HD);
+        const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qs_lds + h * HD + 8 * qf);
         bf16x4 y0, y1;
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -378,62 +396,59 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     __builtin_amdgcn_wave_barrier();
   };
 
-  // One block of 32 positions on the buffers (kc, vc); the next block is claimed and its loads are
-  // issued into (kn, vn) first. Returns the next block index. Only the last block of a range can be
+  // One block of 32 positions from the buffers (kc, vc). Only the last block of a range can be
   // partial; it runs the masked variant (PARTIAL), every other block carries no masking work.
-  auto step = [&](auto partial_tag, int blk, bf16x8 (&kc)[2][KB], bf16x8 (&vc)[VT], bf16x8 (&kn)[2][KB],
-                  bf16x8 (&vn)[VT]) __attribute__((always_inline)) -> int {
+  auto compute = [&](auto partial_tag, int blk, const bf16x8 (&kc)[2][KB], const bf16x8 (&vc)[VT])
+                     __attribute__((always_inline)) {
     constexpr bool PARTIAL = decltype(partial_tag)::value;
-    int nxt = nblk;                       // a partial block is the last one: nothing follows it
-    if constexpr (!PARTIAL) {
-      nxt = blk + NW;
-      if (!a.deterministic) {
-        if (lane == 0) nxt = atomicAdd(ctr, 1);
-        nxt = __shfl(nxt, 0, 64);
-      }
-      if (nxt < nblk) load_blk(s_lo + nxt * BLK, kn, vn);
-    }
-
     const int base = s_lo + blk * BLK;
     if constexpr (!KFULL) make_q(base);
 
-    f32x4 sc[2];
+    f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    if constexpr (KFULL) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      f32x4 s = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (KFULL) {
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) s = mfma16(kc[c][kb], qB[kb], s);
-      } else {
-        f32x4 acc[8];
+        for (int kb = 0; kb < 4; ++kb) sc[c] = mfma16(kc[c][kb], qB[kb], sc[c]);
+    } else {
+      // One 32-dim slice of K^T (row tiles 2*kq, 2*kq + 1) at a time, for both position tiles:
+      // rebuild, rotate, pack, and contract it with the matching query slice right away, so only
+      // 16 accumulator registers are live instead of a whole 128 x 16 tile.
 #pragma unroll
-        for (int rt = 0; rt < 8; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kq = 0; kq < 4; ++kq) {
+        f32x4 acc[2][2];
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {       // independent MFMAs back to back
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int rt = 0; rt < 8; ++rt) {
+          for (int h = 0; h < 2; ++h) acc[c][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int rt = 2 * kq + h;
             bf16x8 ua;
             if constexpr (UK_LDS)
               ua = *reinterpret_cast<const bf16x8*>(ukT + (16 * rt + n) * SM::UKT_STRIDE + 32 * kb + 8 * g);
             else
               ua = ukA[rt][kb];
-            acc[rt] = mfma16(ua, kc[c][kb], acc[rt]);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) acc[c][h] = mfma16(ua, kc[c][kb], acc[c][h]);
           }
-        }
         // RoPE by the block offset of this lane's position: (x0, x1) -> (x0 c - x1 s, x1 c + x0 s).
 #pragma unroll
-        for (int rt = 0; rt < 8; ++rt) {
-          const float4 t = rtab[(c * 8 + rt) * 64 + lane];
-          const float x0 = acc[rt][0], x1 = acc[rt][1], x2 = acc[rt][2], x3 = acc[rt][3];
-          acc[rt][0] = x0 * t.x - x1 * t.y;
-          acc[rt][1] = x1 * t.x + x0 * t.y;
-          acc[rt][2] = x2 * t.z - x3 * t.w;
-          acc[rt][3] = x3 * t.z + x2 * t.w;
-        }
+        for (int c = 0; c < 2; ++c) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) s = mfma16(pack8(acc[2 * kb], acc[2 * kb + 1]), qB[kb], s);
+          for (int h = 0; h < 2; ++h) {
+            const float4 t = rtab[(c * 8 + 2 * kq + h) * 64 + lane];
+            const float x0 = acc[c][h][0], x1 = acc[c][h][1], x2 = acc[c][h][2], x3 = acc[c][h][3];
+            acc[c][h][0] = x0 * t.x - x1 * t.y;
+            acc[c][h][1] = x1 * t.x + x0 * t.y;
+            acc[c][h][2] = x2 * t.z - x3 * t.w;
+            acc[c][h][3] = x3 * t.z + x2 * t.w;
+          }
+          sc[c] = mfma16(pack8(acc[c][0], acc[c][1]), qB[kq], sc[c]);
+        }
       }
-      sc[c] = s;
     }
 
     // Causal / range mask: score register i of tile c is position base + 8*g + 4*c + i.
@@ -491,29 +506,34 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       }
       O[mt] = mfma16(vA, pB, O[mt]);
     }
-    return nxt;
   };
 
   const std::integral_constant<bool, false> full_blk;
   const std::integral_constant<bool, true> partial_blk;
-  const int nfull = (s_hi - s_lo) % BLK != 0 ? nblk - 1 : nblk;
-  int blk = w;
-  bool in_second = false;            // the next block's rows sit in (kln, vln)
-  while (blk < nfull) {
-    blk = step(full_blk, blk, kl, vl, kln, vln);
-    if (blk >= nfull) { in_second = true; break; }
-    blk = step(full_blk, blk, kln, vln, kl, vl);
-  }
-  if (blk < nblk) {                  // the partial last block, already loaded
-    if (in_second) {
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) kl[c][kb] = kln[c][kb];
-#pragma unroll
-      for (int mt = 0; mt < VT; ++mt) vl[mt] = vln[mt];
+  // Pair loop: (kl, vl) holds block 2p on entry, (kln, vln) receives block 2p + 1. Every load is
+  // issued unconditionally and the loop has a single exit, so the compiler waits on exactly the
+  // loads of the block about to be used while the next block streams in.
+  int p = w;
+  while (p < npairs) {
+    int pn = p + NW;
+    if (!a.deterministic) {
+      // readfirstlane keeps the pair index in a scalar register: the loop branches stay uniform.
+      int got = 0;
+      if (lane == 0) got = atomicAdd(ctr, 1);
+      pn = __builtin_amdgcn_readfirstlane(got);
     }
-    step(partial_blk, blk, kl, vl, kln, vln);
+    const int b0 = 2 * p;
+    const bool has1 = b0 + 1 < nfull;
+    load_blk(s_lo + (has1 ? b0 + 1 : b0) * BLK, has1, kln, vln);
+    compute(full_blk, b0, kl, vl);
+    const bool hasn = pn < npairs;
+    load_blk(s_lo + (hasn ? 2 * pn : b0) * BLK, hasn, kl, vl);
+    if (has1) compute(full_blk, b0 + 1, kln, vln);
+    p = pn;
+  }
+  if (nfull < nblk && w == NW - 1) {     // the partial last block
+    load_blk(s_lo + nfull * BLK, true, kl, vl);
+    compute(partial_blk, nfull, kl, vl);
   }
 
   // ---- merge the NW wave partials of this workgroup ---------------------------------------------
