@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--no-stock", action="store_true", help="skip the full-KV comparator")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=2, help="batch rows of the CPU baseline sample")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="before timing, run 3 plain device copies of MIB MiB (the reference kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     ap.add_argument("--traffic", default=str(REPO / "profiles" / "palu_decode_b32_ctx8192_r64_traffic.txt"),
                     help="rocprofv3 --pmc summary holding the measured HBM bytes per launch")
     return ap.parse_args()
@@ -162,6 +165,13 @@ def main():
         sys.exit(2)
     from palu_tt import fused
     dev = torch.device("cuda:0")
+    if a.copy_calib:
+        src = torch.ones(a.copy_calib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     wl = build_workload(a, dev)
     B, S, rk, rv = a.batch, a.ctx, a.rank_k, a.rank_v
     out = torch.empty(1, B, NQ, rv, dtype=torch.bfloat16, device=dev)

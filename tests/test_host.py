@@ -1,0 +1,252 @@
+"""Host-side logic of palu_tt against the oracle, and the C-ABI library on a machine without a GPU.
+
+Nothing here launches a kernel: the C-ABI checks load the library, compare its exports with the
+declarations in include/palu_mi355x.h, and drive argument validation, which the library finishes before
+it touches the HIP runtime.
+"""
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import pytest
+import torch
+from safetensors.torch import save_file
+
+from oracle import palu_oracle as ref
+from palu_tt import _build, _native, convert, fused
+
+REPO = Path(__file__).resolve().parents[1]
+HD = 128
+THETA = 500000.0
+LLAMA3 = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+
+
+# ------------------------------------------------------------------------------------------------
+# Tables (palu_tt/fused.py:36-79 of the reference)
+
+def test_table_builders_equal_the_oracle():
+    for scaling in (LLAMA3, None):
+        assert torch.equal(fused.rope_frequencies(HD, THETA, scaling), ref.inv_freq(HD, THETA, scaling))
+        c1, s1 = fused.cos_sin_tables(HD, 2048, THETA, scaling)
+        c0, s0 = ref.cos_sin_tables(HD, 2048, THETA, scaling)
+        assert torch.equal(c1, c0) and torch.equal(s1, s0)
+    c, s = ref.cos_sin_tables(HD, 1024, THETA, LLAMA3)
+    assert torch.equal(fused.cs_table(c, s, 1000), ref.cs_table(c, s, 1000))
+    assert torch.equal(fused.rot_step_table(c, s, 256), ref.rot_step_table(c, s, 256))
+    assert torch.equal(fused.rope_transformation_matrix(HD), ref.rope_transformation_matrix(HD))
+    assert torch.equal(fused.trans_mat_tile()[0, 0], ref.rope_transformation_matrix(HD)[:32, :32])
+    u = torch.randn(2, 64, HD)
+    torch.testing.assert_close(fused.w_rot_from_u_k(u), ref.w_rot_from_u_k(u))
+    for S in (1, 96, 256, 1000, 1024, 8192, 8224, 65536):
+        assert fused.chunk_size(S) == ref.chunk_size(S)
+    x = torch.randn(3, 5, HD)
+    torch.testing.assert_close(fused.apply_rope_meta(x, c[:5], s[:5]), ref.meta_rotate(x, c[:5], s[:5]))
+
+
+# ------------------------------------------------------------------------------------------------
+# Weight layout (palu_tt/convert.py of the reference)
+
+def test_reverse_permute_equals_the_oracle():
+    W = torch.randn(4 * 16, 7)
+    assert torch.equal(convert.reverse_permute(W, 4, 64, 7), ref.reverse_permute(W, 4, 64, 7))
+
+
+def _layer(seed, hidden=256, nh=4, nkv=2, hd=HD):
+    g = torch.Generator().manual_seed(seed)
+    return {"q": torch.randn(nh * hd, hidden, generator=g) * 0.05, "k": torch.randn(nkv * hd, hidden, generator=g) * 0.05,
+            "v": torch.randn(nkv * hd, hidden, generator=g) * 0.05, "o": torch.randn(hidden, nh * hd, generator=g) * 0.05}
+
+
+@pytest.mark.parametrize("r_k,r_v", [(32, 64), (64, 32), (HD, 64), (32, HD)])
+def test_converted_decode_tensors_reproduce_the_layer_oracle(r_k, r_v):
+    """M-LRD: latents from wk/wv_lat_pad, the op model on (u_k, v latent), wo_fused on the r_v-wide output
+    padded to hd == the HF-convention layer oracle's decode step. Covers the full-rank collapses (r == hd)."""
+    hidden, nh, nkv, T = 256, 4, 2, 9
+    W = _layer(r_k + r_v)
+    Uk, VTk = ref.svd_per_head(W["k"], nkv, r_k)
+    Uv, VTv = ref.svd_per_head(W["v"], nkv, r_v)
+    lr = convert.LowRank(VTk, Uk, VTv, Uv)
+    t = convert.palu_layer_tensors(W, lr, nh, nkv, HD)
+    x = torch.randn(1, T, hidden)
+    layer = ref.PaluRefAttention(nh, nkv, HD, THETA, LLAMA3, W["q"], W["o"], ref.Factors(VTk, Uk, VTv, Uv))
+    layer.forward(x[:, :-1], 0)
+    exp = layer.forward(x[:, -1:], T - 1)[0, 0]
+
+    kl = (x[0] @ t["wk_lat_pad"].T).view(T, nkv, HD)          # per KV head, the first r_k columns
+    vl = (x[0] @ t["wv_lat_pad"].T).view(T, nkv, HD)
+    if r_k == HD:                                               # full K rows (Meta order), u_k = I
+        k_lat, u_k = kl.permute(1, 0, 2)[None], torch.eye(HD).expand(nkv, HD, HD)
+    else:
+        k_lat, u_k = kl[..., :r_k].permute(1, 0, 2)[None], t["u_k"]
+        assert torch.equal(t["w_rot"][..., :HD], u_k)
+    v_lat = vl[..., :r_v].permute(1, 0, 2)[None] if r_v != HD else vl.permute(1, 0, 2)[None]
+    q = (x[0, -1] @ W["q"].T).view(nh, HD)
+    cq, sq = ref.hf_cos_sin(torch.tensor([T - 1]), HD, THETA, LLAMA3)
+    q = q * cq + ref.rotate_half(q) * sq
+    q_meta = torch.stack([ref.reverse_permute(q[h][:, None], 1, HD, 1)[:, 0] for h in range(nh)])
+    cos, sin = ref.cos_sin_tables(HD, T, THETA, LLAMA3)
+    o = ref.reference_decode(q_meta[None, None], k_lat, u_k, v_lat, torch.tensor([T - 1]), cos, sin, HD ** -0.5)
+    o_pad = torch.zeros(nh, HD)
+    o_pad[:, :o.shape[-1]] = o[0, 0]
+    torch.testing.assert_close(o_pad.reshape(-1) @ t["wo_fused"].T, exp, atol=2e-5, rtol=1e-4)
+
+
+def _write_palu_dir(path: Path, layers, hidden, hd, groups_k, groups_v, seed=0):
+    """A Palu factor directory in the on-disk format load_palu_dir reads (reference compress.py:37-46)."""
+    g = torch.Generator().manual_seed(seed)
+    ranks, tensors = {}, {}
+    for i in range(layers):
+        for proj, groups in (("k_proj", groups_k), ("v_proj", groups_v)):
+            key = f"model.layers.{i}.self_attn.{proj}"
+            gs = len(groups[0][1])
+            ranks[key] = [r for r, _ in groups]
+            tensors[f"{key}.VT.weight"] = torch.randn(sum(r for r, _ in groups), hidden, generator=g)
+            for gi, (r, _) in enumerate(groups):
+                tensors[f"{key}.U.{gi}.weight"] = torch.randn(gs * hd, r, generator=g)
+    path.mkdir(parents=True, exist_ok=True)
+    (path / "config.json").write_text(json.dumps({"head_wise_ranks": ranks}))
+    save_file(tensors, str(path / "palu_lowrank.safetensors"))
+    return ranks, tensors
+
+
+def test_load_palu_dir_mlrd_and_glrd(tmp_path):
+    hidden, hd, nkv = 64, 16, 4
+    mlrd = [(24, [0]), (40, [1]), (8, [2]), (32, [3])]            # group size 1, ragged ranks
+    glrd = [(48, [0, 1]), (20, [2, 3])]                           # 2 groups of 2 heads
+    ranks, tensors = _write_palu_dir(tmp_path / "m", 1, hidden, hd, mlrd, glrd)
+    with pytest.raises(AssertionError, match="group size"):
+        convert.load_palu_dir(tmp_path / "m", 1, nkv, hd)
+    ranks, tensors = _write_palu_dir(tmp_path / "g", 2, hidden, hd, glrd, glrd)
+    lr = convert.load_palu_dir(tmp_path / "g", 2, nkv, hd, rank_multiple=32)
+    assert set(lr) == {0, 1} and lr[0].group_size == 2 and lr[0].r_k == 64     # 48 padded up to 64
+    key = "model.layers.1.self_attn.k_proj"
+    VT_all = tensors[f"{key}.VT.weight"]
+    for h in range(nkv):
+        gi = h // 2
+        r = ranks[key][gi]
+        off = sum(ranks[key][:gi])
+        assert torch.equal(lr[1].k_VT[h, :r], VT_all[off:off + r])
+        assert torch.count_nonzero(lr[1].k_VT[h, r:]) == 0 and torch.count_nonzero(lr[1].k_U[h, :, r:]) == 0
+        U_g = tensors[f"{key}.U.{gi}.weight"]
+        assert torch.equal(lr[1].k_U[h, :, :r], U_g[(h % 2) * hd:(h % 2 + 1) * hd])
+    u = convert.load_palu_dir(tmp_path / "g", 2, nkv, hd, latent_scale="unit")
+    for h in range(nkv):
+        torch.testing.assert_close(u[0].k_U[h] @ u[0].k_VT[h], lr[0].k_U[h] @ lr[0].k_VT[h], atol=1e-4, rtol=1e-4)
+    assert torch.count_nonzero(u[0].k_U[2:, :, 20:]) == 0          # rank padding stays zero
+    # with balanced SVD factors (U = U_r sqrt(S), VT = sqrt(S) V_r^T) unit scaling leaves VT orthonormal,
+    # i.e. unit-variance latents for white inputs (reference tests/test_convert.py:453-484)
+    W = torch.randn(nkv * hd, hidden)
+    U, VT = ref.svd_per_head(W, nkv, 12)
+    s = convert.unit_scale_lowrank(convert.LowRank(VT, U, VT.clone(), U.clone()))
+    for h in range(nkv):
+        torch.testing.assert_close(s.k_VT[h] @ s.k_VT[h].T, torch.eye(12), atol=1e-4, rtol=0)
+        torch.testing.assert_close(s.k_U[h] @ s.k_VT[h], U[h] @ VT[h], atol=1e-4, rtol=1e-4)
+    assert convert.palu_dir_cache_id(tmp_path / "g").startswith("g-")
+    assert convert.palu_cache_id_for(tmp_path / "g", "unit").endswith("-unit")
+
+
+def test_glrd_layer_tensors_share_the_group_latent_and_keep_wo():
+    hidden, nh, nkv, gs, r = 256, 8, 4, 2, 64
+    W = _layer(5, hidden, nh, nkv)
+    Uk, VTk = ref.svd_per_head(W["k"], nkv, r)
+    Uv, VTv = ref.svd_per_head(W["v"], nkv, r)
+    for h in range(1, nkv, 2):                 # heads of one group carry the group's VT
+        VTk[h], VTv[h] = VTk[h - 1], VTv[h - 1]
+    t = convert.palu_layer_tensors(W, convert.LowRank(VTk, Uk, VTv, Uv, group_size=gs), nh, nkv, HD)
+    assert torch.equal(t["wo_fused"], W["o"])
+    assert torch.equal(t["wk_lat_pad"][:r], VTk[0]) and torch.count_nonzero(t["wk_lat_pad"][HD:2 * HD]) == 0
+    assert torch.equal(t["wk_lat_pad"][2 * HD:2 * HD + r], VTk[2])
+    assert t["u_v"].shape == (nkv, r, HD) and torch.equal(t["u_v"][1], Uv[1].T)
+
+
+# ------------------------------------------------------------------------------------------------
+# The C-ABI library without a GPU
+
+def _declared_functions():
+    text = (REPO / "include" / "palu_mi355x.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(palu_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _build.library_path().exists():
+        _build.build_native()
+    return _native.load()
+
+
+def test_library_exports_every_declared_function(lib):
+    names = _declared_functions()
+    assert names == sorted(_native.EXPORTED), f"header declares {names}, binding has {sorted(_native.EXPORTED)}"
+    raw = ctypes.CDLL(str(_build.library_path()))
+    for n in names:
+        assert getattr(raw, n) is not None
+    assert lib.palu_abi_version() == _native.ABI_VERSION
+    hdr = (REPO / "include" / "palu_mi355x.h").read_text()
+    assert f"#define PALU_ABI_VERSION {_native.ABI_VERSION}" in hdr
+
+
+def test_workspace_query(lib):
+    # the headline shape (256 items on 256 CUs) needs no split; a long single row splits
+    assert lib.palu_decode_workspace_bytes(32, 8, 8192, 64) == 0
+    ws = lib.palu_decode_workspace_bytes(1, 8, 65536, 64)
+    assert ws > 0 and ws % 4 == 0
+    assert lib.palu_decode_workspace_bytes(0, 8, 8192, 64) == 0
+
+
+_FAKE = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced: validation fails before any use
+
+
+def _sdpa(lib, **kw):
+    a = dict(q=_FAKE, k=_FAKE, w=_FAKE, cs=_FAKE, v=_FAKE, head_dim_v=64, cur=_FAKE, out=_FAKE, rot_step=None,
+             trans_mat=None, u_v=None, scale=0.088, heads_per_core=0, rot_mode=2, table_mcast=1, k_chunk=0,
+             batch=2, n_q=8, n_kv=2, n_groups=2, seq_len=256, r_k=64, r_v=64, w_rot_width=256, cs_rows=256,
+             cs_cols=256, cs_dtype=0, out_dtype=1, layout=0, det=0, ws=None, ws_bytes=0, stream=None)
+    a.update(kw)
+    rc = lib.palu_sdpa_decode(a["q"], a["k"], a["w"], a["cs"], a["v"], a["head_dim_v"], a["cur"], a["out"],
+                              a["rot_step"], a["trans_mat"], a["u_v"], a["scale"], a["heads_per_core"], a["rot_mode"],
+                              a["table_mcast"], a["k_chunk"], a["batch"], a["n_q"], a["n_kv"], a["n_groups"],
+                              a["seq_len"], a["r_k"], a["r_v"], a["w_rot_width"], a["cs_rows"], a["cs_cols"],
+                              a["cs_dtype"], a["out_dtype"], a["layout"], a["det"], a["ws"], a["ws_bytes"], a["stream"])
+    return rc, lib.palu_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(r_k=48), _native.PALU_EINVAL, "r_k"),
+    (dict(cs_cols=128), _native.PALU_EINVAL, "cs_tab"),
+    (dict(cs_rows=100), _native.PALU_EINVAL, "cs_tab"),
+    (dict(w_rot_width=128), _native.PALU_EINVAL, "w_rot"),
+    (dict(rot_step=_FAKE), _native.PALU_EINVAL, "optional together"),
+    (dict(k_chunk=256), _native.PALU_EINVAL, "Phase 1"),
+    (dict(rot_mode=5), _native.PALU_EINVAL, "rot_mode must be"),
+    (dict(n_groups=3, n_kv=4), _native.PALU_EINVAL, "heads_per_group"),
+    (dict(u_v=_FAKE, head_dim_v=64), _native.PALU_EINVAL, "head_dim_v"),
+    (dict(u_v=_FAKE, head_dim_v=128), _native.PALU_EUNSUPPORTED, "u_v"),
+    (dict(head_dim_v=128), _native.PALU_EINVAL, "head_dim_v"),
+    (dict(heads_per_core=4), _native.PALU_EINVAL, "heads_per_core"),
+    (dict(n_q=6, n_kv=4, n_groups=4), _native.PALU_EINVAL, "KV head count"),
+    (dict(n_kv=4, n_groups=2), _native.PALU_EINVAL, "u_v"),                 # grouped V latent without u_v
+    (dict(heads_per_core=2), _native.PALU_EINVAL, "grouped latents"),     # per-head latents cannot be shared
+    (dict(heads_per_core=8, n_q=16, n_kv=4, n_groups=2), _native.PALU_EINVAL, "KV head count"),
+    (dict(heads_per_core=4, n_q=16, n_kv=4, n_groups=2), _native.PALU_EINVAL, "heads_per_group"),
+    (dict(layout=1, seq_len=100, cs_rows=100), _native.PALU_EINVAL, "multiple of 32"),
+    (dict(seq_len=70000, cs_rows=70000), _native.PALU_EUNSUPPORTED, "65536"),
+    (dict(q=ctypes.c_void_p((1 << 20) + 2)), _native.PALU_EINVAL, "aligned"),
+    (dict(out=None), _native.PALU_EINVAL, "null"),
+])
+def test_sdpa_decode_envelope_errors(lib, kw, code, needle):
+    rc, msg = _sdpa(lib, **kw)
+    assert rc == code and needle in msg, (rc, msg)
+
+
+def test_flash_decode_and_append_envelope_errors(lib):
+    rc = lib.palu_flash_decode(_FAKE, _FAKE, _FAKE, _FAKE, _FAKE, 0.1, 2, 6, 4, 256, 128, 1, 0, 0, None, 0, None)
+    assert rc == _native.PALU_EINVAL and "KV head count" in lib.palu_last_error().decode()
+    rc = lib.palu_flash_decode(_FAKE, _FAKE, _FAKE, _FAKE, _FAKE, 0.1, 2, 8, 2, 100, 128, 1, 1, 0, None, 0, None)
+    assert rc == _native.PALU_EINVAL and "multiple of 32" in lib.palu_last_error().decode()
+    rc = lib.palu_latent_append(_FAKE, _FAKE, _FAKE, 2, 2, 256, 12, 0, None)
+    assert rc == _native.PALU_EINVAL and "multiple of 8" in lib.palu_last_error().decode()
+    rc = lib.palu_latent_append(_FAKE, _FAKE, _FAKE, 2, 2, 256, 48, 1, None)
+    assert rc == _native.PALU_EINVAL and "multiple of 32" in lib.palu_last_error().decode()
