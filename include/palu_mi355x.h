@@ -80,7 +80,7 @@ size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_di
  *   seq_len                          at most 65536
  *   rot_step, trans_mat              the reference's Phase 2 constants; optional together. They are
  *                                    validated as the reference does and otherwise unused: this kernel
- *                                    always rotates chunk-relative from cs_tab.
+ *                                    always rotates block-relative (32 positions) from cs_tab.
  *   u_v      [n_kv, r_v, 128] bf16   in-kernel V rebuild for grouped latents (not built yet: returns
  *                                    PALU_EUNSUPPORTED)
  *   scale                            softmax scale (the reference passes head_dim^-0.5)

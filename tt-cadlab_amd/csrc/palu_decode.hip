@@ -9,30 +9,31 @@
 // fp32 model palu_tt/fused.py:82-107).
 //
 // Kernel shape (all MFMA work is v_mfma_f32_16x16x32_bf16, bf16 in / fp32 accumulate):
-//   * A workgroup owns one item and one split of its sequence; its NW waves each own a contiguous
-//     slice of that split, so a wave streams its latent rows straight from HBM into registers with
-//     16-byte loads, one block of 32 positions at a time, prefetching the next block.
+//   * A workgroup owns one item and one split of its sequence. Its NW waves take pairs of 32-position
+//     blocks from an LDS counter (or, in deterministic mode, every NW-th pair) and stream each block
+//     from HBM straight into registers, the next block's loads in flight while the current one is
+//     computed. The block index lives in a scalar register and every load is issued on every path,
+//     so the compiler waits on exactly the loads a step consumes.
 //   * Two cache layouts. ROWS is the reference's logical [B, G, S, r] row-major tensor. TILED stores
-//     every 32-position block as (2 * r / 32) tiles of 1 KB already in MFMA operand order (tile (c, kb),
-//     slot l = 16*g + n holds ranks 32*kb + 8*g .. +7 of position 8*(n/4) + 4*c + n%4 of the block), so
-//     each wave load instruction is one contiguous 1 KB and is issued nontemporal (the stream is read
-//     once per decode step).
-//   * K is rebuilt transposed, K^T[d][p] = u_k^T[d][:] . lat[p][:]: the accumulator layout then gives
-//     every lane one position and 4 consecutive head dims per 16-dim tile, so each RoPE pair
-//     (Meta-interleaved dims 2f, 2f+1) sits in one lane and the rotation is plain VALU work on the
-//     fp32 accumulators.
-//   * RoPE is applied chunk-relative: K rows are rotated by their offset t inside a 128-position
-//     chunk (angle table resident in LDS, laid out in lane order), and the query is rotated back by
-//     the chunk base once per chunk, q~ = R_{-s0} q. Rotations in one plane commute, so
-//     q~ . R_t k = q . R_{s0+t} k, the score of the reference.
-//   * The rebuilt K tile is reused in registers as the A operand of the QK MFMA; the head dim is
-//     contracted in a permuted order that the query operand mirrors, so no lane shuffles are needed.
+//     every 32-position block as r / 16 tiles of 1 KB already in MFMA operand order (K-tile order for
+//     K, V-tile order for V; see include/palu_mi355x.h), so each wave load instruction is one
+//     contiguous 1 KB, issued nontemporal (the stream is read once per decode step).
+//   * K is rebuilt transposed, K^T[d][p] = u_k^T[d][:] . lat[p][:], one 32-dim slice at a time: the
+//     accumulator layout gives every lane one position and 4 consecutive head dims per 16-dim tile, so
+//     each RoPE pair (Meta-interleaved dims 2f, 2f+1) sits in one lane and the rotation is plain VALU
+//     work on the fp32 accumulators.
+//   * RoPE is applied block-relative: K rows are rotated by their offset t < 32 inside the block (an
+//     LDS table in lane order), and the query is rotated back by the block base once per block,
+//     q~ = R_{-base} q, with cos/sin of the base built by angle addition from two small LDS tables
+//     (base = 1024 H + 32 Lo). Rotations in one plane commute, so q~ . R_t k = q . R_{base+t} k, the
+//     score of the reference.
+//   * The rebuilt K slice is packed to bf16 in registers and used as the A operand of the QK MFMA; the
+//     head dim is contracted in a permuted order that the query operand mirrors, so no lane shuffles
+//     are needed.
 //   * Scores come out with one head per lane column. The online softmax runs in the exp2 domain
 //     (scale * log2 e folded into q~) with a lazily refreshed running max, and the probabilities feed
-//     the PV MFMA directly as its B operand.
-//   * The V rows are brought into the PV A-operand layout (8 consecutive positions of one latent
-//     column per lane) by an MFMA against an identity tile: exact in bf16, and it keeps the
-//     transpose on the matrix core instead of LDS or VALU.
+//     the PV MFMA directly as its B operand. TILED V is already the PV A operand; ROWS V is regrouped
+//     by an MFMA against an identity tile (exact in bf16).
 //   * The waves of a workgroup merge their (O, m, l) partials in LDS; several splits of one item are
 //     merged by a second small kernel through a caller-provided workspace.
 #include <hip/hip_runtime.h>

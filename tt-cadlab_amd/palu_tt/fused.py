@@ -17,8 +17,8 @@ fast path); both caches of one call use the same layout.
 
 The reference's Tensix switches (rot_step/trans_mat selecting Phase 2, rot_mode, table_mcast,
 heads_per_core, program_config chunk) are accepted and validated with the reference's messages. The
-MI355X kernel has one schedule: K rows are rotated by their offset inside a 128-position chunk from
-an LDS-resident table and the query is rotated back by the chunk base, which is the reference's Phase 2
+MI355X kernel has one schedule: K rows are rotated by their offset inside a 32-position block from
+an LDS-resident table and the query is rotated back by the block base, which is the reference's Phase 2
 identity (fused.py:1-24) with a fixed chunk; results do not depend on those switches.
 """
 import math
