@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define PALU_ABI_VERSION 4
+#define PALU_ABI_VERSION 5
 
 #define PALU_OK 0
 #define PALU_EINVAL 1       /* arguments outside the op's envelope */
@@ -96,6 +96,25 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
                      int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
                      void* workspace, size_t workspace_bytes, palu_stream_t stream);
 
+/* Paged fused latent flash-decode: palu_sdpa_decode over caches held in fixed-size pages. The reference
+ * keeps contiguous per-row caches (palu_tt/attention.py:86, 274-283); paging follows ttnn's paged decode
+ * interface (paged_scaled_dot_product_attention_decode: page pools plus a per-row page table).
+ *   k_pages     [num_pages, n_groups, page_size, r_k] bf16 pool (row-major, or tiled per 32-position
+ *               block inside each page when cache_layout is PALU_LAYOUT_TILED)
+ *   v_pages     [num_pages, n_groups, page_size, r_v] bf16 pool, same layout
+ *   page_table  [batch, max_pages_per_seq] int32 (device): position p of row b lives on page
+ *               page_table[b][p / page_size], row p % page_size. Ids are clamped into [0, num_pages).
+ *   page_size   a power of two in 32..4096; the logical length is max_pages_per_seq * page_size
+ *               (at most 65536) and cs_tab needs that many rows.
+ * Every other argument as for palu_sdpa_decode; palu_decode_workspace_bytes takes the logical length. */
+int palu_sdpa_decode_paged(const void* q, const void* k_pages, const void* w_rot, const void* cs_tab,
+                           const void* v_pages, int head_dim_v, const int32_t* cur_pos, const int32_t* page_table,
+                           void* out, const float* rot_step, const void* trans_mat, const void* u_v, float scale,
+                           int heads_per_core, int rot_mode, int table_mcast, int k_chunk, int batch, int n_q, int n_kv,
+                           int n_groups, int num_pages, int page_size, int max_pages_per_seq, int r_k, int r_v,
+                           int w_rot_width, int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout,
+                           int deterministic, void* workspace, size_t workspace_bytes, palu_stream_t stream);
+
 /* Stock flash-decode over full, already-rotated K and a V cache of width head_dim_v. Replaces
  * ttnn.transformer.scaled_dot_product_attention_decode (head_dim_v == 128) and
  * ttnn.transformer.flash_multi_latent_attention_decode (head_dim_v == r_v), the two ops the reference's
@@ -108,6 +127,15 @@ int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t
                       int batch, int n_q, int n_kv, int seq_len, int head_dim_v, int out_dtype, int cache_layout,
                       int deterministic, void* workspace, size_t workspace_bytes, palu_stream_t stream);
 
+/* Stock flash-decode over paged full K / V pools ([num_pages, n_kv, page_size, 128] and
+ * [num_pages, n_kv, page_size, head_dim_v]); replaces ttnn.transformer.paged_scaled_dot_product_attention_decode.
+ * Paging arguments as for palu_sdpa_decode_paged, the rest as for palu_flash_decode. */
+int palu_flash_decode_paged(const void* q, const void* k_pages, const void* v_pages, const int32_t* cur_pos,
+                            const int32_t* page_table, void* out, float scale, int batch, int n_q, int n_kv,
+                            int num_pages, int page_size, int max_pages_per_seq, int head_dim_v, int out_dtype,
+                            int cache_layout, int deterministic, void* workspace, size_t workspace_bytes,
+                            palu_stream_t stream);
+
 /* Latent append: cache[b, g, update_idxs[b], :] = new_rows[b, g, :] for every row whose index lies in
  * [0, seq_len) (other rows are skipped). Replaces ttnn.experimental.paged_update_cache on the latent
  * caches (palu_tt/attention.py:622-623).
@@ -116,6 +144,15 @@ int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t
  *   PALU_LAYOUT_TILED (a K cache) or PALU_LAYOUT_TILED_V (a V cache). */
 int palu_latent_append(void* cache, const void* new_rows, const int32_t* update_idxs, int batch, int n_groups,
                        int seq_len, int width, int cache_layout, palu_stream_t stream);
+
+/* Paged latent append: row b goes to page page_table[b][update_idxs[b] / page_size] of the pool
+ * [num_pages, n_groups, page_size, width], row update_idxs[b] % page_size (rows whose position is past
+ * max_pages_per_seq * page_size or whose page id is outside the pool are skipped). Replaces
+ * ttnn.experimental.paged_update_cache with a page table (palu_tt/attention.py:622-623 is its
+ * contiguous use). Layouts as for palu_latent_append. */
+int palu_latent_append_paged(void* cache_pages, const void* new_rows, const int32_t* update_idxs,
+                             const int32_t* page_table, int batch, int n_groups, int num_pages, int page_size,
+                             int max_pages_per_seq, int width, int cache_layout, palu_stream_t stream);
 
 #ifdef __cplusplus
 }

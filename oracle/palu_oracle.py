@@ -29,6 +29,7 @@ How each function is pinned (tests/test_oracle.py):
                                  == fresh prefill (ref tests/test_reference.py:17-35)
   reverse_permute             -- equals the Meta interleave of HF's rotate_half halves
   svd_per_head                -- exact at full rank, error monotone in rank (ref tests/test_compress.py)
+  gather_pages                -- element-by-element position -> (page, row) loop
 """
 import math
 from dataclasses import dataclass
@@ -161,6 +162,15 @@ def reference_decode(q, k_lat, u_k, v_lat, cur_pos, cos, sin, scale: float, u_v=
         p = torch.softmax(sc, dim=-1)
         outs.append(torch.einsum("hs,hsr->hr", p, V))
     return torch.stack(outs)[None]
+
+
+def gather_pages(pool: torch.Tensor, page_table: torch.Tensor) -> torch.Tensor:
+    """Paged cache -> contiguous rows: pool [n_pages, G, page_size, r], page_table [B, max_pages] ->
+    [B, G, max_pages * page_size, r], position p of row b taken from page page_table[b, p // page_size],
+    row p % page_size (the paged-cache convention of ttnn's paged decode and paged_update_cache)."""
+    pages = pool[page_table.long()]                        # [B, max_pages, G, page_size, r]
+    B, mp, G, ps, r = pages.shape
+    return pages.permute(0, 2, 1, 3, 4).reshape(B, G, mp * ps, r)
 
 
 @torch.no_grad()

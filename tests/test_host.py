@@ -250,3 +250,37 @@ def test_flash_decode_and_append_envelope_errors(lib):
     assert rc == _native.PALU_EINVAL and "multiple of 8" in lib.palu_last_error().decode()
     rc = lib.palu_latent_append(_FAKE, _FAKE, _FAKE, 2, 2, 256, 48, 1, None)
     assert rc == _native.PALU_EINVAL and "multiple of 32" in lib.palu_last_error().decode()
+
+
+def test_paged_envelope_errors(lib):
+    pt = _FAKE
+
+    def sdpa_paged(page_table=pt, num_pages=16, page_size=64, max_pages=4, **kw):
+        a = dict(head_dim_v=64, r_k=64, r_v=64, n_groups=2, n_kv=2, cs_rows=256, layout=0)
+        a.update(kw)
+        rc = lib.palu_sdpa_decode_paged(_FAKE, _FAKE, _FAKE, _FAKE, _FAKE, a["head_dim_v"], _FAKE, page_table, _FAKE,
+                                        None, None, None, 0.088, 0, 2, 1, 0, 2, 8, a["n_kv"], a["n_groups"], num_pages,
+                                        page_size, max_pages, a["r_k"], a["r_v"], 256, a["cs_rows"], 256, 0, 1,
+                                        a["layout"], 0, None, 0, None)
+        return rc, lib.palu_last_error().decode()
+
+    assert sdpa_paged(page_table=None) == (_native.PALU_EINVAL, "palu_sdpa_decode_paged: page_table is null")
+    rc, msg = sdpa_paged(page_size=48)
+    assert rc == _native.PALU_EINVAL and "power of two" in msg
+    rc, msg = sdpa_paged(page_size=16)
+    assert rc == _native.PALU_EINVAL and "page_size" in msg
+    rc, msg = sdpa_paged(num_pages=0)
+    assert rc == _native.PALU_EINVAL and "num_pages" in msg
+    rc, msg = sdpa_paged(max_pages=2048, cs_rows=131072)
+    assert rc == _native.PALU_EUNSUPPORTED and "65536" in msg
+    rc, msg = sdpa_paged(cs_rows=200)              # logical length 4 * 64 = 256 > 200 table rows
+    assert rc == _native.PALU_EINVAL and "cs_tab" in msg
+    rc, msg = sdpa_paged(r_k=48)
+    assert rc == _native.PALU_EINVAL and "r_k" in msg
+    rc = lib.palu_flash_decode_paged(_FAKE, _FAKE, _FAKE, _FAKE, None, _FAKE, 0.1, 2, 8, 2, 16, 64, 4, 128, 1, 0, 0,
+                                     None, 0, None)
+    assert rc == _native.PALU_EINVAL and "page_table" in lib.palu_last_error().decode()
+    rc = lib.palu_latent_append_paged(_FAKE, _FAKE, _FAKE, _FAKE, 2, 2, 16, 96, 4, 64, 0, None)
+    assert rc == _native.PALU_EINVAL and "power of two" in lib.palu_last_error().decode()
+    rc = lib.palu_latent_append_paged(_FAKE, _FAKE, _FAKE, _FAKE, 2, 2, 16, 64, 4, 48, 1, None)
+    assert rc == _native.PALU_EINVAL and "multiple of 32" in lib.palu_last_error().decode()

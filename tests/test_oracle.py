@@ -325,3 +325,15 @@ def test_pins_catch_planted_mistakes():
     assert not torch.allclose(a, b, atol=1e-4)
     # (4) plain frequencies where llama3 scaling is asked for -> differ from transformers' llama3 values
     assert not torch.allclose(ref.inv_freq(HD, THETA, None), rot.inv_freq.float(), rtol=1e-3)
+
+
+def test_gather_pages_follows_the_page_table_position_by_position():
+    G, ps, r, B, maxp = 2, 4, 3, 3, 5
+    pool = torch.randn(11, G, ps, r)
+    pt = torch.randint(0, 11, (B, maxp), dtype=torch.int32)
+    rows = ref.gather_pages(pool, pt)
+    assert rows.shape == (B, G, maxp * ps, r)
+    for b in range(B):
+        for g in range(G):
+            for p in range(maxp * ps):
+                assert torch.equal(rows[b, g, p], pool[int(pt[b, p // ps]), g, p % ps])

@@ -1,0 +1,376 @@
+// C-ABI of libpalu_mi355x.so (declarations and argument meaning: include/palu_mi355x.h): argument
+// validation with the reference op's messages, the latent-append kernel, and dispatch to the decode
+// translation units.
+#include "palu_kernel.h"
+
+namespace palu {
+
+thread_local char g_err[1024] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+}  // namespace palu
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_layout(int layout, int seq_len, const char* who) {
+  if (layout != PALU_LAYOUT_ROWS && layout != PALU_LAYOUT_TILED)
+    return fail(PALU_EINVAL, "%s: cache layout must be PALU_LAYOUT_ROWS or PALU_LAYOUT_TILED, got %d", who, layout);
+  if (layout == PALU_LAYOUT_TILED && seq_len % 32 != 0)
+    return fail(PALU_EINVAL, "%s: a tiled cache holds whole 32-position blocks; seq_len %d is not a multiple of 32", who,
+                seq_len);
+  return PALU_OK;
+}
+
+// Paged pools: page_size a power of two in 32..4096 (whole 32-position blocks per page), at least one
+// page, a page table of max_pages_per_seq entries per row. Returns log2(page_size / 32) in *shift.
+int check_pages(const int32_t* page_table, int num_pages, int page_size, int max_pages, int* shift, const char* who) {
+  if (!page_table) return fail(PALU_EINVAL, "%s: page_table is null", who);
+  if (page_size < 32 || page_size > 4096 || (page_size & (page_size - 1)) != 0)
+    return fail(PALU_EINVAL, "%s: page_size must be a power of two in 32..4096, got %d", who, page_size);
+  if (num_pages <= 0 || max_pages <= 0)
+    return fail(PALU_EINVAL, "%s: num_pages and max_pages_per_seq must be positive, got %d and %d", who, num_pages,
+                max_pages);
+  if ((long long)max_pages * page_size > 65536)
+    return fail(PALU_EUNSUPPORTED, "%s: max_pages_per_seq * page_size = %lld positions; this build covers 65536", who,
+                (long long)max_pages * page_size);
+  int s = 0;
+  while ((32 << s) < page_size) ++s;
+  *shift = s;
+  return PALU_OK;
+}
+
+// Offset (elements) of width-index k of position p inside one (b, g) stream of width R, K-tile order.
+__device__ __forceinline__ long long tiled_k_offset(int p, int k, int R) {
+  const int t = p & 31, c = (t >> 2) & 1, nn = ((t >> 3) << 2) | (t & 3);
+  const int kb = k >> 5, gg = (k >> 3) & 3;
+  return (long long)(p >> 5) * (32 * R) + ((c * (R >> 5) + kb) * 64 + 16 * gg + nn) * 8 + (k & 7);
+}
+
+// V-tile order: tile mt = k / 16, slot 16 * (t / 8) + k % 16, element t % 8 (t = p % 32).
+__device__ __forceinline__ long long tiled_v_offset(int p, int k, int R) {
+  const int t = p & 31;
+  return (long long)(p >> 5) * (32 * R) + ((k >> 4) * 64 + 16 * (t >> 3) + (k & 15)) * 8 + (t & 7);
+}
+
+// Latent append: cache[b, g, idx[b], :] = rows[b, g, :]; each thread moves 8 consecutive values. A
+// contiguous cache is [B, G, S, width]; a paged pool is [n_pages, G, S, width] with S the page size,
+// and position p of row b lives on page page_table[b * pt_stride + p / S] (ids outside the pool skip
+// the row).
+template <int LAYOUT, bool PAGED>
+__global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const __bf16* rows, const int32_t* idx,
+                                                          const int32_t* page_table, int pt_stride, int n_pages,
+                                                          int B, int G, int S, int width) {
+  const int vec = width / 8;
+  const long long total = (long long)B * G * vec;
+  for (long long e = blockIdx.x * (long long)blockDim.x + threadIdx.x; e < total; e += (long long)gridDim.x * blockDim.x) {
+    const int v = (int)(e % vec);
+    const long long bg = e / vec;
+    const int b = (int)(bg / G), gi = (int)(bg - (long long)b * G);
+    int p = idx[b];
+    long long slab;
+    if constexpr (PAGED) {
+      if (p < 0 || p >= pt_stride * S) continue;
+      const int pid = page_table[(long long)b * pt_stride + p / S];
+      if (pid < 0 || pid >= n_pages) continue;
+      slab = (long long)pid * G + gi;
+      p &= S - 1;
+    } else {
+      if (p < 0 || p >= S) continue;
+      slab = bg;
+    }
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(rows + bg * width + 8 * v);
+    __bf16* stream = cache + slab * S * width;
+    if constexpr (LAYOUT == PALU_LAYOUT_ROWS) {
+      *reinterpret_cast<bf16x8*>(stream + (long long)p * width + 8 * v) = x;
+    } else if constexpr (LAYOUT == PALU_LAYOUT_TILED) {
+      *reinterpret_cast<bf16x8*>(stream + tiled_k_offset(p, 8 * v, width)) = x;
+    } else {
+      const long long o = tiled_v_offset(p, 8 * v, width);   // 8 slots 16 bytes apart
+#pragma unroll
+      for (int j = 0; j < 8; ++j) stream[o + 8 * j] = x[j];
+    }
+  }
+}
+
+template <bool PAGED>
+int launch_append(void* cache, const void* new_rows, const int32_t* update_idxs, const int32_t* page_table,
+                  int pt_stride, int n_pages, int batch, int n_groups, int S, int width, int layout, hipStream_t stream) {
+  const long long total = (long long)batch * n_groups * (width / 8);
+  int blocks = (int)((total + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  auto* c = static_cast<__bf16*>(cache);
+  auto* r = static_cast<const __bf16*>(new_rows);
+  if (layout == PALU_LAYOUT_TILED)
+    hipLaunchKernelGGL((palu_append_kernel<PALU_LAYOUT_TILED, PAGED>), dim3(blocks), dim3(256), 0, stream, c, r,
+                       update_idxs, page_table, pt_stride, n_pages, batch, n_groups, S, width);
+  else if (layout == PALU_LAYOUT_TILED_V)
+    hipLaunchKernelGGL((palu_append_kernel<PALU_LAYOUT_TILED_V, PAGED>), dim3(blocks), dim3(256), 0, stream, c, r,
+                       update_idxs, page_table, pt_stride, n_pages, batch, n_groups, S, width);
+  else
+    hipLaunchKernelGGL((palu_append_kernel<PALU_LAYOUT_ROWS, PAGED>), dim3(blocks), dim3(256), 0, stream, c, r,
+                       update_idxs, page_table, pt_stride, n_pages, batch, n_groups, S, width);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PALU_EHIP, "append kernel launch: %s", hipGetErrorString(e));
+  return PALU_OK;
+}
+
+int check_append(void* cache, const void* new_rows, const int32_t* update_idxs, int batch, int n_groups, int S,
+                 int width, int layout, const char* who) {
+  if (!cache || !new_rows || !update_idxs) return fail(PALU_EINVAL, "%s: a required pointer is null", who);
+  if (batch <= 0 || n_groups <= 0 || S <= 0 || width <= 0 || width % 8 != 0)
+    return fail(PALU_EINVAL, "%s: width must be a positive multiple of 8, got %d", who, width);
+  if (int rc = check_layout(layout == PALU_LAYOUT_TILED_V ? PALU_LAYOUT_TILED : layout, S, who)) return rc;
+  if (layout != PALU_LAYOUT_ROWS && width % 32 != 0)
+    return fail(PALU_EINVAL, "%s: a tiled cache row is a multiple of 32 wide, got %d", who, width);
+  if (!aligned16(cache) || !aligned16(new_rows)) return fail(PALU_EINVAL, "%s: 16-byte alignment required", who);
+  return PALU_OK;
+}
+
+// Validation shared by the contiguous and paged fused decode; fills every field of a except the
+// cache strides and the paging fields.
+int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w_rot, const void* cs_tab,
+               const void* v_latent, int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step,
+               const void* trans_mat, const void* u_v, float scale, int heads_per_core, int rot_mode, int k_chunk,
+               int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width, int cs_rows,
+               int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic, void* workspace,
+               size_t workspace_bytes, const char* who) {
+  if (!q || !k_latent || !w_rot || !cs_tab || !v_latent || !cur_pos || !out)
+    return fail(PALU_EINVAL, "%s: a required tensor pointer is null", who);
+  if (rot_mode < 0 || rot_mode > 2) return fail(PALU_EINVAL, "rot_mode must be 'legacy', 'pack' or 'dst'");
+  if ((rot_step == nullptr) != (trans_mat == nullptr))
+    return fail(PALU_EINVAL, "rot_step and trans_mat are optional together: pass both (Phase 2) or neither (Phase 1)");
+  if (rot_step == nullptr && k_chunk > 128)
+    return fail(PALU_EINVAL, "Phase 1 streams the angle table per chunk and needs k_chunk_size <= 128, got %d", k_chunk);
+  if (k_chunk < 0 || (k_chunk > 0 && (k_chunk % 32 != 0 || (k_chunk & (k_chunk - 1)) != 0)))
+    return fail(PALU_EINVAL, "k_chunk_size must be 0 or a power of two multiple of 32, got %d", k_chunk);
+  if (batch <= 0 || n_q <= 0 || n_kv <= 0 || n_groups <= 0 || seq_len <= 0)
+    return fail(PALU_EINVAL, "%s: batch, head counts and seq_len must be positive", who);
+  if (r_k <= 0 || r_k % 32 != 0 || r_k > 512)
+    return fail(PALU_EINVAL, "r_k must be a multiple of 32 in 32..512 (the latent width of k_latent), got %d", r_k);
+  if (r_v <= 0 || r_v % 32 != 0 || r_v > 512)
+    return fail(PALU_EINVAL, "r_v must be a multiple of 32 in 32..512 (the latent width of v_latent), got %d", r_v);
+  if (n_kv % n_groups != 0)
+    return fail(PALU_EINVAL, "heads_per_group: %d latent heads do not divide the %d KV heads of w_rot", n_groups, n_kv);
+  const int hpg = n_kv / n_groups;
+  if (w_rot_width != 2 * HD)
+    return fail(PALU_EINVAL, "w_rot must be [1, n_kv, r_k, %d] = [u_k | u_k T], got last dim %d", 2 * HD, w_rot_width);
+  if (cs_cols != 2 * HD) return fail(PALU_EINVAL, "cs_tab must be [1, 1, S, %d] = [cos | sin], got last dim %d", 2 * HD, cs_cols);
+  if (cs_rows < seq_len)
+    return fail(PALU_EINVAL, "cs_tab has %d rows but the latent cache has %d positions", cs_rows, seq_len);
+  if (seq_len > 65536)
+    return fail(PALU_EUNSUPPORTED, "seq_len %d: this build's block-angle tables cover 65536 positions", seq_len);
+  if (n_q % n_kv != 0 || n_q / n_kv > 16)
+    return fail(PALU_EINVAL, "KV head count %d must divide the %d query heads with at most 16 query heads per KV head", n_kv, n_q);
+  if (heads_per_core > 1) {
+    if (heads_per_core > n_kv)
+      return fail(PALU_EINVAL, "heads_per_core %d exceeds the KV head count %d", heads_per_core, n_kv);
+    if (hpg == 1) return fail(PALU_EINVAL, "heads_per_core > 1 shares a latent between heads and needs grouped latents");
+    if (hpg % heads_per_core != 0)
+      return fail(PALU_EINVAL, "heads_per_core %d must divide heads_per_group %d", heads_per_core, hpg);
+  }
+  if (u_v != nullptr) {
+    if (head_dim_v != HD) return fail(PALU_EINVAL, "head_dim_v must be %d when u_v rebuilds V in-kernel, got %d", HD, head_dim_v);
+    return fail(PALU_EUNSUPPORTED, "u_v (in-kernel V rebuild, grouped latents) is not built in this library yet");
+  }
+  if (hpg != 1) return fail(PALU_EINVAL, "grouped V latent (heads_per_group %d) needs u_v", hpg);
+  if (head_dim_v != r_v)
+    return fail(PALU_EINVAL, "head_dim_v %d must equal the V latent width %d on the absorbed-V path", head_dim_v, r_v);
+  if (cs_dtype != PALU_DTYPE_F32 && cs_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "cs_tab dtype must be fp32 or bf16");
+  if (out_dtype != PALU_DTYPE_F32 && out_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "output dtype must be fp32 or bf16");
+  if (int rc = check_layout(cache_layout, seq_len, who)) return rc;
+  if (!aligned16(q) || !aligned16(k_latent) || !aligned16(v_latent) || !aligned16(w_rot) || !aligned16(cs_tab))
+    return fail(PALU_EINVAL, "q, k_latent, v_latent, w_rot and cs_tab must be 16-byte aligned");
+  if ((long long)batch * n_kv > 65535) return fail(PALU_EUNSUPPORTED, "batch * n_kv = %d exceeds the grid limit", batch * n_kv);
+
+  memset(&a, 0, sizeof(a));
+  a.q = static_cast<const __bf16*>(q);
+  a.k = static_cast<const __bf16*>(k_latent);
+  a.v = static_cast<const __bf16*>(v_latent);
+  a.w_rot = static_cast<const __bf16*>(w_rot);
+  a.cs = cs_tab;
+  a.cur_pos = cur_pos;
+  a.out = out;
+  a.ws = static_cast<float*>(workspace);
+  a.ws_bytes = workspace_bytes;
+  a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = hpg; a.S = seq_len; a.cs_rows = cs_rows;
+  a.deterministic = deterministic ? 1 : 0;
+  a.qscale = scale * 1.4426950408889634f;
+  return PALU_OK;
+}
+
+int sdpa_dispatch(const DecodeArgs& a, bool paged, int cache_layout, int r_k, int r_v, int cs_dtype, int out_dtype,
+                  hipStream_t stream) {
+  const bool tiled = cache_layout == PALU_LAYOUT_TILED;
+  if (paged)
+    return tiled ? dispatch_latent_tiled_paged(a, r_k, r_v, cs_dtype, out_dtype, stream)
+                 : dispatch_latent_rows_paged(a, r_k, r_v, cs_dtype, out_dtype, stream);
+  return tiled ? dispatch_latent_tiled(a, r_k, r_v, cs_dtype, out_dtype, stream)
+               : dispatch_latent_rows(a, r_k, r_v, cs_dtype, out_dtype, stream);
+}
+
+int flash_setup(DecodeArgs& a, const void* q, const void* k, const void* v, const int32_t* cur_pos, void* out,
+                float scale, int batch, int n_q, int n_kv, int seq_len, int head_dim_v, int out_dtype, int cache_layout,
+                int deterministic, void* workspace, size_t workspace_bytes, const char* who) {
+  if (!q || !k || !v || !cur_pos || !out) return fail(PALU_EINVAL, "%s: a required tensor pointer is null", who);
+  if (batch <= 0 || n_q <= 0 || n_kv <= 0 || seq_len <= 0)
+    return fail(PALU_EINVAL, "%s: batch, head counts and seq_len must be positive", who);
+  if (n_q % n_kv != 0 || n_q / n_kv > 16)
+    return fail(PALU_EINVAL, "KV head count %d must divide the %d query heads with at most 16 query heads per KV head", n_kv, n_q);
+  if (out_dtype != PALU_DTYPE_F32 && out_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "output dtype must be fp32 or bf16");
+  if (int rc = check_layout(cache_layout, seq_len, who)) return rc;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return fail(PALU_EINVAL, "q, k and v must be 16-byte aligned");
+  if ((long long)batch * n_kv > 65535) return fail(PALU_EUNSUPPORTED, "batch * n_kv = %d exceeds the grid limit", batch * n_kv);
+  memset(&a, 0, sizeof(a));
+  a.q = static_cast<const __bf16*>(q);
+  a.k = static_cast<const __bf16*>(k);
+  a.v = static_cast<const __bf16*>(v);
+  a.cur_pos = cur_pos;
+  a.out = out;
+  a.ws = static_cast<float*>(workspace);
+  a.ws_bytes = workspace_bytes;
+  a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = 1; a.S = seq_len; a.cs_rows = 0;
+  a.deterministic = deterministic ? 1 : 0;
+  a.qscale = scale * 1.4426950408889634f;
+  return PALU_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* palu_last_error(void) { return palu::g_err; }
+
+int palu_abi_version(void) { return PALU_ABI_VERSION; }
+
+size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_dim_v) {
+  if (batch <= 0 || n_kv <= 0 || seq_len <= 0 || head_dim_v <= 0) return 0;
+  // The narrowest workgroup splits the most, so its plan bounds every kernel variant.
+  Plan p = plan_splits(batch * n_kv, seq_len, MIN_NW);
+  return ws_bytes(batch * n_kv, p.n_splits, head_dim_v);
+}
+
+int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab, const void* v_latent,
+                     int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step, const void* trans_mat,
+                     const void* u_v, float scale, int heads_per_core, int rot_mode, int table_mcast, int k_chunk,
+                     int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width,
+                     int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  (void)table_mcast;
+  DecodeArgs a;
+  if (int rc = sdpa_setup(a, q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos, out, rot_step, trans_mat, u_v,
+                          scale, heads_per_core, rot_mode, k_chunk, batch, n_q, n_kv, n_groups, seq_len, r_k, r_v,
+                          w_rot_width, cs_rows, cs_cols, cs_dtype, out_dtype, cache_layout, deterministic, workspace,
+                          workspace_bytes, "palu_sdpa_decode"))
+    return rc;
+  a.k_sg = (long long)seq_len * r_k;
+  a.k_sb = a.k_sg * n_groups;
+  a.v_sg = (long long)seq_len * r_v;
+  a.v_sb = a.v_sg * n_groups;
+  return sdpa_dispatch(a, false, cache_layout, r_k, r_v, cs_dtype, out_dtype, stream);
+}
+
+int palu_sdpa_decode_paged(const void* q, const void* k_pages, const void* w_rot, const void* cs_tab,
+                           const void* v_pages, int head_dim_v, const int32_t* cur_pos, const int32_t* page_table,
+                           void* out, const float* rot_step, const void* trans_mat, const void* u_v, float scale,
+                           int heads_per_core, int rot_mode, int table_mcast, int k_chunk, int batch, int n_q, int n_kv,
+                           int n_groups, int num_pages, int page_size, int max_pages_per_seq, int r_k, int r_v,
+                           int w_rot_width, int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout,
+                           int deterministic, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  (void)table_mcast;
+  int shift = 0;
+  if (int rc = check_pages(page_table, num_pages, page_size, max_pages_per_seq, &shift, "palu_sdpa_decode_paged"))
+    return rc;
+  const int seq_len = max_pages_per_seq * page_size;
+  DecodeArgs a;
+  if (int rc = sdpa_setup(a, q, k_pages, w_rot, cs_tab, v_pages, head_dim_v, cur_pos, out, rot_step, trans_mat, u_v,
+                          scale, heads_per_core, rot_mode, k_chunk, batch, n_q, n_kv, n_groups, seq_len, r_k, r_v,
+                          w_rot_width, cs_rows, cs_cols, cs_dtype, out_dtype, cache_layout, deterministic, workspace,
+                          workspace_bytes, "palu_sdpa_decode_paged"))
+    return rc;
+  a.k_sg = (long long)page_size * r_k;
+  a.k_sb = a.k_sg * n_groups;
+  a.v_sg = (long long)page_size * r_v;
+  a.v_sb = a.v_sg * n_groups;
+  a.page_table = page_table;
+  a.pt_stride = max_pages_per_seq;
+  a.n_pages = num_pages;
+  a.page_shift = shift;
+  return sdpa_dispatch(a, true, cache_layout, r_k, r_v, cs_dtype, out_dtype, stream);
+}
+
+int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t* cur_pos, void* out, float scale,
+                      int batch, int n_q, int n_kv, int seq_len, int head_dim_v, int out_dtype, int cache_layout,
+                      int deterministic, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  DecodeArgs a;
+  if (int rc = flash_setup(a, q, k, v, cur_pos, out, scale, batch, n_q, n_kv, seq_len, head_dim_v, out_dtype,
+                           cache_layout, deterministic, workspace, workspace_bytes, "palu_flash_decode"))
+    return rc;
+  a.k_sg = (long long)seq_len * HD;
+  a.k_sb = a.k_sg * n_kv;
+  a.v_sg = (long long)seq_len * head_dim_v;
+  a.v_sb = a.v_sg * n_kv;
+  return dispatch_full(a, cache_layout == PALU_LAYOUT_TILED, false, head_dim_v, out_dtype == PALU_DTYPE_F32, stream);
+}
+
+int palu_flash_decode_paged(const void* q, const void* k_pages, const void* v_pages, const int32_t* cur_pos,
+                            const int32_t* page_table, void* out, float scale, int batch, int n_q, int n_kv,
+                            int num_pages, int page_size, int max_pages_per_seq, int head_dim_v, int out_dtype,
+                            int cache_layout, int deterministic, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream) {
+  palu::g_err[0] = 0;
+  int shift = 0;
+  if (int rc = check_pages(page_table, num_pages, page_size, max_pages_per_seq, &shift, "palu_flash_decode_paged"))
+    return rc;
+  const int seq_len = max_pages_per_seq * page_size;
+  DecodeArgs a;
+  if (int rc = flash_setup(a, q, k_pages, v_pages, cur_pos, out, scale, batch, n_q, n_kv, seq_len, head_dim_v,
+                           out_dtype, cache_layout, deterministic, workspace, workspace_bytes, "palu_flash_decode_paged"))
+    return rc;
+  a.k_sg = (long long)page_size * HD;
+  a.k_sb = a.k_sg * n_kv;
+  a.v_sg = (long long)page_size * head_dim_v;
+  a.v_sb = a.v_sg * n_kv;
+  a.page_table = page_table;
+  a.pt_stride = max_pages_per_seq;
+  a.n_pages = num_pages;
+  a.page_shift = shift;
+  return dispatch_full(a, cache_layout == PALU_LAYOUT_TILED, true, head_dim_v, out_dtype == PALU_DTYPE_F32, stream);
+}
+
+int palu_latent_append(void* cache, const void* new_rows, const int32_t* update_idxs, int batch, int n_groups,
+                       int seq_len, int width, int cache_layout, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  if (int rc = check_append(cache, new_rows, update_idxs, batch, n_groups, seq_len, width, cache_layout,
+                            "palu_latent_append"))
+    return rc;
+  return launch_append<false>(cache, new_rows, update_idxs, nullptr, 0, 0, batch, n_groups, seq_len, width,
+                              cache_layout, stream);
+}
+
+int palu_latent_append_paged(void* cache_pages, const void* new_rows, const int32_t* update_idxs,
+                             const int32_t* page_table, int batch, int n_groups, int num_pages, int page_size,
+                             int max_pages_per_seq, int width, int cache_layout, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  int shift = 0;
+  if (int rc = check_pages(page_table, num_pages, page_size, max_pages_per_seq, &shift, "palu_latent_append_paged"))
+    return rc;
+  if (int rc = check_append(cache_pages, new_rows, update_idxs, batch, n_groups, page_size, width, cache_layout,
+                            "palu_latent_append_paged"))
+    return rc;
+  return launch_append<true>(cache_pages, new_rows, update_idxs, page_table, max_pages_per_seq, num_pages, batch,
+                             n_groups, page_size, width, cache_layout, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,11 @@
+// Fused latent decode kernels for row-major caches: every latent width and
+// (table, output) dtype pair, instantiated in a translation unit of their own to keep builds parallel.
+#include "palu_kernel.h"
+
+namespace palu {
+
+int dispatch_latent_rows(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s) {
+  return dispatch_dtypes<false, false>(a, rk, rv, cs_dtype, out_dtype, s);
+}
+
+}  // namespace palu

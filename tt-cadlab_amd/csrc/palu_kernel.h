@@ -1,4 +1,5 @@
-// Palu fused latent flash-decode for MI355X (gfx950): HIP kernels and their C-ABI.
+// Palu fused latent flash-decode for MI355X (gfx950): the decode kernels, shared by the translation
+// units that instantiate them (palu_decode_*.hip) and the C-ABI (palu_capi.hip).
 //
 // One work item is one (batch row b, KV head h). Per position p <= cur_pos[b] the item's key is
 // rebuilt from its latent row, K[p] = RoPE_p(lat_k[p] @ u_k[h]), and the GQA group of query heads
@@ -36,6 +37,7 @@
 //     by an MFMA against an identity tile (exact in bf16).
 //   * The waves of a workgroup merge their (O, m, l) partials in LDS; several splits of one item are
 //     merged by a second small kernel through a caller-provided workspace.
+#pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stddef.h>
@@ -47,7 +49,7 @@
 
 #include "../../include/palu_mi355x.h"
 
-namespace {
+namespace palu {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -57,6 +59,79 @@ constexpr int HD = 128;     // head dim
 constexpr int BLK = 32;     // positions per block: two 16-position MFMA tiles, also the rotation chunk
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LAZY_RESCALE_LOG2 = 8.0f;  // running max is refreshed when a score exceeds it by > 2^8
+
+struct DecodeArgs {
+  const __bf16* q;        // [B, n_q, HD], already rotated at its own position
+  const __bf16* k;        // latent [B, n_groups, S, RK]   or full rotated K [B, n_kv, S, HD]
+  const __bf16* v;        // latent [B, n_groups, S, RV]   or full V [B, n_kv, S, RV]
+  const __bf16* w_rot;    // [n_kv, RK, 2*HD]; columns 0..HD-1 are u_k (Meta head order)
+  const void* cs;         // [cs_rows, 2*HD]: [cos | sin], Meta-interleaved, fp32 or bf16
+  const int32_t* cur_pos; // [B], inclusive last valid position
+  void* out;              // [B, n_q, RV]
+  float* ws;              // [items, n_splits, 16, RV + 2] split partials (n_splits > 1)
+  size_t ws_bytes;
+  long long k_sb, k_sg;   // element strides of k: batch, group (row stride is RK / HD)
+  long long v_sb, v_sg;
+  int B, n_q, n_kv, rep, hpg, S, cs_rows;
+  int split_len;          // positions per workgroup split, a multiple of BLK
+  int n_splits;
+  int deterministic;      // 1: wave w takes blocks w, w + NW, ... (reproducible); 0: blocks from a counter
+  float qscale;           // softmax scale * log2(e)
+  // Paged caches: k/v are page pools [n_pages, G, page_size, width] (rows or tiled) and k_sb / v_sb are
+  // page strides; the page of block J of row b is page_table[b * pt_stride + (J >> page_shift)].
+  const int32_t* page_table;
+  int pt_stride, n_pages, page_shift;
+};
+
+// Error reporting (defined in palu_capi.hip): formats the message for palu_last_error, returns code.
+int fail(int code, const char* fmt, ...);
+
+// Waves per workgroup: 8 (two per SIMD) where the kernel fits 256 registers, else 4 (one per SIMD,
+// which lets the compiler use the full 512-entry register file instead of spilling).
+template <int RK, int RV, bool KFULL, bool TILED>
+constexpr int pick_nw() {
+  // 8 waves where the kernel fits 256 VGPRs without spilling (checked per instantiation with
+  // -Rpass-analysis=kernel-resource-usage), else 4 waves with the 512-register budget.
+  if (KFULL) return 8;
+  return (RK == 64 && RV == 128) ? 4 : 8;
+}
+constexpr int MIN_NW = 4;
+constexpr int TARGET_WGS = 256;  // one workgroup per CU at full occupancy of the chip
+
+struct Plan {
+  int n_splits, split_len;
+};
+
+inline Plan plan_splits(int items, int S, int nw) {
+  // Positions per workgroup: about TARGET_WGS workgroups over the whole job, in whole blocks for
+  // every wave; a sequence is split across workgroups only when its items alone cannot fill the chip.
+  const long long total = (long long)items * S;
+  const long long unit = (long long)BLK * nw;
+  long long per_wg = (total + TARGET_WGS - 1) / TARGET_WGS;
+  per_wg = ((per_wg + unit - 1) / unit) * unit;
+  const long long whole = (((long long)S + BLK - 1) / BLK) * BLK;
+  if (per_wg > whole) per_wg = whole;
+  return Plan{(int)((S + per_wg - 1) / per_wg), (int)per_wg};
+}
+
+inline size_t ws_bytes(int items, int n_splits, int rv) {
+  return n_splits <= 1 ? 0 : (size_t)items * n_splits * 16 * (rv + 2) * sizeof(float);
+}
+
+
+// Decode dispatchers, one translation unit each (cs_dtype / out_dtype are PALU_DTYPE_*).
+int dispatch_latent_rows(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
+int dispatch_latent_tiled(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
+int dispatch_latent_rows_paged(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
+int dispatch_latent_tiled_paged(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
+int dispatch_full(const DecodeArgs& a, bool tiled, bool paged, int dv, bool f32_out, hipStream_t s);
+
+}  // namespace palu
+
+// Kernels and launch templates are local to each translation unit that instantiates them.
+namespace {
+
+using namespace palu;
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -86,24 +161,6 @@ __device__ __forceinline__ float wave_sum_xor48(float x) {
   return x;
 }
 
-struct DecodeArgs {
-  const __bf16* q;        // [B, n_q, HD], already rotated at its own position
-  const __bf16* k;        // latent [B, n_groups, S, RK]   or full rotated K [B, n_kv, S, HD]
-  const __bf16* v;        // latent [B, n_groups, S, RV]   or full V [B, n_kv, S, RV]
-  const __bf16* w_rot;    // [n_kv, RK, 2*HD]; columns 0..HD-1 are u_k (Meta head order)
-  const void* cs;         // [cs_rows, 2*HD]: [cos | sin], Meta-interleaved, fp32 or bf16
-  const int32_t* cur_pos; // [B], inclusive last valid position
-  void* out;              // [B, n_q, RV]
-  float* ws;              // [items, n_splits, 16, RV + 2] split partials (n_splits > 1)
-  size_t ws_bytes;
-  long long k_sb, k_sg;   // element strides of k: batch, group (row stride is RK / HD)
-  long long v_sb, v_sg;
-  int B, n_q, n_kv, rep, hpg, S, cs_rows;
-  int split_len;          // positions per workgroup split, a multiple of BLK
-  int n_splits;
-  int deterministic;      // 1: wave w takes blocks w, w + NW, ... (reproducible); 0: blocks from a counter
-  float qscale;           // softmax scale * log2(e)
-};
 
 // LDS map of one workgroup (latent mode; full-K mode keeps only the merge buffer and the counter):
 //   rtab  block-relative K rotation, float4 {cos f, sin f, cos f+1, sin f+1} per (tile, 16-dim row
@@ -135,7 +192,7 @@ struct Smem {
   static constexpr int CTR_OFFSET = ((MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES) + 15) & ~15;
   static constexpr int TH_OFFSET = CTR_OFFSET + 16;
   static_assert(KFULL || QX_BYTES >= 32 * 64 * 8, "the cs_tab staging rows overlay qx");
-  static int bytes(int S) { return TH_OFFSET + (KFULL ? 0 : ((S + 1023) / 1024) * 64 * 8); }
+  __host__ __device__ static int bytes(int S) { return TH_OFFSET + (KFULL ? 0 : ((S + 1023) / 1024) * 64 * 8); }
 };
 
 template <typename T>
@@ -148,7 +205,7 @@ __device__ __forceinline__ float4 load4f<__bf16>(const __bf16* p) {
   return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 
-template <int RK, int RV, bool KFULL, bool TILED, int NW, typename TabT, typename OutT>
+template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, int NW, typename TabT, typename OutT>
 __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a) {
   static_assert(RK % 32 == 0 && RK <= 128, "RK");
   static_assert(RV % 32 == 0 && RV <= 128, "RV");
@@ -166,6 +223,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   float2* kc = reinterpret_cast<float2*>(smem + SM::QX_OFFSET);
   __bf16* qs_lds = reinterpret_cast<__bf16*>(smem + SM::QS_OFFSET);
   int* ctr = reinterpret_cast<int*>(smem + SM::CTR_OFFSET);
+  int* pt_lds = reinterpret_cast<int*>(smem + SM::bytes(a.S));   // paged: this split's page ids
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -182,8 +240,29 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   const int s_hi = min(len, s_lo + a.split_len);
   const int nblk = s_hi > s_lo ? (s_hi - s_lo + BLK - 1) / BLK : 0;
 
-  const __bf16* kbase = a.k + b * a.k_sb + grp * a.k_sg;
-  const __bf16* vbase = a.v + b * a.v_sb + grp * a.v_sg;
+  const __bf16* kbase = a.k + (PAGED ? 0 : b * a.k_sb) + grp * a.k_sg;
+  const __bf16* vbase = a.v + (PAGED ? 0 : b * a.v_sb) + grp * a.v_sg;
+
+  // Paged caches: page ids of the split's blocks, staged in LDS during the prologue (the first block
+  // of each wave reads its id from global memory). Ids are clamped into the pool, so a bad page table
+  // reads wrong rows but never leaves the allocation.
+  const int pg_lo = PAGED ? ((s_lo >> 5) >> a.page_shift) : 0;
+  const int bmask = PAGED ? (1 << a.page_shift) - 1 : 0;
+  auto clamp_page = [&](int p) { return p < 0 ? 0 : (p >= a.n_pages ? a.n_pages - 1 : p); };
+  auto page_global = [&](int base) -> int {
+    if constexpr (!PAGED) return 0;
+    return clamp_page(a.page_table[(long long)b * a.pt_stride + ((base >> 5) >> a.page_shift)]);
+  };
+  auto page_lds = [&](int base) -> int {
+    if constexpr (!PAGED) return 0;
+    return clamp_page(__builtin_amdgcn_readfirstlane(pt_lds[((base >> 5) >> a.page_shift) - pg_lo]));
+  };
+  // Element offset of the 32-position block at position base (page pid when paged) in a stream of
+  // width W whose page (or row) stride is page_stride.
+  auto blk_off = [&](int base, int pid, long long page_stride, int W) -> long long {
+    if constexpr (PAGED) return (long long)pid * page_stride + (long long)((base >> 5) & bmask) * (32 * W);
+    return (long long)(base >> 5) * (32 * W);
+  };
 
   // One block's K (latent or full) and V rows into registers.
   //   K, both layouts: register kd[c][kb] of lane (n, g) = width-index 32*kb + 8*g .. +7 of block
@@ -195,11 +274,11 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   // (past the wave's last block) still issues the same instructions, at the block given, with every
   // lane on the block's first bytes (TILED), so the number of loads in flight is the same on every
   // path; its data is never used.
-  auto load_blk = [&](int base, bool live, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[VT]) {
+  auto load_blk = [&](int base, bool live, int pid, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[VT]) {
     if constexpr (TILED) {
       const int lo = live ? lane * 8 : 0;
-      const __bf16* kt = kbase + (long long)(base >> 5) * (32 * RK) + lo;
-      const __bf16* vt = vbase + (long long)(base >> 5) * (32 * RV) + lo;
+      const __bf16* kt = kbase + blk_off(base, pid, a.k_sb, RK) + lo;
+      const __bf16* vt = vbase + blk_off(base, pid, a.v_sb, RV) + lo;
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -211,10 +290,10 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     } else {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        int p = base + 8 * (n >> 2) + 4 * c + (n & 3);
-        p = p < a.S ? p : a.S - 1;
-        const __bf16* kr = kbase + (long long)p * RK + 8 * g;
-        const __bf16* vr = vbase + (long long)p * RV + 8 * g;
+        int t = 8 * (n >> 2) + 4 * c + (n & 3);     // position in the block
+        if (!PAGED && base + t >= a.S) t = a.S - 1 - base;   // a page always holds whole blocks
+        const __bf16* kr = kbase + blk_off(base, pid, a.k_sb, RK) + (long long)t * RK + 8 * g;
+        const __bf16* vr = vbase + blk_off(base, pid, a.v_sb, RV) + (long long)t * RV + 8 * g;
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) kd[c][kb] = *reinterpret_cast<const bf16x8*>(kr + 32 * kb);
 #pragma unroll
@@ -228,7 +307,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   // timing, and each wave rounds its probabilities to bf16 against its own running max, so calls
   // differ at that rounding level); wave w starts on pair w. The deterministic schedule gives wave w
   // every NW-th pair. A partial last block is taken by wave NW - 1 after its pairs.
-  const int nfull = (s_hi - s_lo) / BLK;
+  const int nfull = s_hi > s_lo ? (s_hi - s_lo) / BLK : 0;   // an empty split (row shorter than s_lo) has none
   const int npairs = (nfull + 1) >> 1;
   if (tid == 0) *ctr = NW;
   bf16x8 kl[2][KB], vl[VT], kln[2][KB], vln[VT];
@@ -263,7 +342,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     const int qh = tid >> 4, qc = (tid & 15) * 8;
     if (tid < 16 * (HD / 8) && qh < a.rep)
       qrow = *reinterpret_cast<const bf16x8*>(a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + qh) * HD + qc);
-    if (w < npairs) load_blk(s_lo + 2 * w * BLK, true, kl, vl);
+    if (w < npairs) load_blk(s_lo + 2 * w * BLK, true, page_global(s_lo + 2 * w * BLK), kl, vl);
     if (tid < 16 * (HD / 8)) *reinterpret_cast<bf16x8*>(qs_lds + qh * HD + qc) = qrow;
     // rows -> [row][f] (cos, sin); lane l < 32 holds cos of f = 2l, 2l+1, lane l >= 32 the sines
 #pragma unroll
@@ -299,7 +378,12 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       rtab[e] = make_float4(x.x, x.y, y.x, y.y);
     }
   } else {
-    if (w < npairs) load_blk(s_lo + 2 * w * BLK, true, kl, vl);
+    if (w < npairs) load_blk(s_lo + 2 * w * BLK, true, page_global(s_lo + 2 * w * BLK), kl, vl);
+  }
+  if constexpr (PAGED) {
+    const int pg_hi = nblk > 0 ? (((s_hi - 1) >> 5) >> a.page_shift) : pg_lo - 1;
+    for (int e = tid; e <= pg_hi - pg_lo; e += NW * 64)
+      pt_lds[e] = clamp_page(a.page_table[(long long)b * a.pt_stride + pg_lo + e]);
   }
   __syncthreads();
 
@@ -525,15 +609,17 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     }
     const int b0 = 2 * p;
     const bool has1 = b0 + 1 < nfull;
-    load_blk(s_lo + (has1 ? b0 + 1 : b0) * BLK, has1, kln, vln);
+    const int base1 = s_lo + (has1 ? b0 + 1 : b0) * BLK;
+    load_blk(base1, has1, page_lds(base1), kln, vln);
     compute(full_blk, b0, kl, vl);
     const bool hasn = pn < npairs;
-    load_blk(s_lo + (hasn ? 2 * pn : b0) * BLK, hasn, kl, vl);
+    const int basen = s_lo + (hasn ? 2 * pn : b0) * BLK;
+    load_blk(basen, hasn, page_lds(basen), kl, vl);
     if (has1) compute(full_blk, b0 + 1, kln, vln);
     p = pn;
   }
   if (nfull < nblk && w == NW - 1) {     // the partial last block
-    load_blk(s_lo + nfull * BLK, true, kl, vl);
+    load_blk(s_lo + nfull * BLK, true, page_lds(s_lo + nfull * BLK), kl, vl);
     compute(partial_blk, nfull, kl, vl);
   }
 
@@ -600,89 +686,8 @@ __global__ __launch_bounds__(256) void palu_merge_kernel(const float* ws, void* 
   }
 }
 
-// Offset (elements) of width-index k of position p inside one (b, g) stream of width R, K-tile order.
-__device__ __forceinline__ long long tiled_k_offset(int p, int k, int R) {
-  const int t = p & 31, c = (t >> 2) & 1, nn = ((t >> 3) << 2) | (t & 3);
-  const int kb = k >> 5, gg = (k >> 3) & 3;
-  return (long long)(p >> 5) * (32 * R) + ((c * (R >> 5) + kb) * 64 + 16 * gg + nn) * 8 + (k & 7);
-}
 
-// V-tile order: tile mt = k / 16, slot 16 * (t / 8) + k % 16, element t % 8 (t = p % 32).
-__device__ __forceinline__ long long tiled_v_offset(int p, int k, int R) {
-  const int t = p & 31;
-  return (long long)(p >> 5) * (32 * R) + ((k >> 4) * 64 + 16 * (t >> 3) + (k & 15)) * 8 + (t & 7);
-}
-
-// Latent append: cache[b, g, idx[b], :] = rows[b, g, :]; each thread moves 8 consecutive values.
-template <int LAYOUT>
-__global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const __bf16* rows, const int32_t* idx,
-                                                          int B, int G, int S, int width) {
-  const int vec = width / 8;
-  const long long total = (long long)B * G * vec;
-  for (long long e = blockIdx.x * (long long)blockDim.x + threadIdx.x; e < total; e += (long long)gridDim.x * blockDim.x) {
-    const int v = (int)(e % vec);
-    const long long bg = e / vec;
-    const int b = (int)(bg / G);
-    const int p = idx[b];
-    if (p < 0 || p >= S) continue;
-    const bf16x8 x = *reinterpret_cast<const bf16x8*>(rows + bg * width + 8 * v);
-    __bf16* stream = cache + bg * S * width;
-    if constexpr (LAYOUT == PALU_LAYOUT_ROWS) {
-      *reinterpret_cast<bf16x8*>(stream + (long long)p * width + 8 * v) = x;
-    } else if constexpr (LAYOUT == PALU_LAYOUT_TILED) {
-      *reinterpret_cast<bf16x8*>(stream + tiled_k_offset(p, 8 * v, width)) = x;
-    } else {
-      const long long o = tiled_v_offset(p, 8 * v, width);   // 8 slots 16 bytes apart
-#pragma unroll
-      for (int j = 0; j < 8; ++j) stream[o + 8 * j] = x[j];
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------------------------------
-// Host side: launch configuration, validation, error reporting.
-
-thread_local char g_err[1024] = "";
-
-int fail(int code, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_err, sizeof(g_err), fmt, ap);
-  va_end(ap);
-  return code;
-}
-
-// Waves per workgroup: 8 (two per SIMD) where the kernel fits 256 registers, else 4 (one per SIMD,
-// which lets the compiler use the full 512-entry register file instead of spilling).
-template <int RK, int RV, bool KFULL, bool TILED>
-constexpr int pick_nw() {
-  if (KFULL) return RV <= 64 ? 8 : 4;
-  return (RK + RV <= 96 || (TILED && RK == 64 && RV == 64)) ? 8 : 4;   // measured register fits
-}
-constexpr int MIN_NW = 4;
-constexpr int TARGET_WGS = 256;  // one workgroup per CU at full occupancy of the chip
-
-struct Plan {
-  int n_splits, split_len;
-};
-
-Plan plan_splits(int items, int S, int nw) {
-  // Positions per workgroup: about TARGET_WGS workgroups over the whole job, in whole blocks for
-  // every wave; a sequence is split across workgroups only when its items alone cannot fill the chip.
-  const long long total = (long long)items * S;
-  const long long unit = (long long)BLK * nw;
-  long long per_wg = (total + TARGET_WGS - 1) / TARGET_WGS;
-  per_wg = ((per_wg + unit - 1) / unit) * unit;
-  const long long whole = (((long long)S + BLK - 1) / BLK) * BLK;
-  if (per_wg > whole) per_wg = whole;
-  return Plan{(int)((S + per_wg - 1) / per_wg), (int)per_wg};
-}
-
-size_t ws_bytes(int items, int n_splits, int rv) {
-  return n_splits <= 1 ? 0 : (size_t)items * n_splits * 16 * (rv + 2) * sizeof(float);
-}
-
-template <int RK, int RV, bool KFULL, bool TILED, typename TabT, typename OutT>
+template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, typename TabT, typename OutT>
 int launch(const DecodeArgs& a0, hipStream_t stream) {
   constexpr int NW = pick_nw<RK, RV, KFULL, TILED>();
   DecodeArgs a = a0;
@@ -694,8 +699,8 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
   if (need > 0 && (a.ws == nullptr || a.ws_bytes < need))
     return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_decode_workspace_bytes), got %zu", need, a.ws_bytes);
   using SM = Smem<RK, RV, KFULL, NW>;
-  auto kern = palu_decode_kernel<RK, RV, KFULL, TILED, NW, TabT, OutT>;
-  const int lds = SM::bytes(a.S);
+  auto kern = palu_decode_kernel<RK, RV, KFULL, TILED, PAGED, NW, TabT, OutT>;
+  const int lds = SM::bytes(a.S) + (PAGED ? ((a.split_len >> 5 >> a.page_shift) + 2) * 4 : 0);
   if (lds > 160 * 1024) return fail(PALU_EUNSUPPORTED, "seq_len %d needs %d bytes of LDS (max 163840)", a.S, lds);
   static int attr_set = 0;
   if (attr_set < lds) {
@@ -715,223 +720,38 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
   return PALU_OK;
 }
 
-template <int RK, bool KFULL, bool TILED, typename TabT, typename OutT>
+template <int RK, bool KFULL, bool TILED, bool PAGED, typename TabT, typename OutT>
 int dispatch_rv(const DecodeArgs& a, int rv, hipStream_t s) {
   switch (rv) {
-    case 32: return launch<RK, 32, KFULL, TILED, TabT, OutT>(a, s);
-    case 64: return launch<RK, 64, KFULL, TILED, TabT, OutT>(a, s);
-    case 96: return launch<RK, 96, KFULL, TILED, TabT, OutT>(a, s);
-    case 128: return launch<RK, 128, KFULL, TILED, TabT, OutT>(a, s);
+    case 32: return launch<RK, 32, KFULL, TILED, PAGED, TabT, OutT>(a, s);
+    case 64: return launch<RK, 64, KFULL, TILED, PAGED, TabT, OutT>(a, s);
+    case 96: return launch<RK, 96, KFULL, TILED, PAGED, TabT, OutT>(a, s);
+    case 128: return launch<RK, 128, KFULL, TILED, PAGED, TabT, OutT>(a, s);
   }
   return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128", rv);
 }
 
-template <bool TILED, typename TabT, typename OutT>
+template <bool TILED, bool PAGED, typename TabT, typename OutT>
 int dispatch_latent(const DecodeArgs& a, int rk, int rv, hipStream_t s) {
   switch (rk) {
-    case 32: return dispatch_rv<32, false, TILED, TabT, OutT>(a, rv, s);
-    case 64: return dispatch_rv<64, false, TILED, TabT, OutT>(a, rv, s);
-    case 96: return dispatch_rv<96, false, TILED, TabT, OutT>(a, rv, s);
-    case 128: return dispatch_rv<128, false, TILED, TabT, OutT>(a, rv, s);
+    case 32: return dispatch_rv<32, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+    case 64: return dispatch_rv<64, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+    case 96: return dispatch_rv<96, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+    case 128: return dispatch_rv<128, false, TILED, PAGED, TabT, OutT>(a, rv, s);
   }
   return fail(PALU_EUNSUPPORTED, "r_k %d: this build rebuilds K from latents of width 32, 64, 96 or 128", rk);
 }
 
-template <typename TabT, typename OutT>
-int dispatch_layout(const DecodeArgs& a, int layout, int rk, int rv, hipStream_t s) {
-  return layout == PALU_LAYOUT_TILED ? dispatch_latent<true, TabT, OutT>(a, rk, rv, s)
-                                     : dispatch_latent<false, TabT, OutT>(a, rk, rv, s);
-}
 
-template <bool TILED>
-int dispatch_full(const DecodeArgs& a, int dv, bool f32o, hipStream_t s) {
-  using B16 = __bf16;
-  switch (dv) {
-    case 32: return f32o ? launch<HD, 32, true, TILED, float, float>(a, s) : launch<HD, 32, true, TILED, float, B16>(a, s);
-    case 64: return f32o ? launch<HD, 64, true, TILED, float, float>(a, s) : launch<HD, 64, true, TILED, float, B16>(a, s);
-    case 96: return f32o ? launch<HD, 96, true, TILED, float, float>(a, s) : launch<HD, 96, true, TILED, float, B16>(a, s);
-    case 128: return f32o ? launch<HD, 128, true, TILED, float, float>(a, s) : launch<HD, 128, true, TILED, float, B16>(a, s);
-  }
-  return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128", dv);
-}
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-int check_layout(int layout, int seq_len, const char* who) {
-  if (layout != PALU_LAYOUT_ROWS && layout != PALU_LAYOUT_TILED)
-    return fail(PALU_EINVAL, "%s: cache layout must be PALU_LAYOUT_ROWS or PALU_LAYOUT_TILED, got %d", who, layout);
-  if (layout == PALU_LAYOUT_TILED && seq_len % 32 != 0)
-    return fail(PALU_EINVAL, "%s: a tiled cache holds whole 32-position blocks; seq_len %d is not a multiple of 32", who,
-                seq_len);
-  return PALU_OK;
+// The four (table dtype, output dtype) instantiations of one cache layout.
+template <bool TILED, bool PAGED>
+int dispatch_dtypes(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s) {
+  const bool f32o = out_dtype == PALU_DTYPE_F32;
+  if (cs_dtype == PALU_DTYPE_F32)
+    return f32o ? dispatch_latent<TILED, PAGED, float, float>(a, rk, rv, s)
+                : dispatch_latent<TILED, PAGED, float, __bf16>(a, rk, rv, s);
+  return f32o ? dispatch_latent<TILED, PAGED, __bf16, float>(a, rk, rv, s)
+              : dispatch_latent<TILED, PAGED, __bf16, __bf16>(a, rk, rv, s);
 }
 
 }  // namespace
-
-// ---------------------------------------------------------------------------------------------------
-extern "C" {
-
-const char* palu_last_error(void) { return g_err; }
-
-int palu_abi_version(void) { return PALU_ABI_VERSION; }
-
-size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_dim_v) {
-  if (batch <= 0 || n_kv <= 0 || seq_len <= 0 || head_dim_v <= 0) return 0;
-  // The narrowest workgroup splits the most, so its plan bounds every kernel variant.
-  Plan p = plan_splits(batch * n_kv, seq_len, MIN_NW);
-  return ws_bytes(batch * n_kv, p.n_splits, head_dim_v);
-}
-
-int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab, const void* v_latent,
-                     int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step, const void* trans_mat,
-                     const void* u_v, float scale, int heads_per_core, int rot_mode, int table_mcast, int k_chunk,
-                     int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width,
-                     int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
-                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  g_err[0] = 0;
-  (void)table_mcast;
-  if (!q || !k_latent || !w_rot || !cs_tab || !v_latent || !cur_pos || !out)
-    return fail(PALU_EINVAL, "palu_sdpa_decode: a required tensor pointer is null");
-  if (rot_mode < 0 || rot_mode > 2) return fail(PALU_EINVAL, "rot_mode must be 'legacy', 'pack' or 'dst'");
-  if ((rot_step == nullptr) != (trans_mat == nullptr))
-    return fail(PALU_EINVAL, "rot_step and trans_mat are optional together: pass both (Phase 2) or neither (Phase 1)");
-  if (rot_step == nullptr && k_chunk > 128)
-    return fail(PALU_EINVAL, "Phase 1 streams the angle table per chunk and needs k_chunk_size <= 128, got %d", k_chunk);
-  if (k_chunk < 0 || (k_chunk > 0 && (k_chunk % 32 != 0 || (k_chunk & (k_chunk - 1)) != 0)))
-    return fail(PALU_EINVAL, "k_chunk_size must be 0 or a power of two multiple of 32, got %d", k_chunk);
-  if (batch <= 0 || n_q <= 0 || n_kv <= 0 || n_groups <= 0 || seq_len <= 0)
-    return fail(PALU_EINVAL, "palu_sdpa_decode: batch, head counts and seq_len must be positive");
-  if (r_k <= 0 || r_k % 32 != 0 || r_k > 512)
-    return fail(PALU_EINVAL, "r_k must be a multiple of 32 in 32..512 (the latent width of k_latent), got %d", r_k);
-  if (r_v <= 0 || r_v % 32 != 0 || r_v > 512)
-    return fail(PALU_EINVAL, "r_v must be a multiple of 32 in 32..512 (the latent width of v_latent), got %d", r_v);
-  if (n_kv % n_groups != 0)
-    return fail(PALU_EINVAL, "heads_per_group: %d latent heads do not divide the %d KV heads of w_rot", n_groups, n_kv);
-  const int hpg = n_kv / n_groups;
-  if (w_rot_width != 2 * HD)
-    return fail(PALU_EINVAL, "w_rot must be [1, n_kv, r_k, %d] = [u_k | u_k T], got last dim %d", 2 * HD, w_rot_width);
-  if (cs_cols != 2 * HD) return fail(PALU_EINVAL, "cs_tab must be [1, 1, S, %d] = [cos | sin], got last dim %d", 2 * HD, cs_cols);
-  if (cs_rows < seq_len)
-    return fail(PALU_EINVAL, "cs_tab has %d rows but the latent cache has %d positions", cs_rows, seq_len);
-  if (seq_len > 65536)
-    return fail(PALU_EUNSUPPORTED, "seq_len %d: this build's block-angle tables cover 65536 positions", seq_len);
-  if (n_q % n_kv != 0 || n_q / n_kv > 16)
-    return fail(PALU_EINVAL, "KV head count %d must divide the %d query heads with at most 16 query heads per KV head", n_kv, n_q);
-  if (heads_per_core > 1) {
-    if (heads_per_core > n_kv)
-      return fail(PALU_EINVAL, "heads_per_core %d exceeds the KV head count %d", heads_per_core, n_kv);
-    if (hpg == 1) return fail(PALU_EINVAL, "heads_per_core > 1 shares a latent between heads and needs grouped latents");
-    if (hpg % heads_per_core != 0)
-      return fail(PALU_EINVAL, "heads_per_core %d must divide heads_per_group %d", heads_per_core, hpg);
-  }
-  if (u_v != nullptr) {
-    if (head_dim_v != HD) return fail(PALU_EINVAL, "head_dim_v must be %d when u_v rebuilds V in-kernel, got %d", HD, head_dim_v);
-    return fail(PALU_EUNSUPPORTED, "u_v (in-kernel V rebuild, grouped latents) is not built in this library yet");
-  }
-  if (hpg != 1) return fail(PALU_EINVAL, "grouped V latent (heads_per_group %d) needs u_v", hpg);
-  if (head_dim_v != r_v)
-    return fail(PALU_EINVAL, "head_dim_v %d must equal the V latent width %d on the absorbed-V path", head_dim_v, r_v);
-  if (cs_dtype != PALU_DTYPE_F32 && cs_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "cs_tab dtype must be fp32 or bf16");
-  if (out_dtype != PALU_DTYPE_F32 && out_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "output dtype must be fp32 or bf16");
-  if (int rc = check_layout(cache_layout, seq_len, "palu_sdpa_decode")) return rc;
-  if (!aligned16(q) || !aligned16(k_latent) || !aligned16(v_latent) || !aligned16(w_rot) || !aligned16(cs_tab))
-    return fail(PALU_EINVAL, "q, k_latent, v_latent, w_rot and cs_tab must be 16-byte aligned");
-
-  const int items = batch * n_kv;
-  if ((long long)items > 65535) return fail(PALU_EUNSUPPORTED, "batch * n_kv = %d exceeds the grid limit", items);
-
-  DecodeArgs a;
-  memset(&a, 0, sizeof(a));
-  a.q = static_cast<const __bf16*>(q);
-  a.k = static_cast<const __bf16*>(k_latent);
-  a.v = static_cast<const __bf16*>(v_latent);
-  a.w_rot = static_cast<const __bf16*>(w_rot);
-  a.cs = cs_tab;
-  a.cur_pos = cur_pos;
-  a.out = out;
-  a.ws = static_cast<float*>(workspace);
-  a.ws_bytes = workspace_bytes;
-  a.k_sg = (long long)seq_len * r_k;
-  a.k_sb = a.k_sg * n_groups;
-  a.v_sg = (long long)seq_len * r_v;
-  a.v_sb = a.v_sg * n_groups;
-  a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = hpg; a.S = seq_len; a.cs_rows = cs_rows;
-  a.deterministic = deterministic ? 1 : 0;
-  a.qscale = scale * 1.4426950408889634f;
-
-  if (cs_dtype == PALU_DTYPE_F32) {
-    return out_dtype == PALU_DTYPE_F32 ? dispatch_layout<float, float>(a, cache_layout, r_k, r_v, stream)
-                                       : dispatch_layout<float, __bf16>(a, cache_layout, r_k, r_v, stream);
-  }
-  return out_dtype == PALU_DTYPE_F32 ? dispatch_layout<__bf16, float>(a, cache_layout, r_k, r_v, stream)
-                                     : dispatch_layout<__bf16, __bf16>(a, cache_layout, r_k, r_v, stream);
-}
-
-int palu_flash_decode(const void* q, const void* k, const void* v, const int32_t* cur_pos, void* out, float scale,
-                      int batch, int n_q, int n_kv, int seq_len, int head_dim_v, int out_dtype, int cache_layout,
-                      int deterministic, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  g_err[0] = 0;
-  if (!q || !k || !v || !cur_pos || !out) return fail(PALU_EINVAL, "palu_flash_decode: a required tensor pointer is null");
-  if (batch <= 0 || n_q <= 0 || n_kv <= 0 || seq_len <= 0)
-    return fail(PALU_EINVAL, "palu_flash_decode: batch, head counts and seq_len must be positive");
-  if (n_q % n_kv != 0 || n_q / n_kv > 16)
-    return fail(PALU_EINVAL, "KV head count %d must divide the %d query heads with at most 16 query heads per KV head", n_kv, n_q);
-  if (out_dtype != PALU_DTYPE_F32 && out_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "output dtype must be fp32 or bf16");
-  if (int rc = check_layout(cache_layout, seq_len, "palu_flash_decode")) return rc;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return fail(PALU_EINVAL, "q, k and v must be 16-byte aligned");
-  const int items = batch * n_kv;
-  if ((long long)items > 65535) return fail(PALU_EUNSUPPORTED, "batch * n_kv = %d exceeds the grid limit", items);
-
-  DecodeArgs a;
-  memset(&a, 0, sizeof(a));
-  a.q = static_cast<const __bf16*>(q);
-  a.k = static_cast<const __bf16*>(k);
-  a.v = static_cast<const __bf16*>(v);
-  a.cur_pos = cur_pos;
-  a.out = out;
-  a.ws = static_cast<float*>(workspace);
-  a.ws_bytes = workspace_bytes;
-  a.k_sg = (long long)seq_len * HD;
-  a.k_sb = a.k_sg * n_kv;
-  a.v_sg = (long long)seq_len * head_dim_v;
-  a.v_sb = a.v_sg * n_kv;
-  a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = 1; a.S = seq_len; a.cs_rows = 0;
-  a.deterministic = deterministic ? 1 : 0;
-  a.qscale = scale * 1.4426950408889634f;
-  const bool f32o = out_dtype == PALU_DTYPE_F32;
-  return cache_layout == PALU_LAYOUT_TILED ? dispatch_full<true>(a, head_dim_v, f32o, stream)
-                                           : dispatch_full<false>(a, head_dim_v, f32o, stream);
-}
-
-int palu_latent_append(void* cache, const void* new_rows, const int32_t* update_idxs, int batch, int n_groups,
-                       int seq_len, int width, int cache_layout, hipStream_t stream) {
-  g_err[0] = 0;
-  if (!cache || !new_rows || !update_idxs) return fail(PALU_EINVAL, "palu_latent_append: a required pointer is null");
-  if (batch <= 0 || n_groups <= 0 || seq_len <= 0 || width <= 0 || width % 8 != 0)
-    return fail(PALU_EINVAL, "palu_latent_append: width must be a positive multiple of 8, got %d", width);
-  if (int rc = check_layout(cache_layout == PALU_LAYOUT_TILED_V ? PALU_LAYOUT_TILED : cache_layout, seq_len,
-                            "palu_latent_append"))
-    return rc;
-  if (cache_layout != PALU_LAYOUT_ROWS && width % 32 != 0)
-    return fail(PALU_EINVAL, "palu_latent_append: a tiled cache row is a multiple of 32 wide, got %d", width);
-  if (!aligned16(cache) || !aligned16(new_rows)) return fail(PALU_EINVAL, "palu_latent_append: 16-byte alignment required");
-  const long long total = (long long)batch * n_groups * (width / 8);
-  int blocks = (int)((total + 255) / 256);
-  if (blocks > 4096) blocks = 4096;
-  auto* c = static_cast<__bf16*>(cache);
-  auto* r = static_cast<const __bf16*>(new_rows);
-  if (cache_layout == PALU_LAYOUT_TILED)
-    hipLaunchKernelGGL(palu_append_kernel<PALU_LAYOUT_TILED>, dim3(blocks), dim3(256), 0, stream, c, r, update_idxs,
-                       batch, n_groups, seq_len, width);
-  else if (cache_layout == PALU_LAYOUT_TILED_V)
-    hipLaunchKernelGGL(palu_append_kernel<PALU_LAYOUT_TILED_V>, dim3(blocks), dim3(256), 0, stream, c, r, update_idxs,
-                       batch, n_groups, seq_len, width);
-  else
-    hipLaunchKernelGGL(palu_append_kernel<PALU_LAYOUT_ROWS>, dim3(blocks), dim3(256), 0, stream, c, r, update_idxs,
-                       batch, n_groups, seq_len, width);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(PALU_EHIP, "append kernel launch: %s", hipGetErrorString(e));
-  return PALU_OK;
-}
-
-}  // extern "C"

@@ -199,10 +199,37 @@ def _cur_pos(cur_pos_tensor: torch.Tensor, batch: int, device) -> torch.Tensor:
     return cp.contiguous()
 
 
+def _page_table(page_table_tensor, batch: int, device) -> torch.Tensor:
+    _require(isinstance(page_table_tensor, torch.Tensor) and page_table_tensor.dim() == 2,
+             "page_table_tensor must be [B, max_pages_per_seq] int32")
+    _require(page_table_tensor.shape[0] == batch,
+             f"page_table_tensor has {page_table_tensor.shape[0]} rows for batch {batch}")
+    pt = page_table_tensor
+    if pt.device != device or pt.dtype != torch.int32:
+        pt = pt.to(device=device, dtype=torch.int32)
+    return pt.contiguous()
+
+
+def _pool_dims(k_shape, v_shape, q, page_table_tensor, dev, what):
+    """(B, n_groups, S, r_k, r_v, page table or None, page_size, n_pages) of contiguous caches
+    [B, G, S, r] or paged pools [n_pages, G, page_size, r] with a [B, max_pages] page table."""
+    if page_table_tensor is None:
+        B, G, S, r_k = k_shape
+        _require(tuple(v_shape[:3]) == (B, G, S), f"v {v_shape} does not match k {k_shape} in [B, {what}, S]")
+        return B, G, S, r_k, v_shape[3], None, 0, 0
+    n_pages, G, page_size, r_k = k_shape
+    _require(tuple(v_shape[:3]) == (n_pages, G, page_size),
+             f"v pool {v_shape} does not match k pool {k_shape} in [n_pages, {what}, page_size]")
+    B = q.shape[1]
+    pt = _page_table(page_table_tensor, B, dev)
+    return B, G, pt.shape[1] * page_size, r_k, v_shape[3], pt, page_size, n_pages
+
+
 def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_tensor, *, rot_step=None,
                      trans_mat=None, u_v=None, scale=None, heads_per_core=None, rot_mode="dst", table_mcast=True,
                      program_config=None, compute_kernel_config=None, memory_config=None,
-                     out_dtype=torch.bfloat16, out=None, workspace=None, deterministic=False) -> torch.Tensor:
+                     out_dtype=torch.bfloat16, out=None, workspace=None, deterministic=False,
+                     page_table_tensor=None) -> torch.Tensor:
     """Fused latent flash-decode (ttnn.transformer.palu_sdpa_decode). Returns [1, B, n_q, head_dim_v].
 
     For every p <= cur_pos[b]: K[p] = RoPE_p(k_latent[p] @ u_k) with u_k = w_rot[..., :128], then
@@ -211,6 +238,9 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
 
     compute_kernel_config and memory_config are accepted for call compatibility and unused (the kernel
     always accumulates in fp32; the output is a fresh tensor unless ``out`` is given).
+    page_table_tensor [B, max_pages] int32 switches to paged caches: k_latent / v_latent are then page
+    pools [n_pages, n_groups, page_size, r] (tensors or LatentCache pools) and position p of row b lives
+    on page page_table[b, p // page_size] (ttnn's paged decode convention).
     deterministic=True fixes which wave of a workgroup sums which 32-position block, so repeated calls
     are bit-identical; the default hands blocks out from a counter (faster; calls differ at the bf16
     rounding of the softmax probabilities, well inside the parity tolerance).
@@ -223,10 +253,8 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
     k_store, k_shape, layout = _cache_arg(k_latent, "k_latent", dev, "k")
     v_store, v_shape, v_layout = _cache_arg(v_latent, "v_latent", dev, "v")
     _require(layout == v_layout, "k_latent and v_latent must use the same cache layout")
-    B, n_groups, S, r_k = k_shape
-    _require(tuple(v_shape[:3]) == (B, n_groups, S),
-             f"v_latent {v_shape} does not match k_latent {k_shape} in [B, n_groups, S]")
-    r_v = v_shape[3]
+    B, n_groups, S, r_k, r_v, pt, page_size, n_pages = _pool_dims(k_shape, v_shape, q, page_table_tensor, dev,
+                                                                 "n_groups")
     _require(q.shape[1] == B, f"q has batch {q.shape[1]} but the latent caches have {B}")
     n_q = q.shape[2]
     w = w_rot.reshape(-1, *w_rot.shape[-2:]) if w_rot.dim() >= 3 else w_rot
@@ -263,21 +291,31 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
         _require(tuple(out.shape) == (1, B, n_q, width), f"out must be [1, {B}, {n_q}, {width}]")
     ws, ws_bytes = _workspace(B, n_kv, S, max(width, 1), dev, workspace)
     lib = _native.load()
-    _native.check(lib.palu_sdpa_decode(
-        _native.ptr(q), _native.ptr(k_store), _native.ptr(w), _native.ptr(cs), _native.ptr(v_store), width,
-        _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv),
-        float(HEAD_DIM ** -0.5 if scale is None else scale), int(heads_per_core or 0), rot, int(bool(table_mcast)),
-        _k_chunk(program_config), B, n_q, n_kv, n_groups, S, r_k, r_v, w_width, cs.shape[0], cs.shape[1],
-        _DTYPES[cs.dtype], _DTYPES[out_dtype], layout, int(bool(deterministic)), _native.ptr(ws), ws_bytes,
-        _native.stream_handle(dev)))
+    sc = float(HEAD_DIM ** -0.5 if scale is None else scale)
+    if pt is None:
+        _native.check(lib.palu_sdpa_decode(
+            _native.ptr(q), _native.ptr(k_store), _native.ptr(w), _native.ptr(cs), _native.ptr(v_store), width,
+            _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv), sc,
+            int(heads_per_core or 0), rot, int(bool(table_mcast)), _k_chunk(program_config), B, n_q, n_kv, n_groups,
+            S, r_k, r_v, w_width, cs.shape[0], cs.shape[1], _DTYPES[cs.dtype], _DTYPES[out_dtype], layout,
+            int(bool(deterministic)), _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
+    else:
+        _native.check(lib.palu_sdpa_decode_paged(
+            _native.ptr(q), _native.ptr(k_store), _native.ptr(w), _native.ptr(cs), _native.ptr(v_store), width,
+            _native.ptr(cp), _native.ptr(pt), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv), sc,
+            int(heads_per_core or 0), rot, int(bool(table_mcast)), _k_chunk(program_config), B, n_q, n_kv, n_groups,
+            n_pages, page_size, pt.shape[1], r_k, r_v, w_width, cs.shape[0], cs.shape[1], _DTYPES[cs.dtype],
+            _DTYPES[out_dtype], layout, int(bool(deterministic)), _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
     return out
 
 
 def flash_decode(q, k, v, cur_pos_tensor, *, scale=None, head_dim_v=None, out_dtype=torch.bfloat16, out=None,
-                 workspace=None, deterministic=False) -> torch.Tensor:
+                 workspace=None, deterministic=False, page_table_tensor=None) -> torch.Tensor:
     """Stock flash-decode over full rotated K [B, n_kv, S, 128] and V [B, n_kv, S, head_dim_v]: the
     MI355X counterpart of ttnn.transformer.scaled_dot_product_attention_decode (head_dim_v 128) and
-    flash_multi_latent_attention_decode (head_dim_v = V width). Returns [1, B, n_q, head_dim_v]."""
+    flash_multi_latent_attention_decode (head_dim_v = V width). Returns [1, B, n_q, head_dim_v].
+    With page_table_tensor, k and v are page pools [n_pages, n_kv, page_size, width] (ttnn's
+    paged_scaled_dot_product_attention_decode)."""
     _require(isinstance(q, torch.Tensor) and q.dim() == 4 and q.shape[0] == 1 and q.shape[3] == HEAD_DIM,
              f"q must be [1, B, n_q, {HEAD_DIM}]")
     dev = q.device
@@ -285,11 +323,11 @@ def flash_decode(q, k, v, cur_pos_tensor, *, scale=None, head_dim_v=None, out_dt
     k_store, k_shape, layout = _cache_arg(k, "k", dev, "k")
     v_store, v_shape, v_layout = _cache_arg(v, "v", dev, "v")
     _require(layout == v_layout, "k and v must use the same cache layout")
-    B, n_kv, S, hd = k_shape
+    B, n_kv, S, hd, v_width, pt, page_size, n_pages = _pool_dims(k_shape, v_shape, q, page_table_tensor, dev, "n_kv")
     _require(hd == HEAD_DIM, f"k must be [B, n_kv, S, {HEAD_DIM}], got {k_shape}")
-    _require(tuple(v_shape[:3]) == (B, n_kv, S), f"v {v_shape} does not match k {k_shape}")
-    width = int(v_shape[3] if head_dim_v is None else head_dim_v)
-    _require(width == v_shape[3], f"head_dim_v {width} != V width {v_shape[3]}")
+    _require(q.shape[1] == B, f"q has batch {q.shape[1]} but the caches have {B}")
+    width = int(v_width if head_dim_v is None else head_dim_v)
+    _require(width == v_width, f"head_dim_v {width} != V width {v_width}")
     n_q = q.shape[2]
     if out_dtype not in _DTYPES:
         raise RuntimeError(f"out_dtype must be torch.float32 or torch.bfloat16, got {out_dtype}")
@@ -298,10 +336,17 @@ def flash_decode(q, k, v, cur_pos_tensor, *, scale=None, head_dim_v=None, out_dt
         out = torch.empty(1, B, n_q, width, dtype=out_dtype, device=dev)
     ws, ws_bytes = _workspace(B, n_kv, S, width, dev, workspace)
     lib = _native.load()
-    _native.check(lib.palu_flash_decode(
-        _native.ptr(q), _native.ptr(k_store), _native.ptr(v_store), _native.ptr(cp), _native.ptr(out),
-        float(HEAD_DIM ** -0.5 if scale is None else scale), B, n_q, n_kv, S, width, _DTYPES[out_dtype], layout,
-        int(bool(deterministic)), _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
+    sc = float(HEAD_DIM ** -0.5 if scale is None else scale)
+    if pt is None:
+        _native.check(lib.palu_flash_decode(
+            _native.ptr(q), _native.ptr(k_store), _native.ptr(v_store), _native.ptr(cp), _native.ptr(out), sc, B, n_q,
+            n_kv, S, width, _DTYPES[out_dtype], layout, int(bool(deterministic)), _native.ptr(ws), ws_bytes,
+            _native.stream_handle(dev)))
+    else:
+        _native.check(lib.palu_flash_decode_paged(
+            _native.ptr(q), _native.ptr(k_store), _native.ptr(v_store), _native.ptr(cp), _native.ptr(pt),
+            _native.ptr(out), sc, B, n_q, n_kv, n_pages, page_size, pt.shape[1], width, _DTYPES[out_dtype], layout,
+            int(bool(deterministic)), _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
     return out
 
 
@@ -315,15 +360,31 @@ def flash_multi_latent_attention_decode(q, k, v, head_dim_v, cur_pos_tensor, sca
     return flash_decode(q, k, v, cur_pos_tensor, scale=scale, head_dim_v=head_dim_v)
 
 
-def paged_update_cache(cache, new_rows: torch.Tensor, update_idxs_tensor: torch.Tensor) -> None:
+def paged_scaled_dot_product_attention_decode(q, k, v, cur_pos_tensor, page_table_tensor, scale=None, **_):
+    """Name-compatible alias of the paged stock decode op (page pools of full K and V)."""
+    return flash_decode(q, k, v, cur_pos_tensor, scale=scale, page_table_tensor=page_table_tensor)
+
+
+def paged_update_cache(cache, new_rows: torch.Tensor, update_idxs_tensor: torch.Tensor, page_table=None) -> None:
     """Latent append (ttnn.experimental.paged_update_cache on a latent cache, attention.py:622-623):
     cache[b, g, update_idxs[b], :] = new_rows[..., b, g, :] for every b with 0 <= idx < S. ``cache`` is a
-    [B, G, S, width] bf16 tensor or a LatentCache."""
+    [B, G, S, width] bf16 tensor or a LatentCache. With ``page_table`` [B, max_pages] int32 the cache is a
+    page pool [n_pages, G, page_size, width] and row b goes to page page_table[b, idx // page_size]."""
     dev = cache.device
-    store, (B, G, S, width), layout = _cache_arg(cache, "cache", dev)
+    store, (N, G, S, width), layout = _cache_arg(cache, "cache", dev)
+    lib = _native.load()
+    if page_table is None:
+        B = N
+        rows = new_rows.reshape(B, G, width)
+        _as_dev(rows, "new_rows", torch.bfloat16, dev)
+        cp = _cur_pos(update_idxs_tensor, B, dev)
+        _native.check(lib.palu_latent_append(_native.ptr(store), _native.ptr(rows), _native.ptr(cp), B, G, S, width,
+                                             layout, _native.stream_handle(dev)))
+        return
+    B = update_idxs_tensor.numel()
     rows = new_rows.reshape(B, G, width)
     _as_dev(rows, "new_rows", torch.bfloat16, dev)
     cp = _cur_pos(update_idxs_tensor, B, dev)
-    lib = _native.load()
-    _native.check(lib.palu_latent_append(_native.ptr(store), _native.ptr(rows), _native.ptr(cp), B, G, S, width, layout,
-                                         _native.stream_handle(dev)))
+    pt = _page_table(page_table, B, dev)
+    _native.check(lib.palu_latent_append_paged(_native.ptr(store), _native.ptr(rows), _native.ptr(cp), _native.ptr(pt),
+                                               B, G, N, S, pt.shape[1], width, layout, _native.stream_handle(dev)))
