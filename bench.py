@@ -103,19 +103,25 @@ def build_workload(a, dev):
 
 
 def time_calls(fn, n_layers, steps, warmup):
-    """Warm up, then time exactly `steps` calls bracketed by synchronize; returns (wall ms/step, mean
-    kernel ms from per-call HIP events on the launch stream, all per-call ms)."""
+    """Warm up, then time exactly `steps` back-to-back calls bracketed by synchronize (wall ms/step);
+    then, in a second pass of the same length, per-call HIP events on the launch stream (torch's
+    current stream, where the library enqueues its kernels) give the kernel duration. The wall pass
+    records no events, so its value is the throughput of plain back-to-back decode calls.
+    Returns (wall ms/step, mean kernel ms, all per-call kernel ms)."""
     for i in range(warmup):
         fn(i % n_layers)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i % n_layers)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for i in range(steps):
         ev[i][0].record()
         fn(i % n_layers)
         ev[i][1].record()
     torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3 / steps
     per = [s.elapsed_time(e) for s, e in ev]
     return wall, statistics.mean(per), per
 

@@ -23,11 +23,11 @@
 //     accumulator layout gives every lane one position and 4 consecutive head dims per 16-dim tile, so
 //     each RoPE pair (Meta-interleaved dims 2f, 2f+1) sits in one lane and the rotation is plain VALU
 //     work on the fp32 accumulators.
-//   * RoPE is applied block-relative: K rows are rotated by their offset t < 32 inside the block (an
-//     LDS table in lane order), and the query is rotated back by the block base once per block,
-//     q~ = R_{-base} q, with cos/sin of the base built by angle addition from two small LDS tables
-//     (base = 1024 H + 32 Lo). Rotations in one plane commute, so q~ . R_t k = q . R_{base+t} k, the
-//     score of the reference.
+//   * RoPE is applied pair-relative: K rows are rotated by their offset t < 64 inside a pair of
+//     blocks (an LDS table in lane order), and the query is rotated back by the pair base once per
+//     pair, q~ = R_{-base} q, with cos/sin of the base built by angle addition from two small LDS
+//     tables (base = 1024 H + 64 Lo). Rotations in one plane commute, so q~ . R_t k = q . R_{base+t} k,
+//     the score of the reference.
 //   * The rebuilt K slice is packed to bf16 in registers and used as the A operand of the QK MFMA; the
 //     head dim is contracted in a permuted order that the query operand mirrors, so no lane shuffles
 //     are needed.
@@ -93,7 +93,7 @@ constexpr int pick_nw() {
   // 8 waves where the kernel fits 256 VGPRs without spilling (checked per instantiation with
   // -Rpass-analysis=kernel-resource-usage), else 4 waves with the 512-register budget.
   if (KFULL) return 8;
-  return (RK == 64 && RV == 128) ? 4 : 8;
+  return ((RK == 64 && RV == 128) || (RK >= 96 && !(RK == 96 && RV == 32))) ? 4 : 8;
 }
 constexpr int MIN_NW = 4;
 constexpr int TARGET_WGS = 256;  // one workgroup per CU at full occupancy of the chip
@@ -163,25 +163,27 @@ __device__ __forceinline__ float wave_sum_xor48(float x) {
 
 
 // LDS map of one workgroup (latent mode; full-K mode keeps only the merge buffer and the counter):
-//   rtab  block-relative K rotation, float4 {cos f, sin f, cos f+1, sin f+1} per (tile, 16-dim row
-//         tile, lane), i.e. exactly the operand order of the rebuilt K^T accumulators   16 KB
+//   rtab  pair-relative K rotation (offset t < 64 inside a pair of blocks), float4 {cos f, sin f,
+//         cos f+1, sin f+1} per (block of the pair, tile, 16-dim row tile, lane), i.e. exactly the
+//         operand order of the rebuilt K^T accumulators                               32 KB
 //   ukT   u_k^T, rows padded by 16 bytes (bank spread)                               HD x (RK + 8) bf16
 //   qx    per wave, the rotated query regrouped into its MFMA operand layout         NW x 4 KB
-//   tl    (cos, sin) of angle 32*Lo*f, Lo < 32: the low part of a block base          [32][64] float2
+//   tl    (cos, sin) of angle 64*Lo*f, Lo < 16: the low part of a pair base           [16][64] float2
 //   qs    the item's query rows (zero rows past rep), so the block loop issues no global load
 //         besides the latent prefetch                                                 [16][128] bf16
 //   ctr   the block counter
 //   th    (cos, sin) of angle 1024*H*f, H < ceil(S / 1024): the high part             [nH][64] float2
-//   kc    staging of rows 0..31 of cs_tab ([t][f] float2) while rtab is built, overlaying qx
+//   kc    staging of rows 0..63 of cs_tab ([t][f] float2) while rtab is built, overlaying qx
 // The wave-merge buffer of the epilogue overlays the front.
 template <int RK, int RV, bool KFULL, int NW>
 struct Smem {
   static constexpr int UKT_STRIDE = RK + 8;
-  static constexpr int RTAB_BYTES = KFULL ? 0 : 2 * 8 * 64 * 16;
+  static constexpr int RTAB_BYTES = KFULL ? 0 : 2 * 2 * 8 * 64 * 16;
+  static constexpr int KC_BYTES = 64 * 64 * 8;
   static constexpr int UKT_BYTES = KFULL ? 0 : HD * UKT_STRIDE * 2;
   static constexpr int QX_WAVE_BYTES = 16 * 4 * 8 * 4 * 2;   // [head 16][g 4][row tile 8][4 dims] bf16
-  static constexpr int QX_BYTES = KFULL ? 0 : NW * QX_WAVE_BYTES;
-  static constexpr int TL_BYTES = KFULL ? 0 : 32 * 64 * 8;
+  static constexpr int QX_BYTES = KFULL ? 0 : (NW * QX_WAVE_BYTES > KC_BYTES ? NW * QX_WAVE_BYTES : KC_BYTES);
+  static constexpr int TL_BYTES = KFULL ? 0 : 16 * 64 * 8;
   static constexpr int QS_BYTES = KFULL ? 0 : 16 * HD * 2;
   static constexpr int UKT_OFFSET = RTAB_BYTES;
   static constexpr int QX_OFFSET = UKT_OFFSET + UKT_BYTES;
@@ -191,7 +193,7 @@ struct Smem {
   static constexpr int MERGE_BYTES = NW * 16 * (RV + 2) * 4;
   static constexpr int CTR_OFFSET = ((MAIN_BYTES > MERGE_BYTES ? MAIN_BYTES : MERGE_BYTES) + 15) & ~15;
   static constexpr int TH_OFFSET = CTR_OFFSET + 16;
-  static_assert(KFULL || QX_BYTES >= 32 * 64 * 8, "the cs_tab staging rows overlay qx");
+  static_assert(KFULL || QX_BYTES >= KC_BYTES, "the cs_tab staging rows overlay qx");
   __host__ __device__ static int bytes(int S) { return TH_OFFSET + (KFULL ? 0 : ((S + 1023) / 1024) * 64 * 8); }
 };
 
@@ -314,18 +316,18 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
 
   // ---- prologue ----------------------------------------------------------------------------------
   // Latent mode: the angle tables and u_k^T go to LDS. The tables come from whole rows of cs_tab, one
-  // coalesced row per wave load (rows t < 32 for K, 32*Lo and 1024*H for the query); these (L2) loads
+  // coalesced row per wave load (rows t < 64 for K, 64*Lo and 1024*H for the query); these (L2) loads
   // are issued before the first latent block's (HBM) loads, so waiting on them does not wait on HBM.
   if constexpr (!KFULL) {
     const TabT* cs = static_cast<const TabT*>(a.cs);
     const int n_hi = (a.S + 1023) / 1024;
-    const int n_rows = 64 + n_hi;               // 32 K rows, 32 low-base rows, n_hi high-base rows
-    constexpr int RPW = (64 + 64 + NW - 1) / NW;  // rows per wave, enough for S <= 65536
+    const int n_rows = 80 + n_hi;               // 64 K rows, 16 low-base rows, n_hi high-base rows
+    constexpr int RPW = (80 + 64 + NW - 1) / NW;  // rows per wave, enough for S <= 65536
     float4 rowv[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
       const int r = w + i * NW;
-      int t = r < 32 ? r : (r < 64 ? 32 * (r - 32) : 1024 * (r - 64));
+      int t = r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80));
       t = (r < n_rows && t < a.cs_rows) ? t : 0;
       rowv[i] = load4f(cs + (long long)t * (2 * HD) + 4 * lane);   // lane < 32: cos, else sin
     }
@@ -349,9 +351,9 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     for (int i = 0; i < RPW; ++i) {
       const int r = w + i * NW;
       if (r < n_rows) {
-        int t = r < 32 ? r : (r < 64 ? 32 * (r - 32) : 1024 * (r - 64));
+        int t = r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80));
         const bool ok = t < a.cs_rows;
-        float2* dst = r < 32 ? kc + r * 64 : (r < 64 ? tl + (r - 32) * 64 : th + (r - 64) * 64);
+        float2* dst = r < 64 ? kc + r * 64 : (r < 80 ? tl + (r - 64) * 64 : th + (r - 80) * 64);
         const int f = 2 * (lane & 31);
         float* d0 = reinterpret_cast<float*>(dst + f) + (lane >> 5);
         d0[0] = ok ? rowv[i].x : (lane < 32 ? 1.f : 0.f);
@@ -368,11 +370,11 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       }
     }
     __syncthreads();
-    // K rotation table in lane order from the staged rows 0..31
-    for (int e = tid; e < 2 * 8 * 64; e += NW * 64) {
-      const int l = e & 63, rt = (e >> 6) & 7, c = e >> 9;
+    // K rotation table in lane order from the staged rows 0..63
+    for (int e = tid; e < 2 * 2 * 8 * 64; e += NW * 64) {
+      const int l = e & 63, rt = (e >> 6) & 7, c = (e >> 9) & 1, hb = e >> 10;
       const int nn = l & 15, gg = l >> 4;
-      const int t = 8 * (nn >> 2) + 4 * c + (nn & 3);
+      const int t = 32 * hb + 8 * (nn >> 2) + 4 * c + (nn & 3);
       const int f = 8 * rt + 2 * gg;
       const float2 x = kc[t * 64 + f], y = kc[t * 64 + f + 1];
       rtab[e] = make_float4(x.x, x.y, y.x, y.y);
@@ -422,7 +424,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   bf16x8 qB[4];
 
   // Query. Full-K mode: q * qscale once, head dim in natural order d = 32*kb + 8*g + j. Latent mode:
-  // q~ = R_{-base} q * qscale per block. The rotation is spread over all 64 lanes (lane l owns query
+  // q~ = R_{-base} q * qscale per pair of blocks (base a multiple of 64). The rotation is spread over all 64 lanes (lane l owns query
   // head l/16 (+4, +8, +12 while < rep) and head dims 8*(l%16) .. +7, i.e. 4 frequency pairs), then
   // regrouped through the wave's LDS area into the operand order d(kb, g, j) =
   // 16*(2*kb + j/4) + 4*g + j%4 that the rebuilt K^T tile has in registers.
@@ -439,10 +441,10 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     }
   }
   auto make_q = [&](int base) {
-    // angle of the block base 32*J, J = 32*H + Lo: (cos, sin) by angle addition of th[H] and tl[Lo]
-    const int J = base >> 5;
-    const float4* lo4 = reinterpret_cast<const float4*>(tl + (J & 31) * 64 + 4 * qf);
-    const float4* hi4 = reinterpret_cast<const float4*>(th + (J >> 5) * 64 + 4 * qf);
+    // angle of the pair base 64*J, J = 16*H + Lo: (cos, sin) by angle addition of th[H] and tl[Lo]
+    const int J = base >> 6;
+    const float4* lo4 = reinterpret_cast<const float4*>(tl + (J & 15) * 64 + 4 * qf);
+    const float4* hi4 = reinterpret_cast<const float4*>(th + (J >> 4) * 64 + 4 * qf);
     const float4 l01 = lo4[0], l23 = lo4[1], h01 = hi4[0], h23 = hi4[1];
     const float lc[4] = {l01.x, l01.z, l23.x, l23.z}, ls[4] = {l01.y, l01.w, l23.y, l23.w};
     const float hc[4] = {h01.x, h01.z, h23.x, h23.z}, hs[4] = {h01.y, h01.w, h23.y, h23.w};
@@ -487,7 +489,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
                      __attribute__((always_inline)) {
     constexpr bool PARTIAL = decltype(partial_tag)::value;
     const int base = s_lo + blk * BLK;
-    if constexpr (!KFULL) make_q(base);
+    const int hb = blk & 1;               // which block of its pair (s_lo is a multiple of 64)
 
     f32x4 sc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
     if constexpr (KFULL) {
@@ -524,7 +526,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
         for (int c = 0; c < 2; ++c) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const float4 t = rtab[(c * 8 + 2 * kq + h) * 64 + lane];
+            const float4 t = rtab[((hb * 2 + c) * 8 + 2 * kq + h) * 64 + lane];
             const float x0 = acc[c][h][0], x1 = acc[c][h][1], x2 = acc[c][h][2], x3 = acc[c][h][3];
             acc[c][h][0] = x0 * t.x - x1 * t.y;
             acc[c][h][1] = x1 * t.x + x0 * t.y;
@@ -611,15 +613,19 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     const bool has1 = b0 + 1 < nfull;
     const int base1 = s_lo + (has1 ? b0 + 1 : b0) * BLK;
     load_blk(base1, has1, page_lds(base1), kln, vln);
+    __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of the compute it overlaps
+    if constexpr (!KFULL) make_q(s_lo + b0 * BLK);   // one query rotation serves both blocks of the pair
     compute(full_blk, b0, kl, vl);
     const bool hasn = pn < npairs;
     const int basen = s_lo + (hasn ? 2 * pn : b0) * BLK;
     load_blk(basen, hasn, page_lds(basen), kl, vl);
+    __builtin_amdgcn_sched_barrier(0);
     if (has1) compute(full_blk, b0 + 1, kln, vln);
     p = pn;
   }
   if (nfull < nblk && w == NW - 1) {     // the partial last block
     load_blk(s_lo + nfull * BLK, true, page_lds(s_lo + nfull * BLK), kl, vl);
+    if constexpr (!KFULL) make_q(s_lo + (nfull & ~1) * BLK);
     compute(partial_blk, nfull, kl, vl);
   }
 
