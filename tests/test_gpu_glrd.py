@@ -1,0 +1,121 @@
+"""GPU parity of the grouped-latent path (G-LRD): heads_per_group KV heads share one K latent and one V
+latent, every KV head rebuilds K with its own u_k slice and V with its own u_v slice in-kernel
+(palu_sdpa_decode with u_v; reference interface docs/superpowers/specs/2026-09-12-palu-tt-stage2b-
+design.md:120-142). Oracle: reference_decode with u_v (fp32), on the same bf16-rounded inputs; bar
+max-abs 2e-2 and cosine 0.9999. Group ranks cover the configuration's set {128, 192, 256, 384, 512}.
+"""
+import pytest
+import torch
+
+from oracle import palu_oracle as ref
+from palu_tt import fused
+from palu_tt.cache import LatentCache
+
+pytestmark = pytest.mark.gpu
+
+HD = 128
+THETA = 500000.0
+LLAMA3 = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+
+
+def _bf(t):
+    return t.to(torch.bfloat16).float()
+
+
+def _case(B, S, r_k, r_v, hpg, seed, nh=32, nkv=8, pos=None):
+    g = torch.Generator().manual_seed(seed)
+    ng = nkv // hpg
+    q = _bf(torch.randn(1, B, nh, HD, generator=g))
+    k = _bf(torch.randn(B, ng, S, r_k, generator=g))
+    v = _bf(torch.randn(B, ng, S, r_v, generator=g))
+    u_k = _bf(torch.randn(nkv, r_k, HD, generator=g) / r_k ** 0.5)
+    u_v = _bf(torch.randn(nkv, r_v, HD, generator=g) / r_v ** 0.5)
+    if pos is None:
+        pos = torch.randint(0, S, (B,), generator=g)
+        pos[0] = S - 1
+        if B > 2:
+            pos[1], pos[2] = 0, 127
+    return q, k, v, u_k, u_v, pos
+
+
+def _run(dev, q, k, v, u_k, u_v, pos, S, out_dtype=torch.float32, cs_dtype=torch.float32, **kw):
+    cos, sin = fused.cos_sin_tables(HD, S, THETA, LLAMA3)
+    out = fused.palu_sdpa_decode(
+        q.to(dev, torch.bfloat16), LatentCache.from_rows(k.to(dev, torch.bfloat16), "k"),
+        fused.w_rot_from_u_k(u_k).to(dev, torch.bfloat16)[None], fused.cs_table(cos, sin, S)[None, None].to(dev, cs_dtype),
+        LatentCache.from_rows(v.to(dev, torch.bfloat16), "v"), HD, pos.to(dev, torch.int32),
+        u_v=u_v.to(dev, torch.bfloat16)[None], scale=HD ** -0.5, out_dtype=out_dtype, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu()
+
+
+def _oracle(q, k, v, u_k, u_v, pos, S):
+    cos, sin = ref.cos_sin_tables(HD, S, THETA, LLAMA3)
+    return ref.reference_decode(q, k, u_k, v, pos, cos, sin, HD ** -0.5, u_v=u_v)
+
+
+def _check(out, exp, max_abs=2e-2, cos=0.9999):
+    ma, cs = ref.max_abs(out, exp), ref.cosine(out, exp)
+    assert torch.isfinite(out).all() and ma <= max_abs and cs >= cos, f"max_abs {ma:.3e}, cosine {cs:.6f}"
+
+
+@pytest.mark.parametrize("r_k,r_v", [(128, 128), (192, 256), (256, 192), (384, 512), (512, 512), (512, 128)])
+def test_glrd_matches_oracle_group_ranks(gpu, r_k, r_v):
+    """Two groups of four KV heads (heads_per_group 4), the configuration's group ranks."""
+    args = _case(4, 1024, r_k, r_v, hpg=4, seed=r_k + r_v)
+    _check(_run(gpu, *args, 1024), _oracle(*args, 1024))
+
+
+@pytest.mark.parametrize("hpg,r_k,r_v", [(1, 64, 96), (2, 160, 32), (8, 96, 320)])
+def test_glrd_other_group_sizes_and_ranks(gpu, hpg, r_k, r_v):
+    """Per-head latents with in-kernel V (group size 1), group sizes 2 and 8, ranks that are not
+    multiples of 64."""
+    args = _case(3, 640, r_k, r_v, hpg=hpg, seed=hpg * 1000 + r_k)
+    _check(_run(gpu, *args, 640), _oracle(*args, 640))
+
+
+@pytest.mark.parametrize("B,S", [(1, 4096), (2, 300), (5, 33)])
+def test_glrd_splits_and_ragged_lengths(gpu, B, S):
+    """Batch 1 splits every sequence across workgroups (merged by the merge kernel); lengths that are
+    not a multiple of the 32-position block and caches shorter than one block group."""
+    S_pad = (S + 31) // 32 * 32
+    args = list(_case(B, S_pad, 256, 256, hpg=4, seed=B * 7 + S))
+    args[5] = torch.minimum(args[5], torch.tensor(S - 1))
+    _check(_run(gpu, *args, S_pad), _oracle(*args, S_pad))
+
+
+def test_glrd_bf16_output_and_table(gpu):
+    args = _case(4, 512, 192, 192, hpg=4, seed=99)
+    exp = _oracle(*args, 512)
+    _check(_run(gpu, *args, 512, out_dtype=torch.bfloat16), exp)
+    _check(_run(gpu, *args, 512, cs_dtype=torch.bfloat16), exp, max_abs=5e-2, cos=0.999)
+
+
+def test_glrd_reference_head_shape(gpu):
+    """The reference op tests' per-chip shape: 16 Q / 4 KV heads, one group of 4."""
+    args = _case(8, 1024, 256, 384, hpg=4, seed=5, nh=16, nkv=4)
+    _check(_run(gpu, *args, 1024), _oracle(*args, 1024))
+
+
+def test_glrd_configuration_shape(gpu):
+    """Batch 16, ctx 16384, 2 groups of 4 heads, group ranks drawn from {128, 192, 256, 384, 512};
+    the oracle checks 3 of the 16 rows (the kernel computes all of them in one call)."""
+    g = torch.Generator().manual_seed(4)
+    choices = [128, 192, 256, 384, 512]
+    r_k = choices[int(torch.randint(0, 5, (1,), generator=g))]
+    r_v = choices[int(torch.randint(0, 5, (1,), generator=g))]
+    B, S = 16, 16384
+    q, k, v, u_k, u_v, pos = _case(B, S, r_k, r_v, hpg=4, seed=44, pos=torch.full((16,), S - 1))
+    pos[3], pos[9] = 5000, 12345
+    out = _run(gpu, q, k, v, u_k, u_v, pos, S)
+    rows = [0, 3, 9]
+    exp = _oracle(q[:, rows], k[rows], v[rows], u_k, u_v, pos[rows], S)
+    _check(out[:, rows], exp)
+
+
+def test_glrd_deterministic_repeat(gpu):
+    args = _case(2, 2048, 256, 256, hpg=4, seed=8)
+    a = _run(gpu, *args, 2048)
+    b = _run(gpu, *args, 2048)
+    assert torch.equal(a, b)

@@ -284,3 +284,17 @@ def test_paged_envelope_errors(lib):
     assert rc == _native.PALU_EINVAL and "power of two" in lib.palu_last_error().decode()
     rc = lib.palu_latent_append_paged(_FAKE, _FAKE, _FAKE, _FAKE, 2, 2, 16, 64, 4, 48, 1, None)
     assert rc == _native.PALU_EINVAL and "multiple of 32" in lib.palu_last_error().decode()
+
+
+def test_glrd_envelope_errors(lib):
+    """Grouped latents with u_v: head_dim_v must be 128, caches tiled, contiguous (not paged)."""
+    rc, msg = _sdpa(lib, u_v=_FAKE, head_dim_v=128, n_kv=4, n_groups=1, n_q=16, layout=0)
+    assert rc == _native.PALU_EUNSUPPORTED and "u_v" in msg and "tiled" in msg
+    rc, msg = _sdpa(lib, u_v=_FAKE, head_dim_v=64, n_kv=4, n_groups=1, n_q=16, layout=1)
+    assert rc == _native.PALU_EINVAL and "head_dim_v" in msg
+    rc, msg = _sdpa(lib, u_v=_FAKE, head_dim_v=128, r_k=544, layout=1)
+    assert rc == _native.PALU_EINVAL and "r_k" in msg
+    rc = lib.palu_sdpa_decode_paged(_FAKE, _FAKE, _FAKE, _FAKE, _FAKE, 128, _FAKE, _FAKE, _FAKE, None, None, _FAKE,
+                                    0.088, 0, 2, 1, 0, 2, 16, 4, 1, 16, 64, 4, 256, 256, 256, 256, 256, 0, 1, 1, 0,
+                                    None, 0, None)
+    assert rc == _native.PALU_EUNSUPPORTED and "paged" in lib.palu_last_error().decode()

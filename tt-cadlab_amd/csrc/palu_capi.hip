@@ -179,11 +179,15 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
   }
   if (u_v != nullptr) {
     if (head_dim_v != HD) return fail(PALU_EINVAL, "head_dim_v must be %d when u_v rebuilds V in-kernel, got %d", HD, head_dim_v);
-    return fail(PALU_EUNSUPPORTED, "u_v (in-kernel V rebuild, grouped latents) is not built in this library yet");
+    if (cache_layout != PALU_LAYOUT_TILED)
+      return fail(PALU_EUNSUPPORTED, "u_v: the in-kernel V rebuild reads latent caches in the tiled layout "
+                                     "(PALU_LAYOUT_TILED); row-major caches are not built for it");
+    if (!aligned16(u_v)) return fail(PALU_EINVAL, "u_v must be 16-byte aligned");
+  } else {
+    if (hpg != 1) return fail(PALU_EINVAL, "grouped V latent (heads_per_group %d) needs u_v", hpg);
+    if (head_dim_v != r_v)
+      return fail(PALU_EINVAL, "head_dim_v %d must equal the V latent width %d on the absorbed-V path", head_dim_v, r_v);
   }
-  if (hpg != 1) return fail(PALU_EINVAL, "grouped V latent (heads_per_group %d) needs u_v", hpg);
-  if (head_dim_v != r_v)
-    return fail(PALU_EINVAL, "head_dim_v %d must equal the V latent width %d on the absorbed-V path", head_dim_v, r_v);
   if (cs_dtype != PALU_DTYPE_F32 && cs_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "cs_tab dtype must be fp32 or bf16");
   if (out_dtype != PALU_DTYPE_F32 && out_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "output dtype must be fp32 or bf16");
   if (int rc = check_layout(cache_layout, seq_len, who)) return rc;
@@ -204,12 +208,19 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
   a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = hpg; a.S = seq_len; a.cs_rows = cs_rows;
   a.deterministic = deterministic ? 1 : 0;
   a.qscale = scale * 1.4426950408889634f;
+  a.u_v = static_cast<const __bf16*>(u_v);
+  a.rk = r_k;
+  a.rv = r_v;
   return PALU_OK;
 }
 
 int sdpa_dispatch(const DecodeArgs& a, bool paged, int cache_layout, int r_k, int r_v, int cs_dtype, int out_dtype,
                   hipStream_t stream) {
   const bool tiled = cache_layout == PALU_LAYOUT_TILED;
+  if (a.u_v != nullptr) {
+    if (paged) return fail(PALU_EUNSUPPORTED, "u_v: the in-kernel V rebuild is not built for paged caches");
+    return dispatch_glrd(a, cs_dtype, out_dtype, stream);
+  }
   if (paged)
     return tiled ? dispatch_latent_tiled_paged(a, r_k, r_v, cs_dtype, out_dtype, stream)
                  : dispatch_latent_rows_paged(a, r_k, r_v, cs_dtype, out_dtype, stream);

@@ -81,6 +81,10 @@ struct DecodeArgs {
   // page strides; the page of block J of row b is page_table[b * pt_stride + (J >> page_shift)].
   const int32_t* page_table;
   int pt_stride, n_pages, page_shift;
+  // Grouped latents with in-kernel V (u_v given): [n_kv, RV, HD] per KV head; k/v are then the group
+  // latents [B, n_groups, S, RK / RV] in the tiled layout, and the output is HD wide.
+  const __bf16* u_v;
+  int rk, rv;             // latent widths of the grouped-latent kernel (runtime there)
 };
 
 // Error reporting (defined in palu_capi.hip): formats the message for palu_last_error, returns code.
@@ -125,6 +129,7 @@ int dispatch_latent_tiled(const DecodeArgs& a, int rk, int rv, int cs_dtype, int
 int dispatch_latent_rows_paged(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
 int dispatch_latent_tiled_paged(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
 int dispatch_full(const DecodeArgs& a, bool tiled, bool paged, int dv, bool f32_out, hipStream_t s);
+int dispatch_glrd(const DecodeArgs& a, int cs_dtype, int out_dtype, hipStream_t s);
 
 }  // namespace palu
 
