@@ -54,6 +54,8 @@ def parse():
                     help="fixed block order inside each workgroup (bit-reproducible) instead of a shared counter")
     ap.add_argument("--no-stock", action="store_true", help="skip the full-KV comparator")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the paged mixed-rank and grouped-latent (G-LRD) measurements")
     ap.add_argument("--cpu-rows", type=int, default=2, help="batch rows of the CPU baseline sample")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="before timing, run 3 plain device copies of MIB MiB (the reference kernel that scales "
@@ -134,6 +136,132 @@ def read_traffic(path):
         if ln.startswith("traffic_bytes_per_launch:"):
             return float(ln.split(":", 1)[1])
     return None
+
+
+def _roof(nbytes, flops, kern_ms):
+    gbps = nbytes / (kern_ms * 1e-3) / 1e9
+    tflops = flops / (kern_ms * 1e-3) / 1e12
+    return {"hbm": {"achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(gbps / HBM_PEAK_GBPS, 4), "algorithmic_bytes": int(nbytes)},
+            "mfma": {"achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "flops": int(flops)}}
+
+
+def measure_paged(dev, steps, warmup):
+    """Paged mixed-rank M-LRD: batch 8, per-row context lengths drawn from U[1024, 32768] (seeded),
+    64-token pages in a shuffled pool, (r_k, r_v) = (32, 128) and (128, 64), tiled bf16 pages."""
+    from palu_tt import fused
+    from palu_tt.cache import LatentCache
+    B, S, ps = 8, 32768, 64
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(1024, S + 1, (B,), generator=g)
+    mp = S // ps
+    cos, sin = fused.cos_sin_tables(HD, S, THETA, LLAMA3)
+    cs = fused.cs_table(cos, sin, S)[None, None].to(dev).contiguous()
+    q = (torch.randn(1, B, NQ, HD, generator=g) * 1.3).to(dev, torch.bfloat16)
+    cur = (lens - 1).to(dev, torch.int32)
+    res = []
+    for r_k, r_v in ((32, 128), (128, 64)):
+        need = [int((l + ps - 1) // ps) for l in lens]
+        n_pages = sum(need) + 8
+        layers, n_layers = [], 4
+        gd = torch.Generator(device=dev).manual_seed(r_k)
+        for _ in range(n_layers):
+            perm = torch.randperm(n_pages, generator=g)
+            pt = torch.zeros(B, mp, dtype=torch.int32)
+            o = 0
+            for b in range(B):
+                pt[b, :need[b]] = perm[o:o + need[b]].to(torch.int32)
+                pt[b, need[b]:] = perm[0]
+                o += need[b]
+            kp = LatentCache.zeros(n_pages, NKV, ps, r_k, dev, "k")
+            vp = LatentCache.zeros(n_pages, NKV, ps, r_v, dev, "v")
+            kp.data.normal_(generator=gd)
+            vp.data.normal_(generator=gd)
+            layers.append((kp, vp, pt.to(dev)))
+        u_k = (torch.randn(NKV, r_k, HD, generator=g) / r_k ** 0.5)
+        w_rot = fused.w_rot_from_u_k(u_k)[None].to(dev, torch.bfloat16).contiguous()
+        out = torch.empty(1, B, NQ, r_v, dtype=torch.bfloat16, device=dev)
+        ws = torch.empty(max(fused._native.load().palu_decode_workspace_bytes(B, NKV, S, r_v), 1), dtype=torch.uint8,
+                         device=dev)
+
+        def step(l):
+            kp, vp, pt = layers[l]
+            fused.palu_sdpa_decode(q, kp, w_rot, cs, vp, r_v, cur, scale=HD ** -0.5, out=out, workspace=ws,
+                                   page_table_tensor=pt)
+
+        wall, kern, _ = time_calls(step, n_layers, steps, warmup)
+        L = int(lens.sum())
+        nbytes = L * NKV * (r_k + r_v) * 2
+        flops = 2 * L * NKV * r_k * HD + 2 * L * NQ * HD + 2 * L * NQ * r_v
+        res.append({"rank_k": r_k, "rank_v": r_v, "us_per_layer": round(wall * 1e3, 2),
+                    "kernel_us": round(kern * 1e3, 2), **_roof(nbytes, flops, kern)})
+        del layers
+        torch.cuda.empty_cache()
+    return {"workload": "paged M-LRD, batch 8, context lengths U[1024, 32768], 64-token pages, tiled bf16",
+            "lengths": [int(x) for x in lens], "ranks": res}
+
+
+def measure_glrd(dev, steps, warmup):
+    """G-LRD group size 4: 8 KV heads in 2 groups sharing one K and one V latent, per-group ranks
+    drawn from {128, 192, 256, 384, 512} (seeded; a layer's latent is as wide as its widest group, the
+    narrower group zero-padded), V rebuilt per head in-kernel; batch 16, ctx 16384, tiled bf16.
+    Also the widest layer (512, 512) and the stock full-KV decode at the same shape."""
+    from palu_tt import fused
+    from palu_tt.cache import LatentCache
+    B, S, hpg = 16, 16384, 4
+    ng = NKV // hpg
+    g = torch.Generator().manual_seed(4)
+    choices = [128, 192, 256, 384, 512]
+    pick = lambda: choices[int(torch.randint(0, 5, (1,), generator=g))]
+    drawn_k, drawn_v = [pick() for _ in range(ng)], [pick() for _ in range(ng)]
+    cos, sin = fused.cos_sin_tables(HD, S, THETA, LLAMA3)
+    cs = fused.cs_table(cos, sin, S)[None, None].to(dev).contiguous()
+    q = (torch.randn(1, B, NQ, HD, generator=g) * 1.3).to(dev, torch.bfloat16)
+    cur = torch.full((B,), S - 1, dtype=torch.int32, device=dev)
+    res = []
+    for r_k, r_v, note in ((max(drawn_k), max(drawn_v), "drawn"), (512, 512, "widest")):
+        n_layers = 2
+        gd = torch.Generator(device=dev).manual_seed(r_k + r_v)
+        layers = []
+        for _ in range(n_layers):
+            k = LatentCache.zeros(B, ng, S, r_k, dev, "k")
+            v = LatentCache.zeros(B, ng, S, r_v, dev, "v")
+            k.data.normal_(generator=gd)
+            v.data.normal_(generator=gd)
+            layers.append((k, v))
+        u_k = torch.randn(NKV, r_k, HD, generator=g) / r_k ** 0.5
+        u_v = (torch.randn(NKV, r_v, HD, generator=g) / r_v ** 0.5)[None].to(dev, torch.bfloat16).contiguous()
+        w_rot = fused.w_rot_from_u_k(u_k)[None].to(dev, torch.bfloat16).contiguous()
+        out = torch.empty(1, B, NQ, HD, dtype=torch.bfloat16, device=dev)
+        ws = torch.empty(max(fused._native.load().palu_decode_workspace_bytes(B, NKV, S, HD), 1), dtype=torch.uint8,
+                         device=dev)
+
+        def step(l):
+            k, v = layers[l]
+            fused.palu_sdpa_decode(q, k, w_rot, cs, v, HD, cur, u_v=u_v, scale=HD ** -0.5, out=out, workspace=ws)
+
+        wall, kern, _ = time_calls(step, n_layers, steps, warmup)
+        nbytes = B * ng * S * (r_k + r_v) * 2
+        flops = 2 * B * NKV * S * r_k * HD + 2 * B * NQ * S * HD + 2 * B * NQ * S * r_v + 2 * B * NQ * r_v * HD
+        res.append({"ranks": note, "rank_k": r_k, "rank_v": r_v, "us_per_layer": round(wall * 1e3, 2),
+                    "kernel_us": round(kern * 1e3, 2), **_roof(nbytes, flops, kern)})
+        del layers
+        torch.cuda.empty_cache()
+    kv = [(LatentCache.zeros(B, NKV, S, HD, dev, "k"), LatentCache.zeros(B, NKV, S, HD, dev, "v")) for _ in range(2)]
+    for kk, vv in kv:
+        kk.data.normal_()
+        vv.data.normal_()
+    out_s = torch.empty(1, B, NQ, HD, dtype=torch.bfloat16, device=dev)
+    ws_s = torch.empty(max(fused._native.load().palu_decode_workspace_bytes(B, NKV, S, HD), 1), dtype=torch.uint8,
+                       device=dev)
+    s_wall, s_kern, _ = time_calls(lambda l: fused.flash_decode(q, kv[l][0], kv[l][1], cur, scale=HD ** -0.5, out=out_s,
+                                                                workspace=ws_s), 2, steps, warmup)
+    del kv
+    torch.cuda.empty_cache()
+    return {"workload": "G-LRD group size 4 (2 groups x 4 KV heads), batch 16, ctx 16384, tiled bf16, V rebuilt "
+                        "per head in-kernel", "drawn_group_ranks": {"k": drawn_k, "v": drawn_v}, "layers": res,
+            "stock_full_kv": {"us_per_layer": round(s_wall * 1e3, 2), "kernel_us": round(s_kern * 1e3, 2)}}
 
 
 def cpu_baseline(a, wl):
@@ -246,6 +374,12 @@ def main():
         res["speedup_vs_stock"] = round(s_wall / wall_ms, 3)
         del kv
         wl["layers"] = None
+    if not a.no_extra:
+        if wl.get("layers") is not None:
+            wl["layers"] = None
+            torch.cuda.empty_cache()
+        res["paged_mixed_ranks"] = measure_paged(dev, max(a.steps // 4, 10), max(a.warmup // 4, 5))
+        res["glrd"] = measure_glrd(dev, max(a.steps // 8, 10), max(a.warmup // 8, 3))
     if not a.no_cpu:
         if wl.get("layers") is None:
             gd = torch.Generator(device=dev).manual_seed(1)

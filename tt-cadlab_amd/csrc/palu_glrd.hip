@@ -163,7 +163,8 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_kernel(const DecodeArgs a
   }
 
   // Loads of one block: this wave's quarter of the K-latent tiles (tile w + 4i) and its V tiles
-  // (tile w * TPW + i). Past the last block (or past the tile count) the same instructions read the
+  // (tile w * TPW + i). They are ordinary (cached) loads: the heads of a group read the same latent
+  // rows at about the same time, and the L2 serves all but the first. Past the last block (or past the tile count) the same instructions read the
   // first tiles of block 0 of the stream, so every path issues the same loads; that data is unused.
   auto load_lat = [&](int j, bf16x8 (&la)[G_LAT_PER_WAVE]) {
     const bool live = j < nblk;
@@ -171,7 +172,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_kernel(const DecodeArgs a
 #pragma unroll
     for (int i = 0; i < G_LAT_PER_WAVE; ++i) {
       const int t = w + G_NW * i;
-      la[i] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(kb0 + (t < NT ? t : 0) * 512));
+      la[i] = *reinterpret_cast<const bf16x8*>(kb0 + (t < NT ? t : 0) * 512);
     }
   };
   auto store_lat = [&](int buf, const bf16x8 (&la)[G_LAT_PER_WAVE]) {
@@ -188,50 +189,43 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_kernel(const DecodeArgs a
 #pragma unroll
     for (int i = 0; i < G_MAXTPW; ++i) {
       const int mt = w * TPW + i;
-      va[i] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(vb0 + ((i < TPW && mt < VT) ? mt : 0) * 512));
+      va[i] = *reinterpret_cast<const bf16x8*>(vb0 + ((i < TPW && mt < VT) ? mt : 0) * 512);
     }
   };
 
-  // Query rotated back by the block base, scaled by scale * log2 e, regrouped into the QK operand;
-  // every wave builds the whole operand and uses its own 32-dim slice qB[w].
-  const int qf = lane & 15;
-  bf16x8 qB[4];
+  // Query rotated back by the block base, scaled by scale * log2 e, for this wave's 32 dims only:
+  // lane (head l/4, dims 32w + 8(l%4) .. +7, i.e. frequency pairs 16w + 4(l%4) .. +3), regrouped
+  // through the wave's LDS area into the QK operand order d(j) = 16*(2w + j/4) + 4*g + j%4.
+  bf16x8 qB;
   auto make_q = [&](int base) {
     const int J = base >> 5;
+    const int hq = lane >> 2, qd = lane & 3;
+    const int qf = 4 * w + qd;                       // 8-dim group of the head dim
     const float4* lo4 = reinterpret_cast<const float4*>(tl + (J & 31) * 64 + 4 * qf);
     const float4* hi4 = reinterpret_cast<const float4*>(th + (J >> 5) * 64 + 4 * qf);
     const float4 l01 = lo4[0], l23 = lo4[1], h01 = hi4[0], h23 = hi4[1];
     const float lc[4] = {l01.x, l01.z, l23.x, l23.z}, ls[4] = {l01.y, l01.w, l23.y, l23.w};
     const float hc[4] = {h01.x, h01.z, h23.x, h23.z}, hs[4] = {h01.y, h01.w, h23.y, h23.w};
-    float cf[4], sf[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      cf[p] = (hc[p] * lc[p] - hs[p] * ls[p]) * a.qscale;
-      sf[p] = (hs[p] * lc[p] + hc[p] * ls[p]) * a.qscale;
-    }
     const int rt = qf >> 1, g0 = 2 * (qf & 1);
+    if (hq < a.rep) {
+      const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qs_lds + hq * HD + 8 * qf);
+      bf16x4 y0, y1;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int h = g + 4 * k;
-      if (h < a.rep) {
-        const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qs_lds + h * HD + 8 * qf);
-        bf16x4 y0, y1;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const float x0 = (float)qv[2 * p], x1 = (float)qv[2 * p + 1];
-          const float r0 = x0 * cf[p] + x1 * sf[p], r1 = x1 * cf[p] - x0 * sf[p];
-          if (p < 2) { y0[2 * p] = (__bf16)r0; y0[2 * p + 1] = (__bf16)r1; }
-          else { y1[2 * p - 4] = (__bf16)r0; y1[2 * p - 3] = (__bf16)r1; }
-        }
-        *reinterpret_cast<bf16x4*>(qx + ((h * 4 + g0) * 8 + rt) * 4) = y0;
-        *reinterpret_cast<bf16x4*>(qx + ((h * 4 + g0 + 1) * 8 + rt) * 4) = y1;
+      for (int p = 0; p < 4; ++p) {
+        const float cf = (hc[p] * lc[p] - hs[p] * ls[p]) * a.qscale;
+        const float sf = (hs[p] * lc[p] + hc[p] * ls[p]) * a.qscale;
+        const float x0 = (float)qv[2 * p], x1 = (float)qv[2 * p + 1];
+        const float r0 = x0 * cf + x1 * sf, r1 = x1 * cf - x0 * sf;      // R_{-base}
+        if (p < 2) { y0[2 * p] = (__bf16)r0; y0[2 * p + 1] = (__bf16)r1; }
+        else { y1[2 * p - 4] = (__bf16)r0; y1[2 * p - 3] = (__bf16)r1; }
       }
+      *reinterpret_cast<bf16x4*>(qx + ((hq * 4 + g0) * 8 + rt) * 4) = y0;
+      *reinterpret_cast<bf16x4*>(qx + ((hq * 4 + g0 + 1) * 8 + rt) * 4) = y1;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) qB[kb] = *reinterpret_cast<const bf16x8*>(qx + ((n * 4 + g) * 8 + 2 * kb) * 4);
+    qB = *reinterpret_cast<const bf16x8*>(qx + ((n * 4 + g) * 8 + 2 * w) * 4);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
   };
@@ -243,7 +237,8 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_kernel(const DecodeArgs a
 
   // One block, all waves together: rebuild this wave's K^T slice from the staged latent, rotate,
   // partial QK, exchange, online softmax, latent-space PV on this wave's V tiles.
-  auto step = [&](int j, int buf, const bf16x8 (&va)[G_MAXTPW]) __attribute__((always_inline)) {
+  auto step = [&](auto partial_tag, int j, int buf, const bf16x8 (&va)[G_MAXTPW]) __attribute__((always_inline)) {
+    constexpr bool partial = decltype(partial_tag)::value;
     const int base = s_lo + j * BLK;
     make_q(base);
     const bf16x8* lt = reinterpret_cast<const bf16x8*>(lat + buf * (G_LAT_TILES * 1024));
@@ -275,7 +270,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_kernel(const DecodeArgs a
         acc[c][h][2] = x2 * t.z - x3 * t.w;
         acc[c][h][3] = x3 * t.z + x2 * t.w;
       }
-      sc[c] = mfma16(pack8(acc[c][0], acc[c][1]), qB[w], f32x4{0.f, 0.f, 0.f, 0.f});
+      sc[c] = mfma16(pack8(acc[c][0], acc[c][1]), qB, f32x4{0.f, 0.f, 0.f, 0.f});
       sbuf[(w * 2 + c) * 64 + lane] = make_float4(sc[c][0], sc[c][1], sc[c][2], sc[c][3]);
     }
     __syncthreads();                                     // partial scores of all waves are in sbuf
@@ -289,8 +284,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_kernel(const DecodeArgs a
       }
       sc[c] = s;
     }
-    const bool partial = base + BLK > s_hi;
-    if (partial) {
+    if constexpr (partial) {
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -320,7 +314,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_kernel(const DecodeArgs a
     for (int i = 0; i < G_MAXTPW; ++i) {
       if (i < TPW && w * TPW + i < VT) {
         bf16x8 vA = va[i];
-        if (partial) {
+        if constexpr (partial) {
 #pragma unroll
           for (int e = 0; e < 8; ++e)
             if (base + 8 * g + e >= s_hi) vA[e] = (__bf16)0.0f;
@@ -333,27 +327,36 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_kernel(const DecodeArgs a
   // Pipeline: block j's latent is in lat buffer j & 1 when step j starts; its registers were loaded
   // two steps earlier. V of block j is loaded one step earlier. Two steps per trip keep the register
   // buffers in fixed roles.
+  // Full blocks run in the pipelined loop; a partial last block (its latent staged by the pipeline)
+  // runs once afterwards with masking, its V tiles loaded then.
+  const std::integral_constant<bool, false> full_blk;
+  const std::integral_constant<bool, true> partial_blk;
+  const int nfull = s_hi > s_lo ? (s_hi - s_lo) / BLK : 0;
   bf16x8 la0[G_LAT_PER_WAVE], la1[G_LAT_PER_WAVE], va0[G_MAXTPW], va1[G_MAXTPW];
   load_lat(0, la0);
   load_v(0, va0);
   load_lat(1, la1);
   store_lat(0, la0);
   __syncthreads();
-  for (int j = 0; j < nblk; j += 2) {
+  for (int j = 0; j < nfull; j += 2) {
     load_lat(j + 2, la0);
     load_v(j + 1, va1);
     __builtin_amdgcn_sched_barrier(0);
-    step(j, 0, va0);
+    step(full_blk, j, 0, va0);
     store_lat(1, la1);
     __syncthreads();
-    if (j + 1 < nblk) {
+    if (j + 1 < nfull) {
       load_lat(j + 3, la1);
       load_v(j + 2, va0);
       __builtin_amdgcn_sched_barrier(0);
-      step(j + 1, 1, va1);
+      step(full_blk, j + 1, 1, va1);
       store_lat(0, la0);
       __syncthreads();
     }
+  }
+  if (nfull < nblk) {
+    load_v(nfull, va0);
+    step(partial_blk, nfull, nfull & 1, va0);
   }
 
   // ---- epilogue: out = O_lat u_v[h] / l -----------------------------------------------------------
