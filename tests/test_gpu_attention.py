@@ -1,0 +1,91 @@
+"""The attention drop-in (palu_tt.attention.PaluAttention) against the HF-convention layer oracle.
+
+A random Llama-shaped layer is compressed with per-head SVD (or per-group SVD for grouped latents),
+converted with convert.palu_layer_tensors, and driven through prefill (two users) and several decode
+steps; every output is compared with oracle.PaluRefAttention (fp32, same factors, same positions).
+The layer runs in bf16 (weights, activations, caches), so the bar is on the whole layer output:
+cosine >= 0.999 and max-abs within 2% of the output's largest magnitude. Covers the fused latent path
+(r < head_dim), the full-rank fast paths (stock K / stock V), grouped latents with in-kernel V, and
+both cache layouts.
+"""
+import pytest
+import torch
+
+from oracle import palu_oracle as ref
+from palu_tt import convert
+from palu_tt.attention import PaluAttention
+
+pytestmark = pytest.mark.gpu
+
+HD = 128
+THETA = 500000.0
+LLAMA3 = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+
+
+class _Args:
+    def __init__(self, dim, nh, nkv, max_seq, max_batch, palu):
+        self.dim, self.n_heads, self.n_kv_heads, self.head_dim = dim, nh, nkv, HD
+        self.max_seq_len, self.max_batch_size = max_seq, max_batch
+        self.rope_theta, self.rope_scaling = THETA, LLAMA3
+        self.palu = palu
+
+
+def _group_svd(W, nkv, gs, rank):
+    """Per-group truncated SVD with Palu's balanced split; every head of a group gets the group's VT
+    and its hd-row slice of the group's U (reference compress.py:12-23, stage2b-design.md:80-86)."""
+    Wg = W.reshape(nkv // gs, gs * HD, -1)
+    U, VT = ref.svd_per_head(Wg.reshape(-1, W.shape[1]), nkv // gs, rank)       # [G, gs*hd, r], [G, r, dim]
+    U_h = U.reshape(nkv // gs, gs, HD, rank).reshape(nkv, HD, rank)
+    VT_h = VT.repeat_interleave(gs, dim=0)
+    return U_h.contiguous(), VT_h.contiguous()
+
+
+def _layer(dim, nh, nkv, r_k, r_v, gs, seed):
+    g = torch.Generator().manual_seed(seed)
+    W = {"q": torch.randn(nh * HD, dim, generator=g) * 0.02, "k": torch.randn(nkv * HD, dim, generator=g) * 0.02,
+         "v": torch.randn(nkv * HD, dim, generator=g) * 0.02, "o": torch.randn(dim, nh * HD, generator=g) * 0.02}
+    Uk, VTk = _group_svd(W["k"], nkv, gs, r_k)
+    Uv, VTv = _group_svd(W["v"], nkv, gs, r_v)
+    lr = convert.LowRank(VTk, Uk, VTv, Uv, group_size=gs)
+    # the model state dict holds wq in Meta (interleaved-pair) order, as the reference's checkpoint loader
+    # leaves it; the converter's K tensors are Meta-ordered too
+    sd = {"layers.0.attention.wq.weight": convert.reverse_permute(W["q"], nh, nh * HD, dim),
+          "layers.0.attention.wo.weight": W["o"]}
+    for name, t in convert.palu_layer_tensors(W, lr, nh, nkv, HD).items():
+        sd[f"layers.0.attention.palu.{name}"] = t
+    palu = convert.PaluConfig(rank_k=[r_k], rank_v=[r_v], cache_id="test", group_size=gs)
+    oracle = ref.PaluRefAttention(nh, nkv, HD, THETA, LLAMA3, W["q"], W["o"], ref.Factors(VTk, Uk, VTv, Uv))
+    return sd, palu, oracle
+
+
+def _close(out, exp, what):
+    out, exp = out.float().cpu(), exp.float()
+    cs = ref.cosine(out, exp)
+    rel = ref.max_abs(out, exp) / float(exp.abs().max())
+    assert cs >= 0.999 and rel <= 0.02, f"{what}: cosine {cs:.6f}, max-abs / max {rel:.4f}"
+
+
+@pytest.mark.parametrize("r_k,r_v,gs,layout", [(64, 64, 1, "tiled"), (64, 64, 1, "rows"), (32, 96, 1, "tiled"),
+                                               (HD, 64, 1, "tiled"), (32, HD, 1, "tiled"), (HD, HD, 1, "rows"),
+                                               (192, 256, 2, "tiled")])
+def test_attention_prefill_then_decode_matches_layer_oracle(gpu, r_k, r_v, gs, layout):
+    dim, nh, nkv, B, S0, steps = 1024, 8, 2, 2, 40, 6
+    sd, palu, oracle = _layer(dim, nh, nkv, r_k, r_v, gs, seed=r_k + r_v + gs)
+    att = PaluAttention(gpu, None, _Args(dim, nh, nkv, 128, B, palu), sd, None, 0, cache_layout=layout)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(B, S0 + steps, dim, generator=g)
+    exp_pre = oracle.forward(x[:, :S0], 0)
+    out_pre = att.forward(x[:, :S0].to(gpu), mode="prefill", user_id=0)
+    _close(out_pre, exp_pre, "prefill")
+    for t in range(S0, S0 + steps):
+        exp = oracle.forward(x[:, t:t + 1], t)[:, 0]
+        out = att.forward(x[:, t].to(gpu), torch.full((B,), t, dtype=torch.int32, device=gpu), mode="decode")
+        torch.cuda.synchronize()
+        _close(out, exp, f"decode step {t}")
+
+
+def test_attention_kv_bytes_per_token(gpu):
+    sd, palu, _ = _layer(512, 4, 2, 64, 32, 1, seed=1)
+    att = PaluAttention(gpu, None, _Args(512, 4, 2, 64, 1, palu), sd, None, 0)
+    assert att.kv_bytes_per_token() == 2 * (64 + 32) * 2.0

@@ -1,0 +1,208 @@
+"""PaluAttention on MI355X: the reference's attention drop-in (palu_tt/attention.py:97-733) over
+PyTorch-ROCm tensors and the HIP decode library.
+
+Same construction inputs and state-dict keys as the reference (``layers.{i}.attention.wq.weight`` /
+``.wo.weight`` and the converter's ``layers.{i}.attention.palu.*``, convert.palu_layer_tensors), the
+same cache contents (latent rows of width r_k / r_v per head or per group, or rotated full K on the
+K-fast path), and the same decode data flow (attention.py:585-733):
+
+  decode:  x @ [wq | wk_lat_pad | wv_lat_pad]^T -> q, latent slots
+           RoPE on q at current_pos (Meta-interleaved)
+           latents (a head's first r columns, or a group's head slots concatenated) appended at
+           current_pos (the latent-append kernel)
+           fused latent flash-decode (palu_sdpa_decode; u_v rebuilds V per head for grouped latents)
+           or, on the K-fast path (r_k == head_dim, per-head factors), flash-decode over the cached
+           rotated K
+           absorbed-V output padded to head_dim, concat heads, @ wo_fused^T
+  prefill: latents rebuilt to full K / V with u_k / u_v (attention.py:380-480), RoPE on q and K,
+           causal SDPA, @ wo^T; the cache receives the latents (or rotated K on the fast path).
+
+Tensors: x is [B, dim] for decode (or the reference's [1, 1, B, dim]) and [1, S, dim] / [1, 1, S, dim]
+for prefill; outputs have the matching shape. The caches are ``LatentCache`` objects (the tiled layout
+the kernels stream fastest) unless ``cache_layout="rows"`` is asked for.
+"""
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from palu_tt import fused
+from palu_tt.cache import LatentCache
+
+
+class PaluAttention(torch.nn.Module):
+    def __init__(self, mesh_device, tt_ccl, args, state_dict, weight_cache_path, layer_num, dtype=torch.bfloat16,
+                 transformation_mats=None, configuration=None, paged_attention_config=None, use_paged_kv_cache=False,
+                 prefetcher=None, cache_layout: str = "tiled"):
+        super().__init__()
+        assert paged_attention_config is None and not use_paged_kv_cache, \
+            "the attention module keeps contiguous per-row caches (the paged kernels are in palu_tt.fused)"
+        assert prefetcher is None, "prefetcher not supported"
+        configuration = configuration if configuration is not None else args
+        assert hasattr(configuration, "palu"), "attach a PaluConfig as configuration.palu"
+        assert cache_layout in ("tiled", "rows")
+        self.device = torch.device(mesh_device) if not isinstance(mesh_device, torch.device) else mesh_device
+        self.dtype = dtype
+        self.layer_num = layer_num
+        self.hidden_size = configuration.dim
+        self.n_heads = configuration.n_heads
+        self.n_kv_heads = configuration.n_kv_heads
+        self.head_dim = configuration.head_dim
+        self.max_seq_len = configuration.max_seq_len
+        self.max_batch_size = configuration.max_batch_size
+        self.scale = self.head_dim ** -0.5
+        self.palu = configuration.palu
+        self.gs = int(self.palu.group_size)
+        assert self.n_kv_heads % self.gs == 0, f"group size {self.gs} must divide {self.n_kv_heads} KV heads"
+        self.n_groups = self.n_kv_heads // self.gs
+        self.r_k = int(self.palu.rank_k[layer_num])
+        self.r_v = int(self.palu.rank_v[layer_num])
+        hd = self.head_dim
+        assert self.r_k % 32 == 0 and self.r_v % 32 == 0 and self.r_k <= self.gs * hd and self.r_v <= self.gs * hd
+        # full-rank per-head factors collapse to stock K / V (reference attention.py:136-141)
+        self.recon_k = self.gs > 1 or self.r_k < hd
+        self.recon_v = self.gs > 1 or self.r_v < hd
+        self.cache_layout = cache_layout
+
+        ln = f"layers.{layer_num}.attention"
+        P = f"{ln}.palu"
+        dev, bf = self.device, torch.bfloat16
+        wq = state_dict[f"{ln}.wq.weight"]
+        wk = state_dict[f"{P}.wk_lat_pad"]
+        wv = state_dict[f"{P}.wv_lat_pad"]
+        # weights stored input-major ([dim, out]) so every projection is a plain x @ W
+        self.wqkv_t = torch.cat([wq, wk, wv], dim=0).T.to(dev, bf).contiguous()      # [dim, (nh + 2 nkv) hd]
+        self.wo_t = state_dict[f"{ln}.wo.weight"].T.to(dev, bf).contiguous()
+        self.wo_fused_t = (state_dict[f"{P}.wo_fused"].T.to(dev, bf).contiguous()
+                           if (self.recon_v and self.gs == 1) else self.wo_t)
+        self.u_k = state_dict[f"{P}.u_k"].to(dev, bf).contiguous() if self.recon_k else None   # [nkv, r_k, hd]
+        self.w_rot = state_dict[f"{P}.w_rot"].to(dev, bf)[None].contiguous() if self.recon_k else None
+        self.u_v = state_dict[f"{P}.u_v"].to(dev, bf).contiguous() if self.recon_v else None   # [nkv, r_v, hd]
+
+        cos, sin = fused.cos_sin_tables(hd, self.max_seq_len, configuration.rope_theta,
+                                        getattr(configuration, "rope_scaling", None))
+        self.cos = cos[:self.max_seq_len].to(dev).contiguous()
+        self.sin = sin[:self.max_seq_len].to(dev).contiguous()
+        self.cs_tab = fused.cs_table(cos, sin, self.max_seq_len)[None, None].to(dev).contiguous()
+
+        B, S = self.max_batch_size, self.max_seq_len
+        k_width = self.r_k if self.recon_k else hd
+        if cache_layout == "tiled":
+            assert S % 32 == 0, "the tiled cache holds whole 32-position blocks"
+            keys = LatentCache.zeros(B, self.n_groups, S, k_width, dev, "k")
+            values = LatentCache.zeros(B, self.n_groups, S, self.r_v, dev, "v")
+        else:
+            keys = torch.zeros(B, self.n_groups, S, k_width, dtype=bf, device=dev)
+            values = torch.zeros(B, self.n_groups, S, self.r_v, dtype=bf, device=dev)
+        self.layer_past = [keys, values]
+
+    # ------------------------------------------------------------------------------------------------
+    def kv_bytes_per_token(self) -> float:
+        """Cache bytes per token per layer (bf16 latents), reference attention.py:352-358."""
+        k_width = self.r_k if self.recon_k else self.head_dim
+        return self.n_groups * (k_width + self.r_v) * 2.0
+
+    def _split(self, xqkv):
+        nh, nkv, hd = self.n_heads, self.n_kv_heads, self.head_dim
+        q = xqkv[..., :nh * hd].unflatten(-1, (nh, hd))
+        k = xqkv[..., nh * hd:(nh + nkv) * hd].unflatten(-1, (nkv, hd))
+        v = xqkv[..., (nh + nkv) * hd:].unflatten(-1, (nkv, hd))
+        return q, k, v
+
+    def _group_latent(self, slots, r):
+        """[..., nkv, hd] head slots -> [..., n_groups, r]: a head's first r columns (group size 1), or a
+        group's head slots concatenated (reference attention.py:545-565)."""
+        g = slots.unflatten(-2, (self.n_groups, self.gs)).flatten(-2)     # [..., n_groups, gs * hd]
+        return g[..., :r]
+
+    def _rope(self, x, pos):
+        """Meta-interleaved RoPE of x [..., heads, hd] at positions pos (broadcast over heads)."""
+        return fused.apply_rope_meta(x, self.cos[pos][..., None, :], self.sin[pos][..., None, :])
+
+    def _append(self, cache, rows, pos):
+        fused.paged_update_cache(cache, rows.to(torch.bfloat16).contiguous(), pos)
+
+    # ------------------------------------------------------------------------------------------------
+    def forward_decode(self, x, current_pos, rot_mats=None, page_table=None, kv_cache=None):
+        assert page_table is None and kv_cache is None
+        shape = x.shape
+        x2 = x.reshape(-1, self.hidden_size).to(torch.bfloat16)
+        B = x2.shape[0]
+        pos = current_pos.reshape(-1).to(self.device, torch.int32)
+        assert pos.numel() == B
+        q_pre, k_slots, v_slots = self._split(x2 @ self.wqkv_t)             # [B, nh | nkv, hd]
+        q = self._rope(q_pre.float(), pos.long()).to(torch.bfloat16)
+        keys, values = self.layer_past
+        if B != self.max_batch_size:
+            raise ValueError(f"decode batch {B} != max_batch_size {self.max_batch_size}")
+        if self.recon_k:
+            k_new = self._group_latent(k_slots, self.r_k)
+        else:
+            k_new = self._rope(k_slots.float(), pos.long())                # stock K path: rotated full K
+        v_new = self._group_latent(v_slots, self.r_v)
+        self._append(keys, k_new, pos)
+        self._append(values, v_new, pos)
+        q4 = q[None].contiguous()                                          # [1, B, nh, hd]
+        if self.recon_k:
+            grouped = self.gs > 1
+            attn = fused.palu_sdpa_decode(q4, keys, self.w_rot, self.cs_tab, values,
+                                          self.head_dim if grouped else self.r_v, pos,
+                                          u_v=self.u_v[None] if grouped else None, scale=self.scale,
+                                          out_dtype=torch.bfloat16)
+        else:
+            attn = fused.flash_multi_latent_attention_decode(q4, keys, values, self.r_v, pos, scale=self.scale)
+        if attn.shape[-1] < self.head_dim:
+            attn = F.pad(attn, (0, self.head_dim - attn.shape[-1]))
+        out = attn[0].reshape(B, self.n_heads * self.head_dim) @ self.wo_fused_t
+        return out.reshape(*shape[:-1], self.hidden_size)
+
+    def forward_prefill(self, x, rot_mats=None, user_id=0, page_table=None, chunk_page_table=None,
+                        chunk_start_idx=None, kv_cache=None):
+        """Prefill of one user (x [1, S, dim] or [1, 1, S, dim], cache row user_id) or of U users at once
+        (x [U, S, dim], cache rows user_id .. user_id + U - 1), positions 0 .. S-1."""
+        assert page_table is None and chunk_start_idx is None and kv_cache is None
+        shape = x.shape
+        x3 = x.reshape(-1, shape[-2], self.hidden_size).to(torch.bfloat16)          # [U, S, dim]
+        U, S = x3.shape[0], x3.shape[1]
+        assert 0 < S <= self.max_seq_len and user_id + U <= self.max_batch_size
+        outs = []
+        for u in range(U):
+            outs.append(self._prefill_one(x3[u], user_id + u))
+        return torch.stack(outs).reshape(*shape[:-1], self.hidden_size)
+
+    def _prefill_one(self, x2, user):
+        S = x2.shape[0]
+        q_pre, k_slots, v_slots = self._split(x2 @ self.wqkv_t)             # [S, nh | nkv, hd]
+        pos = torch.arange(S, device=self.device)
+        k_lat = self._group_latent(k_slots, self.r_k) if self.recon_k else None    # [S, n_groups, r_k]
+        v_lat = self._group_latent(v_slots, self.r_v)
+        rep_g = lambda t: t.repeat_interleave(self.gs, dim=1)                       # group latent per head
+        K = torch.einsum("sgr,grd->sgd", rep_g(k_lat).float(), self.u_k.float()) if self.recon_k else k_slots.float()
+        V = torch.einsum("sgr,grd->sgd", rep_g(v_lat).float(), self.u_v.float()) if self.recon_v else v_slots.float()
+        q = self._rope(q_pre.float(), pos)
+        K = self._rope(K, pos)
+        keys, values = self.layer_past
+        self._fill(keys, k_lat if self.recon_k else K, user)
+        self._fill(values, v_lat, user)
+        rep = self.n_heads // self.n_kv_heads
+        qh = q.transpose(0, 1)[None]                                                # [1, nh, S, hd] fp32
+        Kh = K.repeat_interleave(rep, dim=1).transpose(0, 1)[None].contiguous()
+        Vh = V.repeat_interleave(rep, dim=1).transpose(0, 1)[None].contiguous()
+        attn = F.scaled_dot_product_attention(qh, Kh, Vh, is_causal=True, scale=self.scale)
+        attn = attn[0].transpose(0, 1).reshape(S, self.n_heads * self.head_dim).to(torch.bfloat16)
+        return attn @ self.wo_t
+
+    def _fill(self, cache, rows, user_id):
+        """Rows [S, G, w] into cache row user_id at positions 0..S-1 (reference ttnn.fill_cache)."""
+        r = rows.to(torch.bfloat16).transpose(0, 1)                       # [G, S, w]
+        if isinstance(cache, LatentCache):
+            cache.write_rows(user_id, 0, r)
+        else:
+            cache[user_id, :, :r.shape[1]] = r
+
+    def forward(self, x, current_pos=None, rot_mats=None, user_id=0, mode="decode", page_table=None,
+                chunk_page_table=None, chunk_start_idx=None, kv_cache=None):
+        if str(mode).lower().endswith("prefill"):
+            return self.forward_prefill(x, rot_mats, user_id, page_table=page_table, chunk_page_table=chunk_page_table,
+                                        chunk_start_idx=chunk_start_idx, kv_cache=kv_cache)
+        return self.forward_decode(x, current_pos, rot_mats, page_table=page_table, kv_cache=kv_cache)

@@ -77,6 +77,14 @@ class LatentCache:
     def to_rows(self) -> torch.Tensor:
         return tiled_to_rows(self.data, self.role)
 
+    def write_rows(self, b: int, start: int, rows: torch.Tensor) -> None:
+        """cache[b, :, start:start + n, :] = rows ([G, n, width]); converts only the blocks it touches."""
+        G, n, w = rows.shape
+        b0, b1 = start // BLOCK, (start + n + BLOCK - 1) // BLOCK
+        cur = tiled_to_rows(self.data[b:b + 1, :, b0:b1], self.role)          # [1, G, (b1 - b0) * 32, w]
+        cur[0, :, start - b0 * BLOCK:start - b0 * BLOCK + n] = rows.to(cur.dtype)
+        self.data[b:b + 1, :, b0:b1] = rows_to_tiled(cur, self.role)
+
     @property
     def shape(self) -> Tuple[int, int, int, int]:
         B, G, nblk, ntile = self.data.shape[:4]
