@@ -57,6 +57,14 @@ def parse():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the paged mixed-rank and grouped-latent (G-LRD) measurements")
     ap.add_argument("--cpu-rows", type=int, default=2, help="batch rows of the CPU baseline sample")
+    ap.add_argument("--e2e", action="store_true",
+                    help="also run the end-to-end 32-layer decoder (batch 64, 2048-token prompts, greedy decode) "
+                         "with Palu ranks and with stock full-rank K/V, reporting decode tokens/s")
+    ap.add_argument("--e2e-batch", type=int, default=64)
+    ap.add_argument("--e2e-prompt", type=int, default=2048)
+    ap.add_argument("--e2e-tokens", type=int, default=256, help="greedy tokens generated per row")
+    ap.add_argument("--e2e-layers", type=int, default=32)
+    ap.add_argument("--e2e-no-graph", action="store_true", help="eager decode steps instead of one HIP graph per step")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="before timing, run 3 plain device copies of MIB MiB (the reference kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -264,6 +272,57 @@ def measure_glrd(dev, steps, warmup):
             "stock_full_kv": {"us_per_layer": round(s_wall * 1e3, 2), "kernel_us": round(s_kern * 1e3, 2)}}
 
 
+def measure_e2e(a, dev):
+    """Llama-3.1-8B-shaped decoder (32 layers, vocab 128256, FFN 14336 SwiGLU, RMSNorm eps 1e-5), random-init
+    bf16 weights; per-layer M-LRD ranks drawn from [32, 128] in steps of 8 with mean 64 (K and V drawn
+    separately, seeded), padded to a multiple of 32. Batch rows get random-id prompts, are prefilled, then
+    decode greedily; decode tokens/s = batch x timed decode steps / decode wall time (the first generated
+    token comes from prefill and is not timed). Then the same model shape with full-rank (128) K and V: the
+    stock bf16 full-KV decode through the same engine."""
+    from palu_tt import model as pm
+    B, P, n_new, L = a.e2e_batch, a.e2e_prompt, a.e2e_tokens, a.e2e_layers
+    ranks_k, ranks_v = pm.draw_ranks(L, seed=1), pm.draw_ranks(L, seed=2)
+    out = {"workload": f"{L}-layer Llama-3.1-8B-shaped decoder, batch {B}, {P}-token random prompts, "
+                       f"{n_new} greedy tokens, random-init bf16 weights",
+           "graph": not a.e2e_no_graph}
+    for kind, rk, rv in (("palu", ranks_k, ranks_v), ("stock", [HD] * L, [HD] * L)):
+        args = pm.ModelArgs(n_layers=L, max_batch_size=B, max_seq_len=(P + n_new + 31) // 32 * 32)
+        t0 = time.perf_counter()
+        model = pm.Transformer(args, pm.random_palu_state_dict(args, rk, rv, dev, seed=0), dev)
+        torch.cuda.synchronize()
+        t_build = time.perf_counter() - t0
+        prompts = torch.randint(0, args.vocab_size, (B, P), generator=torch.Generator().manual_seed(7)).to(dev)
+        t0 = time.perf_counter()
+        tok = pm.prefill_all(model, prompts).argmax(-1)
+        torch.cuda.synchronize()
+        t_pre = time.perf_counter() - t0
+        step = model.decode if a.e2e_no_graph else model.decode_graph
+        pos = torch.full((B,), P, dtype=torch.int32, device=dev)
+        step(tok, pos)                                    # capture / warm-up at position P (rewritten below)
+        torch.cuda.synchronize()
+        toks = [tok]
+        t0 = time.perf_counter()
+        for _ in range(n_new - 1):
+            tok = step(tok, pos).argmax(-1)
+            toks.append(tok)
+            pos += 1
+        torch.cuda.synchronize()
+        t_dec = time.perf_counter() - t0
+        att = [Ld["attn"] for Ld in model.layers]
+        kv_tok = sum(x.kv_bytes_per_token() for x in att)
+        out[kind] = {"decode_tokens_per_s": round(B * (n_new - 1) / t_dec, 1),
+                     "ms_per_decode_step": round(t_dec * 1e3 / (n_new - 1), 3),
+                     "prefill_s": round(t_pre, 2), "build_s": round(t_build, 1),
+                     "kv_cache_bytes_per_token": int(kv_tok),
+                     "ranks_drawn_mean": {"k": sum(rk) / L, "v": sum(rv) / L},
+                     "ranks_padded": {"k": args.palu.rank_k, "v": args.palu.rank_v},
+                     "generated_ids_checksum": int(torch.stack(toks).sum())}
+        del model, att, step
+        torch.cuda.empty_cache()
+    out["speedup_vs_stock"] = round(out["palu"]["decode_tokens_per_s"] / out["stock"]["decode_tokens_per_s"], 3)
+    return out
+
+
 def cpu_baseline(a, wl):
     from oracle import palu_oracle as ref
     cores = len(os.sched_getaffinity(0))
@@ -380,6 +439,11 @@ def main():
             torch.cuda.empty_cache()
         res["paged_mixed_ranks"] = measure_paged(dev, max(a.steps // 4, 10), max(a.warmup // 4, 5))
         res["glrd"] = measure_glrd(dev, max(a.steps // 8, 10), max(a.warmup // 8, 3))
+    if a.e2e:
+        if wl.get("layers") is not None:
+            wl["layers"] = None
+            torch.cuda.empty_cache()
+        res["e2e_decoder"] = measure_e2e(a, dev)
     if not a.no_cpu:
         if wl.get("layers") is None:
             gd = torch.Generator(device=dev).manual_seed(1)

@@ -9,8 +9,9 @@ Everything here is a restatement, written from the mathematics the reference imp
 * palu_tt/fused.py:36-107  -- pair-rotation matrix T, [u_k | u_k T], chunk rule, Meta-interleaved
   cos/sin tables, [cos | sin] table, Phase 2 step row, and ``reference_decode`` (the fp32 model of
   ttnn.transformer.palu_sdpa_decode);
-* palu_tt/reference.py:14-71 -- ``PaluRefAttention`` (HF conventions: rotate_half RoPE on unpermuted
-  heads, latent caches, full K/V rebuild, GQA, causal softmax, o_proj) and ``LowRankProj``;
+* palu_tt/reference.py:14-92 -- ``PaluRefAttention`` (HF conventions: rotate_half RoPE on unpermuted
+  heads, latent caches, full K/V rebuild, GQA, causal softmax, o_proj), ``LowRankProj`` and the
+  low-rank Llama (``lowrank_llama``, on transformers' LlamaForCausalLM);
 * palu_tt/compress.py:12-23  -- per-head truncated SVD with Palu's balanced split;
 * tt-metal load_checkpoints.reverse_permute (HF head order -> Meta interleaved order), as the
   reference's audit restates it (docs/audit/reports/scripts/math_check.py:10-11);
@@ -30,6 +31,9 @@ How each function is pinned (tests/test_oracle.py):
   reverse_permute             -- equals the Meta interleave of HF's rotate_half halves
   svd_per_head                -- exact at full rank, error monotone in rank (ref tests/test_compress.py)
   gather_pages                -- element-by-element position -> (page, row) loop
+  LowRankProj / lowrank_llama -- LowRankProj == the dense U @ VT projection; at full-rank factors the
+                                 model equals transformers' dense LlamaForCausalLM on the same weights,
+                                 and its last-layer attention equals PaluRefAttention on the same input
 """
 import math
 from dataclasses import dataclass
@@ -263,6 +267,41 @@ class PaluRefAttention:
         scores = scores.masked_fill(~mask, float("-inf"))
         out = (torch.softmax(scores, dim=-1) @ V).transpose(1, 2).reshape(B, S, self.nh * self.hd)
         return out @ self.wo.T
+
+
+class LowRankProj(torch.nn.Module):
+    """x -> concat_h (x @ VT_h^T) @ U_h^T: a k_proj / v_proj drop-in that computes through the latent
+    (palu_tt/reference.py:58-71)."""
+
+    def __init__(self, VT: torch.Tensor, U: torch.Tensor):
+        super().__init__()
+        self.VT = VT.float()                                       # [n, r, dim]
+        self.U = U.float()                                         # [n, hd, r]
+
+    def forward(self, x):
+        lat = torch.einsum("...d,hrd->...hr", x, self.VT)
+        return torch.einsum("...hr,hdr->...hd", lat, self.U).flatten(-2)
+
+
+def lowrank_llama(cfg: dict, weights: dict, factors):
+    """fp32 transformers LlamaForCausalLM whose k_proj / v_proj are LowRankProj(factors[i]) (palu_tt/
+    reference.py:74-92, built from given weights instead of a checkpoint directory). cfg: dim, n_layers,
+    n_heads, n_kv_heads, head_dim, vocab_size, ffn_dim, norm_eps, rope_theta, rope_scaling. weights: the
+    HF state dict minus k_proj / v_proj (q_proj in HF head order)."""
+    import transformers
+    hf_cfg = transformers.LlamaConfig(
+        vocab_size=cfg["vocab_size"], hidden_size=cfg["dim"], intermediate_size=cfg["ffn_dim"],
+        num_hidden_layers=cfg["n_layers"], num_attention_heads=cfg["n_heads"], num_key_value_heads=cfg["n_kv_heads"],
+        head_dim=cfg["head_dim"], rms_norm_eps=cfg["norm_eps"], rope_theta=cfg["rope_theta"],
+        rope_scaling=cfg["rope_scaling"], max_position_embeddings=131072, tie_word_embeddings=False,
+        attn_implementation="eager")
+    model = transformers.LlamaForCausalLM(hf_cfg).float().eval()
+    missing, unexpected = model.load_state_dict({k: v.float() for k, v in weights.items()}, strict=False)
+    assert not unexpected and all(k.endswith(("k_proj.weight", "v_proj.weight")) for k in missing), (missing, unexpected)
+    for layer, f in zip(model.model.layers, factors):
+        layer.self_attn.k_proj = LowRankProj(f.k_VT, f.k_U)
+        layer.self_attn.v_proj = LowRankProj(f.v_VT, f.v_U)
+    return model
 
 
 # ------------------------------------------------------------------------------------------------

@@ -1,0 +1,97 @@
+"""End-to-end decoder (palu_tt.model.Transformer) against the fp32 low-rank Llama oracle, teacher-forced,
+as the reference's decode-fidelity harness compares models (palu_tt/decode_check.py:47-133: one prefill,
+then decode steps fed the same next tokens, PCC per step).
+
+The model is random-init with per-layer ranks that exercise every attention path at once: fused latent
+decode (r < head_dim), the full-rank K fast path and the stock full-KV path (r_k = r_v = head_dim), and
+rank padding to a multiple of 32. The oracle is transformers' LlamaForCausalLM in fp32 with k_proj / v_proj
+computed through the same factors (oracle.lowrank_llama), run once over prompt + teacher tokens. The GPU
+model runs in bf16, so the bar is on logits: PCC >= 0.999 per step and max-abs within 3% of the largest
+logit magnitude. The HIP-graph decode step must reproduce the eager step.
+"""
+import pytest
+import torch
+
+from oracle import palu_oracle as ref
+from palu_tt import model as pm
+
+pytestmark = pytest.mark.gpu
+
+
+def _hf_weights(sd, dense, n_layers):
+    """HF-named fp32 weights of the bf16 model (q_proj back in HF head order from the dense copy)."""
+    f = lambda k: sd[k].float().cpu()
+    w = {"model.embed_tokens.weight": f("tok_embeddings.weight"), "model.norm.weight": f("norm.weight"),
+         "lm_head.weight": f("output.weight")}
+    for i in range(n_layers):
+        p, q = f"layers.{i}.", f"model.layers.{i}."
+        w[q + "self_attn.q_proj.weight"] = dense[i][0]["q"].to(torch.bfloat16).float()
+        w[q + "self_attn.o_proj.weight"] = f(p + "attention.wo.weight")
+        w[q + "mlp.gate_proj.weight"] = f(p + "feed_forward.w1.weight")
+        w[q + "mlp.up_proj.weight"] = f(p + "feed_forward.w3.weight")
+        w[q + "mlp.down_proj.weight"] = f(p + "feed_forward.w2.weight")
+        w[q + "input_layernorm.weight"] = f(p + "attention_norm.weight")
+        w[q + "post_attention_layernorm.weight"] = f(p + "ffn_norm.weight")
+    return w
+
+
+def _check(out, exp, what):
+    out, exp = out.float().cpu(), exp.float()
+    for b in range(out.shape[0]):
+        p = ref.pcc(out[b], exp[b])
+        rel = ref.max_abs(out[b], exp[b]) / float(exp[b].abs().max())
+        assert p >= 0.999 and rel <= 0.03, f"{what} row {b}: pcc {p:.6f}, max-abs / max {rel:.4f}"
+
+
+@pytest.mark.parametrize("layout", ["tiled", "rows"])
+def test_decoder_teacher_forced_matches_lowrank_llama(gpu, layout):
+    pytest.importorskip("transformers")
+    args = pm.ModelArgs(dim=512, n_layers=3, n_heads=4, n_kv_heads=2, vocab_size=1000, ffn_dim=1024,
+                        max_seq_len=128, max_batch_size=2)
+    dense = []
+    sd = pm.random_palu_state_dict(args, [40, 64, 128], [32, 128, 72], gpu, seed=11, std=0.05, dense_out=dense)
+    assert args.palu.rank_k == [64, 64, 128] and args.palu.rank_v == [32, 128, 96]
+    hf_w = _hf_weights(sd, dense, args.n_layers)
+    cfg = dict(dim=args.dim, n_layers=args.n_layers, n_heads=args.n_heads, n_kv_heads=args.n_kv_heads,
+               head_dim=args.head_dim, vocab_size=args.vocab_size, ffn_dim=args.ffn_dim, norm_eps=args.norm_eps,
+               rope_theta=args.rope_theta, rope_scaling=args.rope_scaling)
+    oracle = ref.lowrank_llama(cfg, hf_w, [ref.Factors(lr.k_VT, lr.k_U, lr.v_VT, lr.v_U) for _, lr in dense])
+    model = pm.Transformer(args, sd, gpu, cache_layout=layout)
+
+    B, S, steps = 2, 45, 7
+    g = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, args.vocab_size, (B, S + steps), generator=g)
+    with torch.no_grad():
+        exp = oracle(ids).logits                                          # [B, S + steps, vocab]
+    _check(pm.prefill_all(model, ids[:, :S].to(gpu), users_per_chunk=1), exp[:, S - 1], "prefill")
+    for t in range(steps):
+        tok = ids[:, S + t].to(gpu)
+        pos = torch.full((B,), S + t, dtype=torch.int32, device=gpu)
+        eager = model.decode(tok, pos)
+        graph = model.decode_graph(tok, pos).clone()                      # rewrites the same cache rows
+        torch.cuda.synchronize()
+        _check(eager, exp[:, S + t], f"decode step {t}")
+        assert ref.cosine(graph.cpu(), eager.cpu()) >= 0.99999, f"graph replay differs at step {t}"
+
+
+def test_generate_greedy_is_consistent_with_decode(gpu):
+    """generate() (graph decode) returns, at every step, the argmax of the eager decode's logits for the
+    tokens it generated (teacher-forced replay on a fresh model built from the same seed)."""
+    mk = lambda: pm.ModelArgs(dim=512, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=512, ffn_dim=768,
+                              max_seq_len=96, max_batch_size=3)
+    a1 = mk()
+    m1 = pm.Transformer(a1, pm.random_palu_state_dict(a1, [48, 96], [64, 32], gpu, seed=5, std=0.1), gpu)
+    prompts = torch.randint(0, 512, (3, 33), generator=torch.Generator().manual_seed(8)).to(gpu)
+    out = pm.generate(m1, prompts, n_new=6)
+    assert out.shape == (3, 6)
+    a2 = mk()
+    m2 = pm.Transformer(a2, pm.random_palu_state_dict(a2, [48, 96], [64, 32], gpu, seed=5, std=0.1), gpu)
+    logits = pm.prefill_all(m2, prompts)
+    margins = []
+    for t in range(6):
+        top2 = logits.topk(2, dim=-1).values
+        margins.append(top2[:, 0] - top2[:, 1])
+        close = margins[-1] < 1e-2 * top2[:, 0].abs().clamp_min(1.0)       # near-ties may flip in bf16
+        assert torch.all((logits.argmax(-1) == out[:, t]) | close), f"step {t}"
+        if t < 5:
+            logits = m2.decode(out[:, t], torch.full((3,), 33 + t, dtype=torch.int32, device=gpu))

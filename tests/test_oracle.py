@@ -245,6 +245,74 @@ def test_identity_factor_layer_equals_transformers_llama_attention():
     torch.testing.assert_close(out, exp, atol=1e-4, rtol=1e-4)
 
 
+def _tiny_llama_weights(cfg, seed):
+    g = torch.Generator().manual_seed(seed)
+    d, f, hd, nh, nkv, V = cfg["dim"], cfg["ffn_dim"], cfg["head_dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["vocab_size"]
+    r = lambda *s: torch.randn(*s, generator=g) * 0.05
+    w = {"model.embed_tokens.weight": r(V, d), "model.norm.weight": 1 + r(d), "lm_head.weight": r(V, d)}
+    dense = []
+    for i in range(cfg["n_layers"]):
+        p = f"model.layers.{i}."
+        w.update({p + "self_attn.q_proj.weight": r(nh * hd, d), p + "self_attn.o_proj.weight": r(d, nh * hd),
+                  p + "mlp.gate_proj.weight": r(f, d), p + "mlp.up_proj.weight": r(f, d), p + "mlp.down_proj.weight": r(d, f),
+                  p + "input_layernorm.weight": 1 + r(d), p + "post_attention_layernorm.weight": 1 + r(d)})
+        dense.append((r(nkv * hd, d), r(nkv * hd, d)))
+    return w, dense
+
+
+_TINY = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, vocab_size=97, ffn_dim=384, norm_eps=1e-5,
+             rope_theta=THETA, rope_scaling=LLAMA3)
+
+
+def test_lowrank_proj_is_the_dense_factor_product():
+    g = torch.Generator().manual_seed(5)
+    VT, U = torch.randn(3, 8, 40, generator=g), torch.randn(3, 16, 8, generator=g)
+    x = torch.randn(2, 7, 40, generator=g)
+    dense = torch.cat([U[h] @ VT[h] for h in range(3)])                  # [3 * 16, 40]
+    torch.testing.assert_close(ref.LowRankProj(VT, U)(x), x @ dense.T, atol=1e-4, rtol=1e-4)
+
+
+def test_lowrank_llama_full_rank_equals_transformers_dense_model():
+    transformers = pytest.importorskip("transformers")
+    w, dense = _tiny_llama_weights(_TINY, seed=3)
+    nkv, hd = _TINY["n_kv_heads"], _TINY["head_dim"]
+    model = ref.lowrank_llama(_TINY, w, [ref.identity_factors(k, v, nkv, hd) for k, v in dense])
+    m2 = ref.lowrank_llama(_TINY, w, [ref.identity_factors(k, v, nkv, hd) for k, v in dense])
+    for i, (k, v) in enumerate(dense):                    # back to plain dense projections
+        att = m2.model.layers[i].self_attn
+        att.k_proj = torch.nn.Linear(_TINY["dim"], nkv * hd, bias=False)
+        att.v_proj = torch.nn.Linear(_TINY["dim"], nkv * hd, bias=False)
+        with torch.no_grad():
+            att.k_proj.weight.copy_(k); att.v_proj.weight.copy_(v)
+    ids = torch.randint(0, _TINY["vocab_size"], (2, 21), generator=torch.Generator().manual_seed(0))
+    with torch.no_grad():
+        a, b = model(ids).logits, m2(ids).logits
+    torch.testing.assert_close(a, b, atol=1e-4, rtol=1e-4)
+    assert isinstance(m2, transformers.LlamaForCausalLM)
+
+
+def test_lowrank_llama_attention_is_the_layer_oracle():
+    """The low-rank model's attention sublayer (inputs captured by a hook) equals PaluRefAttention with
+    the same truncated factors: ties the model-level oracle to the layer oracle."""
+    pytest.importorskip("transformers")
+    cfg = dict(_TINY, n_layers=1)
+    w, dense = _tiny_llama_weights(cfg, seed=4)
+    nkv, hd, nh = cfg["n_kv_heads"], cfg["head_dim"], cfg["n_heads"]
+    Uk, VTk = ref.svd_per_head(dense[0][0], nkv, 24)
+    Uv, VTv = ref.svd_per_head(dense[0][1], nkv, 40)
+    f = ref.Factors(VTk, Uk, VTv, Uv)
+    model = ref.lowrank_llama(cfg, w, [f])
+    seen = {}
+    att = model.model.layers[0].self_attn
+    att.register_forward_hook(lambda m, a, kw, out: seen.update(x=kw["hidden_states"], y=out[0]), with_kwargs=True)
+    ids = torch.randint(0, cfg["vocab_size"], (1, 17), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        model(ids)
+    layer = ref.PaluRefAttention(nh, nkv, hd, THETA, LLAMA3, w["model.layers.0.self_attn.q_proj.weight"],
+                                 w["model.layers.0.self_attn.o_proj.weight"], f)
+    torch.testing.assert_close(layer.forward(seen["x"], 0), seen["y"], atol=1e-4, rtol=1e-4)
+
+
 def test_layer_prefill_then_decode_equals_fresh_prefill():
     hidden, nh, nkv, hd = 256, 4, 2, 64
     W = _small_layer(seed=1)

@@ -177,10 +177,11 @@ def palu_layer_tensors(hf_attn: Dict[str, torch.Tensor], lr: LowRank, n_heads: i
     hidden = hf_attn["q"].shape[1]
     r_k, r_v, gs = lr.r_k, lr.r_v, lr.group_size
     hd = head_dim
-    wk_lat_pad = torch.zeros(n_kv_heads * hd, hidden)
-    wv_lat_pad = torch.zeros(n_kv_heads * hd, hidden)
+    dev = lr.k_VT.device
+    wk_lat_pad = torch.zeros(n_kv_heads * hd, hidden, device=dev)
+    wv_lat_pad = torch.zeros(n_kv_heads * hd, hidden, device=dev)
     fast_v = gs == 1 and r_v == hd
-    u_v_eff = torch.eye(hd).expand(n_kv_heads, hd, hd) if fast_v else lr.v_U     # [n_kv, hd, r_v]
+    u_v_eff = torch.eye(hd, device=dev).expand(n_kv_heads, hd, hd) if fast_v else lr.v_U     # [n_kv, hd, r_v]
     for h in range(n_kv_heads):
         g, hh = divmod(h, gs)
         slot = slice(g * gs * hd, g * gs * hd + r_k)
@@ -201,7 +202,7 @@ def palu_layer_tensors(hf_attn: Dict[str, torch.Tensor], lr: LowRank, n_heads: i
         rep = n_heads // n_kv_heads
         wo_heads = wo.reshape(wo.shape[0], n_heads, hd)                       # [hidden, n_q, hd]
         folded = torch.einsum("oqd,qdr->oqr", wo_heads, u_v_eff.repeat_interleave(rep, dim=0))
-        wo_fused = torch.zeros(wo.shape[0], n_heads, hd)
+        wo_fused = torch.zeros(wo.shape[0], n_heads, hd, device=dev)
         wo_fused[:, :, :r_v] = folded
         wo_fused = wo_fused.reshape(wo.shape[0], n_heads * hd)
     return {"wk_lat_pad": wk_lat_pad, "wv_lat_pad": wv_lat_pad, "u_k": u_k.contiguous(), "u_v": u_v,

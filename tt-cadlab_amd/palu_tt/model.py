@@ -1,0 +1,199 @@
+"""A Llama-3.1-shaped decoder whose attention layers are PaluAttention (latent caches, fused latent
+decode on MI355X): the end-to-end path of the reference's palu_tt/model.py + generate.py:53-62 and
+decode_check.py:47-133, on PyTorch-ROCm.
+
+Weights follow the tt_transformers state-dict names the reference loads (tok_embeddings, layers.{i}.
+attention_norm / attention.wq|wk|wv|wo / ffn_norm / feed_forward.w1|w2|w3, norm, output) plus the
+converter's layers.{i}.attention.palu.*. ``random_palu_state_dict`` builds a random-init model with
+per-layer M-LRD ranks (per-head SVD of random k/v projections, ranks padded up to a multiple of 32 as
+convert.load_palu_dir does), which is what the end-to-end benchmark uses.
+
+Decode runs every layer's projections as plain GEMMs (hipBLASLt through torch) and the attention core
+through the HIP library; ``Transformer.decode_graph`` captures a whole decode step in a HIP graph so a
+step is one graph launch.
+"""
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import torch
+import torch.nn.functional as F
+
+from palu_tt import compress, convert
+from palu_tt.attention import PaluAttention
+
+LLAMA3_SCALING = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                  "original_max_position_embeddings": 8192}
+
+
+@dataclass
+class ModelArgs:
+    dim: int = 4096
+    n_layers: int = 32
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    vocab_size: int = 128256
+    ffn_dim: int = 14336
+    norm_eps: float = 1e-5
+    rope_theta: float = 500000.0
+    rope_scaling: Optional[dict] = field(default_factory=lambda: dict(LLAMA3_SCALING))
+    max_seq_len: int = 2304
+    max_batch_size: int = 1
+    palu: Optional[convert.PaluConfig] = None
+
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(x.dtype)
+
+
+class Transformer(torch.nn.Module):
+    def __init__(self, args: ModelArgs, state_dict: dict, device, cache_layout: str = "tiled"):
+        super().__init__()
+        assert args.palu is not None, "ModelArgs.palu must hold the per-layer ranks (a PaluConfig)"
+        self.args = args
+        self.device = torch.device(device)
+        bf, dev = torch.bfloat16, self.device
+        t = lambda k: state_dict.pop(k).to(dev, bf)
+        self.tok_embeddings = t("tok_embeddings.weight")
+        self.norm_w = t("norm.weight")
+        self.output_t = t("output.weight").T.contiguous()
+        self.layers = []
+        for i in range(args.n_layers):
+            p = f"layers.{i}"
+            attn_sd = {k: v for k, v in state_dict.items() if k.startswith(f"{p}.attention.")}
+            attn = PaluAttention(dev, None, args, attn_sd, None, i, cache_layout=cache_layout)
+            for k in attn_sd:
+                state_dict.pop(k)
+            self.layers.append(dict(
+                attn=attn, attn_norm=t(f"{p}.attention_norm.weight"), ffn_norm=t(f"{p}.ffn_norm.weight"),
+                w13_t=torch.cat([t(f"{p}.feed_forward.w1.weight"), t(f"{p}.feed_forward.w3.weight")], 0).T.contiguous(),
+                w2_t=t(f"{p}.feed_forward.w2.weight").T.contiguous()))
+        self._graph = None
+
+    def _ffn(self, L, h):
+        gu = h @ L["w13_t"]
+        g, u = gu.chunk(2, dim=-1)
+        return (F.silu(g.float()) * u.float()).to(h.dtype) @ L["w2_t"]
+
+    @torch.no_grad()
+    def prefill(self, tokens: torch.Tensor, user_id: int = 0) -> torch.Tensor:
+        """tokens [U, S] for cache rows user_id .. user_id + U - 1 (positions 0 .. S-1); returns the
+        logits of the last position of every row, [U, vocab]."""
+        eps = self.args.norm_eps
+        h = self.tok_embeddings[tokens]                                  # [U, S, dim]
+        for L in self.layers:
+            h = h + L["attn"].forward_prefill(rms_norm(h, L["attn_norm"], eps), user_id=user_id)
+            h = h + self._ffn(L, rms_norm(h, L["ffn_norm"], eps))
+        return (rms_norm(h[:, -1], self.norm_w, eps) @ self.output_t).float()
+
+    @torch.no_grad()
+    def decode(self, tokens: torch.Tensor, current_pos: torch.Tensor) -> torch.Tensor:
+        """One decode step for all max_batch_size rows: tokens [B] at positions current_pos [B] (int32,
+        device); returns logits [B, vocab] fp32."""
+        eps = self.args.norm_eps
+        h = self.tok_embeddings[tokens]                                  # [B, dim]
+        for L in self.layers:
+            h = h + L["attn"].forward_decode(rms_norm(h, L["attn_norm"], eps), current_pos)
+            h = h + self._ffn(L, rms_norm(h, L["ffn_norm"], eps))
+        return (rms_norm(h, self.norm_w, eps) @ self.output_t).float()
+
+    @torch.no_grad()
+    def decode_graph(self, tokens: torch.Tensor, current_pos: torch.Tensor) -> torch.Tensor:
+        """decode() replayed from a HIP graph captured on first use; tokens and current_pos are copied into
+        the graph's static inputs (the caller's tensors may change between steps)."""
+        if self._graph is None:
+            self._tok = tokens.clone()
+            self._pos = current_pos.clone()
+            s = torch.cuda.Stream(self.device)
+            s.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(s):
+                self._graph_warm = self.decode(self._tok, self._pos)     # sets kernel attributes outside capture
+            torch.cuda.current_stream(self.device).wait_stream(s)
+            self._graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self._graph):
+                self._logits = self.decode(self._tok, self._pos)
+        self._tok.copy_(tokens)
+        self._pos.copy_(current_pos)
+        self._graph.replay()
+        return self._logits
+
+
+def draw_ranks(n_layers: int, seed: int, lo: int = 32, hi: int = 128, step: int = 8, mean: float = 64.0) -> List[int]:
+    """Per-layer ranks in [lo, hi] in steps of `step`, mean about `mean`: lo + step * Binomial(n, p) with
+    n = (hi - lo) / step and p chosen for the mean."""
+    g = torch.Generator().manual_seed(seed)
+    n = (hi - lo) // step
+    p = (mean - lo) / (hi - lo)
+    return [lo + step * int(torch.bernoulli(torch.full((n,), p), generator=g).sum()) for _ in range(n_layers)]
+
+
+def random_palu_state_dict(args: ModelArgs, ranks_k: List[int], ranks_v: List[int], device, seed: int = 0,
+                           std: float = 0.02, rank_multiple: int = 32, dense_out: Optional[list] = None) -> dict:
+    """Random-init weights N(0, std) generated on `device`, and per-layer per-head SVD factors of the
+    k / v projections at the given ranks (on `device` too), zero-padded to a multiple of rank_multiple
+    (convert.load_palu_dir's padding). Every tensor is left in bf16 on `device`. Sets args.palu. With
+    dense_out, every layer's fp32 projections (HF head order) and padded factors are appended to it as
+    (W, LowRank) on the host."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    bf = torch.bfloat16
+    randn = lambda *s: torch.randn(*s, device=device, generator=g) * std
+    hd, nh, nkv, dim = args.head_dim, args.n_heads, args.n_kv_heads, args.dim
+    sd = {"tok_embeddings.weight": randn(args.vocab_size, dim).to(bf), "output.weight": randn(args.vocab_size, dim).to(bf),
+          "norm.weight": torch.ones(dim, dtype=bf, device=device)}
+    pad = lambda r: int(math.ceil(r / rank_multiple) * rank_multiple)
+    rk_pad, rv_pad = [], []
+    for i in range(args.n_layers):
+        W = {"q": randn(nh * hd, dim), "k": randn(nkv * hd, dim), "v": randn(nkv * hd, dim), "o": randn(dim, nh * hd)}
+        fac = []
+        for w, r in ((W["k"], ranks_k[i]), (W["v"], ranks_v[i])):
+            U, VT = compress.svd_per_head(w, nkv, r)
+            rp = min(pad(r), hd)
+            fac += [F.pad(VT, (0, 0, 0, rp - r)), F.pad(U, (0, rp - r))]
+        lr = convert.LowRank(*fac)
+        rk_pad.append(lr.r_k)
+        rv_pad.append(lr.r_v)
+        p = f"layers.{i}"
+        sd[f"{p}.attention.wq.weight"] = convert.reverse_permute(W["q"], nh, nh * hd, dim).to(bf)
+        sd[f"{p}.attention.wo.weight"] = W["o"].to(bf)
+        for name, t in convert.palu_layer_tensors(W, lr, nh, nkv, hd).items():
+            sd[f"{p}.attention.palu.{name}"] = t.to(bf)
+        if dense_out is not None:
+            dense_out.append(({k: v.cpu() for k, v in W.items()},
+                              convert.LowRank(*[t.cpu() for t in (lr.k_VT, lr.k_U, lr.v_VT, lr.v_U)])))
+        del W, lr, fac
+        sd[f"{p}.attention_norm.weight"] = torch.ones(dim, dtype=bf, device=device)
+        sd[f"{p}.ffn_norm.weight"] = torch.ones(dim, dtype=bf, device=device)
+        sd[f"{p}.feed_forward.w1.weight"] = randn(args.ffn_dim, dim).to(bf)
+        sd[f"{p}.feed_forward.w3.weight"] = randn(args.ffn_dim, dim).to(bf)
+        sd[f"{p}.feed_forward.w2.weight"] = randn(dim, args.ffn_dim).to(bf)
+    args.palu = convert.PaluConfig(rank_k=rk_pad, rank_v=rv_pad, cache_id=f"random-seed{seed}")
+    return sd
+
+
+@torch.no_grad()
+def prefill_all(model: Transformer, prompts: torch.Tensor, users_per_chunk: int = 4) -> torch.Tensor:
+    """Prefill every cache row from prompts [B, S], users_per_chunk rows per pass (bounds the prefill
+    activations); returns the last-position logits [B, vocab]."""
+    outs = [model.prefill(prompts[u:u + users_per_chunk], user_id=u)
+            for u in range(0, prompts.shape[0], users_per_chunk)]
+    return torch.cat(outs)
+
+
+@torch.no_grad()
+def generate(model: Transformer, prompts: torch.Tensor, n_new: int, use_graph: bool = True):
+    """Greedy decode (reference generate.py:53-62): prefill every row's prompt, then n_new steps of
+    argmax sampling. prompts [B, S] with B == max_batch_size. Returns the generated ids [B, n_new]."""
+    B, S = prompts.shape
+    assert B == model.args.max_batch_size and S + n_new <= model.args.max_seq_len
+    tok = prefill_all(model, prompts).argmax(-1)
+    out = [tok]
+    pos = torch.full((B,), S, dtype=torch.int32, device=model.device)
+    step = model.decode_graph if use_graph else model.decode
+    for t in range(n_new - 1):
+        logits = step(tok, pos)
+        tok = logits.argmax(-1)
+        out.append(tok)
+        pos += 1
+    return torch.stack(out, dim=1)
