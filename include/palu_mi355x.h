@@ -81,8 +81,10 @@ size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_di
  *   rot_step, trans_mat              the reference's Phase 2 constants; optional together. They are
  *                                    validated as the reference does and otherwise unused: this kernel
  *                                    always rotates block-relative (32 positions) from cs_tab.
- *   u_v      [n_kv, r_v, 128] bf16   in-kernel V rebuild for grouped latents (not built yet: returns
- *                                    PALU_EUNSUPPORTED)
+ *   u_v      [n_kv, r_v, 128] bf16   optional: in-kernel V rebuild (G-LRD). The output is then
+ *                                    softmax(q K^T) (v_latent u_v[h]), 128 wide (head_dim_v == 128);
+ *                                    needs PALU_LAYOUT_TILED, r_k and r_v in 32 .. 512 (multiples of
+ *                                    32), and is not built for the paged entry point (PALU_EUNSUPPORTED)
  *   scale                            softmax scale (the reference passes head_dim^-0.5)
  *   heads_per_core, rot_mode, table_mcast, k_chunk
  *                                    the reference's Tensix work-split switches; validated, and
