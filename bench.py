@@ -242,8 +242,8 @@ def measure_glrd(dev, steps, warmup):
         u_v = (torch.randn(NKV, r_v, HD, generator=g) / r_v ** 0.5)[None].to(dev, torch.bfloat16).contiguous()
         w_rot = fused.w_rot_from_u_k(u_k)[None].to(dev, torch.bfloat16).contiguous()
         out = torch.empty(1, B, NQ, HD, dtype=torch.bfloat16, device=dev)
-        ws = torch.empty(max(fused._native.load().palu_decode_workspace_bytes(B, NKV, S, HD), 1), dtype=torch.uint8,
-                         device=dev)
+        ws = torch.empty(max(fused._native.load().palu_glrd_workspace_bytes(B, NQ, NKV, ng, S, r_v), 1),
+                         dtype=torch.uint8, device=dev)
 
         def step(l):
             k, v = layers[l]

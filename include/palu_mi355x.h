@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define PALU_ABI_VERSION 5
+#define PALU_ABI_VERSION 6
 
 #define PALU_OK 0
 #define PALU_EINVAL 1       /* arguments outside the op's envelope */
@@ -58,6 +58,13 @@ int palu_abi_version(void);
 /* Bytes of fp32 workspace palu_sdpa_decode / palu_flash_decode need for these shapes (0 when the
  * sequence is not split across workgroups). head_dim_v is the output width of the call. */
 size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_dim_v);
+
+/* Bytes of workspace palu_sdpa_decode needs with u_v (grouped latents, in-kernel V rebuild): the fp32
+ * partial scores of both head-dim halves ([B, n_q, 2, S]) plus the per-split latent PV partials. The
+ * grouped path runs three kernels on the stream and passes data between them through this buffer.
+ * No counterpart in the reference (its op keeps these in device L1); needed because the MI355X path
+ * splits the op into passes. */
+size_t palu_glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_v);
 
 /* Fused latent flash-decode. Replaces ttnn.transformer.palu_sdpa_decode, the op PaluAttention's decode
  * branch calls (palu_tt/attention.py:632-639; interface in

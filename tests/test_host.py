@@ -196,6 +196,15 @@ def test_workspace_query(lib):
     assert lib.palu_decode_workspace_bytes(0, 8, 8192, 64) == 0
 
 
+def test_grouped_latent_workspace_query(lib):
+    # partial scores of both head-dim halves ([B, n_q, 2, S] fp32) plus the PV partials
+    B, nq, nkv, G, S, rv = 16, 32, 8, 2, 16384, 512
+    ws = lib.palu_glrd_workspace_bytes(B, nq, nkv, G, S, rv)
+    assert ws >= B * nq * 2 * S * 4 and ws < B * nq * 2 * S * 4 + B * nq * 129 * (rv + 4) * 4 + 512
+    assert lib.palu_glrd_workspace_bytes(B, nq, nkv, 3, S, rv) == 0          # groups must divide the KV heads
+    assert lib.palu_glrd_workspace_bytes(0, nq, nkv, G, S, rv) == 0
+
+
 _FAKE = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced: validation fails before any use
 
 

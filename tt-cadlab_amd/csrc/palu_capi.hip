@@ -269,6 +269,10 @@ size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_di
   return ws_bytes(batch * n_kv, p.n_splits, head_dim_v);
 }
 
+size_t palu_glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_v) {
+  return glrd_workspace_bytes(batch, n_q, n_kv, n_groups, seq_len, r_v);
+}
+
 int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab, const void* v_latent,
                      int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step, const void* trans_mat,
                      const void* u_v, float scale, int heads_per_core, int rot_mode, int table_mcast, int k_chunk,

@@ -14,7 +14,7 @@ from palu_tt._build import library_path
 
 PALU_OK, PALU_EINVAL, PALU_EUNSUPPORTED, PALU_EHIP = 0, 1, 2, 3
 DTYPE_F32, DTYPE_BF16 = 0, 1
-ABI_VERSION = 5
+ABI_VERSION = 6
 LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_TILED_V = 0, 1, 2
 
 _vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
@@ -23,6 +23,7 @@ _SIGNATURES = {
     "palu_last_error": (ctypes.c_char_p, []),
     "palu_abi_version": (_i, []),
     "palu_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "palu_glrd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "palu_sdpa_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i,
                               _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "palu_flash_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),

@@ -190,6 +190,16 @@ def _workspace(batch: int, n_kv: int, seq_len: int, width: int, device, workspac
     return torch.empty(need, dtype=torch.uint8, device=device), need
 
 
+def _glrd_workspace(batch: int, n_q: int, n_kv: int, n_groups: int, seq_len: int, r_v: int, device, workspace):
+    """Workspace of the grouped-latent path: partial scores and latent PV partials between its passes."""
+    need = _native.load().palu_glrd_workspace_bytes(batch, n_q, n_kv, n_groups, seq_len, r_v)
+    if workspace is not None:
+        _require(workspace.is_cuda and workspace.numel() * workspace.element_size() >= need,
+                 f"workspace must hold {need} bytes on the GPU (palu_glrd_workspace_bytes)")
+        return workspace, workspace.numel() * workspace.element_size()
+    return torch.empty(max(need, 1), dtype=torch.uint8, device=device), need
+
+
 def _cur_pos(cur_pos_tensor: torch.Tensor, batch: int, device) -> torch.Tensor:
     _require(isinstance(cur_pos_tensor, torch.Tensor), "cur_pos_tensor must be a torch.Tensor")
     cp = cur_pos_tensor.reshape(-1)
@@ -289,7 +299,10 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
     else:
         _as_dev(out, "out", out_dtype, dev)
         _require(tuple(out.shape) == (1, B, n_q, width), f"out must be [1, {B}, {n_q}, {width}]")
-    ws, ws_bytes = _workspace(B, n_kv, S, max(width, 1), dev, workspace)
+    if uv is not None and pt is None:
+        ws, ws_bytes = _glrd_workspace(B, n_q, n_kv, n_groups, S, r_v, dev, workspace)
+    else:
+        ws, ws_bytes = _workspace(B, n_kv, S, max(width, 1), dev, workspace)
     lib = _native.load()
     sc = float(HEAD_DIM ** -0.5 if scale is None else scale)
     if pt is None:
