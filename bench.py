@@ -57,9 +57,9 @@ def parse():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the paged mixed-rank and grouped-latent (G-LRD) measurements")
     ap.add_argument("--cpu-rows", type=int, default=2, help="batch rows of the CPU baseline sample")
-    ap.add_argument("--e2e", action="store_true",
-                    help="also run the end-to-end 32-layer decoder (batch 64, 2048-token prompts, greedy decode) "
-                         "with Palu ranks and with stock full-rank K/V, reporting decode tokens/s")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the end-to-end 32-layer decoder (batch 64, 2048-token prompts, greedy decode) with "
+                         "Palu ranks and with stock full-rank K/V")
     ap.add_argument("--e2e-batch", type=int, default=64)
     ap.add_argument("--e2e-prompt", type=int, default=2048)
     ap.add_argument("--e2e-tokens", type=int, default=256, help="greedy tokens generated per row")
@@ -439,7 +439,7 @@ def main():
             torch.cuda.empty_cache()
         res["paged_mixed_ranks"] = measure_paged(dev, max(a.steps // 4, 10), max(a.warmup // 4, 5))
         res["glrd"] = measure_glrd(dev, max(a.steps // 8, 10), max(a.warmup // 8, 3))
-    if a.e2e:
+    if not a.no_e2e:
         if wl.get("layers") is not None:
             wl["layers"] = None
             torch.cuda.empty_cache()

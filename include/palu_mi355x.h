@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define PALU_ABI_VERSION 6
+#define PALU_ABI_VERSION 7
 
 #define PALU_OK 0
 #define PALU_EINVAL 1       /* arguments outside the op's envelope */
@@ -162,6 +162,34 @@ int palu_latent_append(void* cache, const void* new_rows, const int32_t* update_
 int palu_latent_append_paged(void* cache_pages, const void* new_rows, const int32_t* update_idxs,
                              const int32_t* page_table, int batch, int n_groups, int num_pages, int page_size,
                              int max_pages_per_seq, int width, int cache_layout, palu_stream_t stream);
+
+/* ---- Decoder-step helpers ---------------------------------------------------------------------------
+ * No counterpart in the reference's op interface. palu_tt.attention and palu_tt.model use them to fuse
+ * the elementwise work around the decode op, which the reference runs as separate ttnn ops
+ * (palu_tt/attention.py:585-733: rotary_embedding_llama, the latent slices, paged_update_cache; the
+ * tt_transformers decoder's RMSNorm and SwiGLU MLP). bf16 tensors, fp32 arithmetic. */
+
+/* Latent append from a strided source: cache[b, g, update_idxs[b], :] = src[b * src_batch_stride +
+ * g * src_group_stride + 0 .. width - 1] (element strides, multiples of 8), e.g. the latent columns of
+ * a fused QKV projection's output; everything else as palu_latent_append. */
+int palu_latent_append_strided(void* cache, const void* src, long long src_batch_stride, long long src_group_stride,
+                               const int32_t* update_idxs, int batch, int n_groups, int seq_len, int width,
+                               int cache_layout, palu_stream_t stream);
+
+/* Per row of [rows, dim]: h = x + res (res may be NULL: h = x), rounded to bf16 and stored to h_out when
+ * h_out is not NULL; y_out = h * rsqrt(mean(h^2) + eps) * weight. dim a multiple of 8, at most 8192. */
+int palu_rmsnorm(const void* x, const void* res, void* h_out, void* y_out, const void* weight, int rows, int dim,
+                 float eps, palu_stream_t stream);
+
+/* out[r][f] = silu(gu[r][f]) * gu[r][ffn + f] for gu [rows, 2 ffn], out [rows, ffn]; ffn a multiple of 8. */
+int palu_swiglu(const void* gu, void* out, int rows, int ffn, palu_stream_t stream);
+
+/* Meta-interleaved RoPE of `heads` 128-wide heads per row at the row's position:
+ * dst[b, h, :] = rotate(src[b * src_row_stride + h * 128 .. +127], pos[b]), pairs (2i, 2i+1) ->
+ * (x0 c - x1 s, x1 c + x0 s) with c = cos_table[p][2i], s = sin_table[p][2i] (fp32 [table_rows, 128],
+ * fused.cos_sin_tables). Positions outside the table are clamped into it. dst is [rows, heads, 128]. */
+int palu_rope_rows(const void* src, long long src_row_stride, void* dst, const int32_t* pos, const float* cos_table,
+                   const float* sin_table, int table_rows, int rows, int heads, palu_stream_t stream);
 
 #ifdef __cplusplus
 }

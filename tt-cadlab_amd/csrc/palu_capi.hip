@@ -48,25 +48,14 @@ int check_pages(const int32_t* page_table, int num_pages, int page_size, int max
   return PALU_OK;
 }
 
-// Offset (elements) of width-index k of position p inside one (b, g) stream of width R, K-tile order.
-__device__ __forceinline__ long long tiled_k_offset(int p, int k, int R) {
-  const int t = p & 31, c = (t >> 2) & 1, nn = ((t >> 3) << 2) | (t & 3);
-  const int kb = k >> 5, gg = (k >> 3) & 3;
-  return (long long)(p >> 5) * (32 * R) + ((c * (R >> 5) + kb) * 64 + 16 * gg + nn) * 8 + (k & 7);
-}
-
-// V-tile order: tile mt = k / 16, slot 16 * (t / 8) + k % 16, element t % 8 (t = p % 32).
-__device__ __forceinline__ long long tiled_v_offset(int p, int k, int R) {
-  const int t = p & 31;
-  return (long long)(p >> 5) * (32 * R) + ((k >> 4) * 64 + 16 * (t >> 3) + (k & 15)) * 8 + (t & 7);
-}
-
-// Latent append: cache[b, g, idx[b], :] = rows[b, g, :]; each thread moves 8 consecutive values. A
+// Latent append: cache[b, g, idx[b], :] = rows[b * sb + g * sg + 0 .. width - 1]; each thread moves 8
+// consecutive values. A
 // contiguous cache is [B, G, S, width]; a paged pool is [n_pages, G, S, width] with S the page size,
 // and position p of row b lives on page page_table[b * pt_stride + p / S] (ids outside the pool skip
 // the row).
 template <int LAYOUT, bool PAGED>
-__global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const __bf16* rows, const int32_t* idx,
+__global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const __bf16* rows, long long sb,
+                                                          long long sg, const int32_t* idx,
                                                           const int32_t* page_table, int pt_stride, int n_pages,
                                                           int B, int G, int S, int width) {
   const int vec = width / 8;
@@ -87,7 +76,7 @@ __global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const _
       if (p < 0 || p >= S) continue;
       slab = bg;
     }
-    const bf16x8 x = *reinterpret_cast<const bf16x8*>(rows + bg * width + 8 * v);
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(rows + b * sb + gi * sg + 8 * v);
     __bf16* stream = cache + slab * S * width;
     if constexpr (LAYOUT == PALU_LAYOUT_ROWS) {
       *reinterpret_cast<bf16x8*>(stream + (long long)p * width + 8 * v) = x;
@@ -103,20 +92,22 @@ __global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const _
 
 template <bool PAGED>
 int launch_append(void* cache, const void* new_rows, const int32_t* update_idxs, const int32_t* page_table,
-                  int pt_stride, int n_pages, int batch, int n_groups, int S, int width, int layout, hipStream_t stream) {
+                  int pt_stride, int n_pages, int batch, int n_groups, int S, int width, int layout, hipStream_t stream,
+                  long long sb = -1, long long sg = -1) {
+  if (sb < 0) { sb = (long long)n_groups * width; sg = width; }
   const long long total = (long long)batch * n_groups * (width / 8);
   int blocks = (int)((total + 255) / 256);
   if (blocks > 4096) blocks = 4096;
   auto* c = static_cast<__bf16*>(cache);
   auto* r = static_cast<const __bf16*>(new_rows);
   if (layout == PALU_LAYOUT_TILED)
-    hipLaunchKernelGGL((palu_append_kernel<PALU_LAYOUT_TILED, PAGED>), dim3(blocks), dim3(256), 0, stream, c, r,
+    hipLaunchKernelGGL((palu_append_kernel<PALU_LAYOUT_TILED, PAGED>), dim3(blocks), dim3(256), 0, stream, c, r, sb, sg,
                        update_idxs, page_table, pt_stride, n_pages, batch, n_groups, S, width);
   else if (layout == PALU_LAYOUT_TILED_V)
-    hipLaunchKernelGGL((palu_append_kernel<PALU_LAYOUT_TILED_V, PAGED>), dim3(blocks), dim3(256), 0, stream, c, r,
+    hipLaunchKernelGGL((palu_append_kernel<PALU_LAYOUT_TILED_V, PAGED>), dim3(blocks), dim3(256), 0, stream, c, r, sb, sg,
                        update_idxs, page_table, pt_stride, n_pages, batch, n_groups, S, width);
   else
-    hipLaunchKernelGGL((palu_append_kernel<PALU_LAYOUT_ROWS, PAGED>), dim3(blocks), dim3(256), 0, stream, c, r,
+    hipLaunchKernelGGL((palu_append_kernel<PALU_LAYOUT_ROWS, PAGED>), dim3(blocks), dim3(256), 0, stream, c, r, sb, sg,
                        update_idxs, page_table, pt_stride, n_pages, batch, n_groups, S, width);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "append kernel launch: %s", hipGetErrorString(e));
@@ -372,6 +363,20 @@ int palu_latent_append(void* cache, const void* new_rows, const int32_t* update_
     return rc;
   return launch_append<false>(cache, new_rows, update_idxs, nullptr, 0, 0, batch, n_groups, seq_len, width,
                               cache_layout, stream);
+}
+
+int palu_latent_append_strided(void* cache, const void* src, long long src_batch_stride, long long src_group_stride,
+                               const int32_t* update_idxs, int batch, int n_groups, int seq_len, int width,
+                               int cache_layout, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  if (int rc = check_append(cache, src, update_idxs, batch, n_groups, seq_len, width, cache_layout,
+                            "palu_latent_append_strided"))
+    return rc;
+  if (src_batch_stride < 0 || src_group_stride < 0 || src_batch_stride % 8 || src_group_stride % 8)
+    return fail(PALU_EINVAL, "palu_latent_append_strided: source strides must be non-negative multiples of 8, got %lld "
+                             "and %lld", src_batch_stride, src_group_stride);
+  return launch_append<false>(cache, src, update_idxs, nullptr, 0, 0, batch, n_groups, seq_len, width, cache_layout,
+                              stream, src_batch_stride, src_group_stride);
 }
 
 int palu_latent_append_paged(void* cache_pages, const void* new_rows, const int32_t* update_idxs,

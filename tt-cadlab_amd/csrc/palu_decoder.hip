@@ -1,0 +1,169 @@
+// Decoder-step helpers: the elementwise work around the decode op, fused so that one Llama decoder layer
+// is a handful of launches (palu_tt.model and palu_tt.attention). They have no counterpart in the
+// reference's op interface; the arithmetic is the reference model's (tt_transformers' RMSNorm, SwiGLU
+// MLP and rotary_embedding_llama on Meta-interleaved heads, as palu_tt/attention.py:585-733 and
+// palu_tt/model.py drive them), computed in fp32 with bf16 inputs and outputs.
+#include "palu_kernel.h"
+
+namespace {
+
+__device__ __forceinline__ float bf(const __bf16 x) { return (float)x; }
+
+// One workgroup per row: h = x (+ res), stored when h_out is given; y = h * rsqrt(mean(h^2) + eps) * w.
+// Each thread holds up to RMS_VEC vectors of 8 elements in registers between the two passes.
+constexpr int RMS_THREADS = 256;
+constexpr int RMS_VEC = 4;               // dim <= 256 * 8 * 4 = 8192
+
+__global__ __launch_bounds__(RMS_THREADS) void palu_rmsnorm_kernel(const __bf16* x, const __bf16* res, __bf16* h_out,
+                                                                   __bf16* y_out, const __bf16* w, int dim, float eps) {
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const __bf16* xr = x + (long long)row * dim;
+  const __bf16* rr = res ? res + (long long)row * dim : nullptr;
+  float v[RMS_VEC][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < RMS_VEC; ++i) {
+    const int e = (tid + i * RMS_THREADS) * 8;
+    if (e < dim) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(xr + e);
+      bf16x8 hv;
+      if (rr) {
+        const bf16x8 c = *reinterpret_cast<const bf16x8*>(rr + e);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hv[j] = (__bf16)(bf(a[j]) + bf(c[j]));   // bf16 residual stream
+      } else {
+        hv = a;
+      }
+      if (h_out) *reinterpret_cast<bf16x8*>(h_out + (long long)row * dim + e) = hv;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[i][j] = bf(hv[j]);
+        ss += v[i][j] * v[i][j];
+      }
+    }
+  }
+  __shared__ float part[RMS_THREADS / 64];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < RMS_THREADS / 64; ++k) tot += part[k];
+  const float r = rsqrtf(tot / (float)dim + eps);
+#pragma unroll
+  for (int i = 0; i < RMS_VEC; ++i) {
+    const int e = (tid + i * RMS_THREADS) * 8;
+    if (e < dim) {
+      const bf16x8 wv = *reinterpret_cast<const bf16x8*>(w + e);
+      bf16x8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = (__bf16)((v[i][j] * r) * bf(wv[j]));
+      *reinterpret_cast<bf16x8*>(y_out + (long long)row * dim + e) = o;
+    }
+  }
+}
+
+// out[r][f] = silu(g) * u with g = gu[r][f], u = gu[r][ffn + f]; 8 elements per thread.
+__global__ __launch_bounds__(256) void palu_swiglu_kernel(const __bf16* gu, __bf16* out, int rows, int ffn) {
+  const long long vecs = (long long)rows * (ffn / 8);
+  for (long long e = blockIdx.x * 256LL + threadIdx.x; e < vecs; e += (long long)gridDim.x * 256) {
+    const int r = (int)(e / (ffn / 8)), f = (int)(e % (ffn / 8)) * 8;
+    const bf16x8 g = *reinterpret_cast<const bf16x8*>(gu + (long long)r * 2 * ffn + f);
+    const bf16x8 u = *reinterpret_cast<const bf16x8*>(gu + (long long)r * 2 * ffn + ffn + f);
+    bf16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float gv = bf(g[j]);
+      o[j] = (__bf16)((gv / (1.f + __expf(-gv))) * bf(u[j]));
+    }
+    *reinterpret_cast<bf16x8*>(out + (long long)r * ffn + f) = o;
+  }
+}
+
+// dst[b][h][:] = Meta-interleaved RoPE of src[b * stride + h * 128 ...] at position pos[b] (clamped into
+// the table): pairs (2i, 2i+1) -> (x0 c - x1 s, x1 c + x0 s) with c = cos[p][2i], s = sin[p][2i].
+// One thread per (row, head, 8 dims).
+__global__ __launch_bounds__(256) void palu_rope_rows_kernel(const __bf16* src, long long stride, __bf16* dst,
+                                                             const int32_t* pos, const float* cos_t, const float* sin_t,
+                                                             int table_rows, int rows, int heads) {
+  const long long vecs = (long long)rows * heads * (HD / 8);
+  for (long long e = blockIdx.x * 256LL + threadIdx.x; e < vecs; e += (long long)gridDim.x * 256) {
+    const int d8 = (int)(e % (HD / 8)) * 8;
+    const long long bh = e / (HD / 8);
+    const int h = (int)(bh % heads), b = (int)(bh / heads);
+    int p = pos[b];
+    p = p < 0 ? 0 : (p >= table_rows ? table_rows - 1 : p);
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(src + b * stride + (long long)h * HD + d8);
+    const float4 c0 = *reinterpret_cast<const float4*>(cos_t + (long long)p * HD + d8);
+    const float4 c1 = *reinterpret_cast<const float4*>(cos_t + (long long)p * HD + d8 + 4);
+    const float4 s0 = *reinterpret_cast<const float4*>(sin_t + (long long)p * HD + d8);
+    const float4 s1 = *reinterpret_cast<const float4*>(sin_t + (long long)p * HD + d8 + 4);
+    const float c[4] = {c0.x, c0.z, c1.x, c1.z}, s[4] = {s0.x, s0.z, s1.x, s1.z};
+    bf16x8 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x0 = bf(x[2 * i]), x1 = bf(x[2 * i + 1]);
+      o[2 * i] = (__bf16)(x0 * c[i] - x1 * s[i]);
+      o[2 * i + 1] = (__bf16)(x1 * c[i] + x0 * s[i]);
+    }
+    *reinterpret_cast<bf16x8*>(dst + bh * HD + d8) = o;
+  }
+}
+
+int grid_for(long long work) {
+  long long blocks = (work + 255) / 256;
+  return (int)(blocks > 8192 ? 8192 : (blocks < 1 ? 1 : blocks));
+}
+
+inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int launched(const char* what) {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? PALU_OK : fail(PALU_EHIP, "%s launch: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace
+
+extern "C" {
+
+int palu_rmsnorm(const void* x, const void* res, void* h_out, void* y_out, const void* weight, int rows, int dim,
+                 float eps, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  if (!x || !y_out || !weight) return fail(PALU_EINVAL, "palu_rmsnorm: a required pointer is null");
+  if (rows <= 0 || dim <= 0 || dim % 8 != 0 || dim > RMS_THREADS * 8 * RMS_VEC)
+    return fail(PALU_EINVAL, "palu_rmsnorm: dim must be a multiple of 8 up to %d, got %d", RMS_THREADS * 8 * RMS_VEC, dim);
+  if (!a16(x) || !a16(y_out) || !a16(weight) || (res && !a16(res)) || (h_out && !a16(h_out)))
+    return fail(PALU_EINVAL, "palu_rmsnorm: 16-byte alignment required");
+  hipLaunchKernelGGL(palu_rmsnorm_kernel, dim3(rows), dim3(RMS_THREADS), 0, stream, static_cast<const __bf16*>(x),
+                     static_cast<const __bf16*>(res), static_cast<__bf16*>(h_out), static_cast<__bf16*>(y_out),
+                     static_cast<const __bf16*>(weight), dim, eps);
+  return launched("palu_rmsnorm");
+}
+
+int palu_swiglu(const void* gu, void* out, int rows, int ffn, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  if (!gu || !out) return fail(PALU_EINVAL, "palu_swiglu: a required pointer is null");
+  if (rows <= 0 || ffn <= 0 || ffn % 8 != 0) return fail(PALU_EINVAL, "palu_swiglu: ffn must be a multiple of 8, got %d", ffn);
+  if (!a16(gu) || !a16(out)) return fail(PALU_EINVAL, "palu_swiglu: 16-byte alignment required");
+  hipLaunchKernelGGL(palu_swiglu_kernel, dim3(grid_for((long long)rows * (ffn / 8))), dim3(256), 0, stream,
+                     static_cast<const __bf16*>(gu), static_cast<__bf16*>(out), rows, ffn);
+  return launched("palu_swiglu");
+}
+
+int palu_rope_rows(const void* src, long long src_row_stride, void* dst, const int32_t* pos, const float* cos_table,
+                   const float* sin_table, int table_rows, int rows, int heads, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  if (!src || !dst || !pos || !cos_table || !sin_table) return fail(PALU_EINVAL, "palu_rope_rows: a required pointer is null");
+  if (rows <= 0 || heads <= 0 || table_rows <= 0) return fail(PALU_EINVAL, "palu_rope_rows: sizes must be positive");
+  if (src_row_stride < (long long)heads * HD || src_row_stride % 8 != 0)
+    return fail(PALU_EINVAL, "palu_rope_rows: row stride %lld must be a multiple of 8 and hold %d heads", src_row_stride, heads);
+  if (!a16(src) || !a16(dst) || !a16(cos_table) || !a16(sin_table))
+    return fail(PALU_EINVAL, "palu_rope_rows: 16-byte alignment required");
+  hipLaunchKernelGGL(palu_rope_rows_kernel, dim3(grid_for((long long)rows * heads * (HD / 8))), dim3(256), 0, stream,
+                     static_cast<const __bf16*>(src), src_row_stride, static_cast<__bf16*>(dst), pos, cos_table,
+                     sin_table, table_rows, rows, heads);
+  return launched("palu_rope_rows");
+}
+
+}  // extern "C"

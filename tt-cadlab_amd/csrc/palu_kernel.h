@@ -89,6 +89,7 @@ struct DecodeArgs {
 
 // Error reporting (defined in palu_capi.hip): formats the message for palu_last_error, returns code.
 int fail(int code, const char* fmt, ...);
+extern thread_local char g_err[1024];
 
 // Waves per workgroup: 8 (two per SIMD) where the kernel fits 256 registers, else 4 (one per SIMD,
 // which lets the compiler use the full 512-entry register file instead of spilling).
@@ -138,6 +139,19 @@ size_t glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int seq_
 namespace {
 
 using namespace palu;
+
+// Offset (elements) of width-index k of position p inside one (b, g) stream of width R, K-tile order.
+__device__ __forceinline__ long long tiled_k_offset(int p, int k, int R) {
+  const int t = p & 31, c = (t >> 2) & 1, nn = ((t >> 3) << 2) | (t & 3);
+  const int kb = k >> 5, gg = (k >> 3) & 3;
+  return (long long)(p >> 5) * (32 * R) + ((c * (R >> 5) + kb) * 64 + 16 * gg + nn) * 8 + (k & 7);
+}
+
+// V-tile order: tile mt = k / 16, slot 16 * (t / 8) + k % 16, element t % 8 (t = p % 32).
+__device__ __forceinline__ long long tiled_v_offset(int p, int k, int R) {
+  const int t = p & 31;
+  return (long long)(p >> 5) * (32 * R) + ((k >> 4) * 64 + 16 * (t >> 3) + (k & 15)) * 8 + (t & 7);
+}
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

@@ -14,10 +14,10 @@ from palu_tt._build import library_path
 
 PALU_OK, PALU_EINVAL, PALU_EUNSUPPORTED, PALU_EHIP = 0, 1, 2, 3
 DTYPE_F32, DTYPE_BF16 = 0, 1
-ABI_VERSION = 6
+ABI_VERSION = 7
 LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_TILED_V = 0, 1, 2
 
-_vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+_vp, _i, _f, _sz, _ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_longlong
 
 _SIGNATURES = {
     "palu_last_error": (ctypes.c_char_p, []),
@@ -33,6 +33,10 @@ _SIGNATURES = {
     "palu_flash_decode_paged": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i,
                                      _vp, _sz, _vp]),
     "palu_latent_append_paged": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "palu_latent_append_strided": (_i, [_vp, _vp, _ll, _ll, _vp, _i, _i, _i, _i, _i, _vp]),
+    "palu_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
+    "palu_swiglu": (_i, [_vp, _vp, _i, _i, _vp]),
+    "palu_rope_rows": (_i, [_vp, _ll, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
 }
 EXPORTED = tuple(_SIGNATURES)
 

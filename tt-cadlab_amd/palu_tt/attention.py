@@ -6,14 +6,15 @@ Same construction inputs and state-dict keys as the reference (``layers.{i}.atte
 same cache contents (latent rows of width r_k / r_v per head or per group, or rotated full K on the
 K-fast path), and the same decode data flow (attention.py:585-733):
 
-  decode:  x @ [wq | wk_lat_pad | wv_lat_pad]^T -> q, latent slots
-           RoPE on q at current_pos (Meta-interleaved)
+  decode:  x @ [wq | wk_lat_pad | wv_lat_pad]^T -> q, latent slots (one GEMM)
+           RoPE on q at current_pos (Meta-interleaved), read straight from the GEMM output
            latents (a head's first r columns, or a group's head slots concatenated) appended at
-           current_pos (the latent-append kernel)
+           current_pos from the GEMM output's latent columns (the strided latent-append kernel)
            fused latent flash-decode (palu_sdpa_decode; u_v rebuilds V per head for grouped latents)
            or, on the K-fast path (r_k == head_dim, per-head factors), flash-decode over the cached
            rotated K
-           absorbed-V output padded to head_dim, concat heads, @ wo_fused^T
+           absorbed-V output @ the r_v rows per head of wo_fused^T (the reference pads the output to
+           head_dim and multiplies the full wo_fused; the padded rows contribute zero)
   prefill: latents rebuilt to full K / V with u_k / u_v (attention.py:380-480), RoPE on q and K,
            causal SDPA, @ wo^T; the cache receives the latents (or rotated K on the fast path).
 
@@ -26,7 +27,7 @@ from typing import Optional
 import torch
 import torch.nn.functional as F
 
-from palu_tt import fused
+from palu_tt import decoder_ops, fused
 from palu_tt.cache import LatentCache
 
 
@@ -70,11 +71,15 @@ class PaluAttention(torch.nn.Module):
         wq = state_dict[f"{ln}.wq.weight"]
         wk = state_dict[f"{P}.wk_lat_pad"]
         wv = state_dict[f"{P}.wv_lat_pad"]
-        # weights stored input-major ([dim, out]) so every projection is a plain x @ W
-        self.wqkv_t = torch.cat([wq, wk, wv], dim=0).T.to(dev, bf).contiguous()      # [dim, (nh + 2 nkv) hd]
-        self.wo_t = state_dict[f"{ln}.wo.weight"].T.to(dev, bf).contiguous()
-        self.wo_fused_t = (state_dict[f"{P}.wo_fused"].T.to(dev, bf).contiguous()
-                           if (self.recon_v and self.gs == 1) else self.wo_t)
+        # weights in the nn.Linear layout [out, in]: the M=B GEMMs of decode stream them fastest that way
+        self.wqkv = torch.cat([wq, wk, wv], dim=0).to(dev, bf).contiguous()          # [(nh + 2 nkv) hd, dim]
+        self.wo = state_dict[f"{ln}.wo.weight"].to(dev, bf).contiguous()
+        wo_fused = (state_dict[f"{P}.wo_fused"].to(dev, bf) if (self.recon_v and self.gs == 1) else self.wo)
+        # decode output width per head: the absorbed-V latent (r_v) or, with u_v / stock V, head_dim; the
+        # output projection keeps only those rows of wo_fused (the rest multiply the zero padding)
+        self.out_width = self.head_dim if (self.gs > 1 or not self.recon_v) else self.r_v
+        self.wo_out = (wo_fused.view(-1, self.n_heads, self.head_dim)[:, :, :self.out_width]
+                       .reshape(-1, self.n_heads * self.out_width).contiguous())
         self.u_k = state_dict[f"{P}.u_k"].to(dev, bf).contiguous() if self.recon_k else None   # [nkv, r_k, hd]
         self.w_rot = state_dict[f"{P}.w_rot"].to(dev, bf)[None].contiguous() if self.recon_k else None
         self.u_v = state_dict[f"{P}.u_v"].to(dev, bf).contiguous() if self.recon_v else None   # [nkv, r_v, hd]
@@ -119,30 +124,31 @@ class PaluAttention(torch.nn.Module):
         """Meta-interleaved RoPE of x [..., heads, hd] at positions pos (broadcast over heads)."""
         return fused.apply_rope_meta(x, self.cos[pos][..., None, :], self.sin[pos][..., None, :])
 
-    def _append(self, cache, rows, pos):
-        fused.paged_update_cache(cache, rows.to(torch.bfloat16).contiguous(), pos)
-
     # ------------------------------------------------------------------------------------------------
     def forward_decode(self, x, current_pos, rot_mats=None, page_table=None, kv_cache=None):
+        """One decode step for all max_batch_size rows: QKV projection; RoPE of q (and of K on the K-fast
+        path) read straight from the projection; latent append from its latent columns; the fused op
+        (or the stock decode over rotated K); output projection over the out_width rows per head."""
         assert page_table is None and kv_cache is None
         shape = x.shape
         x2 = x.reshape(-1, self.hidden_size).to(torch.bfloat16)
         B = x2.shape[0]
-        pos = current_pos.reshape(-1).to(self.device, torch.int32)
-        assert pos.numel() == B
-        q_pre, k_slots, v_slots = self._split(x2 @ self.wqkv_t)             # [B, nh | nkv, hd]
-        q = self._rope(q_pre.float(), pos.long()).to(torch.bfloat16)
-        keys, values = self.layer_past
         if B != self.max_batch_size:
             raise ValueError(f"decode batch {B} != max_batch_size {self.max_batch_size}")
+        pos = current_pos.reshape(-1).to(self.device, torch.int32)
+        assert pos.numel() == B
+        nh, nkv, hd = self.n_heads, self.n_kv_heads, self.head_dim
+        xqkv = F.linear(x2, self.wqkv)                                      # [B, (nh + 2 nkv) hd]
+        q = decoder_ops.rope_rows(xqkv, nh, pos, self.cos, self.sin)         # [B, nh, hd]
+        keys, values = self.layer_past
+        kcols, vcols = xqkv[:, nh * hd:], xqkv[:, (nh + nkv) * hd:]
         if self.recon_k:
-            k_new = self._group_latent(k_slots, self.r_k)
-        else:
-            k_new = self._rope(k_slots.float(), pos.long())                # stock K path: rotated full K
-        v_new = self._group_latent(v_slots, self.r_v)
-        self._append(keys, k_new, pos)
-        self._append(values, v_new, pos)
-        q4 = q[None].contiguous()                                          # [1, B, nh, hd]
+            decoder_ops.append_from(keys, kcols, self.gs * hd, self.r_k, pos)
+        else:                                                                # stock K path: rotated full K
+            k_rot = decoder_ops.rope_rows(kcols, nkv, pos, self.cos, self.sin)
+            decoder_ops.append_from(keys, k_rot.view(B, nkv * hd), hd, hd, pos)
+        decoder_ops.append_from(values, vcols, self.gs * hd, self.r_v, pos)
+        q4 = q[None]                                                         # [1, B, nh, hd]
         if self.recon_k:
             grouped = self.gs > 1
             attn = fused.palu_sdpa_decode(q4, keys, self.w_rot, self.cs_tab, values,
@@ -151,9 +157,7 @@ class PaluAttention(torch.nn.Module):
                                           out_dtype=torch.bfloat16)
         else:
             attn = fused.flash_multi_latent_attention_decode(q4, keys, values, self.r_v, pos, scale=self.scale)
-        if attn.shape[-1] < self.head_dim:
-            attn = F.pad(attn, (0, self.head_dim - attn.shape[-1]))
-        out = attn[0].reshape(B, self.n_heads * self.head_dim) @ self.wo_fused_t
+        out = F.linear(attn[0].reshape(B, nh * self.out_width), self.wo_out)
         return out.reshape(*shape[:-1], self.hidden_size)
 
     def forward_prefill(self, x, rot_mats=None, user_id=0, page_table=None, chunk_page_table=None,
@@ -172,7 +176,7 @@ class PaluAttention(torch.nn.Module):
 
     def _prefill_one(self, x2, user):
         S = x2.shape[0]
-        q_pre, k_slots, v_slots = self._split(x2 @ self.wqkv_t)             # [S, nh | nkv, hd]
+        q_pre, k_slots, v_slots = self._split(F.linear(x2, self.wqkv))      # [S, nh | nkv, hd]
         pos = torch.arange(S, device=self.device)
         k_lat = self._group_latent(k_slots, self.r_k) if self.recon_k else None    # [S, n_groups, r_k]
         v_lat = self._group_latent(v_slots, self.r_v)
@@ -190,7 +194,7 @@ class PaluAttention(torch.nn.Module):
         Vh = V.repeat_interleave(rep, dim=1).transpose(0, 1)[None].contiguous()
         attn = F.scaled_dot_product_attention(qh, Kh, Vh, is_causal=True, scale=self.scale)
         attn = attn[0].transpose(0, 1).reshape(S, self.n_heads * self.head_dim).to(torch.bfloat16)
-        return attn @ self.wo_t
+        return F.linear(attn, self.wo)
 
     def _fill(self, cache, rows, user_id):
         """Rows [S, G, w] into cache row user_id at positions 0..S-1 (reference ttnn.fill_cache)."""

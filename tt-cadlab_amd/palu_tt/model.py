@@ -8,9 +8,12 @@ converter's layers.{i}.attention.palu.*. ``random_palu_state_dict`` builds a ran
 per-layer M-LRD ranks (per-head SVD of random k/v projections, ranks padded up to a multiple of 32 as
 convert.load_palu_dir does), which is what the end-to-end benchmark uses.
 
-Decode runs every layer's projections as plain GEMMs (hipBLASLt through torch) and the attention core
-through the HIP library; ``Transformer.decode_graph`` captures a whole decode step in a HIP graph so a
-step is one graph launch.
+Decode runs every layer's projections as plain GEMMs (hipBLASLt through torch; the gate/up weight
+input-major, the others in the nn.Linear layout, whichever streams faster at M = batch), the attention
+core and
+the elementwise work around it (RMSNorm with the residual add, RoPE, latent append, SwiGLU) through the
+HIP library; ``Transformer.decode_graph`` captures a whole decode step in a HIP graph so a step is one
+graph launch.
 """
 import math
 from dataclasses import dataclass, field
@@ -19,7 +22,7 @@ from typing import List, Optional
 import torch
 import torch.nn.functional as F
 
-from palu_tt import compress, convert
+from palu_tt import compress, convert, decoder_ops
 from palu_tt.attention import PaluAttention
 
 LLAMA3_SCALING = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
@@ -58,7 +61,7 @@ class Transformer(torch.nn.Module):
         t = lambda k: state_dict.pop(k).to(dev, bf)
         self.tok_embeddings = t("tok_embeddings.weight")
         self.norm_w = t("norm.weight")
-        self.output_t = t("output.weight").T.contiguous()
+        self.output = t("output.weight")                                 # [vocab, dim] (nn.Linear layout)
         self.layers = []
         for i in range(args.n_layers):
             p = f"layers.{i}"
@@ -69,13 +72,13 @@ class Transformer(torch.nn.Module):
             self.layers.append(dict(
                 attn=attn, attn_norm=t(f"{p}.attention_norm.weight"), ffn_norm=t(f"{p}.ffn_norm.weight"),
                 w13_t=torch.cat([t(f"{p}.feed_forward.w1.weight"), t(f"{p}.feed_forward.w3.weight")], 0).T.contiguous(),
-                w2_t=t(f"{p}.feed_forward.w2.weight").T.contiguous()))
+                w2=t(f"{p}.feed_forward.w2.weight")))
         self._graph = None
 
     def _ffn(self, L, h):
         gu = h @ L["w13_t"]
         g, u = gu.chunk(2, dim=-1)
-        return (F.silu(g.float()) * u.float()).to(h.dtype) @ L["w2_t"]
+        return F.linear((F.silu(g.float()) * u.float()).to(h.dtype), L["w2"])
 
     @torch.no_grad()
     def prefill(self, tokens: torch.Tensor, user_id: int = 0) -> torch.Tensor:
@@ -86,18 +89,23 @@ class Transformer(torch.nn.Module):
         for L in self.layers:
             h = h + L["attn"].forward_prefill(rms_norm(h, L["attn_norm"], eps), user_id=user_id)
             h = h + self._ffn(L, rms_norm(h, L["ffn_norm"], eps))
-        return (rms_norm(h[:, -1], self.norm_w, eps) @ self.output_t).float()
+        return F.linear(rms_norm(h[:, -1], self.norm_w, eps), self.output).float()
 
     @torch.no_grad()
     def decode(self, tokens: torch.Tensor, current_pos: torch.Tensor) -> torch.Tensor:
         """One decode step for all max_batch_size rows: tokens [B] at positions current_pos [B] (int32,
-        device); returns logits [B, vocab] fp32."""
+        device); returns logits [B, vocab] fp32. The residual stream h is updated in place: each RMSNorm
+        kernel first adds the previous sublayer's output to it."""
         eps = self.args.norm_eps
         h = self.tok_embeddings[tokens]                                  # [B, dim]
+        f = None
         for L in self.layers:
-            h = h + L["attn"].forward_decode(rms_norm(h, L["attn_norm"], eps), current_pos)
-            h = h + self._ffn(L, rms_norm(h, L["ffn_norm"], eps))
-        return (rms_norm(h, self.norm_w, eps) @ self.output_t).float()
+            y = decoder_ops.rmsnorm(h, L["attn_norm"], eps, res=f, h_out=h)
+            o = L["attn"].forward_decode(y, current_pos)
+            y = decoder_ops.rmsnorm(h, L["ffn_norm"], eps, res=o, h_out=h)
+            f = F.linear(decoder_ops.swiglu(y @ L["w13_t"]), L["w2"])
+        y = decoder_ops.rmsnorm(h, self.norm_w, eps, res=f)
+        return F.linear(y, self.output).float()
 
     @torch.no_grad()
     def decode_graph(self, tokens: torch.Tensor, current_pos: torch.Tensor) -> torch.Tensor:
