@@ -95,10 +95,11 @@ extern thread_local char g_err[1024];
 // which lets the compiler use the full 512-entry register file instead of spilling).
 template <int RK, int RV, bool KFULL, bool TILED>
 constexpr int pick_nw() {
-  // 8 waves where the kernel fits 256 VGPRs without spilling (checked per instantiation with
-  // -Rpass-analysis=kernel-resource-usage), else 4 waves with the 512-register budget.
+  // 8 waves where the kernel fits 256 VGPRs without spilling (checked per instantiation and layout with
+  // -Rpass-analysis=kernel-resource-usage: every latent width pair but r_k 64 / r_v 128 does), else 4
+  // waves with the 512-register budget.
   if (KFULL) return 8;
-  return ((RK == 64 && RV == 128) || (RK >= 96 && !(RK == 96 && RV == 32))) ? 4 : 8;
+  return (RK == 64 && RV == 128) ? 4 : 8;
 }
 constexpr int MIN_NW = 4;
 constexpr int TARGET_WGS = 256;  // one workgroup per CU at full occupancy of the chip
