@@ -26,7 +26,8 @@
 
 namespace {
 
-constexpr int G_NW = 8;                 // waves per workgroup (scores and PV kernels)
+constexpr int G_NW = 8;                 // waves per workgroup (PV kernel)
+constexpr int G_NWS = 8;                // waves per workgroup (scores kernel)
 constexpr int G_D = 64;                 // head dims per scores workgroup
 constexpr int G_RT = G_D / 16;          // 16-dim row tiles per scores workgroup
 constexpr int G_QS = HD + 8;            // padded query row (bf16), spreads the 16 rows over the banks
@@ -49,7 +50,7 @@ struct GlrdPlan {
 inline GlrdPlan glrd_plan(int B, int n_q, int n_kv, int n_groups, int S, int rv) {
   GlrdPlan p;
   const int hpg = n_kv / n_groups;
-  const Plan p1 = plan_splits(B * n_kv * 2, S, 2 * G_NW);
+  const Plan p1 = plan_splits(B * n_kv * 2, S, 2 * G_NWS);
   p.n_splits1 = p1.n_splits;
   p.split_len1 = p1.split_len;
   p.n_streams1 = B * n_groups * p.n_splits1;
@@ -88,7 +89,7 @@ struct G1Smem {
 };
 
 template <int KBP, typename TabT>
-__global__ __launch_bounds__(G_NW * 64) void palu_glrd_scores_kernel(const DecodeArgs a, float* scores) {
+__global__ __launch_bounds__(G_NWS * 64) void palu_glrd_scores_kernel(const DecodeArgs a, float* scores) {
   constexpr int R = (KBP % 4 == 0) ? 4 : 2;       // rank blocks of latent tiles in flight per wave
   using SM = G1Smem<KBP>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -135,11 +136,11 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_scores_kernel(const Decod
     const TabT* cs = static_cast<const TabT*>(a.cs);
     const int n_hi = (a.S + 1023) / 1024;
     const int n_rows = 64 + 16 + n_hi;             // 64 K rows, 16 low-base rows, n_hi high-base rows
-    constexpr int RPW = (64 + 16 + 64 + G_NW - 1) / G_NW;
+    constexpr int RPW = (64 + 16 + 64 + G_NWS - 1) / G_NWS;
     float4 rowv[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-      const int r = w + i * G_NW;
+      const int r = w + i * G_NWS;
       int t = r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80));
       t = (r < n_rows && t < a.cs_rows) ? t : 0;
       rowv[i] = load4f(cs + (long long)t * (2 * HD) + 4 * lane);
@@ -153,7 +154,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_scores_kernel(const Decod
     }
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-      const int r = w + i * G_NW;
+      const int r = w + i * G_NWS;
       if (r < n_rows) {
         const int t = r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80));
         const bool ok = t < a.cs_rows;
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_scores_kernel(const Decod
     __syncthreads();
     // rtab[(hb, c, rt)][lane (n, g)]: offset t = 32 hb + 8(n/4) + 4c + n%4 inside the pair, frequency
     // pairs f, f + 1 with f = 32 dpart + 8 rt + 2 g (the lane's dims 16 rt + 4 g .. +3 of this half).
-    for (int e = tid; e < 2 * 2 * G_RT * 64; e += G_NW * 64) {
+    for (int e = tid; e < 2 * 2 * G_RT * 64; e += G_NWS * 64) {
       const int l = e & 63, rt = (e >> 6) & (G_RT - 1), c = (e >> 8) & 1, hb = e >> 9;
       const int nn = l & 15, gg = l >> 4;
       const int t = 32 * hb + 8 * (nn >> 2) + 4 * c + (nn & 3);
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_scores_kernel(const Decod
     // Each thread reads 8 consecutive dims of one rank row (16 B) and scatters them.
     const __bf16* ukp = a.w_rot + (long long)kvh * a.rk * (2 * HD) + G_D * dpart;
     __bf16* ukt16 = reinterpret_cast<__bf16*>(ukt);
-    for (int e = tid; e < KBP * 32 * (G_D / 8); e += G_NW * 64) {
+    for (int e = tid; e < KBP * 32 * (G_D / 8); e += G_NWS * 64) {
       const int r = e >> 3, d8 = (e & 7) * 8;
       bf16x8 v = bf16x8{};
       if (r < a.rk) v = *reinterpret_cast<const bf16x8*>(ukp + (long long)r * (2 * HD) + d8);
@@ -241,7 +242,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_scores_kernel(const Decod
   bf16x8 ring[R][4];
 #pragma unroll
   for (int kb = 0; kb < R; ++kb) load_kb(w, kb, ring[kb]);
-  for (int pp = w; pp < npairs; pp += G_NW) {
+  for (int pp = w; pp < npairs; pp += G_NWS) {
     bf16x8 qB[2];
     make_q(s_lo + pp * 2 * BLK, qB);
     f32x4 acc[4][G_RT];
@@ -266,7 +267,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_scores_kernel(const Decod
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) acc[cc][rt] = mfma16(A[kb & 1][rt], ring[slot][cc], acc[cc][rt]);
       if (kb + R < KBP) load_kb(pp, kb + R, ring[slot]);
-      else load_kb(pp + G_NW, kb + R - KBP, ring[slot]);
+      else load_kb(pp + G_NWS, kb + R - KBP, ring[slot]);
       __builtin_amdgcn_sched_barrier(0);                 // keep the reads of one rank block ahead, not more
     }
     // rotate, pack, contract with the query: scores of 16 positions x 16 heads per (block, tile c)
@@ -430,22 +431,25 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
 }
 
 // ---------------------------------------------------------------------------------------------------
-// Pass 3: merge the splits of every query head of one (row, KV head) and apply u_v, one quarter of the
-// output dims per workgroup. The split weights 2^(m_s - M) are computed once per head, so the merge of
-// each latent column is a dot product over independent loads.
-constexpr int G_OUT_DIMS = 32;          // output dims per merge workgroup
+// Pass 3: merge the splits of every query head of one (row, KV head) and apply u_v. The split weights
+// 2^(m_s - M) are computed once per head, each latent column of O_lat is merged once (a dot product over
+// independent loads), and the projection reads u_v in 16-byte pieces: thread (head group of 4, rank
+// slice, 8 output dims) accumulates 4 x 8 outputs over its slice; the slices are summed through LDS.
 constexpr int G_MAX_SPLITS2 = 128;      // split partials per head the merge workgroup stages
+
+// Dynamic LDS: red [16 rank slices][4 heads][HD], olat [rep][rv], wsplit [rep][G_MAX_SPLITS2], lsum [16].
+__host__ __device__ inline int glrd_out_lds(int rep, int rv) { return (16 * 4 * HD + rep * rv + rep * G_MAX_SPLITS2 + 16) * 4; }
 
 template <typename OutT>
 __global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, const float* part, int n_splits2) {
-  __shared__ float olat[16 * 512];
-  __shared__ float wsplit[16 * G_MAX_SPLITS2];
-  __shared__ float lsum[16];
-  __shared__ float red[8][16][G_OUT_DIMS];
-  const int item = blockIdx.x / (HD / G_OUT_DIMS);
-  const int dq = blockIdx.x % (HD / G_OUT_DIMS);
-  const int b = item / a.n_kv, kvh = item - b * a.n_kv;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
   const int rv = a.rv, rep = a.rep;
+  float* red = reinterpret_cast<float*>(smem);
+  float* olat = red + 16 * 4 * HD;
+  float* wsplit = olat + rep * rv;
+  float* lsum = wsplit + rep * G_MAX_SPLITS2;
+  const int item = blockIdx.x;
+  const int b = item / a.n_kv, kvh = item - b * a.n_kv;
   const int stride = rv + G_PSTRIDE_PAD;
   const int tid = threadIdx.x;
   const float* p0 = part + (long long)(b * a.n_q + kvh * rep) * n_splits2 * stride;
@@ -478,35 +482,45 @@ __global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, 
     float acc = 0.f;
 #pragma unroll 8
     for (int s = 0; s < n_splits2; ++s) acc += pr[(long long)s * stride] * wh[s];
-    olat[h * 512 + r] = acc;
+    olat[h * rv + r] = acc;
   }
   __syncthreads();
-  // thread (rank eighth q, dim d): partial sums of out[h][32 dq + d] over ranks q * rv/8 .. for every head
-  const int q = tid >> 5, d = tid & 31;
-  const __bf16* uv = a.u_v + (long long)kvh * rv * HD + G_OUT_DIMS * dq + d;
-  float acc[16];
+  const int dg = tid & 15, rs = tid >> 4;             // 8 output dims, one of 16 rank slices
+  const int per = rv / 16;                              // rv is a multiple of 32
+  const __bf16* uv = a.u_v + (long long)kvh * rv * HD + 8 * dg;
+  for (int hg = 0; hg < rep; hg += 4) {                 // heads hg .. hg + 3 of this KV head
+    float acc[4][8];
 #pragma unroll
-  for (int h = 0; h < 16; ++h) acc[h] = 0.f;
-  const int r0 = q * (rv / 8), r1 = r0 + rv / 8;
-#pragma unroll 16
-  for (int r = r0; r < r1; ++r) {
-    const float u = (float)uv[(long long)r * HD];
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int h = 0; h < 16; ++h)
-      if (h < rep) acc[h] += olat[h * 512 + r] * u;
-  }
+      for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
+#pragma unroll 4
+    for (int r = rs * per; r < rs * per + per; ++r) {
+      const bf16x8 u = *reinterpret_cast<const bf16x8*>(uv + (long long)r * HD);
 #pragma unroll
-  for (int h = 0; h < 16; ++h)
-    if (h < rep) red[q][h][d] = acc[h];
-  __syncthreads();
-  for (int e = tid; e < rep * G_OUT_DIMS; e += 256) {
-    const int h = e / G_OUT_DIMS, dd = e - h * G_OUT_DIMS;
-    float s = 0.f;
+      for (int i = 0; i < 4; ++i) {
+        const float o = (hg + i < rep) ? olat[(hg + i) * rv + r] : 0.f;
 #pragma unroll
-    for (int qq = 0; qq < 8; ++qq) s += red[qq][h][dd];
-    const float Ls = lsum[h];
-    OutT* o = static_cast<OutT*>(a.out) + ((long long)b * a.n_q + (long long)kvh * rep + h) * HD + G_OUT_DIMS * dq + dd;
-    store_out(o, Ls > 0.f ? s / Ls : 0.f);
+        for (int j = 0; j < 8; ++j) acc[i][j] += o * (float)u[j];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) red[(rs * 4 + i) * HD + 8 * dg + j] = acc[i][j];
+    __syncthreads();
+    for (int e = tid; e < 4 * HD; e += 256) {
+      const int i = e / HD, d = e - i * HD, h = hg + i;
+      if (h < rep) {
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) sum += red[(q * 4 + i) * HD + d];
+        const float Ls = lsum[h];
+        OutT* o = static_cast<OutT*>(a.out) + ((long long)b * a.n_q + (long long)kvh * rep + h) * HD + d;
+        store_out(o, Ls > 0.f ? sum / Ls : 0.f);
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -522,7 +536,7 @@ int launch_scores(const DecodeArgs& a, float* scores, int n_wg, hipStream_t stre
     if (e != hipSuccess) return fail(PALU_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
     attr_set = lds;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(G_NW * 64), lds, stream, a, scores);
+  hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(G_NWS * 64), lds, stream, a, scores);
   return PALU_OK;
 }
 
@@ -539,6 +553,17 @@ int scores_kb(const DecodeArgs& a, float* scores, int n_wg, hipStream_t s) {
     case 8: return launch_scores<16, TabT>(a, scores, n_wg, s);
   }
   return fail(PALU_EUNSUPPORTED, "grouped-latent r_k %d (32 .. 512 in steps of 32)", a.rk);
+}
+
+template <typename K>
+int set_out_lds(K kern, int lds) {
+  static int attr_set = 0;                 // one static per kernel instantiation
+  if (attr_set < lds) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return fail(PALU_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    attr_set = lds;
+  }
+  return PALU_OK;
 }
 
 int launch_pv(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, hipStream_t s) {
@@ -585,12 +610,14 @@ int dispatch_glrd(const DecodeArgs& a0, int cs_dtype, int out_dtype, hipStream_t
   if (int rc2 = launch_pv(a, scores, part, p, s)) return rc2;
   e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent PV kernel launch: %s", hipGetErrorString(e));
-  if (out_dtype == PALU_DTYPE_F32)
-    hipLaunchKernelGGL(palu_glrd_out_kernel<float>, dim3(a.B * a.n_kv * (HD / G_OUT_DIMS)), dim3(256), 0, s, a, part,
-                       p.n_splits2);
-  else
-    hipLaunchKernelGGL(palu_glrd_out_kernel<__bf16>, dim3(a.B * a.n_kv * (HD / G_OUT_DIMS)), dim3(256), 0, s, a, part,
-                       p.n_splits2);
+  const int out_lds = glrd_out_lds(a.rep, a.rv);
+  if (out_dtype == PALU_DTYPE_F32) {
+    if (int rc3 = set_out_lds(palu_glrd_out_kernel<float>, out_lds)) return rc3;
+    hipLaunchKernelGGL(palu_glrd_out_kernel<float>, dim3(a.B * a.n_kv), dim3(256), out_lds, s, a, part, p.n_splits2);
+  } else {
+    if (int rc3 = set_out_lds(palu_glrd_out_kernel<__bf16>, out_lds)) return rc3;
+    hipLaunchKernelGGL(palu_glrd_out_kernel<__bf16>, dim3(a.B * a.n_kv), dim3(256), out_lds, s, a, part, p.n_splits2);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent output kernel launch: %s", hipGetErrorString(e));
   return PALU_OK;
