@@ -295,10 +295,22 @@ __global__ __launch_bounds__(G_NWS * 64) void palu_glrd_scores_kernel(const Deco
 }
 
 // ---------------------------------------------------------------------------------------------------
-// Pass 2: latent PV. TPW = V tiles per wave (r_v / 16 spread over the 8 waves).
+// Pass 2: latent PV. The 8 waves form TG tile groups x PG position groups (TG * PG = 8, TG the smallest
+// power of two with TG * 8 >= r_v / 16): wave (tg, pg) owns V tiles tg * TPW .. tg * TPW + TPW - 1 and
+// the blocks j = pg, pg + PG, ... of the split, with its own online softmax; the PG partials of a tile
+// group are merged through LDS at the end. A block's scores are thus loaded and exponentiated by TG
+// waves, not by all 8.
+__host__ __device__ inline int glrd_pv_tg(int vt) {
+  int tg = 1;
+  while (tg * 8 < vt) tg *= 2;
+  return tg;
+}
+__host__ __device__ inline int glrd_pv_lds(int tpw) { return G_NW * (16 * tpw * 16 + 2 * 16) * 4; }
+
 template <int TPW>
 __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArgs a, const float* scores, float* part,
                                                                  int n_ht, int n_splits2, int split_len2) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
   const int n_groups = a.n_kv / a.hpg;
   const int QH = a.hpg * a.rep;
   const int NB = a.S / BLK;
@@ -314,6 +326,8 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int VT = a.rv >> 4;
+  const int TG = glrd_pv_tg(VT), PG = G_NW / TG;
+  const int tg = w % TG, pg = w / TG;
   const int head = ht * 16 + n;                       // head of this lane column inside the group
   const bool head_live = head < QH;
   const int head_c = head_live ? head : QH - 1;
@@ -335,7 +349,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
     float4 s[4];             // positions 8g .. 8g+7 of this lane's head, both dim halves
     bf16x8 v[TPW];
   };
-  // Loads of block j (past the split's data: its first block, unused).
+  // Loads of block j (past the split's data: its first block, unused; tiles past r_v: tile 0, unused).
   auto load = [&](int j, Blk& x) {
     const int jj = j < nblk ? j : 0;
     const float* p0 = sc0 + jj * blk_stride;
@@ -345,7 +359,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
     x.s[3] = *reinterpret_cast<const float4*>(p0 + half_stride + 4);
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-      const int mt = w + G_NW * i;
+      const int mt = tg * TPW + i;
       x.v[i] = *reinterpret_cast<const bf16x8*>(vbase + (long long)jj * (32 * a.rv) + (mt < VT ? mt : 0) * 512);
     }
   };
@@ -399,34 +413,52 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
   const std::integral_constant<bool, false> full_blk;
   const std::integral_constant<bool, true> partial_blk;
   Blk x0, x1;
-  load(0, x0);
-  load(1, x1);
-  int j = 0;
-  for (; j + 1 < nfull; j += 2) {
+  load(pg, x0);
+  load(pg + PG, x1);
+  int j = pg;
+  for (; j + PG < nfull; j += 2 * PG) {
     step(full_blk, j, x0);
-    load(j + 2, x0);
-    step(full_blk, j + 1, x1);
-    load(j + 3, x1);
+    load(j + 2 * PG, x0);
+    step(full_blk, j + PG, x1);
+    load(j + 3 * PG, x1);
   }
   if (j < nfull) {
     step(full_blk, j, x0);
-    ++j;
-    if (j < nblk) step(partial_blk, j, x1);
+    j += PG;
+    if (j < nblk) step(partial_blk, j, x1);         // then j == nfull: the partial last block
   } else if (j < nblk) {
     step(partial_blk, j, x0);
   }
+  l_run = wave_sum_xor48(l_run);                      // over the wave's 4 position groups
 
-  // l over the wave's 4 position groups; every wave holds the same (m, l)
-  l_run = wave_sum_xor48(l_run);
-  if (head_live) {
-    const int qh = (b * n_groups + grp) * QH + head;  // == b * n_q + global query head
-    float* prow = part + ((long long)qh * n_splits2 + split) * (a.rv + G_PSTRIDE_PAD);
+  // merge the PG position groups of every tile group: wave w's partial in LDS, [16 heads][TPW * 16]
+  // columns plus (m, l) per head
+  float* ow = reinterpret_cast<float*>(smem) + w * (16 * TPW * 16 + 32);
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      const int mt = w + G_NW * i;
-      if (mt < VT) *reinterpret_cast<float4*>(prow + 16 * mt + 4 * g) = make_float4(O[i][0], O[i][1], O[i][2], O[i][3]);
+  for (int i = 0; i < TPW; ++i)
+    *reinterpret_cast<float4*>(ow + n * (TPW * 16) + 16 * i + 4 * g) = make_float4(O[i][0], O[i][1], O[i][2], O[i][3]);
+  if (g == 0) { ow[16 * TPW * 16 + n] = m_run; ow[16 * TPW * 16 + 16 + n] = l_run; }
+  __syncthreads();
+  const int ncols = TG * TPW * 16;                    // >= r_v
+  for (int e = tid; e < 16 * ncols; e += G_NW * 64) {
+    const int hh = e / ncols, col = e - hh * ncols;
+    const int t = col / (TPW * 16), c = col - t * (TPW * 16);
+    if (ht * 16 + hh >= QH || col >= a.rv) continue;
+    float M = NEG_INF;
+    for (int q = 0; q < PG; ++q) M = fmaxf(M, reinterpret_cast<const float*>(smem)[(q * TG + t) * (16 * TPW * 16 + 32) + 16 * TPW * 16 + hh]);
+    float acc = 0.f, Ls = 0.f;
+    if (M != NEG_INF) {
+      for (int q = 0; q < PG; ++q) {
+        const float* oq = reinterpret_cast<const float*>(smem) + (q * TG + t) * (16 * TPW * 16 + 32);
+        const float f = __builtin_amdgcn_exp2f(oq[16 * TPW * 16 + hh] - M);
+        acc += oq[hh * (TPW * 16) + c] * f;
+        Ls += oq[16 * TPW * 16 + 16 + hh] * f;
+      }
     }
-    if (w == 0 && g == 0) { prow[a.rv] = m_run; prow[a.rv + 1] = l_run; }
+    const int qh = (b * n_groups + grp) * QH + ht * 16 + hh;    // == b * n_q + global query head
+    float* prow = part + ((long long)qh * n_splits2 + split) * (a.rv + G_PSTRIDE_PAD);
+    prow[col] = acc;
+    if (col == 0) { prow[a.rv] = M; prow[a.rv + 1] = Ls; }
   }
 }
 
@@ -566,17 +598,35 @@ int set_out_lds(K kern, int lds) {
   return PALU_OK;
 }
 
-int launch_pv(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, hipStream_t s) {
-  const int tpw = ((a.rv >> 4) + G_NW - 1) / G_NW;
-  const dim3 grid((unsigned)p.n_wg2), block(G_NW * 64);
-  switch (tpw) {
-    case 1: hipLaunchKernelGGL(palu_glrd_pv_kernel<1>, grid, block, 0, s, a, scores, part, p.n_ht, p.n_splits2, p.split_len2); break;
-    case 2: hipLaunchKernelGGL(palu_glrd_pv_kernel<2>, grid, block, 0, s, a, scores, part, p.n_ht, p.n_splits2, p.split_len2); break;
-    case 3: hipLaunchKernelGGL(palu_glrd_pv_kernel<3>, grid, block, 0, s, a, scores, part, p.n_ht, p.n_splits2, p.split_len2); break;
-    case 4: hipLaunchKernelGGL(palu_glrd_pv_kernel<4>, grid, block, 0, s, a, scores, part, p.n_ht, p.n_splits2, p.split_len2); break;
-    default: return fail(PALU_EUNSUPPORTED, "grouped-latent r_v %d (32 .. 512 in steps of 32)", a.rv);
+template <int TPW>
+int launch_pv_t(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, hipStream_t s) {
+  const int lds = glrd_pv_lds(TPW);
+  static int attr_set = 0;
+  if (attr_set < lds) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(palu_glrd_pv_kernel<TPW>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return fail(PALU_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    attr_set = lds;
   }
+  hipLaunchKernelGGL(palu_glrd_pv_kernel<TPW>, dim3((unsigned)p.n_wg2), dim3(G_NW * 64), lds, s, a, scores, part, p.n_ht,
+                     p.n_splits2, p.split_len2);
   return PALU_OK;
+}
+
+int launch_pv(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, hipStream_t s) {
+  const int vt = a.rv >> 4;
+  const int tpw = (vt + glrd_pv_tg(vt) - 1) / glrd_pv_tg(vt);
+  switch (tpw) {
+    case 1: return launch_pv_t<1>(a, scores, part, p, s);
+    case 2: return launch_pv_t<2>(a, scores, part, p, s);
+    case 3: return launch_pv_t<3>(a, scores, part, p, s);
+    case 4: return launch_pv_t<4>(a, scores, part, p, s);
+    case 5: return launch_pv_t<5>(a, scores, part, p, s);
+    case 6: return launch_pv_t<6>(a, scores, part, p, s);
+    case 7: return launch_pv_t<7>(a, scores, part, p, s);
+    case 8: return launch_pv_t<8>(a, scores, part, p, s);
+  }
+  return fail(PALU_EUNSUPPORTED, "grouped-latent r_v %d (32 .. 512 in steps of 32)", a.rv);
 }
 
 }  // namespace
