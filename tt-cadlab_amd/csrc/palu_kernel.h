@@ -54,6 +54,9 @@ namespace palu {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int HD = 128;     // head dim
 constexpr int BLK = 32;     // positions per block: two 16-position MFMA tiles, also the rotation chunk
@@ -157,6 +160,23 @@ __device__ __forceinline__ long long tiled_v_offset(int p, int k, int R) {
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// fp32 pair -> fp16 pair, rounded toward zero: finite inputs beyond the fp16 range saturate to
+// +-65504 instead of becoming infinite.
+__device__ __forceinline__ f16x2 to_f16x2(float a, float b) {
+  return __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
+// max of 8 without NaN canonicalisation (v_maximum3_f32)
+__device__ __forceinline__ float max8(f32x4 a, f32x4 b) {
+  const float x = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a[0], a[1]), a[2]);
+  const float y = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a[3], b[0]), b[1]);
+  const float z = __builtin_elementwise_maximum(__builtin_elementwise_maximum(b[2], b[3]), x);
+  return __builtin_elementwise_maximum(y, z);
+}
 
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(__bf16 x) { return (float)x; }
@@ -184,11 +204,11 @@ __device__ __forceinline__ float wave_sum_xor48(float x) {
 
 
 // LDS map of one workgroup (latent mode; full-K mode keeps only the merge buffer and the counter):
-//   rtab  pair-relative K rotation (offset t < 64 inside a pair of blocks), float4 {cos f, sin f,
-//         cos f+1, sin f+1} per (block of the pair, tile, 16-dim row tile, lane), i.e. exactly the
-//         operand order of the rebuilt K^T accumulators                               32 KB
+//   rtab  pair-relative K rotation (offset t < 64 inside a pair of blocks), fp16 x 8 {cos f, cos f,
+//         -sin f, sin f, cos f+1, cos f+1, -sin f+1, sin f+1} per (block of the pair, tile, 16-dim row
+//         tile, lane), i.e. exactly the operand order of the rebuilt K^T accumulators  32 KB
 //   ukT   u_k^T, rows padded by 16 bytes (bank spread)                               HD x (RK + 8) bf16
-//   qx    per wave, the rotated query regrouped into its MFMA operand layout         NW x 4 KB
+//   qx    per wave, the rotated query (fp16) regrouped into its MFMA operand layout  NW x 4 KB
 //   tl    (cos, sin) of angle 64*Lo*f, Lo < 16: the low part of a pair base           [16][64] float2
 //   qs    the item's query rows (zero rows past rep), so the block loop issues no global load
 //         besides the latent prefetch                                                 [16][128] bf16
@@ -202,7 +222,7 @@ struct Smem {
   static constexpr int RTAB_BYTES = KFULL ? 0 : 2 * 2 * 8 * 64 * 16;
   static constexpr int KC_BYTES = 64 * 64 * 8;
   static constexpr int UKT_BYTES = KFULL ? 0 : HD * UKT_STRIDE * 2;
-  static constexpr int QX_WAVE_BYTES = 16 * 4 * 8 * 4 * 2;   // [head 16][g 4][row tile 8][4 dims] bf16
+  static constexpr int QX_WAVE_BYTES = 16 * 4 * 8 * 4 * 2;   // [head 16][g 4][row tile 8][4 dims] fp16
   static constexpr int QX_BYTES = KFULL ? 0 : (NW * QX_WAVE_BYTES > KC_BYTES ? NW * QX_WAVE_BYTES : KC_BYTES);
   static constexpr int TL_BYTES = KFULL ? 0 : 16 * 64 * 8;
   static constexpr int QS_BYTES = KFULL ? 0 : 16 * HD * 2;
@@ -239,7 +259,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   using SM = Smem<RK, RV, KFULL, NW>;
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  float4* rtab = reinterpret_cast<float4*>(smem);
+  f16x8* rtab = reinterpret_cast<f16x8*>(smem);
   __bf16* ukT = reinterpret_cast<__bf16*>(smem + SM::UKT_OFFSET);
   float2* tl = reinterpret_cast<float2*>(smem + SM::TL_OFFSET);
   float2* th = reinterpret_cast<float2*>(smem + SM::TH_OFFSET);
@@ -255,7 +275,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   const int item = blockIdx.y, split = blockIdx.x;
   const int b = item / a.n_kv, kvh = item - b * a.n_kv;
   const int grp = KFULL ? kvh : kvh / a.hpg;
-  __bf16* qx = reinterpret_cast<__bf16*>(smem + SM::QX_OFFSET + w * SM::QX_WAVE_BYTES);
+  _Float16* qx = reinterpret_cast<_Float16*>(smem + SM::QX_OFFSET + w * SM::QX_WAVE_BYTES);
 
   int len = a.cur_pos[b] + 1;
   len = len < 0 ? 0 : (len > a.S ? a.S : len);
@@ -397,8 +417,9 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       const int nn = l & 15, gg = l >> 4;
       const int t = 32 * hb + 8 * (nn >> 2) + 4 * c + (nn & 3);
       const int f = 8 * rt + 2 * gg;
-      const float2 x = kc[t * 64 + f], y = kc[t * 64 + f + 1];
-      rtab[e] = make_float4(x.x, x.y, y.x, y.y);
+      const float2 x = kc[t * 64 + f], y = kc[t * 64 + f + 1];   // (cos, sin) of frequencies f, f + 1
+      rtab[e] = f16x8{(_Float16)x.x, (_Float16)x.x, (_Float16)-x.y, (_Float16)x.y,
+                      (_Float16)y.x, (_Float16)y.x, (_Float16)-y.y, (_Float16)y.y};
     }
   } else {
     if (w < npairs) load_blk(s_lo + 2 * w * BLK, true, page_global(s_lo + 2 * w * BLK), kl, vl);
@@ -442,7 +463,9 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
 #pragma unroll
   for (int i = 0; i < VT; ++i) O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = NEG_INF, l_run = 0.f;
-  bf16x8 qB[4];
+  // The query operand: bf16 against full bf16 K; fp16 against the rebuilt K, which is rotated in fp16.
+  using QV = typename std::conditional<KFULL, bf16x8, f16x8>::type;
+  QV qB[4];
 
   // Query. Full-K mode: q * qscale once, head dim in natural order d = 32*kb + 8*g + j. Latent mode:
   // q~ = R_{-base} q * qscale per pair of blocks (base a multiple of 64). The rotation is spread over all 64 lanes (lane l owns query
@@ -482,24 +505,25 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       const int h = g + 4 * k;
       if (h < a.rep) {
         const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qs_lds + h * HD + 8 * qf);
-        bf16x4 y0, y1;
+        f16x4 y0, y1;
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const float x0 = (float)qv[2 * p], x1 = (float)qv[2 * p + 1];
           const float r0 = x0 * cf[p] + x1 * sf[p], r1 = x1 * cf[p] - x0 * sf[p];  // R_{-base}
-          if (p < 2) { y0[2 * p] = (__bf16)r0; y0[2 * p + 1] = (__bf16)r1; }
-          else { y1[2 * p - 4] = (__bf16)r0; y1[2 * p - 3] = (__bf16)r1; }
+          if (p < 2) { y0[2 * p] = (_Float16)r0; y0[2 * p + 1] = (_Float16)r1; }
+          else { y1[2 * p - 4] = (_Float16)r0; y1[2 * p - 3] = (_Float16)r1; }
         }
         // dims 16*rt + 4*g0 + 0..3 and 16*rt + 4*(g0+1) + 0..3 of head h
-        *reinterpret_cast<bf16x4*>(qx + ((h * 4 + g0) * 8 + rt) * 4) = y0;
-        *reinterpret_cast<bf16x4*>(qx + ((h * 4 + g0 + 1) * 8 + rt) * 4) = y1;
+        *reinterpret_cast<f16x4*>(qx + ((h * 4 + g0) * 8 + rt) * 4) = y0;
+        *reinterpret_cast<f16x4*>(qx + ((h * 4 + g0 + 1) * 8 + rt) * 4) = y1;
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) qB[kb] = *reinterpret_cast<const bf16x8*>(qx + ((n * 4 + g) * 8 + 2 * kb) * 4);
+    for (int kb = 0; kb < 4; ++kb)
+      qB[kb] = __builtin_bit_cast(QV, *reinterpret_cast<const f16x8*>(qx + ((n * 4 + g) * 8 + 2 * kb) * 4));
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
   };
@@ -542,19 +566,24 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
 #pragma unroll
             for (int c = 0; c < 2; ++c) acc[c][h] = mfma16(ua, kc[c][kb], acc[c][h]);
           }
-        // RoPE by the block offset of this lane's position: (x0, x1) -> (x0 c - x1 s, x1 c + x0 s).
+        // RoPE by the block offset of this lane's position, (x0, x1) -> (x0 c - x1 s, x1 c + x0 s), in
+        // packed fp16: (x0, x1) * (c, c) + (x1, x0) * (-s, s) is one multiply and one fma per pair. The
+        // rotated slice is the fp16 A operand of the QK product as it stands.
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
+          f16x2 r[2][2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const float4 t = rtab[((hb * 2 + c) * 8 + 2 * kq + h) * 64 + lane];
-            const float x0 = acc[c][h][0], x1 = acc[c][h][1], x2 = acc[c][h][2], x3 = acc[c][h][3];
-            acc[c][h][0] = x0 * t.x - x1 * t.y;
-            acc[c][h][1] = x1 * t.x + x0 * t.y;
-            acc[c][h][2] = x2 * t.z - x3 * t.w;
-            acc[c][h][3] = x3 * t.z + x2 * t.w;
+            const f16x8 t = rtab[((hb * 2 + c) * 8 + 2 * kq + h) * 64 + lane];
+            const f16x2 c0 = {t[0], t[1]}, s0 = {t[2], t[3]}, c1 = {t[4], t[5]}, s1 = {t[6], t[7]};
+            const f16x2 x01 = to_f16x2(acc[c][h][0], acc[c][h][1]);
+            const f16x2 x23 = to_f16x2(acc[c][h][2], acc[c][h][3]);
+            r[h][0] = x01 * c0 + x01.yx * s0;
+            r[h][1] = x23 * c1 + x23.yx * s1;
           }
-          sc[c] = mfma16(pack8(acc[c][0], acc[c][1]), qB[kq], sc[c]);
+          const f16x8 kA = {r[0][0][0], r[0][0][1], r[0][1][0], r[0][1][1],
+                            r[1][0][0], r[1][0][1], r[1][1][0], r[1][1][1]};
+          sc[c] = mfma16(kA, qB[kq], sc[c]);
         }
       }
     }
@@ -568,11 +597,12 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
           if (base + 8 * g + 4 * c + i >= s_hi) sc[c][i] = NEG_INF;
     }
 
-    // Online softmax, exp2 domain; lanes n, n+16, n+32, n+48 hold query head n.
-    float bm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
-                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
-    bm = wave_max_xor48(bm);
+    // Online softmax, exp2 domain; lanes n, n+16, n+32, n+48 hold query head n. Each lane tests its
+    // own scores against the running max; only when some score passes it by more than 2^8 does the
+    // wave reduce the block max across lanes and refresh the running max.
+    float bm = max8(sc[0], sc[1]);
     if (__any(bm > m_run + LAZY_RESCALE_LOG2)) {
+      bm = wave_max_xor48(bm);
       const float mn = fmaxf(m_run, bm);
       const float alpha = (m_run == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(m_run - mn);
 #pragma unroll
