@@ -255,9 +255,9 @@ int palu_abi_version(void) { return PALU_ABI_VERSION; }
 
 size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_dim_v) {
   if (batch <= 0 || n_kv <= 0 || seq_len <= 0 || head_dim_v <= 0) return 0;
-  // The narrowest workgroup splits the most, so its plan bounds every kernel variant.
-  Plan p = plan_splits(batch * n_kv, seq_len, MIN_NW);
-  return ws_bytes(batch * n_kv, p.n_splits, head_dim_v);
+  // One partial slot per workgroup of the length-aware plan (none when the items fill whole chip-fills).
+  (void)seq_len;
+  return decode_ws_bytes(batch * n_kv, head_dim_v);
 }
 
 size_t palu_glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_v) {

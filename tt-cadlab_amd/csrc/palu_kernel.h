@@ -71,13 +71,15 @@ struct DecodeArgs {
   const void* cs;         // [cs_rows, 2*HD]: [cos | sin], Meta-interleaved, fp32 or bf16
   const int32_t* cur_pos; // [B], inclusive last valid position
   void* out;              // [B, n_q, RV]
-  float* ws;              // [items, n_splits, 16, RV + 2] split partials (n_splits > 1)
+  float* ws;              // split partials: [n_wg, 16, RV + 2] (M-LRD / stock), see glrd for its own
   size_t ws_bytes;
   long long k_sb, k_sg;   // element strides of k: batch, group (row stride is RK / HD)
   long long v_sb, v_sg;
   int B, n_q, n_kv, rep, hpg, S, cs_rows;
-  int split_len;          // positions per workgroup split, a multiple of BLK
+  int split_len;          // grouped-latent kernels: positions per workgroup split, a multiple of BLK
   int n_splits;
+  int n_wg;               // M-LRD / stock decode: workgroups launched; n_wg > B * n_kv splits items by length
+  int balanced;           // 1 when n_wg > B * n_kv (length-aware chunks, merged through ws)
   int deterministic;      // 1: wave w takes blocks w, w + NW, ... (reproducible); 0: blocks from a counter
   float qscale;           // softmax scale * log2(e)
   // Paged caches: k/v are page pools [n_pages, G, page_size, width] (rows or tiled) and k_sb / v_sb are
@@ -125,6 +127,15 @@ inline Plan plan_splits(int items, int S, int nw) {
 
 inline size_t ws_bytes(int items, int n_splits, int rv) {
   return n_splits <= 1 ? 0 : (size_t)items * n_splits * 16 * (rv + 2) * sizeof(float);
+}
+
+// M-LRD / stock decode: workgroups per launch, a whole number of chip-fills of TARGET_WGS. When the
+// work items fill it exactly, each workgroup owns one item; otherwise items are cut into chunks by
+// their actual lengths (device side, from cur_pos) and the partials of the split ones are merged.
+inline int decode_workgroups(int items) { return ((items + TARGET_WGS - 1) / TARGET_WGS) * TARGET_WGS; }
+inline size_t decode_ws_bytes(int items, int rv) {
+  const int wg = decode_workgroups(items);
+  return wg == items ? 0 : (size_t)wg * 16 * (rv + 2) * sizeof(float);
 }
 
 
@@ -203,6 +214,52 @@ __device__ __forceinline__ float wave_sum_xor48(float x) {
 }
 
 
+// ---- length-aware chunk plan ------------------------------------------------------------------
+// With `items` = B * n_kv work items and G = n_wg > items workgroups, every workgroup derives the same
+// plan from cur_pos: chunks are whole pairs of blocks (64 positions); row b has np_b pairs; the chunk
+// length T (pairs) is the smallest of 64 candidates between ceil(W / G) and ceil(W / (G - items))
+// (W = n_kv * sum_b np_b) for which n_kv * sum_b max(1, ceil(np_b / T)) <= G. The upper end always
+// qualifies, since sum_b max(1, ceil(np_b / T)) <= W / (n_kv T) + B. Item (b, kvh) is cut into
+// n_b = max(1, ceil(np_b / T)) near-equal chunks; chunks are numbered row by row, then KV head by KV
+// head, and chunk number = workgroup index = workspace slot.
+
+// n / d for 0 <= n < 2^22, 1 <= d, with 1/d precomputed: one float multiply, one correction step.
+struct FDiv {
+  int d;
+  float r;
+};
+__device__ __forceinline__ FDiv make_fdiv(int d) { return FDiv{d, 1.0f / (float)d}; }
+__device__ __forceinline__ int fdiv(int n, FDiv f) {
+  int q = (int)((float)n * f.r);
+  const int r = n - q * f.d;
+  return q + (r >= f.d ? 1 : 0) - (r < 0 ? 1 : 0);
+}
+__device__ __forceinline__ int ceil_fdiv(int n, FDiv f) { return fdiv(n + f.d - 1, f); }
+
+__device__ __forceinline__ int row_len(const DecodeArgs& a, int b) {
+  const int len = a.cur_pos[b] + 1;
+  return len < 0 ? 0 : (len > a.S ? a.S : len);
+}
+__device__ __forceinline__ int row_pairs(const DecodeArgs& a, int b) { return (row_len(a, b) + 63) >> 6; }
+
+// The plan's chunk length T in pairs (the same value in every lane of every wave that calls it).
+__device__ int plan_chunk_pairs(const DecodeArgs& a) {
+  const int lane = threadIdx.x & 63;
+  const int G = a.n_wg, items = a.B * a.n_kv;
+  int W = 0;
+  for (int b = 0; b < a.B; ++b) W += row_pairs(a, b);
+  W *= a.n_kv;
+  const int lo = max(1, (W + G - 1) / G);
+  const int hi = max(lo, (W + (G - items) - 1) / (G - items));
+  const int step = max(1, (hi - lo + 62) / 63);
+  const int T = lo + lane * step;           // lane 63: T >= hi
+  const FDiv fT = make_fdiv(T);
+  int C = 0;
+  for (int b = 0; b < a.B; ++b) C += max(1, ceil_fdiv(row_pairs(a, b), fT));
+  const unsigned long long ok = __ballot(C * a.n_kv <= G);
+  return lo + __builtin_ctzll(ok) * step;
+}
+
 // LDS map of one workgroup (latent mode; full-K mode keeps only the merge buffer and the counter):
 //   rtab  pair-relative K rotation (offset t < 64 inside a pair of blocks), fp16 x 8 {cos f, cos f,
 //         -sin f, sin f, cos f+1, cos f+1, -sin f+1, sin f+1} per (block of the pair, tile, 16-dim row
@@ -272,15 +329,40 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, held in a scalar register
   const int n = lane & 15, g = lane >> 4;
-  const int item = blockIdx.y, split = blockIdx.x;
-  const int b = item / a.n_kv, kvh = item - b * a.n_kv;
-  const int grp = KFULL ? kvh : kvh / a.hpg;
   _Float16* qx = reinterpret_cast<_Float16*>(smem + SM::QX_OFFSET + w * SM::QX_WAVE_BYTES);
 
-  int len = a.cur_pos[b] + 1;
-  len = len < 0 ? 0 : (len > a.S ? a.S : len);
-  const int s_lo = split * a.split_len;
-  const int s_hi = min(len, s_lo + a.split_len);
+  // This workgroup's item and position range: the whole sequence of item blockIdx.x, or one chunk of
+  // the length-aware plan (computed identically, and uniformly, by every wave).
+  int b, kvh, s_lo, s_hi, n_chunks = 1;
+  if (!a.balanced) {
+    b = blockIdx.x / a.n_kv;
+    kvh = blockIdx.x - b * a.n_kv;
+    s_lo = 0;
+    s_hi = row_len(a, b);
+  } else {
+    const FDiv fT = make_fdiv(plan_chunk_pairs(a));
+    int base = 0, rb = -1, np = 0;
+    const int gid = blockIdx.x;
+    for (int r = 0; r < a.B; ++r) {
+      np = row_pairs(a, r);
+      n_chunks = max(1, ceil_fdiv(np, fT));
+      if (gid < base + a.n_kv * n_chunks) { rb = r; break; }
+      base += a.n_kv * n_chunks;
+    }
+    if (rb < 0) return;                     // past the plan's last chunk (uniform: no barrier reached)
+    const FDiv fn = make_fdiv(n_chunks);
+    b = rb;
+    kvh = fdiv(gid - base, fn);
+    const int j = gid - base - kvh * n_chunks;
+    s_lo = 64 * fdiv(j * np, fn);
+    s_hi = min(row_len(a, b), 64 * fdiv((j + 1) * np, fn));
+  }
+  b = __builtin_amdgcn_readfirstlane(b);
+  kvh = __builtin_amdgcn_readfirstlane(kvh);
+  s_lo = __builtin_amdgcn_readfirstlane(s_lo);
+  s_hi = __builtin_amdgcn_readfirstlane(s_hi);
+  n_chunks = __builtin_amdgcn_readfirstlane(n_chunks);
+  const int grp = KFULL ? kvh : kvh / a.hpg;
   const int nblk = s_hi > s_lo ? (s_hi - s_lo + BLK - 1) / BLK : 0;
 
   const __bf16* kbase = a.k + (PAGED ? 0 : b * a.k_sb) + grp * a.k_sg;
@@ -708,37 +790,44 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
         acc += row[r] * f;
       }
     }
-    if (a.n_splits == 1) {
+    if (n_chunks == 1) {
       OutT* o = static_cast<OutT*>(a.out) + ((long long)b * a.n_q + (long long)kvh * a.rep + h) * RV + r;
       store_out(o, L > 0.f ? acc / L : 0.f);
     } else {
-      float* wrow = a.ws + (((long long)item * a.n_splits + split) * 16 + h) * (RV + 2);
+      float* wrow = a.ws + ((long long)blockIdx.x * 16 + h) * (RV + 2);
       wrow[r] = acc;
       if (r == 0) { wrow[RV] = M; wrow[RV + 1] = L; }
     }
   }
 }
 
-// Merge the split partials of every item: out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// Merge the chunk partials of every split item (length-aware plan): out = sum_s O_s 2^(m_s - M) /
+// sum_s l_s 2^(m_s - M) over the item's chunks, found by recomputing the plan. Items in one chunk
+// were written by the decode kernel itself.
 template <int RV, typename OutT>
-__global__ __launch_bounds__(256) void palu_merge_kernel(const float* ws, void* out, int n_splits, int rep,
-                                                         int n_q, int n_kv) {
+__global__ __launch_bounds__(256) void palu_merge_kernel(const DecodeArgs a) {
   const int item = blockIdx.x;
-  const int b = item / n_kv, kvh = item - b * n_kv;
-  for (int e = threadIdx.x; e < rep * RV; e += blockDim.x) {
+  const int b = item / a.n_kv, kvh = item - b * a.n_kv;
+  const FDiv fT = make_fdiv(plan_chunk_pairs(a));
+  int base = 0;
+  for (int r = 0; r < b; ++r) base += a.n_kv * max(1, ceil_fdiv(row_pairs(a, r), fT));
+  const int nc = max(1, ceil_fdiv(row_pairs(a, b), fT));
+  if (nc == 1) return;
+  const float* ws = a.ws + (long long)(base + kvh * nc) * 16 * (RV + 2);
+  for (int e = threadIdx.x; e < a.rep * RV; e += blockDim.x) {
     const int h = e / RV, r = e - h * RV;
     float M = NEG_INF;
-    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ws[(((long long)item * n_splits + s) * 16 + h) * (RV + 2) + RV]);
+    for (int s = 0; s < nc; ++s) M = fmaxf(M, ws[((long long)s * 16 + h) * (RV + 2) + RV]);
     float L = 0.f, acc = 0.f;
     if (M != NEG_INF) {
-      for (int s = 0; s < n_splits; ++s) {
-        const float* row = ws + (((long long)item * n_splits + s) * 16 + h) * (RV + 2);
+      for (int s = 0; s < nc; ++s) {
+        const float* row = ws + ((long long)s * 16 + h) * (RV + 2);
         const float f = __builtin_amdgcn_exp2f(row[RV] - M);
         L += row[RV + 1] * f;
         acc += row[r] * f;
       }
     }
-    OutT* o = static_cast<OutT*>(out) + ((long long)b * n_q + (long long)kvh * rep + h) * RV + r;
+    OutT* o = static_cast<OutT*>(a.out) + ((long long)b * a.n_q + (long long)kvh * a.rep + h) * RV + r;
     store_out(o, L > 0.f ? acc / L : 0.f);
   }
 }
@@ -749,15 +838,15 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
   constexpr int NW = pick_nw<RK, RV, KFULL, TILED>();
   DecodeArgs a = a0;
   const int items = a.B * a.n_kv;
-  const Plan p = plan_splits(items, a.S, NW);
-  a.split_len = p.split_len;
-  a.n_splits = p.n_splits;
-  const size_t need = ws_bytes(items, p.n_splits, RV);
+  a.n_wg = decode_workgroups(items);
+  a.balanced = a.n_wg > items ? 1 : 0;
+  if (!a.balanced) a.n_wg = items;
+  const size_t need = decode_ws_bytes(items, RV);
   if (need > 0 && (a.ws == nullptr || a.ws_bytes < need))
     return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_decode_workspace_bytes), got %zu", need, a.ws_bytes);
   using SM = Smem<RK, RV, KFULL, NW>;
   auto kern = palu_decode_kernel<RK, RV, KFULL, TILED, PAGED, NW, TabT, OutT>;
-  const int lds = SM::bytes(a.S) + (PAGED ? ((a.split_len >> 5 >> a.page_shift) + 2) * 4 : 0);
+  const int lds = SM::bytes(a.S) + (PAGED ? ((a.S >> 5 >> a.page_shift) + 2) * 4 : 0);
   if (lds > 160 * 1024) return fail(PALU_EUNSUPPORTED, "seq_len %d needs %d bytes of LDS (max 163840)", a.S, lds);
   static int attr_set = 0;
   if (attr_set < lds) {
@@ -765,12 +854,11 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
     if (e != hipSuccess) return fail(PALU_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
     attr_set = lds;
   }
-  hipLaunchKernelGGL(kern, dim3(a.n_splits, items), dim3(NW * 64), lds, stream, a);
+  hipLaunchKernelGGL(kern, dim3(a.n_wg), dim3(NW * 64), lds, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "decode kernel launch: %s", hipGetErrorString(e));
-  if (a.n_splits > 1) {
-    hipLaunchKernelGGL((palu_merge_kernel<RV, OutT>), dim3(items), dim3(256), 0, stream, a.ws, a.out, a.n_splits,
-                       a.rep, a.n_q, a.n_kv);
+  if (a.balanced) {
+    hipLaunchKernelGGL((palu_merge_kernel<RV, OutT>), dim3(items), dim3(256), 0, stream, a);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(PALU_EHIP, "merge kernel launch: %s", hipGetErrorString(e));
   }
