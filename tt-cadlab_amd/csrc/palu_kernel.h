@@ -135,7 +135,8 @@ inline size_t ws_bytes(int items, int n_splits, int rv) {
 inline int decode_workgroups(int items) { return ((items + TARGET_WGS - 1) / TARGET_WGS) * TARGET_WGS; }
 inline size_t decode_ws_bytes(int items, int rv) {
   const int wg = decode_workgroups(items);
-  return wg == items ? 0 : (size_t)wg * 16 * (rv + 2) * sizeof(float);
+  // partial slots [wg][16][rv + 2] floats, then one (first slot, chunk count) int pair per item
+  return wg == items ? 0 : (size_t)wg * 16 * (rv + 2) * sizeof(float) + (size_t)items * 2 * sizeof(int);
 }
 
 
@@ -354,6 +355,11 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     b = rb;
     kvh = fdiv(gid - base, fn);
     const int j = gid - base - kvh * n_chunks;
+    if (j == 0 && threadIdx.x == 0) {       // the item's entry for the merge kernel
+      int* ent = reinterpret_cast<int*>(a.ws + (long long)a.n_wg * 16 * (RV + 2)) + 2 * (b * a.n_kv + kvh);
+      ent[0] = gid;
+      ent[1] = n_chunks;
+    }
     s_lo = 64 * fdiv(j * np, fn);
     s_hi = min(row_len(a, b), 64 * fdiv((j + 1) * np, fn));
   }
@@ -801,35 +807,33 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   }
 }
 
-// Merge the chunk partials of every split item (length-aware plan): out = sum_s O_s 2^(m_s - M) /
-// sum_s l_s 2^(m_s - M) over the item's chunks, found by recomputing the plan. Items in one chunk
-// were written by the decode kernel itself.
+// Merge the chunk partials of every split item: out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)
+// over the item's chunks. One workgroup per (item, query head), one thread per output column; the
+// item's first chunk left (first slot, chunk count) after the partial slots. Items in one chunk were
+// written by the decode kernel itself.
 template <int RV, typename OutT>
-__global__ __launch_bounds__(256) void palu_merge_kernel(const DecodeArgs a) {
-  const int item = blockIdx.x;
+__global__ __launch_bounds__(RV) void palu_merge_kernel(const DecodeArgs a) {
+  const int item = blockIdx.x / a.rep, h = blockIdx.x - item * a.rep;
   const int b = item / a.n_kv, kvh = item - b * a.n_kv;
-  const FDiv fT = make_fdiv(plan_chunk_pairs(a));
-  int base = 0;
-  for (int r = 0; r < b; ++r) base += a.n_kv * max(1, ceil_fdiv(row_pairs(a, r), fT));
-  const int nc = max(1, ceil_fdiv(row_pairs(a, b), fT));
-  if (nc == 1) return;
-  const float* ws = a.ws + (long long)(base + kvh * nc) * 16 * (RV + 2);
-  for (int e = threadIdx.x; e < a.rep * RV; e += blockDim.x) {
-    const int h = e / RV, r = e - h * RV;
-    float M = NEG_INF;
-    for (int s = 0; s < nc; ++s) M = fmaxf(M, ws[((long long)s * 16 + h) * (RV + 2) + RV]);
-    float L = 0.f, acc = 0.f;
-    if (M != NEG_INF) {
-      for (int s = 0; s < nc; ++s) {
-        const float* row = ws + ((long long)s * 16 + h) * (RV + 2);
-        const float f = __builtin_amdgcn_exp2f(row[RV] - M);
-        L += row[RV + 1] * f;
-        acc += row[r] * f;
-      }
+  const int* ent = reinterpret_cast<const int*>(a.ws + (long long)a.n_wg * 16 * (RV + 2)) + 2 * item;
+  const int first = ent[0], nc = ent[1];
+  if (nc <= 1) return;
+  const int r = threadIdx.x;
+  const float* ws = a.ws + ((long long)first * 16 + h) * (RV + 2);
+  constexpr long long SLOT = 16 * (RV + 2);
+  float M = NEG_INF;
+  for (int s = 0; s < nc; ++s) M = fmaxf(M, ws[s * SLOT + RV]);
+  float L = 0.f, acc = 0.f;
+  if (M != NEG_INF) {
+    for (int s = 0; s < nc; ++s) {
+      const float* row = ws + s * SLOT;
+      const float f = __builtin_amdgcn_exp2f(row[RV] - M);
+      L += row[RV + 1] * f;
+      acc += row[r] * f;
     }
-    OutT* o = static_cast<OutT*>(a.out) + ((long long)b * a.n_q + (long long)kvh * a.rep + h) * RV + r;
-    store_out(o, L > 0.f ? acc / L : 0.f);
   }
+  OutT* o = static_cast<OutT*>(a.out) + ((long long)b * a.n_q + (long long)kvh * a.rep + h) * RV + r;
+  store_out(o, L > 0.f ? acc / L : 0.f);
 }
 
 
@@ -858,7 +862,7 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "decode kernel launch: %s", hipGetErrorString(e));
   if (a.balanced) {
-    hipLaunchKernelGGL((palu_merge_kernel<RV, OutT>), dim3(items), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((palu_merge_kernel<RV, OutT>), dim3(items * a.rep), dim3(RV), 0, stream, a);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(PALU_EHIP, "merge kernel launch: %s", hipGetErrorString(e));
   }
