@@ -73,7 +73,8 @@ inline GlrdPlan glrd_plan(int B, int n_q, int n_kv, int n_groups, int S, int rv)
 // LDS map (KBP = rank blocks rounded up to even):
 //   ukt   u_k^T slice as A tiles [row tile 4][rank block KBP][lane] bf16x8 (zero past r_k); at least
 //         32 KB, because the prologue stages cs_tab rows 0..63 ([t][f] float2) in the same place
-//   rtab  pair-relative K rotation [block of pair 2][tile c 2][row tile 4][lane] float4     16 KB
+//   rtab  pair-relative K rotation [block of pair 2][tile c 2][row tile 4][lane] fp16 x 8
+//         {cos f, cos f, -sin f, sin f, cos f+1, cos f+1, -sin f+1, sin f+1}              16 KB
 //   tl    (cos, sin) of angle 64*Lo*f, Lo < 16                                              8 KB
 //   qs    the KV head's query rows, padded to G_QS                                    16 x G_QS bf16
 //   th    (cos, sin) of angle 1024*H*f, H < ceil(S / 1024)                         S/1024 x 512 B
@@ -95,7 +96,7 @@ __global__ __launch_bounds__(G_NWS * 64) void palu_glrd_scores_kernel(const Deco
   extern __shared__ __attribute__((aligned(16))) char smem[];
   bf16x8* ukt = reinterpret_cast<bf16x8*>(smem + SM::UKT);
   float2* kc = reinterpret_cast<float2*>(smem + SM::UKT);
-  float4* rtab = reinterpret_cast<float4*>(smem + SM::RTAB);
+  f16x8* rtab = reinterpret_cast<f16x8*>(smem + SM::RTAB);
   float2* tl = reinterpret_cast<float2*>(smem + SM::TL);
   float2* th = reinterpret_cast<float2*>(smem + SM::TH);
   __bf16* qs_lds = reinterpret_cast<__bf16*>(smem + SM::QS);
@@ -172,8 +173,9 @@ __global__ __launch_bounds__(G_NWS * 64) void palu_glrd_scores_kernel(const Deco
       const int nn = l & 15, gg = l >> 4;
       const int t = 32 * hb + 8 * (nn >> 2) + 4 * c + (nn & 3);
       const int f = 32 * dpart + 8 * rt + 2 * gg;
-      const float2 x = kc[t * 64 + f], y = kc[t * 64 + f + 1];
-      rtab[e] = make_float4(x.x, x.y, y.x, y.y);
+      const float2 x = kc[t * 64 + f], y = kc[t * 64 + f + 1];   // (cos, sin) of frequencies f, f + 1
+      rtab[e] = f16x8{(_Float16)x.x, (_Float16)x.x, (_Float16)-x.y, (_Float16)x.y,
+                      (_Float16)y.x, (_Float16)y.x, (_Float16)-y.y, (_Float16)y.y};
     }
     __syncthreads();                                    // kc is overwritten by the u_k^T tiles below
     // u_k^T tiles: tile (rt, kb) lane (m, g) element j = u_k[rank 32 kb + 8 g + j][dim 64 dpart + 16 rt + m].
@@ -210,10 +212,10 @@ __global__ __launch_bounds__(G_NWS * 64) void palu_glrd_scores_kernel(const Deco
     }
   };
 
-  // Query of this KV head rotated back by the pair base, scaled by scale * log2 e, as the B operand of
-  // the QK MFMA for the rebuilt dims 32 t + {4g .. 4g+3, 16+4g .. 16+4g+3} of this half (the order the
-  // packed K^T accumulators give the A operand).
-  auto make_q = [&](int base, bf16x8 (&qB)[2]) {
+  // Query of this KV head rotated back by the pair base, scaled by scale * log2 e, in fp16 as the B
+  // operand of the QK MFMA for the rebuilt dims 32 t + {4g .. 4g+3, 16+4g .. 16+4g+3} of this half (the
+  // order the packed K^T slices give the A operand).
+  auto make_q = [&](int base, f16x8 (&qB)[2]) {
     const int J = base >> 6;
     const float2* lo = tl + (J & 15) * 64;
     const float2* hi = th + (J >> 4) * 64;
@@ -231,8 +233,8 @@ __global__ __launch_bounds__(G_NWS * 64) void palu_glrd_scores_kernel(const Deco
           const float cf = (hc[p] * lc[p] - hs[p] * ls[p]) * a.qscale;
           const float sf = (hs[p] * lc[p] + hc[p] * ls[p]) * a.qscale;
           const float x0 = (float)qv[2 * p], x1 = (float)qv[2 * p + 1];
-          qB[t][4 * half + 2 * p] = (__bf16)(x0 * cf + x1 * sf);      // R_{-base}
-          qB[t][4 * half + 2 * p + 1] = (__bf16)(x1 * cf - x0 * sf);
+          qB[t][4 * half + 2 * p] = (_Float16)(x0 * cf + x1 * sf);      // R_{-base}
+          qB[t][4 * half + 2 * p + 1] = (_Float16)(x1 * cf - x0 * sf);
         }
       }
     }
@@ -243,7 +245,7 @@ __global__ __launch_bounds__(G_NWS * 64) void palu_glrd_scores_kernel(const Deco
 #pragma unroll
   for (int kb = 0; kb < R; ++kb) load_kb(w, kb, ring[kb]);
   for (int pp = w; pp < npairs; pp += G_NWS) {
-    bf16x8 qB[2];
+    f16x8 qB[2];
     make_q(s_lo + pp * 2 * BLK, qB);
     f32x4 acc[4][G_RT];
 #pragma unroll
@@ -270,20 +272,25 @@ __global__ __launch_bounds__(G_NWS * 64) void palu_glrd_scores_kernel(const Deco
       else load_kb(pp + G_NWS, kb + R - KBP, ring[slot]);
       __builtin_amdgcn_sched_barrier(0);                 // keep the reads of one rank block ahead, not more
     }
-    // rotate, pack, contract with the query: scores of 16 positions x 16 heads per (block, tile c)
+    // Rotate in packed fp16 ((x0, x1) * (c, c) + (x1, x0) * (-s, s): one multiply and one fma per pair,
+    // fp32 -> fp16 rounded toward zero so finite values saturate), then contract with the query on the
+    // fp16 MFMA: scores of 16 positions x 16 heads per (block, tile c).
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
+      f16x2 r[G_RT][2];
 #pragma unroll
       for (int rt = 0; rt < G_RT; ++rt) {
-        const float4 t = rtab[(cc * G_RT + rt) * 64 + lane];
-        const float x0 = acc[cc][rt][0], x1 = acc[cc][rt][1], x2 = acc[cc][rt][2], x3 = acc[cc][rt][3];
-        acc[cc][rt][0] = x0 * t.x - x1 * t.y;
-        acc[cc][rt][1] = x1 * t.x + x0 * t.y;
-        acc[cc][rt][2] = x2 * t.z - x3 * t.w;
-        acc[cc][rt][3] = x3 * t.z + x2 * t.w;
+        const f16x8 t = rtab[(cc * G_RT + rt) * 64 + lane];
+        const f16x2 c0 = {t[0], t[1]}, s0 = {t[2], t[3]}, c1 = {t[4], t[5]}, s1 = {t[6], t[7]};
+        const f16x2 x01 = to_f16x2(acc[cc][rt][0], acc[cc][rt][1]);
+        const f16x2 x23 = to_f16x2(acc[cc][rt][2], acc[cc][rt][3]);
+        r[rt][0] = x01 * c0 + x01.yx * s0;
+        r[rt][1] = x23 * c1 + x23.yx * s1;
       }
-      f32x4 sc = mfma16(pack8(acc[cc][0], acc[cc][1]), qB[0], f32x4{0.f, 0.f, 0.f, 0.f});
-      sc = mfma16(pack8(acc[cc][2], acc[cc][3]), qB[1], sc);
+      const f16x8 k0 = {r[0][0][0], r[0][0][1], r[0][1][0], r[0][1][1], r[1][0][0], r[1][0][1], r[1][1][0], r[1][1][1]};
+      const f16x8 k1 = {r[2][0][0], r[2][0][1], r[2][1][0], r[2][1][1], r[3][0][0], r[3][0][1], r[3][1][0], r[3][1][1]};
+      f32x4 sc = mfma16(k0, qB[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      sc = mfma16(k1, qB[1], sc);
       const int hb = cc >> 1, c = cc & 1;
       const int blk = 2 * pp + hb;
       // lane (head n, g) holds positions 8g + 4c .. +3 of block blk
