@@ -131,6 +131,49 @@ def test_deterministic_mode_repeats_and_default_mode_agrees(gpu, B, S):
         assert ref.max_abs(d, a) <= 5e-3 and ref.cosine(d, a) >= 0.99999
 
 
+def _skewed_positions(B, S, seed):
+    """One row at the cache end, empty rows (cur_pos -1: nothing attended, output zero), one-token and
+    block-edge rows, and random lengths for the rest: the length-aware chunk plan gives every item at
+    least one chunk and cuts the long rows into many."""
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.randint(0, S, (B,), generator=g)
+    fixed = [S - 1, -1, 0, 31, 32, -1, 63, 64]
+    pos[:min(B, len(fixed))] = torch.tensor(fixed[:min(B, len(fixed))])
+    return pos
+
+
+@pytest.mark.parametrize("B,S", [(33, 256), (40, 160), (6, 4096), (9, 2048)])
+def test_length_aware_plan_skewed_rows(gpu, B, S):
+    """Chunk plan envelope: 33 and 40 rows x 8 KV heads are more items than one chip-fill of 256
+    workgroups and not a multiple of it (512 workgroups, items cut in about two), and short batches with
+    one long row among empty and one-token rows; deterministic mode stays bit-reproducible under the plan."""
+    q, k_lat, u_k, v, _, cos, sin = _inputs(B, S, 64, 64, seed=B)
+    pos = _skewed_positions(B, S, seed=S)
+    exp = ref.reference_decode(q, k_lat, u_k, v, pos, cos, sin, HD ** -0.5)
+    assert torch.equal(exp[0, 1], torch.zeros_like(exp[0, 1]))        # the empty row attends nothing
+    out = _run_fused(gpu, q, k_lat, u_k, v, pos, cos, sin, S)
+    _check(out, exp)
+    assert torch.equal(out[0, 1], torch.zeros_like(out[0, 1]))
+    a = _run_fused(gpu, q, k_lat, u_k, v, pos, cos, sin, S, deterministic=True)
+    assert torch.equal(a, _run_fused(gpu, q, k_lat, u_k, v, pos, cos, sin, S, deterministic=True))
+    _check(a, exp)
+
+
+@pytest.mark.parametrize("B,S", [(33, 256), (6, 4096)])
+def test_stock_decode_length_aware_plan_skewed_rows(gpu, B, S):
+    """The stock full-KV decode shares the chunk plan: same skewed batches against the full-KV oracle."""
+    g = torch.Generator().manual_seed(B + S)
+    q = _bf(torch.randn(1, B, 32, HD, generator=g))
+    k = _bf(torch.randn(B, 8, S, HD, generator=g))
+    v = _bf(torch.randn(B, 8, S, HD, generator=g))
+    pos = _skewed_positions(B, S, seed=S + 1)
+    exp = ref.full_kv_decode(q, k, v, pos, HD ** -0.5)
+    out = fused.flash_decode(q.to(gpu, torch.bfloat16), k.to(gpu, torch.bfloat16), v.to(gpu, torch.bfloat16),
+                             pos.to(gpu, torch.int32), scale=HD ** -0.5, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _check(out.cpu(), exp)
+
+
 def test_fused_headline_shape_full_size(gpu):
     """B=32, 32 Q / 8 KV, every row at context 8192, r_k = r_v = 64 (the headline workload), against
     the oracle at full size."""

@@ -118,6 +118,19 @@ def test_paged_mixed_ranks_long_ragged_rows(gpu, r_k, r_v):
     _check(_decode(gpu, q, kp, vp, u_k, pos, pt, S, "tiled"), exp)
 
 
+def test_paged_skewed_rows_more_items_than_one_fill(gpu):
+    """Length-aware chunk plan over pages: 34 rows x 8 KV heads (272 items: 512 workgroups), lengths from
+    one token to the whole cache, 64-token pages in a shuffled pool."""
+    B, S, ps = 34, 512, 64
+    g = torch.Generator().manual_seed(77)
+    lengths = torch.randint(1, S + 1, (B,), generator=g).tolist()
+    lengths[0], lengths[1], lengths[2] = S, 1, 33
+    q, k, v, u_k, pos, kp, vp, pt = _case(B, S, 64, 64, ps, seed=5, lengths=lengths)
+    cos, sin = ref.cos_sin_tables(HD, S, THETA, LLAMA3)
+    exp = ref.reference_decode(q, k, u_k, v, pos, cos, sin, HD ** -0.5)
+    _check(_decode(gpu, q, kp, vp, u_k, pos, pt, S, "tiled"), exp)
+
+
 @pytest.mark.parametrize("layout", ["rows", "tiled"])
 def test_paged_append_then_decode(gpu, layout):
     """Append one new latent row per sequence through the page table, then decode at that position."""
