@@ -237,8 +237,14 @@ __device__ __forceinline__ int fdiv(int n, FDiv f) {
 }
 __device__ __forceinline__ int ceil_fdiv(int n, FDiv f) { return fdiv(n + f.d - 1, f); }
 
+// A uniform int32 read through the scalar path (the data is not written during the kernel): it waits on
+// the scalar counter, so vector loads issued around it are not held up by it.
+__device__ __forceinline__ int load_uniform(const int32_t* p, long long i) {
+  return reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(reinterpret_cast<uintptr_t>(p))[i];
+}
+
 __device__ __forceinline__ int row_len(const DecodeArgs& a, int b) {
-  const int len = a.cur_pos[b] + 1;
+  const int len = load_uniform(a.cur_pos, b) + 1;
   return len < 0 ? 0 : (len > a.S ? a.S : len);
 }
 __device__ __forceinline__ int row_pairs(const DecodeArgs& a, int b) { return (row_len(a, b) + 63) >> 6; }
@@ -382,7 +388,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   auto clamp_page = [&](int p) { return p < 0 ? 0 : (p >= a.n_pages ? a.n_pages - 1 : p); };
   auto page_global = [&](int base) -> int {
     if constexpr (!PAGED) return 0;
-    return clamp_page(a.page_table[(long long)b * a.pt_stride + ((base >> 5) >> a.page_shift)]);
+    return clamp_page(load_uniform(a.page_table, (long long)b * a.pt_stride + ((base >> 5) >> a.page_shift)));
   };
   auto page_lds = [&](int base) -> int {
     if constexpr (!PAGED) return 0;
@@ -460,21 +466,35 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       t = (r < n_rows && t < a.cs_rows) ? t : 0;
       rowv[i] = load4f(cs + (long long)t * (2 * HD) + 4 * lane);   // lane < 32: cos, else sin
     }
+    // Every prologue load below is unconditional, its index clamped into the tensor: a load under a
+    // branch makes the compiler wait for all outstanding loads where the branch joins, which would hold
+    // the first latent block back until the tables had arrived.
     constexpr int UPT = (RK * (HD / 8) + NW * 64 - 1) / (NW * 64);
     bf16x8 ukv[UPT];
     const __bf16* ukp = a.w_rot + (long long)kvh * RK * (2 * HD);
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
-      const int e = tid + i * NW * 64;   // consecutive lanes: consecutive ranks, one 8-column block
-      if (e < RK * (HD / 8)) ukv[i] = *reinterpret_cast<const bf16x8*>(ukp + (long long)(e % RK) * (2 * HD) + (e / RK) * 8);
+      int e = tid + i * NW * 64;         // consecutive lanes: consecutive ranks, one 8-column block
+      e = e < RK * (HD / 8) ? e : 0;
+      ukv[i] = *reinterpret_cast<const bf16x8*>(ukp + (long long)(e % RK) * (2 * HD) + (e / RK) * 8);
     }
-    // query rows: 16 heads x 256 B, 16 bytes per thread for the first 256 threads
-    bf16x8 qrow = bf16x8{};
+    // query rows: 16 heads x 256 B, 16 bytes per thread for the first 256 threads (zero rows past rep)
     const int qh = tid >> 4, qc = (tid & 15) * 8;
-    if (tid < 16 * (HD / 8) && qh < a.rep)
-      qrow = *reinterpret_cast<const bf16x8*>(a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + qh) * HD + qc);
-    if (w < npairs) load_blk(s_lo + 2 * w * BLK, true, page_global(s_lo + 2 * w * BLK), kl, vl);
-    if (tid < 16 * (HD / 8)) *reinterpret_cast<bf16x8*>(qs_lds + qh * HD + qc) = qrow;
+    const bool qlive = tid < 16 * (HD / 8) && qh < a.rep;
+    const bf16x8 qrow = *reinterpret_cast<const bf16x8*>(
+        a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + (qlive ? qh : 0)) * HD + (qlive ? qc : 0));
+    // The wave's first block, issued before the row length is known (a wave whose first pair lies past
+    // the row's data loads a block inside the cache instead and never uses it) and after every table
+    // load: loads complete in issue order for the wait counter, so the prologue's waits on the tables
+    // then leave this block in flight. The scheduling fences keep that order.
+    {
+      const int fb = min(s_lo + 2 * w * BLK, ((a.S - 1) / BLK) * BLK);
+      const int pid = page_global(fb);
+      __builtin_amdgcn_sched_barrier(0);
+      load_blk(fb, true, pid, kl, vl);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (tid < 16 * (HD / 8)) *reinterpret_cast<bf16x8*>(qs_lds + qh * HD + qc) = qlive ? qrow : bf16x8{};
     // rows -> [row][f] (cos, sin); lane l < 32 holds cos of f = 2l, 2l+1, lane l >= 32 the sines
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
@@ -510,7 +530,8 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
                       (_Float16)y.x, (_Float16)y.x, (_Float16)-y.y, (_Float16)y.y};
     }
   } else {
-    if (w < npairs) load_blk(s_lo + 2 * w * BLK, true, page_global(s_lo + 2 * w * BLK), kl, vl);
+    const int fb = min(s_lo + 2 * w * BLK, ((a.S - 1) / BLK) * BLK);
+    load_blk(fb, true, page_global(fb), kl, vl);
   }
   if constexpr (PAGED) {
     const int pg_hi = nblk > 0 ? (((s_hi - 1) >> 5) >> a.page_shift) : pg_lo - 1;
