@@ -119,3 +119,15 @@ def test_glrd_deterministic_repeat(gpu):
     a = _run(gpu, *args, 2048)
     b = _run(gpu, *args, 2048)
     assert torch.equal(a, b)
+
+
+def test_pinned_heads_per_core_that_does_not_fit_the_grid_is_rejected(gpu):
+    """A pinned heads_per_core is checked against the program config's core grid
+    (reference tests/test_palu_sdpa_device.py:490-503): batch 4 of one group of 4 KV heads on a 2 x 2
+    grid, 2 heads per core, wants 8 cores and is rejected before any launch; 4 heads per core (the whole
+    group on one core, 4 items) fits and decodes to the oracle."""
+    args = _case(4, 256, 128, 128, hpg=4, seed=21, nh=16, nkv=4)
+    cfg = fused.SDPAProgramConfig(compute_with_storage_grid_size=(2, 2), k_chunk_size=128)
+    with pytest.raises(RuntimeError, match="only 4 available"):
+        _run(gpu, *args, 256, heads_per_core=2, program_config=cfg)
+    _check(_run(gpu, *args, 256, heads_per_core=4, program_config=cfg), _oracle(*args, 256))

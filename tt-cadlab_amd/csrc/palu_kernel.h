@@ -9,7 +9,8 @@
 // ttnn.transformer.palu_sdpa_decode (docs/superpowers/specs/2026-09-10-palu-tt-stage2-design.md:47-81,
 // fp32 model palu_tt/fused.py:82-107).
 //
-// Kernel shape (all MFMA work is v_mfma_f32_16x16x32_bf16, bf16 in / fp32 accumulate):
+// Kernel shape (MFMA work is v_mfma_f32_16x16x32_bf16 for the K rebuild and PV, _f16 for QK against
+// the fp16 rotated K; fp32 accumulate):
 //   * A workgroup owns one item and one split of its sequence. Its NW waves take pairs of 32-position
 //     blocks from an LDS counter (or, in deterministic mode, every NW-th pair) and stream each block
 //     from HBM straight into registers, the next block's loads in flight while the current one is
@@ -22,21 +23,23 @@
 //   * K is rebuilt transposed, K^T[d][p] = u_k^T[d][:] . lat[p][:], one 32-dim slice at a time: the
 //     accumulator layout gives every lane one position and 4 consecutive head dims per 16-dim tile, so
 //     each RoPE pair (Meta-interleaved dims 2f, 2f+1) sits in one lane and the rotation is plain VALU
-//     work on the fp32 accumulators.
+//     work: each fp32 accumulator pair is converted to fp16 (round toward zero, saturating) and
+//     rotated with packed fp16 multiplies.
 //   * RoPE is applied pair-relative: K rows are rotated by their offset t < 64 inside a pair of
 //     blocks (an LDS table in lane order), and the query is rotated back by the pair base once per
 //     pair, q~ = R_{-base} q, with cos/sin of the base built by angle addition from two small LDS
 //     tables (base = 1024 H + 64 Lo). Rotations in one plane commute, so q~ . R_t k = q . R_{base+t} k,
 //     the score of the reference.
-//   * The rebuilt K slice is packed to bf16 in registers and used as the A operand of the QK MFMA; the
-//     head dim is contracted in a permuted order that the query operand mirrors, so no lane shuffles
-//     are needed.
+//   * The rotated fp16 K slice is the A operand of the QK MFMA as it stands; the head dim is
+//     contracted in a permuted order that the query operand mirrors, so no lane shuffles are needed.
 //   * Scores come out with one head per lane column. The online softmax runs in the exp2 domain
 //     (scale * log2 e folded into q~) with a lazily refreshed running max, and the probabilities feed
 //     the PV MFMA directly as its B operand. TILED V is already the PV A operand; ROWS V is regrouped
 //     by an MFMA against an identity tile (exact in bf16).
-//   * The waves of a workgroup merge their (O, m, l) partials in LDS; several splits of one item are
-//     merged by a second small kernel through a caller-provided workspace.
+//   * The waves of a workgroup merge their (O, m, l) partials in LDS. When B * n_kv is not a whole
+//     number of chip-fills, items are cut into length-aware chunks (planned on the device from
+//     cur_pos) and the chunks of one item are merged by a second small kernel through a
+//     caller-provided workspace.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -411,43 +414,68 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   // (past the wave's last block) still issues the same instructions, at the block given, with every
   // lane on the block's first bytes (TILED), so the number of loads in flight is the same on every
   // path; its data is never used.
-  auto load_blk = [&](int base, bool live, int pid, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[VT]) {
+  auto row_in_blk = [&](int base, int c) {
+    int t = 8 * (n >> 2) + 4 * c + (n & 3);     // position in the block
+    if (!PAGED && base + t >= a.S) t = a.S - 1 - base;   // a page always holds whole blocks
+    return t;
+  };
+  auto load_k = [&](int base, bool live, int pid, bf16x8 (&kd)[2][KB]) {
     if constexpr (TILED) {
-      const int lo = live ? lane * 8 : 0;
-      const __bf16* kt = kbase + blk_off(base, pid, a.k_sb, RK) + lo;
-      const __bf16* vt = vbase + blk_off(base, pid, a.v_sb, RV) + lo;
+      const __bf16* kt = kbase + blk_off(base, pid, a.k_sb, RK) + (live ? lane * 8 : 0);
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
           kd[c][kb] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(kt + (c * KB + kb) * 512));
+    } else {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const __bf16* kr = kbase + blk_off(base, pid, a.k_sb, RK) + (long long)row_in_blk(base, c) * RK + 8 * g;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) kd[c][kb] = *reinterpret_cast<const bf16x8*>(kr + 32 * kb);
+      }
+    }
+  };
+  auto load_v = [&](int base, bool live, int pid, bf16x8 (&vd)[VT]) {
+    if constexpr (TILED) {
+      const __bf16* vt = vbase + blk_off(base, pid, a.v_sb, RV) + (live ? lane * 8 : 0);
 #pragma unroll
       for (int mt = 0; mt < VT; ++mt)
         vd[mt] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(vt + mt * 512));
     } else {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        int t = 8 * (n >> 2) + 4 * c + (n & 3);     // position in the block
-        if (!PAGED && base + t >= a.S) t = a.S - 1 - base;   // a page always holds whole blocks
-        const __bf16* kr = kbase + blk_off(base, pid, a.k_sb, RK) + (long long)t * RK + 8 * g;
-        const __bf16* vr = vbase + blk_off(base, pid, a.v_sb, RV) + (long long)t * RV + 8 * g;
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) kd[c][kb] = *reinterpret_cast<const bf16x8*>(kr + 32 * kb);
+        const __bf16* vr = vbase + blk_off(base, pid, a.v_sb, RV) + (long long)row_in_blk(base, c) * RV + 8 * g;
 #pragma unroll
         for (int vb = 0; vb < VB; ++vb) vd[c * VB + vb] = *reinterpret_cast<const bf16x8*>(vr + 32 * vb);
       }
     }
+  };
+  auto load_blk = [&](int base, bool live, int pid, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[VT]) {
+    load_k(base, live, pid, kd);
+    load_v(base, live, pid, vd);
   };
 
   // Work is handed out in pairs of full blocks (pair p = blocks 2p, 2p + 1) from an LDS counter, so
   // that the waves of a workgroup finish together (which wave sums which blocks then depends on
   // timing, and each wave rounds its probabilities to bf16 against its own running max, so calls
   // differ at that rounding level); wave w starts on pair w. The deterministic schedule gives wave w
-  // every NW-th pair. A partial last block is taken by wave NW - 1 after its pairs.
+  // every NW-th pair. The loop runs complete pairs only; the one or two blocks left after them (an odd
+  // full block, a partial last block) go to the wave whose next pair index is npairs, which exactly
+  // one wave holds when the loop ends (the indices are w < NW, then counter values NW, NW + 1, ...).
   const int nfull = s_hi > s_lo ? (s_hi - s_lo) / BLK : 0;   // an empty split (row shorter than s_lo) has none
-  const int npairs = (nfull + 1) >> 1;
+  const int npairs = nfull >> 1;
   if (tid == 0) *ctr = NW;
   bf16x8 kl[2][KB], vl[VT], kln[2][KB], vln[VT];
+  auto fence = []() __attribute__((always_inline)) { __builtin_amdgcn_sched_barrier(0); };
+  // Block i (0, 1) of the wave's first pair, clamped inside the cache.
+  auto load_first = [&](int i, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[VT]) {
+    const int f = min(s_lo + (2 * w + i) * BLK, ((a.S - 1) / BLK) * BLK);
+    const int pid = page_global(f);
+    fence();
+    load_blk(f, true, pid, kd, vd);
+    fence();
+  };
 
   // ---- prologue ----------------------------------------------------------------------------------
   // Latent mode: the angle tables and u_k^T go to LDS. The tables come from whole rows of cs_tab, one
@@ -486,14 +514,9 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     // The wave's first block, issued before the row length is known (a wave whose first pair lies past
     // the row's data loads a block inside the cache instead and never uses it) and after every table
     // load: loads complete in issue order for the wait counter, so the prologue's waits on the tables
-    // then leave this block in flight. The scheduling fences keep that order.
-    {
-      const int fb = min(s_lo + 2 * w * BLK, ((a.S - 1) / BLK) * BLK);
-      const int pid = page_global(fb);
-      __builtin_amdgcn_sched_barrier(0);
-      load_blk(fb, true, pid, kl, vl);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    // then leave this block in flight. The scheduling fences keep that order. The pair's second block
+    // follows once the table registers are written out.
+    load_first(0, kl, vl);
     if (tid < 16 * (HD / 8)) *reinterpret_cast<bf16x8*>(qs_lds + qh * HD + qc) = qlive ? qrow : bf16x8{};
     // rows -> [row][f] (cos, sin); lane l < 32 holds cos of f = 2l, 2l+1, lane l >= 32 the sines
 #pragma unroll
@@ -518,6 +541,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
         for (int j = 0; j < 8; ++j) ukT[(d0 + j) * SM::UKT_STRIDE + r] = ukv[i][j];
       }
     }
+    load_first(1, kln, vln);
     __syncthreads();
     // K rotation table in lane order from the staged rows 0..63
     for (int e = tid; e < 2 * 2 * 8 * 64; e += NW * 64) {
@@ -530,8 +554,8 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
                       (_Float16)y.x, (_Float16)y.x, (_Float16)-y.y, (_Float16)y.y};
     }
   } else {
-    const int fb = min(s_lo + 2 * w * BLK, ((a.S - 1) / BLK) * BLK);
-    load_blk(fb, true, page_global(fb), kl, vl);
+    load_first(0, kl, vl);
+    load_first(1, kln, vln);
   }
   if constexpr (PAGED) {
     const int pg_hi = nblk > 0 ? (((s_hi - 1) >> 5) >> a.page_shift) : pg_lo - 1;
@@ -639,8 +663,10 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
 
   // One block of 32 positions from the buffers (kc, vc). Only the last block of a range can be
   // partial; it runs the masked variant (PARTIAL), every other block carries no masking work.
-  auto compute = [&](auto partial_tag, int blk, const bf16x8 (&kc)[2][KB], const bf16x8 (&vc)[VT])
-                     __attribute__((always_inline)) {
+  // after_k() runs once the K registers are consumed (scores done), before the softmax and PV: the
+  // loop refills the K buffer there.
+  auto compute = [&](auto partial_tag, int blk, const bf16x8 (&kc)[2][KB], const bf16x8 (&vc)[VT],
+                     auto&& after_k) __attribute__((always_inline)) {
     constexpr bool PARTIAL = decltype(partial_tag)::value;
     const int base = s_lo + blk * BLK;
     const int hb = blk & 1;               // which block of its pair (s_lo is a multiple of 64)
@@ -655,6 +681,11 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       // One 32-dim slice of K^T (row tiles 2*kq, 2*kq + 1) at a time, for both position tiles:
       // rebuild, rotate, pack, and contract it with the matching query slice right away, so only
       // 16 accumulator registers are live instead of a whole 128 x 16 tile.
+      // u_k^T rows from LDS (r_k > 64): the lane's row offset passes through an empty asm per block, so
+      // the compiler re-reads the tiles where they are used instead of hoisting every tile of the
+      // loop-invariant table into registers.
+      int uk_off = n * SM::UKT_STRIDE + 8 * g;
+      if constexpr (UK_LDS) asm volatile("" : "+v"(uk_off));
 #pragma unroll
       for (int kq = 0; kq < 4; ++kq) {
         f32x4 acc[2][2];
@@ -669,7 +700,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
             const int rt = 2 * kq + h;
             bf16x8 ua;
             if constexpr (UK_LDS)
-              ua = *reinterpret_cast<const bf16x8*>(ukT + (16 * rt + n) * SM::UKT_STRIDE + 32 * kb + 8 * g);
+              ua = *reinterpret_cast<const bf16x8*>(ukT + uk_off + 16 * rt * SM::UKT_STRIDE + 32 * kb);
             else
               ua = ukA[rt][kb];
 #pragma unroll
@@ -696,6 +727,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
         }
       }
     }
+    after_k();
 
     // Causal / range mask: score register i of tile c is position base + 8*g + 4*c + i.
     if constexpr (PARTIAL) {
@@ -757,9 +789,15 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
 
   const std::integral_constant<bool, false> full_blk;
   const std::integral_constant<bool, true> partial_blk;
-  // Pair loop: (kl, vl) holds block 2p on entry, (kln, vln) receives block 2p + 1. Every load is
-  // issued unconditionally and the loop has a single exit, so the compiler waits on exactly the
-  // loads of the block about to be used while the next block streams in.
+  // Pair loop. On entry the loads of pair p are issued: block 2p into (kl, vl), block 2p + 1 into
+  // (kln, vln). Each buffer is refilled with the next pair's block as soon as its part is consumed: K
+  // once the block's scores are done, V once its PV product is. Every load is issued unconditionally
+  // (a dummy in-cache address when there is no next pair) and the loop body has no other branch, so
+  // the compiler waits on exactly the loads a step consumes while about two blocks stream in.
+  // The early K refill keeps one more K buffer live through the softmax and PV; it is used where
+  // that still fits the register budget without spilling (full K, r_k <= 64, r_k + r_v <= 192; the
+  // rest refill K together with V after the PV product).
+  constexpr bool EARLY_K = KFULL || RK <= 64 || RK + RV <= 192;
   int p = w;
   while (p < npairs) {
     int pn = p + NW;
@@ -770,23 +808,35 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       pn = __builtin_amdgcn_readfirstlane(got);
     }
     const int b0 = 2 * p;
-    const bool has1 = b0 + 1 < nfull;
-    const int base1 = s_lo + (has1 ? b0 + 1 : b0) * BLK;
-    load_blk(base1, has1, page_lds(base1), kln, vln);
-    __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of the compute it overlaps
-    if constexpr (!KFULL) make_q(s_lo + b0 * BLK);   // one query rotation serves both blocks of the pair
-    compute(full_blk, b0, kl, vl);
     const bool hasn = pn < npairs;
-    const int basen = s_lo + (hasn ? 2 * pn : b0) * BLK;
-    load_blk(basen, hasn, page_lds(basen), kl, vl);
-    __builtin_amdgcn_sched_barrier(0);
-    if (has1) compute(full_blk, b0 + 1, kln, vln);
+    const int nb0 = s_lo + (hasn ? 2 * pn : b0) * BLK, nb1 = nb0 + BLK;
+    const int pid0 = page_lds(nb0), pid1 = page_lds(nb1);
+    if constexpr (!KFULL) make_q(s_lo + b0 * BLK);   // one query rotation serves both blocks of the pair
+    compute(full_blk, b0, kl, vl, [&] {
+      if constexpr (EARLY_K) { fence(); load_k(nb0, hasn, pid0, kl); fence(); }
+    });
+    fence();
+    if constexpr (!EARLY_K) load_k(nb0, hasn, pid0, kl);
+    load_v(nb0, hasn, pid0, vl);
+    fence();
+    compute(full_blk, b0 + 1, kln, vln, [&] {
+      if constexpr (EARLY_K) { fence(); load_k(nb1, hasn, pid1, kln); fence(); }
+    });
+    fence();
+    if constexpr (!EARLY_K) load_k(nb1, hasn, pid1, kln);
+    load_v(nb1, hasn, pid1, vln);
+    fence();
     p = pn;
   }
-  if (nfull < nblk && w == NW - 1) {     // the partial last block
-    load_blk(s_lo + nfull * BLK, true, page_lds(s_lo + nfull * BLK), kl, vl);
-    if constexpr (!KFULL) make_q(s_lo + (nfull & ~1) * BLK);
-    compute(partial_blk, nfull, kl, vl);
+  if (p == npairs) {   // an odd full block and / or the partial last block, one at a time
+    auto none = [] {};
+    for (int e = 2 * npairs; e < nblk; ++e) {
+      const int base = s_lo + e * BLK;
+      load_blk(base, true, page_lds(base), kl, vl);
+      if constexpr (!KFULL) make_q(s_lo + (e & ~1) * BLK);
+      if (e < nfull) compute(full_blk, e, kl, vl, none);
+      else compute(partial_blk, e, kl, vl, none);
+    }
   }
 
   // ---- merge the NW wave partials of this workgroup ---------------------------------------------
