@@ -612,10 +612,12 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
       x.s[2] = *reinterpret_cast<const float4*>(p0 + half_stride);
       x.s[3] = *reinterpret_cast<const float4*>(p0 + half_stride + 4);
     }
+    // The V latent is read once per decode step (one workgroup per row, group and split): nontemporal.
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int mt = tg * TPW + i;
-      x.v[i] = *reinterpret_cast<const bf16x8*>(vbase + (long long)jj * (32 * a.rv) + (mt < VT ? mt : 0) * 512);
+      x.v[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const bf16x8*>(vbase + (long long)jj * (32 * a.rv) + (mt < VT ? mt : 0) * 512));
     }
   };
 
