@@ -417,19 +417,28 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
       }
     }
     __syncthreads();                                    // kc is overwritten by the u_k^T tiles below
-    // u_k^T tiles: tile (rt, kb) lane (m, g) element j = u_k[rank 32 kb + 8 g + j][dim 16 rt + m]. Each
-    // thread reads 8 consecutive dims of one rank row (16 B) and scatters them.
-    const __bf16* ukp = a.w_rot + (long long)kvh * a.rk * (2 * HD);
-    __bf16* ukt16 = reinterpret_cast<__bf16*>(ukt);
-    for (int e = tid; e < KBP * 32 * (HD / 8); e += G2_NW * 64) {
-      const int r = e >> 4, d8 = (e & 15) * 8;
-      bf16x8 v = bf16x8{};
-      if (r < a.rk) v = *reinterpret_cast<const bf16x8*>(ukp + (long long)r * (2 * HD) + d8);
-      const int kb = r >> 5, gg = (r >> 3) & 3, j = r & 7;
+    // u_k^T tiles: tile (rt, kb) lane (m, gg) element j = u_k[rank 32 kb + 8 gg + j][dim 16 rt + m]. Wave
+    // w stages rank blocks kb = w, w + G2_NW, ...; its lane (gg, mh, rt) reads ranks 32 kb + 8 gg .. +7 at
+    // dims 16 rt + 8 mh .. +7 (8 rows of 16 bytes; the wave reads 4 rows x 256 contiguous bytes per
+    // step), transposes the 8 x 8 block in registers and writes 8 whole 16-byte tile slots. Rank blocks
+    // past r_k (r_k is a multiple of 32, so the test is uniform) are zero.
+    {
+      const int gg = lane & 3, mh = (lane >> 2) & 1, rt = lane >> 3;
+      const __bf16* ukp = a.w_rot + (long long)kvh * a.rk * (2 * HD) + 16 * rt + 8 * mh;
+      for (int kb = w; kb < KBP; kb += G2_NW) {
+        bf16x8 v[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int d = d8 + i, rt = d >> 4, m = d & 15;
-        ukt16[((rt * KBP + kb) * 64 + m + 16 * gg) * 8 + j] = v[i];
+        for (int j = 0; j < 8; ++j) {
+          const int r = 32 * kb + 8 * gg + j;
+          v[j] = kb < KB ? *reinterpret_cast<const bf16x8*>(ukp + (long long)r * (2 * HD)) : bf16x8{};
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          bf16x8 o;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) o[j] = v[j][i];
+          ukt[(rt * KBP + kb) * 64 + 16 * gg + 8 * mh + i] = o;
+        }
       }
     }
     __syncthreads();
