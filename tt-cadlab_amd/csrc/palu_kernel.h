@@ -341,6 +341,24 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   const int n = lane & 15, g = lane >> 4;
   _Float16* qx = reinterpret_cast<_Float16*>(smem + SM::QX_OFFSET + w * SM::QX_WAVE_BYTES);
 
+  // Latent mode: the angle-table rows are the same for every workgroup and depend on nothing below, so
+  // their loads are issued first, ahead of the plan's scalar reads of cur_pos. Rows t < 64 serve the K
+  // rotation, 64*Lo (Lo < 16) and 1024*H the query's pair base; one coalesced row per wave load.
+  const int n_rows = KFULL ? 0 : 80 + (a.S + 1023) / 1024;
+  constexpr int RPW = (80 + 64 + NW - 1) / NW;  // rows per wave, enough for S <= 65536
+  auto row_t = [](int r) { return r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80)); };
+  float4 rowv[KFULL ? 1 : RPW];
+  if constexpr (!KFULL) {
+    const TabT* cs = static_cast<const TabT*>(a.cs);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int r = w + i * NW;
+      int t = row_t(r);
+      t = (r < n_rows && t < a.cs_rows) ? t : 0;
+      rowv[i] = load4f(cs + (long long)t * (2 * HD) + 4 * lane);   // lane < 32: cos, else sin
+    }
+  }
+
   // This workgroup's item and position range: the whole sequence of item blockIdx.x, or one chunk of
   // the length-aware plan (computed identically, and uniformly, by every wave).
   int b, kvh, s_lo, s_hi, n_chunks = 1;
@@ -482,18 +500,6 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   // coalesced row per wave load (rows t < 64 for K, 64*Lo and 1024*H for the query); these (L2) loads
   // are issued before the first latent block's (HBM) loads, so waiting on them does not wait on HBM.
   if constexpr (!KFULL) {
-    const TabT* cs = static_cast<const TabT*>(a.cs);
-    const int n_hi = (a.S + 1023) / 1024;
-    const int n_rows = 80 + n_hi;               // 64 K rows, 16 low-base rows, n_hi high-base rows
-    constexpr int RPW = (80 + 64 + NW - 1) / NW;  // rows per wave, enough for S <= 65536
-    float4 rowv[RPW];
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      const int r = w + i * NW;
-      int t = r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80));
-      t = (r < n_rows && t < a.cs_rows) ? t : 0;
-      rowv[i] = load4f(cs + (long long)t * (2 * HD) + 4 * lane);   // lane < 32: cos, else sin
-    }
     // Every prologue load below is unconditional, its index clamped into the tensor: a load under a
     // branch makes the compiler wait for all outstanding loads where the branch joins, which would hold
     // the first latent block back until the tables had arrived.
@@ -511,6 +517,10 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     const bool qlive = tid < 16 * (HD / 8) && qh < a.rep;
     const bf16x8 qrow = *reinterpret_cast<const bf16x8*>(
         a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + (qlive ? qh : 0)) * HD + (qlive ? qc : 0));
+    // Every wave's table, u_k and query loads are issued before any wave's first latent block: the CU's
+    // vector-memory pipeline serves them in order, so the (L2-hit) table loads of later waves do not
+    // queue behind earlier waves' HBM latent loads.
+    __syncthreads();
     // The wave's first block, issued before the row length is known (a wave whose first pair lies past
     // the row's data loads a block inside the cache instead and never uses it) and after every table
     // load: loads complete in issue order for the wait counter, so the prologue's waits on the tables
@@ -523,7 +533,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     for (int i = 0; i < RPW; ++i) {
       const int r = w + i * NW;
       if (r < n_rows) {
-        int t = r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80));
+        const int t = row_t(r);
         const bool ok = t < a.cs_rows;
         float2* dst = r < 64 ? kc + r * 64 : (r < 80 ? tl + (r - 64) * 64 : th + (r - 80) * 64);
         const int f = 2 * (lane & 31);
