@@ -795,7 +795,7 @@ __global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, 
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
-#pragma unroll 4
+#pragma unroll 8                                      // 8 u_v rows in flight (unroll 4: 14.5 us, 16: 13.8)
     for (int r = rs * per; r < rs * per + per; ++r) {
       const bf16x8 u = *reinterpret_cast<const bf16x8*>(uv + (long long)r * HD);
 #pragma unroll
