@@ -70,6 +70,8 @@ def parse():
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     ap.add_argument("--traffic", default=str(REPO / "profiles" / "palu_decode_b32_ctx8192_r64_traffic.txt"),
                     help="rocprofv3 --pmc summary holding the measured HBM bytes per launch")
+    ap.add_argument("--mfma-counters", default=str(REPO / "profiles" / "palu_decode_mfma_counters.md"),
+                    help="rocprofv3 --pmc summary holding the headline kernel's MFMA busy fraction")
     return ap.parse_args()
 
 
@@ -142,14 +144,19 @@ def time_calls(fn, n_layers, steps, warmup):
     return wall, kern, per
 
 
-def read_traffic(path):
+def read_profile_value(path, key):
+    """The number after `key:` at the start of a line of a committed rocprofv3 summary, or None."""
     p = Path(path)
     if not p.exists():
         return None
     for ln in p.read_text().splitlines():
-        if ln.startswith("traffic_bytes_per_launch:"):
+        if ln.startswith(key + ":"):
             return float(ln.split(":", 1)[1])
     return None
+
+
+def read_traffic(path):
+    return read_profile_value(path, "traffic_bytes_per_launch")
 
 
 def _roof(nbytes, flops, kern_ms):
@@ -412,7 +419,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": read_traffic(a.traffic),
                      "algorithmic_bytes": lat_bytes},
         "mfma": {"achieved_tflops": round(flops / (kern_ms * 1e-3) / 1e12, 2), "peak_tflops": BF16_PEAK_TFLOPS,
-                 "frac": round(flops / (kern_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4), "flops": flops},
+                 "frac": round(flops / (kern_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4), "flops": flops,
+                 "busy_counter": read_profile_value(a.mfma_counters, "mfma_busy_headline")},
     }
     if not a.no_stock:
         wl_layers = wl.pop("layers")       # free the latent caches before the full-KV ones
