@@ -307,3 +307,29 @@ def test_glrd_envelope_errors(lib):
                                     0.088, 0, 2, 1, 0, 2, 16, 4, 1, 16, 64, 4, 256, 256, 256, 256, 256, 0, 1, 1, 0,
                                     None, 0, None)
     assert rc == _native.PALU_EUNSUPPORTED and "paged" in lib.palu_last_error().decode()
+
+
+def test_bench_reads_the_committed_counter_summaries():
+    """The bench line's roofline.traffic and mfma.busy_counter come from committed rocprofv3 summaries;
+    both keys must be present and plausible (traffic at least the algorithmic latent bytes)."""
+    import importlib.util
+    root = Path(__file__).resolve().parent.parent
+    spec = importlib.util.spec_from_file_location("bench_mod", root / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    traffic = bench.read_traffic(root / "profiles" / "palu_decode_b32_ctx8192_r64_traffic.txt")
+    busy = bench.read_profile_value(root / "profiles" / "palu_decode_mfma_counters.md", "mfma_busy_headline")
+    algorithmic = 32 * 8 * 8192 * (64 + 64) * 2
+    assert traffic is not None and algorithmic <= traffic < 1.1 * algorithmic
+    assert busy is not None and 0.0 < busy < 1.0
+    assert bench.read_profile_value(root / "profiles" / "palu_decode_mfma_counters.md", "no_such_key") is None
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import subprocess
+    import sys
+    root = Path(__file__).resolve().parent.parent
+    res = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                         timeout=300)
+    assert res.returncode == 2
+    assert "exactly one GPU" in json.loads(res.stdout.strip().splitlines()[-1])["error"]
