@@ -98,13 +98,17 @@ def test_glrd_reference_head_shape(gpu):
     _check(_run(gpu, *args, 1024), _oracle(*args, 1024))
 
 
-def test_glrd_configuration_shape(gpu):
-    """Batch 16, ctx 16384, 2 groups of 4 heads, group ranks drawn from {128, 192, 256, 384, 512};
-    the oracle checks 3 of the 16 rows (the kernel computes all of them in one call)."""
+@pytest.mark.parametrize("ranks", [None, (512, 384), (512, 512)])
+def test_glrd_configuration_shape(gpu, ranks):
+    """Batch 16, ctx 16384, 2 groups of 4 heads, group ranks drawn from {128, 192, 256, 384, 512}, and
+    the two layers the benchmark times (the drawn widest pair (512, 384), and (512, 512)); the oracle
+    checks 3 of the 16 rows (the kernel computes all of them in one call)."""
     g = torch.Generator().manual_seed(4)
     choices = [128, 192, 256, 384, 512]
     r_k = choices[int(torch.randint(0, 5, (1,), generator=g))]
     r_v = choices[int(torch.randint(0, 5, (1,), generator=g))]
+    if ranks is not None:
+        r_k, r_v = ranks
     B, S = 16, 16384
     q, k, v, u_k, u_v, pos = _case(B, S, r_k, r_v, hpg=4, seed=44, pos=torch.full((16,), S - 1))
     pos[3], pos[9] = 5000, 12345
