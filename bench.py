@@ -56,7 +56,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the paged mixed-rank and grouped-latent (G-LRD) measurements")
-    ap.add_argument("--cpu-rows", type=int, default=2, help="batch rows of the CPU baseline sample")
+    ap.add_argument("--cpu-iters", type=int, default=5, help="timed oracle calls of the CPU baseline (after 2 warm-ups)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="skip the end-to-end 32-layer decoder (batch 64, 2048-token prompts, greedy decode) with "
                          "Palu ranks and with stock full-rank K/V")
@@ -263,10 +263,15 @@ def measure_glrd(dev, steps, warmup):
             fused.palu_sdpa_decode(q, k, w_rot, cs, v, HD, cur, u_v=u_v, scale=HD ** -0.5, out=out, workspace=ws)
 
         wall, kern, _ = time_calls(step, n_layers, steps, warmup)
-        nbytes = B * ng * S * (r_k + r_v) * 2
-        flops = 2 * B * NKV * S * r_k * HD + 2 * B * NQ * S * HD + 2 * B * NQ * S * r_v + 2 * B * NQ * r_v * HD
-        res.append({"ranks": note, "rank_k": r_k, "rank_v": r_v, "us_per_layer": round(wall * 1e3, 2),
-                    "kernel_us": round(kern * 1e3, 2), **_roof(nbytes, flops, kern)})
+        # algorithmic work counts each group at its own ranks (the drawn layer's narrower group is
+        # zero-padded to the layer width in the cache; those padding bytes are not algorithmic)
+        gk, gv = (drawn_k, drawn_v) if note == "drawn" else ([r_k] * ng, [r_v] * ng)
+        nbytes = B * S * (sum(gk) + sum(gv)) * 2
+        flops = sum(2 * B * hpg * S * rk_g * HD + 2 * B * hpg * NQ // NKV * S * (HD + rv_g) +
+                    2 * B * hpg * NQ // NKV * rv_g * HD for rk_g, rv_g in zip(gk, gv))
+        res.append({"ranks": note, "rank_k": r_k, "rank_v": r_v, "group_ranks": {"k": gk, "v": gv},
+                    "us_per_layer": round(wall * 1e3, 2), "kernel_us": round(kern * 1e3, 2),
+                    "cache_bytes_read": B * ng * S * (r_k + r_v) * 2, **_roof(nbytes, flops, kern)})
         del layers
         torch.cuda.empty_cache()
     kv = [(LatentCache.zeros(B, NKV, S, HD, dev, "k"), LatentCache.zeros(B, NKV, S, HD, dev, "v")) for _ in range(2)]
@@ -337,29 +342,39 @@ def measure_e2e(a, dev):
 
 
 def cpu_baseline(a, wl):
+    """The oracle's fp32 reference_decode (the CPU restatement of the reference's op model) on the whole
+    workload -- every batch row of the first layer's caches -- on this host's cores: 2 warm-up calls, then
+    --cpu-iters timed calls; median and min. Timed with all the cores this process may run on and again
+    with the reference's own 12 threads (palu_tt/reference.py:75, tests/conftest.py:15)."""
     from oracle import palu_oracle as ref
     cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    rows = max(1, min(a.cpu_rows, a.batch))
     k, v = wl["layers"][0]
     if not isinstance(k, torch.Tensor):
         k, v = k.to_rows(), v.to_rows()
-    kc, vc = k[:rows].float().cpu(), v[:rows].float().cpu()
-    qc = wl["q"][:, :rows].float().cpu()
+    kc, vc = k.float().cpu(), v.float().cpu()
+    qc = wl["q"].float().cpu()
     u_k = wl["w_rot"][0, :, :, :HD].float().cpu()
-    cur = torch.full((rows,), a.ctx - 1)
+    cur = wl["cur"].cpu()
     run = lambda: ref.reference_decode(qc, kc, u_k, vc, cur, wl["cos"], wl["sin"], HD ** -0.5)
-    run()
-    ts = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        run()
-        ts.append(time.perf_counter() - t0)
-    per_layer_us = statistics.median(ts) * 1e6 * (a.batch / rows)
-    return {"value": round(per_layer_us, 1), "unit": "us/layer", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle reference_decode (fp32 torch) on {rows} of {a.batch} batch rows of the same workload, "
-                      f"median of 3 after 1 warm-up, scaled x{a.batch / rows:g} to the full batch; "
-                      f"min {min(ts) * 1e6 * a.batch / rows:.0f} us/layer"}
+
+    def timed(threads):
+        torch.set_num_threads(threads)
+        for _ in range(2):
+            run()
+        ts = []
+        for _ in range(max(a.cpu_iters, 1)):
+            t0 = time.perf_counter()
+            run()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts) * 1e6, min(ts) * 1e6, torch.get_num_threads()
+
+    med12, min12, t12 = timed(min(12, cores))
+    med, mn, threads = timed(cores)
+    return {"value": round(med, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "sample": f"oracle reference_decode (fp32 torch) on the whole workload ({a.batch} of {a.batch} rows, "
+                      f"ctx {a.ctx}, r_k {a.rank_k}, r_v {a.rank_v}), median of {max(a.cpu_iters, 1)} after 2 warm-ups",
+            "min": round(mn, 1), "affinity_cores": cores, "torch_threads": threads,
+            "reference_threads_12": {"threads": t12, "median": round(med12, 1), "min": round(min12, 1)}}
 
 
 def main():
@@ -393,6 +408,8 @@ def main():
     lat_bytes = B * NKV * S * (rk + rv) * 2
     flops = 2 * B * NKV * S * rk * HD + 2 * B * NQ * S * HD + 2 * B * NQ * S * rv
     achieved = lat_bytes / (kern_ms * 1e-3) / 1e9
+    # the committed rocprofv3 counter summaries were taken on the default workload; other shapes get none
+    profiled = (B, S, rk, rv, a.layout) == (32, 8192, 64, 64, "tiled")
     res = {
         "metric": "fused latent decode us/layer + HBM TB/s frac (B=32, ctx 8K, r=64, 1 GPU)",
         "value": round(wall_ms * 1e3, 2),
@@ -416,12 +433,16 @@ def main():
         "kernel_us_percall_events": round(statistics.mean(per) * 1e3, 2),
         "tokens_per_s": round(B / (N_LAYERS_MODEL * wall_ms * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": read_traffic(a.traffic),
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": read_traffic(a.traffic) if profiled else None,
                      "algorithmic_bytes": lat_bytes},
         "mfma": {"achieved_tflops": round(flops / (kern_ms * 1e-3) / 1e12, 2), "peak_tflops": BF16_PEAK_TFLOPS,
                  "frac": round(flops / (kern_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4), "flops": flops,
-                 "busy_counter": read_profile_value(a.mfma_counters, "mfma_busy_headline")},
+                 "busy_counter": read_profile_value(a.mfma_counters, "mfma_busy_headline") if profiled else None},
     }
+    if profiled:
+        res["roofline"]["traffic_source"] = os.path.relpath(a.traffic, REPO)
+        res["mfma"]["busy_counter_source"] = os.path.relpath(a.mfma_counters, REPO)
     if not a.no_stock:
         wl_layers = wl.pop("layers")       # free the latent caches before the full-KV ones
         del wl_layers

@@ -60,7 +60,7 @@ int palu_abi_version(void);
 size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_dim_v);
 
 /* Bytes of workspace palu_sdpa_decode needs with u_v (grouped latents, in-kernel V rebuild): the fp32
- * partial scores of both head-dim halves ([B, n_q, 2, S]) plus the per-split latent PV partials. The
+ * scores ([B, n_q, S]) plus the per-split latent PV partials. The
  * grouped path runs three kernels on the stream and passes data between them through this buffer.
  * No counterpart in the reference (its op keeps these in device L1); needed because the MI355X path
  * splits the op into passes. */

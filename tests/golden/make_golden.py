@@ -1,13 +1,24 @@
 #!/usr/bin/env python
-"""Writes tests/golden/decode_small.safetensors: inputs and the oracle's fp32 output of one fused
-latent decode on a small ragged batch.
-
-The output comes from oracle.palu_oracle.reference_decode, which tests/test_oracle.py pins against
-transformers' rotary embedding and attention, brute-force loops and the reference's own test
-properties. The fixture freezes those pinned values so the oracle cannot drift silently, and gives the
-GPU path an input/output pair it must reproduce. Run from the repository root:
+"""Writes the committed golden fixtures of the oracle. Run from the repository root:
 
     python tests/golden/make_golden.py
+
+decode_small.safetensors: inputs and the oracle's fp32 output of one fused latent decode on a small
+ragged batch (oracle.palu_oracle.reference_decode).
+
+config1_layer.safetensors: the CPU plumbing configuration of the hot path, one Llama-3.1-8B-shaped
+attention layer through the layer oracle (oracle.palu_oracle.PaluRefAttention, the restatement of the
+reference's palu_tt/reference.py:14-55): hidden 4096, 32 Q / 8 KV heads, head_dim 128, RoPE theta 5e5
+with llama3 scaling (factor 8, low 1, high 4, original context 8192); q/k/v/o_proj ~ N(0, 0.02) in fp32;
+per-head truncated SVD of k_proj / v_proj at rank 64 (Palu's balanced split); batch 1, a 256-token
+prefill of hidden states ~ N(0, 1), then 16 decode steps; seed 0. The inputs are regenerated from the
+seed by config1_inputs() (the draw order is fixed there), so the fixture holds only the outputs -- the
+16 decode outputs and four prefill rows -- and fingerprints of the inputs that detect a change in the
+random stream.
+
+Both outputs come from oracle functions that tests/test_oracle.py pins (transformers' rotary embedding
+and attention, brute-force loops, the reference's own test properties). The fixtures freeze those pinned
+values so the oracle cannot drift silently, and give the GPU path input/output pairs to reproduce.
 """
 import sys
 from pathlib import Path
@@ -40,8 +51,61 @@ def make():
     return {"q": q, "k_latent": k_lat, "v_latent": v_lat, "u_k": u_k, "cur_pos": cur, "out": out.float().contiguous()}
 
 
+# ------------------------------------------------------------------------------------------------
+# Configuration 1: one Llama-3.1-8B attention layer, 256-token prefill + 16 decode steps, seed 0
+
+C1_HIDDEN, C1_NQ, C1_NKV, C1_RANK, C1_PREFILL, C1_STEPS = 4096, 32, 8, 64, 256, 16
+C1_PREFILL_ROWS = (0, 1, 127, 255)
+
+
+def config1_inputs():
+    """(weights {q, k, v, o} fp32 in HF layout, hidden states x [1, 272, 4096]) drawn from seed 0 in the
+    fixed order Wq, Wk, Wv, Wo, x."""
+    g = torch.Generator().manual_seed(0)
+    W = {"q": torch.randn(C1_NQ * HD, C1_HIDDEN, generator=g) * 0.02,
+         "k": torch.randn(C1_NKV * HD, C1_HIDDEN, generator=g) * 0.02,
+         "v": torch.randn(C1_NKV * HD, C1_HIDDEN, generator=g) * 0.02,
+         "o": torch.randn(C1_HIDDEN, C1_NQ * HD, generator=g) * 0.02}
+    x = torch.randn(1, C1_PREFILL + C1_STEPS, C1_HIDDEN, generator=g)
+    return W, x
+
+
+def config1_fingerprint(W, x):
+    """fp64 [10]: the sums of the five inputs and five single elements, to detect a changed random stream."""
+    return torch.tensor([float(W["q"].double().sum()), float(W["k"].double().sum()), float(W["v"].double().sum()),
+                         float(W["o"].double().sum()), float(x.double().sum()), float(W["q"][7, 11]),
+                         float(W["k"][1023, 4095]), float(W["v"][0, 0]), float(W["o"][100, 200]),
+                         float(x[0, 271, 17])], dtype=torch.float64)
+
+
+def config1_oracle_outputs(W, x):
+    """(prefill output [1, 256, 4096], decode outputs [16, 4096]) of the layer oracle."""
+    Uk, VTk = ref.svd_per_head(W["k"], C1_NKV, C1_RANK)
+    Uv, VTv = ref.svd_per_head(W["v"], C1_NKV, C1_RANK)
+    layer = ref.PaluRefAttention(C1_NQ, C1_NKV, HD, THETA, LLAMA3, W["q"], W["o"], ref.Factors(VTk, Uk, VTv, Uv))
+    pre = layer.forward(x[:, :C1_PREFILL], 0)
+    dec = [layer.forward(x[:, C1_PREFILL + t:C1_PREFILL + t + 1], C1_PREFILL + t)[0, 0] for t in range(C1_STEPS)]
+    return pre, torch.stack(dec)
+
+
+def make_config1():
+    W, x = config1_inputs()
+    pre, dec = config1_oracle_outputs(W, x)
+    return {"decode_out": dec.float().contiguous(), "prefill_rows": pre[0, list(C1_PREFILL_ROWS)].float().contiguous(),
+            "prefill_row_index": torch.tensor(C1_PREFILL_ROWS, dtype=torch.int32),
+            "input_fingerprint": config1_fingerprint(W, x)}
+
+
 if __name__ == "__main__":
-    path = Path(__file__).resolve().parent / "decode_small.safetensors"
+    here = Path(__file__).resolve().parent
+    path = here / "decode_small.safetensors"
     save_file(make(), str(path), metadata={"theta": str(THETA), "rope": "llama3 factor 8, low 1, high 4, orig 8192",
                                            "scale": "head_dim ** -0.5", "generator": "tests/golden/make_golden.py"})
+    print(f"wrote {path} ({path.stat().st_size} bytes)")
+    torch.set_num_threads(8)
+    path = here / "config1_layer.safetensors"
+    save_file(make_config1(), str(path), metadata={
+        "layer": "hidden 4096, 32 Q / 8 KV heads, head_dim 128, rank_k = rank_v = 64 (per-head SVD)",
+        "rope": "llama3 theta 5e5 factor 8, low 1, high 4, orig 8192", "steps": "256-token prefill, 16 decode",
+        "seed": "0 (draw order Wq, Wk, Wv, Wo, x; see config1_inputs)", "generator": "tests/golden/make_golden.py"})
     print(f"wrote {path} ({path.stat().st_size} bytes)")

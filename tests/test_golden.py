@@ -1,6 +1,17 @@
-"""The committed fixture tests/golden/decode_small.safetensors (written by tests/golden/make_golden.py):
-the oracle must still produce it (CPU), and the HIP op must reproduce it from the stored inputs (GPU),
-in both cache layouts, to the decode bar (max-abs 2e-2, cosine 0.9999)."""
+"""The committed fixtures of tests/golden/ (written by tests/golden/make_golden.py).
+
+decode_small.safetensors: the oracle must still produce it (CPU), and the HIP op must reproduce it from
+the stored inputs (GPU), in both cache layouts, to the decode bar (max-abs 2e-2, cosine 0.9999).
+
+config1_layer.safetensors: one Llama-3.1-8B attention layer (hidden 4096, 32 Q / 8 KV heads, per-head
+SVD at rank 64), a 256-token prefill and 16 decode steps from seed 0 through the layer oracle. The oracle
+must still produce it (CPU); the PaluAttention drop-in, built from the same seeded weights with the
+package's own SVD and converter, must reproduce every decode step (GPU), through the fused op and
+through the naive path. The layer runs in bf16 (weights, activations, latent caches), so the GPU bar is
+on the whole layer output: cosine >= 0.999 and max-abs within 2% of the output's largest magnitude, the
+bar of the attention drop-in tests.
+"""
+import sys
 from pathlib import Path
 
 import pytest
@@ -10,6 +21,9 @@ from safetensors.torch import load_file
 from oracle import palu_oracle as ref
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "decode_small.safetensors"
+CONFIG1 = Path(__file__).resolve().parent / "golden" / "config1_layer.safetensors"
+sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+import make_golden as mg  # noqa: E402
 HD = 128
 THETA = 500000.0
 LLAMA3 = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
@@ -46,3 +60,65 @@ def test_hip_op_reproduces_the_fixture(gpu, fx, layout):
     out = out.cpu()
     assert ref.max_abs(out, fx["out"]) <= 2e-2 and ref.cosine(out, fx["out"]) >= 0.9999, \
         (ref.max_abs(out, fx["out"]), ref.cosine(out, fx["out"]))
+
+
+@pytest.fixture(scope="module")
+def c1():
+    return load_file(str(CONFIG1))
+
+
+@pytest.fixture(scope="module")
+def c1_inputs(c1):
+    W, x = mg.config1_inputs()
+    torch.testing.assert_close(mg.config1_fingerprint(W, x), c1["input_fingerprint"], atol=1e-9, rtol=1e-12,
+                               msg="the seeded input stream changed; the fixture no longer matches its inputs")
+    return W, x
+
+
+def test_oracle_reproduces_the_config1_fixture(c1, c1_inputs):
+    W, x = c1_inputs
+    pre, dec = mg.config1_oracle_outputs(W, x)
+    scale = float(c1["decode_out"].abs().max())
+    torch.testing.assert_close(dec, c1["decode_out"], atol=1e-5 * scale, rtol=1e-4)
+    torch.testing.assert_close(pre[0, c1["prefill_row_index"].long()], c1["prefill_rows"], atol=1e-5 * scale, rtol=1e-4)
+    assert dec.shape == (mg.C1_STEPS, mg.C1_HIDDEN)
+
+
+def _close_layer(out, exp, what):
+    out, exp = out.float().cpu(), exp.float()
+    cs = ref.cosine(out, exp)
+    rel = ref.max_abs(out, exp) / float(exp.abs().max())
+    assert cs >= 0.999 and rel <= 0.02, f"{what}: cosine {cs:.6f}, max-abs / max {rel:.4f}"
+    return cs, rel
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("use_fused_k", [True, False])
+def test_attention_reproduces_the_config1_fixture(gpu, c1, c1_inputs, use_fused_k):
+    from palu_tt import compress, convert
+    from palu_tt.attention import PaluAttention
+    W, x = c1_inputs
+    nh, nkv, r, hidden = mg.C1_NQ, mg.C1_NKV, mg.C1_RANK, mg.C1_HIDDEN
+    Uk, VTk = compress.svd_per_head(W["k"], nkv, r)
+    Uv, VTv = compress.svd_per_head(W["v"], nkv, r)
+    sd = {"layers.0.attention.wq.weight": convert.reverse_permute(W["q"], nh, nh * HD, hidden),
+          "layers.0.attention.wo.weight": W["o"]}
+    for name, t in convert.palu_layer_tensors(W, convert.LowRank(VTk, Uk, VTv, Uv), nh, nkv, HD).items():
+        sd[f"layers.0.attention.palu.{name}"] = t
+
+    class Args:
+        dim, n_heads, n_kv_heads, head_dim = hidden, nh, nkv, HD
+        max_seq_len, max_batch_size = 288, 1
+        rope_theta, rope_scaling = THETA, LLAMA3
+        palu = convert.PaluConfig(rank_k=[r], rank_v=[r], cache_id="config1",
+                                  runtime=convert.PaluRuntime(use_fused_k=use_fused_k))
+
+    att = PaluAttention(gpu, None, Args, sd, None, 0)
+    assert att.use_fused_k == use_fused_k
+    pre = att.forward(x[:, :mg.C1_PREFILL].to(gpu), mode="prefill")
+    _close_layer(pre[0, c1["prefill_row_index"].long()], c1["prefill_rows"], "prefill rows")
+    for t in range(mg.C1_STEPS):
+        p = mg.C1_PREFILL + t
+        out = att.forward(x[:, p].to(gpu), torch.tensor([p], dtype=torch.int32, device=gpu), mode="decode")
+        torch.cuda.synchronize()
+        _close_layer(out[0], c1["decode_out"][t], f"decode step {t} (position {p})")

@@ -5,8 +5,9 @@ converted with convert.palu_layer_tensors, and driven through prefill (two users
 steps; every output is compared with oracle.PaluRefAttention (fp32, same factors, same positions).
 The layer runs in bf16 (weights, activations, caches), so the bar is on the whole layer output:
 cosine >= 0.999 and max-abs within 2% of the output's largest magnitude. Covers the fused latent path
-(r < head_dim), the full-rank fast paths (stock K / stock V), grouped latents with in-kernel V, and
-both cache layouts.
+(r < head_dim), the naive path the reference runs when PaluRuntime.use_fused_k is off (K rebuilt and
+rotated on the GPU, then the stock flash-decode; reference attention.py:657-710), the full-rank fast
+paths (stock K / stock V), grouped latents with in-kernel V, and both cache layouts.
 """
 import pytest
 import torch
@@ -41,7 +42,7 @@ def _group_svd(W, nkv, gs, rank):
     return U_h.contiguous(), VT_h.contiguous()
 
 
-def _layer(dim, nh, nkv, r_k, r_v, gs, seed):
+def _layer(dim, nh, nkv, r_k, r_v, gs, seed, use_fused_k=True, recon_len=None):
     g = torch.Generator().manual_seed(seed)
     W = {"q": torch.randn(nh * HD, dim, generator=g) * 0.02, "k": torch.randn(nkv * HD, dim, generator=g) * 0.02,
          "v": torch.randn(nkv * HD, dim, generator=g) * 0.02, "o": torch.randn(dim, nh * HD, generator=g) * 0.02}
@@ -54,7 +55,8 @@ def _layer(dim, nh, nkv, r_k, r_v, gs, seed):
           "layers.0.attention.wo.weight": W["o"]}
     for name, t in convert.palu_layer_tensors(W, lr, nh, nkv, HD).items():
         sd[f"layers.0.attention.palu.{name}"] = t
-    palu = convert.PaluConfig(rank_k=[r_k], rank_v=[r_v], cache_id="test", group_size=gs)
+    palu = convert.PaluConfig(rank_k=[r_k], rank_v=[r_v], cache_id="test", group_size=gs,
+                              runtime=convert.PaluRuntime(use_fused_k=use_fused_k, recon_len=recon_len, check=True))
     oracle = ref.PaluRefAttention(nh, nkv, HD, THETA, LLAMA3, W["q"], W["o"], ref.Factors(VTk, Uk, VTv, Uv))
     return sd, palu, oracle
 
@@ -66,13 +68,17 @@ def _close(out, exp, what):
     assert cs >= 0.999 and rel <= 0.02, f"{what}: cosine {cs:.6f}, max-abs / max {rel:.4f}"
 
 
-@pytest.mark.parametrize("r_k,r_v,gs,layout", [(64, 64, 1, "tiled"), (64, 64, 1, "rows"), (32, 96, 1, "tiled"),
-                                               (HD, 64, 1, "tiled"), (32, HD, 1, "tiled"), (HD, HD, 1, "rows"),
-                                               (192, 256, 2, "tiled")])
-def test_attention_prefill_then_decode_matches_layer_oracle(gpu, r_k, r_v, gs, layout):
+@pytest.mark.parametrize("r_k,r_v,gs,layout,fused,recon_len", [
+    (64, 64, 1, "tiled", True, None), (64, 64, 1, "rows", True, None), (32, 96, 1, "tiled", True, None),
+    (HD, 64, 1, "tiled", True, None), (32, HD, 1, "tiled", True, None), (HD, HD, 1, "rows", True, None),
+    (192, 256, 2, "tiled", True, None),
+    (64, 64, 1, "tiled", False, None), (32, 96, 1, "rows", False, 50), (192, 256, 2, "tiled", False, None),
+    (32, HD, 1, "tiled", False, 64)])
+def test_attention_prefill_then_decode_matches_layer_oracle(gpu, r_k, r_v, gs, layout, fused, recon_len):
     dim, nh, nkv, B, S0, steps = 1024, 8, 2, 2, 40, 6
-    sd, palu, oracle = _layer(dim, nh, nkv, r_k, r_v, gs, seed=r_k + r_v + gs)
+    sd, palu, oracle = _layer(dim, nh, nkv, r_k, r_v, gs, seed=r_k + r_v + gs, use_fused_k=fused, recon_len=recon_len)
     att = PaluAttention(gpu, None, _Args(dim, nh, nkv, 128, B, palu), sd, None, 0, cache_layout=layout)
+    assert att.use_fused_k == (fused and att.recon_k)
     g = torch.Generator().manual_seed(9)
     x = torch.randn(B, S0 + steps, dim, generator=g)
     exp_pre = oracle.forward(x[:, :S0], 0)

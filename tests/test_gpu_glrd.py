@@ -118,6 +118,17 @@ def test_glrd_configuration_shape(gpu, ranks):
     _check(out[:, rows], exp)
 
 
+@pytest.mark.parametrize("S,pos", [(49152, [49151, 40000, 16383]), (65536, [65535, 32768, 16384])])
+def test_glrd_widest_ranks_at_long_context(gpu, S, pos):
+    """r_k = r_v = 512 (u_k^T of 128 KB in LDS) at contexts past 40k and at the 65536 maximum: every
+    pair base angle comes from the three small angle tables (no table grows with the context). Rows end
+    at the last position, mid-cache and on 16384-position boundaries (where the top table's row
+    changes); all three rows are checked."""
+    B = len(pos)
+    q, k, v, u_k, u_v, p = _case(B, S, 512, 512, hpg=4, seed=S, pos=torch.tensor(pos))
+    _check(_run(gpu, q, k, v, u_k, u_v, p, S), _oracle(q, k, v, u_k, u_v, p, S))
+
+
 def test_glrd_deterministic_repeat(gpu):
     args = _case(2, 2048, 256, 256, hpg=4, seed=8)
     a = _run(gpu, *args, 2048)

@@ -14,7 +14,7 @@ import torch
 from safetensors.torch import save_file
 
 from oracle import palu_oracle as ref
-from palu_tt import _build, _native, convert, fused
+from palu_tt import _build, _native, compress, convert, fused
 
 REPO = Path(__file__).resolve().parents[1]
 HD = 128
@@ -116,7 +116,7 @@ def test_load_palu_dir_mlrd_and_glrd(tmp_path):
     mlrd = [(24, [0]), (40, [1]), (8, [2]), (32, [3])]            # group size 1, ragged ranks
     glrd = [(48, [0, 1]), (20, [2, 3])]                           # 2 groups of 2 heads
     ranks, tensors = _write_palu_dir(tmp_path / "m", 1, hidden, hd, mlrd, glrd)
-    with pytest.raises(AssertionError, match="group size"):
+    with pytest.raises(ValueError, match="group size"):
         convert.load_palu_dir(tmp_path / "m", 1, nkv, hd)
     ranks, tensors = _write_palu_dir(tmp_path / "g", 2, hidden, hd, glrd, glrd)
     lr = convert.load_palu_dir(tmp_path / "g", 2, nkv, hd, rank_multiple=32)
@@ -145,6 +145,98 @@ def test_load_palu_dir_mlrd_and_glrd(tmp_path):
         torch.testing.assert_close(s.k_U[h] @ s.k_VT[h], U[h] @ VT[h], atol=1e-4, rtol=1e-4)
     assert convert.palu_dir_cache_id(tmp_path / "g").startswith("g-")
     assert convert.palu_cache_id_for(tmp_path / "g", "unit").endswith("-unit")
+
+
+def test_palu_dir_round_trip_reproduces_the_weights_at_full_rank(tmp_path):
+    """compress.factor_layers -> convert.save_palu_dir -> convert.load_palu_dir: at full rank (r = group
+    rows) every head's U @ VT is its own rows of W, for per-head (M-LRD) and grouped (G-LRD) factors; at
+    ragged ranks the loaded head equals the truncated group SVD's slice, zero-padded."""
+    hidden, hd, nkv = 96, 16, 4
+    g = torch.Generator().manual_seed(3)
+    W = {i: {"k": torch.randn(nkv * hd, hidden, generator=g), "v": torch.randn(nkv * hd, hidden, generator=g)}
+         for i in range(2)}
+    for gs in (1, 2):
+        ng = nkv // gs
+        full = [[gs * hd] * ng] * 2
+        d = convert.save_palu_dir(tmp_path / f"full{gs}", compress.factor_layers(W, nkv, full, full))
+        lr = convert.load_palu_dir(d, 2, nkv, hd, rank_multiple=16)
+        for i in range(2):
+            assert lr[i].group_size == gs and lr[i].r_k == gs * hd
+            for h in range(nkv):
+                torch.testing.assert_close(lr[i].k_U[h] @ lr[i].k_VT[h], W[i]["k"][h * hd:(h + 1) * hd],
+                                           atol=2e-4, rtol=1e-4)
+                torch.testing.assert_close(lr[i].v_U[h] @ lr[i].v_VT[h], W[i]["v"][h * hd:(h + 1) * hd],
+                                           atol=2e-4, rtol=1e-4)
+    ragged_k, ragged_v = [[10, 7], [16, 3]], [[5, 12], [9, 9]]
+    fac = compress.factor_layers(W, nkv, ragged_k, ragged_v)
+    d = convert.save_palu_dir(tmp_path / "ragged", fac, meta={"note": "ragged"})
+    assert json.loads((d / "config.json").read_text())["head_wise_ranks"]["model.layers.1.self_attn.k_proj"] == [16, 3]
+    lr = convert.load_palu_dir(d, 2, nkv, hd, rank_multiple=8)
+    assert lr[0].r_k == 16 and lr[1].r_v == 16 and lr[1].r_k == 16
+    for h in range(nkv):
+        gi, hh = divmod(h, 2)
+        U_g, VT_g = fac[1]["k_proj"][gi]
+        r = VT_g.shape[0]
+        assert torch.equal(lr[1].k_VT[h, :r], VT_g) and torch.count_nonzero(lr[1].k_VT[h, r:]) == 0
+        assert torch.equal(lr[1].k_U[h, :, :r], U_g[hh * hd:(hh + 1) * hd]) and torch.count_nonzero(lr[1].k_U[h, :, r:]) == 0
+    # the balanced split matches the oracle's per-head SVD (group size 1)
+    U, VT = compress.svd_per_head(W[0]["k"], nkv, 5)
+    Ur, VTr = ref.svd_per_head(W[0]["k"], nkv, 5)
+    torch.testing.assert_close(U @ VT, Ur @ VTr, atol=1e-4, rtol=1e-4)
+
+
+def test_palu_dir_cache_id_tracks_content(tmp_path):
+    """The id is dirname-<8 hex>, stable across reads and file touches, and changes when one byte of
+    config.json changes or the tensors are regenerated with the same shapes."""
+    import os
+    import re
+    groups = [(32, [0]), (32, [1]), (32, [2]), (32, [3])]
+    d = tmp_path / "my dump 0.5"
+    _write_palu_dir(d, 1, 64, 32, groups, groups, seed=1)
+    cid = convert.palu_dir_cache_id(d)
+    assert re.fullmatch(r"my_dump_0\.5-[0-9a-f]{8}", cid), cid
+    shard = d / "palu_lowrank.safetensors"
+    os.utime(shard, ns=(1, 1))
+    assert convert.palu_dir_cache_id(d) == cid
+    cj = d / "config.json"
+    cj.write_text(cj.read_text() + " ")
+    cid2 = convert.palu_dir_cache_id(d)
+    assert cid2 != cid and cid2.startswith("my_dump_0.5-")
+    _write_palu_dir(d, 1, 64, 32, groups, groups, seed=2)
+    assert convert.palu_dir_cache_id(d) not in (cid, cid2)
+    assert convert.palu_cache_id_for(d, "balanced") == convert.palu_dir_cache_id(d)
+
+
+def test_add_palu_to_state_dict_from_hf_and_palu_dirs(tmp_path):
+    """The converter over an HF checkpoint directory: identity factors without a dump (cache id
+    "identity", stock collapse: wo_fused == wo), and a dump's factors laid out per layer as
+    palu_layer_tensors lays them (reference convert.py:291-312 is the interface)."""
+    hidden, nh, nkv, L = 256, 8, 4, 2
+    g = torch.Generator().manual_seed(5)
+    hf_dir = tmp_path / "hf"
+    hf_dir.mkdir()
+    Ws = {i: _layer(10 + i, hidden, nh, nkv) for i in range(L)}
+    save_file({f"model.layers.{i}.self_attn.{p}_proj.weight": w[p].contiguous() for i, w in Ws.items()
+               for p in "qkvo"} | {"model.embed_tokens.weight": torch.randn(16, hidden, generator=g)},
+              str(hf_dir / "model.safetensors"))
+    w1 = convert.hf_attn_weights(hf_dir, 1)
+    assert set(w1) == {"q", "k", "v", "o"} and torch.equal(w1["k"], Ws[1]["k"])
+    with pytest.raises(KeyError):
+        convert.hf_attn_weights(hf_dir, 5)
+    sd = {}
+    cfg = convert.add_palu_to_state_dict(sd, hf_dir, None, L, nh, nkv, HD)
+    assert cfg.cache_id == "identity" and cfg.rank_k == [HD, HD] and cfg.group_size == 1
+    assert torch.equal(sd["layers.0.attention.palu.wo_fused"], Ws[0]["o"].float())
+    ranks = [[64] * nkv, [32] * nkv]
+    pd = convert.save_palu_dir(tmp_path / "dump", compress.factor_layers({i: Ws[i] for i in range(L)}, nkv, ranks, ranks))
+    sd = {}
+    cfg = convert.add_palu_to_state_dict(sd, hf_dir, pd, L, nh, nkv, HD)
+    assert cfg.rank_k == [64, 32] and cfg.rank_v == [64, 32] and cfg.cache_id.startswith("dump-")
+    lrs = convert.load_palu_dir(pd, L, nkv, HD)
+    for i in range(L):
+        exp = convert.palu_layer_tensors(Ws[i], lrs[i], nh, nkv, HD)
+        for k, t in exp.items():
+            assert torch.equal(sd[f"layers.{i}.attention.palu.{k}"], t), (i, k)
 
 
 def test_glrd_layer_tensors_share_the_group_latent_and_keep_wo():
@@ -197,10 +289,10 @@ def test_workspace_query(lib):
 
 
 def test_grouped_latent_workspace_query(lib):
-    # partial scores of both head-dim halves ([B, n_q, 2, S] fp32) plus the PV partials
+    # scores ([B, n_q, S] fp32) plus the PV partials
     B, nq, nkv, G, S, rv = 16, 32, 8, 2, 16384, 512
     ws = lib.palu_glrd_workspace_bytes(B, nq, nkv, G, S, rv)
-    assert ws >= B * nq * 2 * S * 4 and ws < B * nq * 2 * S * 4 + B * nq * 129 * (rv + 4) * 4 + 512
+    assert ws >= B * nq * S * 4 and ws < B * nq * S * 4 + B * nq * 129 * (rv + 4) * 4 + 512
     assert lib.palu_glrd_workspace_bytes(B, nq, nkv, 3, S, rv) == 0          # groups must divide the KV heads
     assert lib.palu_glrd_workspace_bytes(0, nq, nkv, G, S, rv) == 0
 

@@ -4,32 +4,28 @@
 // 120-142, fp32 model palu_tt/fused.py:82-107 with u_v).
 //
 // Three launches on the caller's stream:
-//   1. Scores. One workgroup per (row, KV head, half of the head dim, sequence split), 8 waves that each
-//      take their own pairs of 32-position blocks (no barrier in the loop). The workgroup's 64 x r_k
-//      slice of u_k^T sits in LDS as ready MFMA A tiles; the K latent streams from HBM straight into
-//      registers (tiled layout: every load is one operand tile), a ring of rank blocks in flight. A wave
-//      rebuilds K^T (64 dims x 64 positions) on v_mfma_f32_16x16x32_bf16 (each A tile read from LDS
-//      feeds four MFMAs), rotates it in-lane (pair-relative RoPE table in LDS, query rotated back by the
-//      pair base) and contracts it with its query heads. The partial scores of the two dim halves go
-//      to the workspace as fp32 [block][head][32], already scaled by scale * log2 e.
+//   1. Scores. One workgroup per (row, KV head, sequence split), 4 waves (one per SIMD) that each take
+//      their own pairs of 32-position blocks (no barrier in the loop). The KV head's whole u_k^T sits in
+//      LDS as ready MFMA A tiles; the K latent streams from HBM straight into registers (tiled layout:
+//      every load is one operand tile), a ring of rank blocks in flight. A wave rebuilds K^T (128 dims x
+//      64 positions) on v_mfma_f32_16x16x32_bf16, rotates it in-lane (pair-relative RoPE table in
+//      registers, query rotated back by the pair base) and contracts it with its query heads. The
+//      scores go to the workspace as fp32 [block][head][32], already scaled by scale * log2 e.
 //   2. Latent PV. One workgroup per (row, latent group, 16-head tile, sequence split); all query heads
-//      of a group share the V latent, so the PV MFMA has the group's heads as its N dimension. Every
-//      wave walks every block of the split, sums the two score halves, runs the same online softmax
-//      (exp2 domain, lazy rescale) and accumulates O_lat^T = V_lat^T P^T for its own V tiles, streamed
-//      from HBM two blocks ahead. Partials (O_lat, m, l) per head and split go to the workspace.
+//      of a group share the V latent, so the PV MFMA has the group's heads as its N dimension. The waves
+//      split the V tiles and the blocks of the split, run the online softmax (exp2 domain, lazy
+//      rescale) and accumulate O_lat^T = V_lat^T P^T for their V tiles, streamed from HBM two blocks
+//      ahead. Partials (O_lat, m, l) per head and split go to the workspace.
 //   3. Merge and V rebuild. One workgroup per (row, KV head): log-sum-exp merge of the splits, then
-//      out = O_lat u_v[h] / l in fp32 — the same sum as softmax(q K^T) (V_lat u_v[h]), V never built.
-// The K latent of a group is read by 2 * heads_per_group scores workgroups; they are numbered so they
-// land on one XCD (the dispatcher deals consecutive workgroup ids round-robin over the 8 XCDs) and meet
-// in its L2.
+//      out = O_lat u_v[h] / l in fp32 -- the same sum as softmax(q K^T) (V_lat u_v[h]), V never built.
+// The K latent of a group is read by heads_per_group scores workgroups; they are numbered so they land
+// on one XCD (the dispatcher deals consecutive workgroup ids round-robin over the 8 XCDs) and meet in
+// its L2.
 #include "palu_kernel.h"
 
 namespace {
 
 constexpr int G_NW = 8;                 // waves per workgroup (PV kernel)
-constexpr int G_NWS = 8;                // waves per workgroup (scores kernel)
-constexpr int G_D = 64;                 // head dims per scores workgroup
-constexpr int G_RT = G_D / 16;          // 16-dim row tiles per scores workgroup
 constexpr int G_QS = HD + 8;            // padded query row (bf16), spreads the 16 rows over the banks
 constexpr int G_PSTRIDE_PAD = 4;        // partial row: r_v values, m, l, 2 pad (16-byte rows)
 
@@ -42,19 +38,13 @@ inline int glrd_pv_splits(int items2, int nb) {
 }
 
 struct GlrdPlan {
-  int n_splits1, split_len1, n_streams1, n_wg1;
   int n_ht, n_splits2, split_len2, n_wg2;
   size_t scores_floats, part_floats;
 };
 
 inline GlrdPlan glrd_plan(int B, int n_q, int n_kv, int n_groups, int S, int rv) {
   GlrdPlan p;
-  const int hpg = n_kv / n_groups;
-  const Plan p1 = plan_splits(B * n_kv * 2, S, 2 * G_NWS);
-  p.n_splits1 = p1.n_splits;
-  p.split_len1 = p1.split_len;
-  p.n_streams1 = B * n_groups * p.n_splits1;
-  p.n_wg1 = ((p.n_streams1 + 7) / 8) * 8 * 2 * hpg;
+  (void)n_kv;
   const int QH = n_q / n_groups;
   p.n_ht = (QH + 15) / 16;
   const int nb = (S + BLK - 1) / BLK;
@@ -62,271 +52,40 @@ inline GlrdPlan glrd_plan(int B, int n_q, int n_kv, int n_groups, int S, int rv)
   p.split_len2 = ((nb + s2 - 1) / s2) * BLK;
   p.n_splits2 = (nb * BLK + p.split_len2 - 1) / p.split_len2;
   p.n_wg2 = B * n_groups * p.n_ht * p.n_splits2;
-  p.scores_floats = (size_t)B * n_q * 2 * nb * BLK;
+  p.scores_floats = (size_t)B * n_q * nb * BLK;
   p.part_floats = (size_t)B * n_q * p.n_splits2 * (rv + G_PSTRIDE_PAD);
   return p;
 }
 
 // ---------------------------------------------------------------------------------------------------
-// Pass 1: scores.
+// Pass 1: scores. One workgroup per (row, KV head, sequence split), 4 waves, one per SIMD, so each wave
+// may hold up to 512 registers. The KV head's whole u_k^T (128 dims x r_k) sits in LDS as A tiles; each
+// wave takes its own pairs of 32-position blocks and rebuilds K^T for all 128 dims x 64 positions at
+// once (128 accumulator registers). A latent tile read from memory then feeds 8 MFMAs (one per 16-dim
+// row tile) and a u_k^T tile read from LDS feeds 4 (one per 16-position tile). The pair-relative K
+// rotation is the same for every pair, so it lives in registers as fp16 (cos, sin) pairs. Each query
+// head's score is complete here; the PV pass reads one score per (head, position).
 //
-// LDS map (KBP = rank blocks rounded up to even):
-//   ukt   u_k^T slice as A tiles [row tile 4][rank block KBP][lane] bf16x8 (zero past r_k); at least
-//         32 KB, because the prologue stages cs_tab rows 0..63 ([t][f] float2) in the same place
-//   rtab  pair-relative K rotation [block of pair 2][tile c 2][row tile 4][lane] fp16 x 8
-//         {cos f, cos f, -sin f, sin f, cos f+1, cos f+1, -sin f+1, sin f+1}              16 KB
-//   tl    (cos, sin) of angle 64*Lo*f, Lo < 16                                              8 KB
-//   qs    the KV head's query rows, padded to G_QS                                    16 x G_QS bf16
-//   th    (cos, sin) of angle 1024*H*f, H < ceil(S / 1024)                         S/1024 x 512 B
-template <int KBP>
-struct G1Smem {
-  static constexpr int UKT_BYTES = (G_RT * KBP * 1024 > 32768) ? G_RT * KBP * 1024 : 32768;
-  static constexpr int UKT = 0;
-  static constexpr int RTAB = UKT + UKT_BYTES;
-  static constexpr int TL = RTAB + 2 * 2 * G_RT * 64 * 16;
-  static constexpr int QS = TL + 16 * 64 * 8;
-  static constexpr int TH = QS + 16 * G_QS * 2;
-  __host__ __device__ static int bytes(int S) { return TH + ((S + 1023) / 1024) * 64 * 8; }
-};
-
-template <int KBP, typename TabT>
-__global__ __launch_bounds__(G_NWS * 64) void palu_glrd_scores_kernel(const DecodeArgs a, float* scores) {
-  constexpr int R = (KBP % 4 == 0) ? 4 : 2;       // rank blocks of latent tiles in flight per wave
-  using SM = G1Smem<KBP>;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  bf16x8* ukt = reinterpret_cast<bf16x8*>(smem + SM::UKT);
-  float2* kc = reinterpret_cast<float2*>(smem + SM::UKT);
-  f16x8* rtab = reinterpret_cast<f16x8*>(smem + SM::RTAB);
-  float2* tl = reinterpret_cast<float2*>(smem + SM::TL);
-  float2* th = reinterpret_cast<float2*>(smem + SM::TH);
-  __bf16* qs_lds = reinterpret_cast<__bf16*>(smem + SM::QS);
-
-  // Workgroup id -> (latent stream, KV head in group, dim half): ids 8*q + x with the same x share an
-  // XCD, and the 2 * hpg workgroups of one stream get consecutive q.
-  const int n_groups = a.n_kv / a.hpg;
-  const int per_stream = 2 * a.hpg;
-  const int L = blockIdx.x;
-  const int x8 = L & 7, q8 = L >> 3;
-  const int sub = q8 % per_stream;
-  const int sigma = (q8 / per_stream) * 8 + x8;
-  if (sigma >= a.B * n_groups * a.n_splits) return;   // padding workgroup (uniform)
-  const int hig = sub >> 1, dpart = sub & 1;
-  const int split = sigma % a.n_splits;
-  const int bg = sigma / a.n_splits;
-  const int b = bg / n_groups, grp = bg - b * n_groups;
-  const int kvh = grp * a.hpg + hig;
-  const int QH = a.hpg * a.rep;
-  const int NB = a.S / BLK;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = lane & 15, g = lane >> 4;
-  const int KB = a.rk >> 5;
-
-  int len = a.cur_pos[b] + 1;
-  len = len < 0 ? 0 : (len > a.S ? a.S : len);
-  const int s_lo = split * a.split_len;
-  const int s_hi = min(len, s_lo + a.split_len);
-  const int nblk = s_hi > s_lo ? (s_hi - s_lo + BLK - 1) / BLK : 0;
-  const int npairs = (nblk + 1) >> 1;
-  const __bf16* kbase = a.k + b * a.k_sb + grp * a.k_sg;
-
-  // ---- prologue -----------------------------------------------------------------------------------
-  {
-    const TabT* cs = static_cast<const TabT*>(a.cs);
-    const int n_hi = (a.S + 1023) / 1024;
-    const int n_rows = 64 + 16 + n_hi;             // 64 K rows, 16 low-base rows, n_hi high-base rows
-    constexpr int RPW = (64 + 16 + 64 + G_NWS - 1) / G_NWS;
-    float4 rowv[RPW];
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      const int r = w + i * G_NWS;
-      int t = r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80));
-      t = (r < n_rows && t < a.cs_rows) ? t : 0;
-      rowv[i] = load4f(cs + (long long)t * (2 * HD) + 4 * lane);
-    }
-    if (tid < 256) {
-      const int qh = tid >> 4, qc = (tid & 15) * 8;    // 16 rows x 16 pieces of 8
-      bf16x8 qrow = bf16x8{};
-      if (qh < a.rep)
-        qrow = *reinterpret_cast<const bf16x8*>(a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + qh) * HD + qc);
-      *reinterpret_cast<bf16x8*>(qs_lds + qh * G_QS + qc) = qrow;
-    }
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      const int r = w + i * G_NWS;
-      if (r < n_rows) {
-        const int t = r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80));
-        const bool ok = t < a.cs_rows;
-        float2* dst = r < 64 ? kc + r * 64 : (r < 80 ? tl + (r - 64) * 64 : th + (r - 80) * 64);
-        float* d0 = reinterpret_cast<float*>(dst + 2 * (lane & 31)) + (lane >> 5);
-        d0[0] = ok ? rowv[i].x : (lane < 32 ? 1.f : 0.f);
-        d0[2] = ok ? rowv[i].z : (lane < 32 ? 1.f : 0.f);
-      }
-    }
-    __syncthreads();
-    // rtab[(hb, c, rt)][lane (n, g)]: offset t = 32 hb + 8(n/4) + 4c + n%4 inside the pair, frequency
-    // pairs f, f + 1 with f = 32 dpart + 8 rt + 2 g (the lane's dims 16 rt + 4 g .. +3 of this half).
-    for (int e = tid; e < 2 * 2 * G_RT * 64; e += G_NWS * 64) {
-      const int l = e & 63, rt = (e >> 6) & (G_RT - 1), c = (e >> 8) & 1, hb = e >> 9;
-      const int nn = l & 15, gg = l >> 4;
-      const int t = 32 * hb + 8 * (nn >> 2) + 4 * c + (nn & 3);
-      const int f = 32 * dpart + 8 * rt + 2 * gg;
-      const float2 x = kc[t * 64 + f], y = kc[t * 64 + f + 1];   // (cos, sin) of frequencies f, f + 1
-      rtab[e] = f16x8{(_Float16)x.x, (_Float16)x.x, (_Float16)-x.y, (_Float16)x.y,
-                      (_Float16)y.x, (_Float16)y.x, (_Float16)-y.y, (_Float16)y.y};
-    }
-    __syncthreads();                                    // kc is overwritten by the u_k^T tiles below
-    // u_k^T tiles: tile (rt, kb) lane (m, g) element j = u_k[rank 32 kb + 8 g + j][dim 64 dpart + 16 rt + m].
-    // Each thread reads 8 consecutive dims of one rank row (16 B) and scatters them.
-    const __bf16* ukp = a.w_rot + (long long)kvh * a.rk * (2 * HD) + G_D * dpart;
-    __bf16* ukt16 = reinterpret_cast<__bf16*>(ukt);
-    for (int e = tid; e < KBP * 32 * (G_D / 8); e += G_NWS * 64) {
-      const int r = e >> 3, d8 = (e & 7) * 8;
-      bf16x8 v = bf16x8{};
-      if (r < a.rk) v = *reinterpret_cast<const bf16x8*>(ukp + (long long)r * (2 * HD) + d8);
-      const int kb = r >> 5, gg = (r >> 3) & 3, j = r & 7;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int d = d8 + i, rt = d >> 4, m = d & 15;
-        ukt16[((rt * KBP + kb) * 64 + m + 16 * gg) * 8 + j] = v[i];
-      }
-    }
-    __syncthreads();
-  }
-
-  // Tile loads of a pair of blocks: tile (kb, hb, c) of pair pp is block 2 pp + hb, K-tile c * KB + kb.
-  // Rank blocks past r_k read the same tile order's kb 0 (the matching u_k^T tiles are zero, and the
-  // tile's columns are the same positions, so nothing from another position leaks in); blocks past the
-  // split's data read the split's first block. Every path issues the same loads.
-  auto load_kb = [&](int pp, int kb, bf16x8 (&t)[4]) {
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      const int blk = 2 * pp + hb;
-      const bool live = pp < npairs && blk < nblk;
-      const __bf16* bp = kbase + (long long)((s_lo >> 5) + (live ? blk : 0)) * (32 * a.rk) + lane * 8;
-      const int kbr = kb < KB ? kb : 0;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) t[2 * hb + c] = *reinterpret_cast<const bf16x8*>(bp + (c * KB + kbr) * 512);
-    }
-  };
-
-  // Query of this KV head rotated back by the pair base, scaled by scale * log2 e, in fp16 as the B
-  // operand of the QK MFMA for the rebuilt dims 32 t + {4g .. 4g+3, 16+4g .. 16+4g+3} of this half (the
-  // order the packed K^T slices give the A operand).
-  auto make_q = [&](int base, f16x8 (&qB)[2]) {
-    const int J = base >> 6;
-    const float2* lo = tl + (J & 15) * 64;
-    const float2* hi = th + (J >> 4) * 64;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int d0 = G_D * dpart + 32 * t + 16 * half + 4 * g;      // 4 dims = 2 frequency pairs
-        const bf16x4 qv = *reinterpret_cast<const bf16x4*>(qs_lds + n * G_QS + d0);
-        const float4 l4 = *reinterpret_cast<const float4*>(lo + (d0 >> 1));
-        const float4 h4 = *reinterpret_cast<const float4*>(hi + (d0 >> 1));
-        const float lc[2] = {l4.x, l4.z}, ls[2] = {l4.y, l4.w}, hc[2] = {h4.x, h4.z}, hs[2] = {h4.y, h4.w};
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const float cf = (hc[p] * lc[p] - hs[p] * ls[p]) * a.qscale;
-          const float sf = (hs[p] * lc[p] + hc[p] * ls[p]) * a.qscale;
-          const float x0 = (float)qv[2 * p], x1 = (float)qv[2 * p + 1];
-          qB[t][4 * half + 2 * p] = (_Float16)(x0 * cf + x1 * sf);      // R_{-base}
-          qB[t][4 * half + 2 * p + 1] = (_Float16)(x1 * cf - x0 * sf);
-        }
-      }
-    }
-  };
-
-  float* srow = scores + ((long long)((b * n_groups + grp) * 2 + dpart) * NB + (s_lo >> 5)) * QH * BLK;
-  bf16x8 ring[R][4];
-#pragma unroll
-  for (int kb = 0; kb < R; ++kb) load_kb(w, kb, ring[kb]);
-  for (int pp = w; pp < npairs; pp += G_NWS) {
-    f16x8 qB[2];
-    make_q(s_lo + pp * 2 * BLK, qB);
-    f32x4 acc[4][G_RT];
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-      for (int rt = 0; rt < G_RT; ++rt) acc[cc][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // u_k^T tiles double-buffered across rank blocks: the LDS reads of block kb + 1 are issued before
-    // the MFMAs of block kb, so their latency hides behind them.
-    bf16x8 A[2][G_RT];
-#pragma unroll
-    for (int rt = 0; rt < G_RT; ++rt) A[0][rt] = ukt[rt * KBP * 64 + lane];
-#pragma unroll
-    for (int kb = 0; kb < KBP; ++kb) {
-      const int slot = kb % R;
-      if (kb + 1 < KBP) {
-#pragma unroll
-        for (int rt = 0; rt < G_RT; ++rt) A[(kb + 1) & 1][rt] = ukt[(rt * KBP + kb + 1) * 64 + lane];
-      }
-#pragma unroll
-      for (int rt = 0; rt < G_RT; ++rt)
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) acc[cc][rt] = mfma16(A[kb & 1][rt], ring[slot][cc], acc[cc][rt]);
-      if (kb + R < KBP) load_kb(pp, kb + R, ring[slot]);
-      else load_kb(pp + G_NWS, kb + R - KBP, ring[slot]);
-      __builtin_amdgcn_sched_barrier(0);                 // keep the reads of one rank block ahead, not more
-    }
-    // Rotate in packed fp16 ((x0, x1) * (c, c) + (x1, x0) * (-s, s): one multiply and one fma per pair,
-    // fp32 -> fp16 rounded toward zero so finite values saturate), then contract with the query on the
-    // fp16 MFMA: scores of 16 positions x 16 heads per (block, tile c).
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      f16x2 r[G_RT][2];
-#pragma unroll
-      for (int rt = 0; rt < G_RT; ++rt) {
-        const f16x8 t = rtab[(cc * G_RT + rt) * 64 + lane];
-        const f16x2 c0 = {t[0], t[1]}, s0 = {t[2], t[3]}, c1 = {t[4], t[5]}, s1 = {t[6], t[7]};
-        const f16x2 x01 = to_f16x2(acc[cc][rt][0], acc[cc][rt][1]);
-        const f16x2 x23 = to_f16x2(acc[cc][rt][2], acc[cc][rt][3]);
-        r[rt][0] = x01 * c0 + x01.yx * s0;
-        r[rt][1] = x23 * c1 + x23.yx * s1;
-      }
-      const f16x8 k0 = {r[0][0][0], r[0][0][1], r[0][1][0], r[0][1][1], r[1][0][0], r[1][0][1], r[1][1][0], r[1][1][1]};
-      const f16x8 k1 = {r[2][0][0], r[2][0][1], r[2][1][0], r[2][1][1], r[3][0][0], r[3][0][1], r[3][1][0], r[3][1][1]};
-      f32x4 sc = mfma16(k0, qB[0], f32x4{0.f, 0.f, 0.f, 0.f});
-      sc = mfma16(k1, qB[1], sc);
-      const int hb = cc >> 1, c = cc & 1;
-      const int blk = 2 * pp + hb;
-      // lane (head n, g) holds positions 8g + 4c .. +3 of block blk
-      if (blk < nblk && n < a.rep)
-        *reinterpret_cast<float4*>(srow + ((long long)blk * QH + hig * a.rep + n) * BLK + 8 * g + 4 * c) =
-            make_float4(sc[0], sc[1], sc[2], sc[3]);
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------------------------------
-// Pass 1, whole-head form (used whenever its LDS fits). One workgroup per (row, KV head, sequence
-// split), 4 waves, one per SIMD, so each wave may hold up to 512 registers. The KV head's whole u_k^T
-// (128 dims x r_k) sits in LDS as A tiles; each wave takes its own pairs of 32-position blocks and
-// rebuilds K^T for all 128 dims x 64 positions at once (128 accumulator registers). A latent tile read
-// from memory then feeds 8 MFMAs (one per 16-dim row tile) and a u_k^T tile read from LDS feeds 4 (one
-// per 16-position tile), which halves the operand traffic per MFMA of the half-head form on both paths.
-// The pair-relative K rotation is the same for every pair, so it lives in registers as fp16 (cos, sin)
-// pairs. Each query head's score is complete here; the PV pass reads one score per (head, position).
-//
-// LDS map (KBP = rank blocks rounded up to even):
+// LDS map (KBP = rank blocks rounded up to even), at most 150.3 KB (r_k 512) at every length:
 //   ukt   u_k^T as A tiles [row tile 8][rank block KBP][lane] bf16x8 (zero past r_k); at least 32 KB,
 //         because the prologue stages cs_tab rows 0..63 ([t][f] float2) in the same place
 //   tl    (cos, sin) of angle 64*Lo*f, Lo < 16                                              8 KB
+//   tm    (cos, sin) of angle 1024*Mi*f, Mi < 16                                            8 KB
+//   tt    (cos, sin) of angle 16384*T*f, T < 4                                              2 KB
 //   qs    the KV head's query rows, padded to G_QS                                    16 x G_QS bf16
-//   th    (cos, sin) of angle 1024*H*f, H < ceil(S / 1024)                         S/1024 x 512 B
-constexpr int G2_NW = 4;                // waves per workgroup of the whole-head scores kernel
+// A pair base 64 J (J = 256 T + 16 Mi + Lo) takes its angle by two angle additions of these rows.
+constexpr int G2_NW = 4;                // waves per workgroup of the scores kernel
 
 template <int KBP>
 struct G2Smem {
   static constexpr int UKT_BYTES = (8 * KBP * 1024 > 32768) ? 8 * KBP * 1024 : 32768;
   static constexpr int UKT = 0;
   static constexpr int TL = UKT + UKT_BYTES;
-  static constexpr int QS = TL + 16 * 64 * 8;
-  static constexpr int TH = QS + 16 * G_QS * 2;
-  __host__ __device__ static int bytes(int S) { return TH + ((S + 1023) / 1024) * 64 * 8; }
+  static constexpr int TM = TL + 16 * 64 * 8;
+  static constexpr int TT = TM + 16 * 64 * 8;
+  static constexpr int QS = TT + 4 * 64 * 8;
+  static constexpr int BYTES = QS + 16 * G_QS * 2;
+  static_assert(BYTES <= 160 * 1024, "scores kernel LDS");
 };
 
 template <int KBP, typename TabT>
@@ -337,7 +96,8 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   bf16x8* ukt = reinterpret_cast<bf16x8*>(smem + SM::UKT);
   float2* kc = reinterpret_cast<float2*>(smem + SM::UKT);
   float2* tl = reinterpret_cast<float2*>(smem + SM::TL);
-  float2* th = reinterpret_cast<float2*>(smem + SM::TH);
+  float2* tm = reinterpret_cast<float2*>(smem + SM::TM);
+  float2* tt = reinterpret_cast<float2*>(smem + SM::TT);
   __bf16* qs_lds = reinterpret_cast<__bf16*>(smem + SM::QS);
 
   // Workgroup id -> (latent stream, KV head in group): ids 8*q + x with the same x share an XCD, and the
@@ -375,14 +135,15 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   f16x4 rot[4][8];
   {
     const TabT* cs = static_cast<const TabT*>(a.cs);
-    const int n_hi = (a.S + 1023) / 1024;
-    const int n_rows = 64 + 16 + n_hi;             // 64 K rows, 16 low-base rows, n_hi high-base rows
-    constexpr int RPW = (64 + 16 + 64 + G2_NW - 1) / G2_NW;
+    // rows: 64 K rows (t < 64), then 16 of 64 Lo, 16 of 1024 Mi, and ceil(S / 16384) of 16384 T
+    const int n_rows = 96 + (a.S + 16383) / 16384;
+    auto row_t = [](int r) { return r < 64 ? r : (r < 80 ? 64 * (r - 64) : (r < 96 ? 1024 * (r - 80) : 16384 * (r - 96))); };
+    constexpr int RPW = (100 + G2_NW - 1) / G2_NW;
     float4 rowv[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
       const int r = w + i * G2_NW;
-      int t = r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80));
+      int t = row_t(r);
       t = (r < n_rows && t < a.cs_rows) ? t : 0;
       rowv[i] = load4f(cs + (long long)t * (2 * HD) + 4 * lane);
     }
@@ -397,9 +158,9 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
     for (int i = 0; i < RPW; ++i) {
       const int r = w + i * G2_NW;
       if (r < n_rows) {
-        const int t = r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80));
+        const int t = row_t(r);
         const bool ok = t < a.cs_rows;
-        float2* dst = r < 64 ? kc + r * 64 : (r < 80 ? tl + (r - 64) * 64 : th + (r - 80) * 64);
+        float2* dst = r < 64 ? kc + r * 64 : (r < 80 ? tl + (r - 64) * 64 : (r < 96 ? tm + (r - 80) * 64 : tt + (r - 96) * 64));
         float* d0 = reinterpret_cast<float*>(dst + 2 * (lane & 31)) + (lane >> 5);
         d0[0] = ok ? rowv[i].x : (lane < 32 ? 1.f : 0.f);
         d0[2] = ok ? rowv[i].z : (lane < 32 ? 1.f : 0.f);
@@ -468,7 +229,8 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   auto make_q = [&](int base, f16x8 (&qB)[4]) {
     const int J = base >> 6;
     const float2* lo = tl + (J & 15) * 64;
-    const float2* hi = th + (J >> 4) * 64;
+    const float2* mi = tm + ((J >> 4) & 15) * 64;
+    const float2* hi = tt + (J >> 8) * 64;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -476,12 +238,15 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
         const int d0 = 32 * t + 16 * half + 4 * g;     // 4 dims = 2 frequency pairs
         const bf16x4 qv = *reinterpret_cast<const bf16x4*>(qs_lds + n * G_QS + d0);
         const float4 l4 = *reinterpret_cast<const float4*>(lo + (d0 >> 1));
+        const float4 m4 = *reinterpret_cast<const float4*>(mi + (d0 >> 1));
         const float4 h4 = *reinterpret_cast<const float4*>(hi + (d0 >> 1));
-        const float lc[2] = {l4.x, l4.z}, ls[2] = {l4.y, l4.w}, hc[2] = {h4.x, h4.z}, hs[2] = {h4.y, h4.w};
+        const float lc[2] = {l4.x, l4.z}, ls[2] = {l4.y, l4.w}, mc[2] = {m4.x, m4.z}, ms[2] = {m4.y, m4.w};
+        const float tc[2] = {h4.x, h4.z}, ts[2] = {h4.y, h4.w};
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
-          const float cf = (hc[p] * lc[p] - hs[p] * ls[p]) * a.qscale;
-          const float sf = (hs[p] * lc[p] + hc[p] * ls[p]) * a.qscale;
+          const float hc = tc[p] * mc[p] - ts[p] * ms[p], hs = ts[p] * mc[p] + tc[p] * ms[p];
+          const float cf = (hc * lc[p] - hs * ls[p]) * a.qscale;
+          const float sf = (hs * lc[p] + hc * ls[p]) * a.qscale;
           const float x0 = (float)qv[2 * p], x1 = (float)qv[2 * p + 1];
           qB[t][4 * half + 2 * p] = (_Float16)(x0 * cf + x1 * sf);      // R_{-base}
           qB[t][4 * half + 2 * p + 1] = (_Float16)(x1 * cf - x0 * sf);
@@ -490,7 +255,7 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
     }
   };
 
-  float* srow = scores + ((long long)((b * n_groups + grp) * 2) * NB + (s_lo >> 5)) * QH * BLK;
+  float* srow = scores + ((long long)(b * n_groups + grp) * NB + (s_lo >> 5)) * QH * BLK;
   bf16x8 ring[R][4];
 #pragma unroll
   for (int kb = 0; kb < R; ++kb) load_kb(w, kb, ring[kb]);
@@ -569,7 +334,7 @@ __host__ __device__ inline int glrd_pv_tg(int vt) {
 }
 __host__ __device__ inline int glrd_pv_lds(int tpw) { return G_NW * (16 * tpw * 16 + 2 * 16) * 4; }
 
-template <int TPW, int HALVES>
+template <int TPW>
 __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArgs a, const float* scores, float* part,
                                                                  int n_ht, int n_splits2, int split_len2) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -601,14 +366,13 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
   const int nblk = s_hi > s_lo ? (s_hi - s_lo + BLK - 1) / BLK : 0;
   const int nfull = s_hi > s_lo ? (s_hi - s_lo) / BLK : 0;
 
-  const float* sc0 = scores + ((long long)((b * n_groups + grp) * 2 + 0) * NB + (s_lo >> 5)) * QH * BLK +
+  const float* sc0 = scores + ((long long)(b * n_groups + grp) * NB + (s_lo >> 5)) * QH * BLK +
                      (long long)head_c * BLK + 8 * g;
-  const long long half_stride = (long long)NB * QH * BLK;
   const long long blk_stride = (long long)QH * BLK;
   const __bf16* vbase = a.v + b * a.v_sb + grp * a.v_sg + (long long)(s_lo >> 5) * (32 * a.rv) + lane * 8;
 
   struct Blk {
-    float4 s[2 * HALVES];    // positions 8g .. 8g+7 of this lane's head, per dim half
+    float4 s[2];             // positions 8g .. 8g+7 of this lane's head
     bf16x8 v[TPW];
   };
   // Loads of block j (past the split's data: its first block, unused; tiles past r_v: tile 0, unused).
@@ -617,10 +381,6 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
     const float* p0 = sc0 + jj * blk_stride;
     x.s[0] = *reinterpret_cast<const float4*>(p0);
     x.s[1] = *reinterpret_cast<const float4*>(p0 + 4);
-    if constexpr (HALVES == 2) {
-      x.s[2] = *reinterpret_cast<const float4*>(p0 + half_stride);
-      x.s[3] = *reinterpret_cast<const float4*>(p0 + half_stride + 4);
-    }
     // The V latent is read once per decode step (one workgroup per row, group and split): nontemporal.
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
@@ -639,10 +399,6 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
     constexpr bool partial = decltype(partial_tag)::value;
     const int base = s_lo + j * BLK;
     float s[8] = {x.s[0].x, x.s[0].y, x.s[0].z, x.s[0].w, x.s[1].x, x.s[1].y, x.s[1].z, x.s[1].w};
-    if constexpr (HALVES == 2) {
-      s[0] += x.s[2].x; s[1] += x.s[2].y; s[2] += x.s[2].z; s[3] += x.s[2].w;
-      s[4] += x.s[3].x; s[5] += x.s[3].y; s[6] += x.s[3].z; s[7] += x.s[3].w;
-    }
     if constexpr (partial) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
@@ -825,26 +581,10 @@ __global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, 
   }
 }
 
-// ---------------------------------------------------------------------------------------------------
-template <int KBP, typename TabT>
-int launch_scores(const DecodeArgs& a, float* scores, int n_wg, hipStream_t stream) {
-  auto kern = palu_glrd_scores_kernel<KBP, TabT>;
-  const int lds = G1Smem<KBP>::bytes(a.S);
-  if (lds > 160 * 1024) return fail(PALU_EUNSUPPORTED, "grouped-latent decode needs %d bytes of LDS (max 163840)", lds);
-  static int attr_set = 0;
-  if (attr_set < lds) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e != hipSuccess) return fail(PALU_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-    attr_set = lds;
-  }
-  hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(G_NWS * 64), lds, stream, a, scores);
-  return PALU_OK;
-}
-
 template <int KBP, typename TabT>
 int launch_scores_full(const DecodeArgs& a, float* scores, int n_wg, hipStream_t stream) {
   auto kern = palu_glrd_scores_full_kernel<KBP, TabT>;
-  const int lds = G2Smem<KBP>::bytes(a.S);
+  const int lds = G2Smem<KBP>::BYTES;
   static int attr_set = 0;
   if (attr_set < lds) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -853,13 +593,6 @@ int launch_scores_full(const DecodeArgs& a, float* scores, int n_wg, hipStream_t
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)n_wg), dim3(G2_NW * 64), lds, stream, a, scores);
   return PALU_OK;
-}
-
-// LDS of the whole-head scores kernel for r_k and S (the half-head form takes over above 160 KB).
-inline int glrd_full_lds(int rk, int S) {
-  const int kbp = ((rk / 32 + 1) / 2) * 2;
-  const int ukt = 8 * kbp * 1024 > 32768 ? 8 * kbp * 1024 : 32768;
-  return ukt + 16 * 64 * 8 + 16 * G_QS * 2 + ((S + 1023) / 1024) * 64 * 8;
 }
 
 template <typename TabT>
@@ -877,21 +610,6 @@ int scores_full_kb(const DecodeArgs& a, float* scores, int n_wg, hipStream_t s) 
   return fail(PALU_EUNSUPPORTED, "grouped-latent r_k %d (32 .. 512 in steps of 32)", a.rk);
 }
 
-template <typename TabT>
-int scores_kb(const DecodeArgs& a, float* scores, int n_wg, hipStream_t s) {
-  switch ((a.rk / 32 + 1) / 2) {                  // rank blocks rounded up to even
-    case 1: return launch_scores<2, TabT>(a, scores, n_wg, s);
-    case 2: return launch_scores<4, TabT>(a, scores, n_wg, s);
-    case 3: return launch_scores<6, TabT>(a, scores, n_wg, s);
-    case 4: return launch_scores<8, TabT>(a, scores, n_wg, s);
-    case 5: return launch_scores<10, TabT>(a, scores, n_wg, s);
-    case 6: return launch_scores<12, TabT>(a, scores, n_wg, s);
-    case 7: return launch_scores<14, TabT>(a, scores, n_wg, s);
-    case 8: return launch_scores<16, TabT>(a, scores, n_wg, s);
-  }
-  return fail(PALU_EUNSUPPORTED, "grouped-latent r_k %d (32 .. 512 in steps of 32)", a.rk);
-}
-
 template <typename K>
 int set_out_lds(K kern, int lds) {
   static int attr_set = 0;                 // one static per kernel instantiation
@@ -903,10 +621,10 @@ int set_out_lds(K kern, int lds) {
   return PALU_OK;
 }
 
-template <int TPW, int HALVES>
-int launch_pv_h(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, hipStream_t s) {
+template <int TPW>
+int launch_pv_t(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, hipStream_t s) {
   const int lds = glrd_pv_lds(TPW);
-  auto kern = palu_glrd_pv_kernel<TPW, HALVES>;
+  auto kern = palu_glrd_pv_kernel<TPW>;
   static int attr_set = 0;
   if (attr_set < lds) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -918,23 +636,18 @@ int launch_pv_h(const DecodeArgs& a, const float* scores, float* part, const Glr
   return PALU_OK;
 }
 
-template <int TPW>
-int launch_pv_t(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, int halves, hipStream_t s) {
-  return halves == 2 ? launch_pv_h<TPW, 2>(a, scores, part, p, s) : launch_pv_h<TPW, 1>(a, scores, part, p, s);
-}
-
-int launch_pv(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, int halves, hipStream_t s) {
+int launch_pv(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, hipStream_t s) {
   const int vt = a.rv >> 4;
   const int tpw = (vt + glrd_pv_tg(vt) - 1) / glrd_pv_tg(vt);
   switch (tpw) {
-    case 1: return launch_pv_t<1>(a, scores, part, p, halves, s);
-    case 2: return launch_pv_t<2>(a, scores, part, p, halves, s);
-    case 3: return launch_pv_t<3>(a, scores, part, p, halves, s);
-    case 4: return launch_pv_t<4>(a, scores, part, p, halves, s);
-    case 5: return launch_pv_t<5>(a, scores, part, p, halves, s);
-    case 6: return launch_pv_t<6>(a, scores, part, p, halves, s);
-    case 7: return launch_pv_t<7>(a, scores, part, p, halves, s);
-    case 8: return launch_pv_t<8>(a, scores, part, p, halves, s);
+    case 1: return launch_pv_t<1>(a, scores, part, p, s);
+    case 2: return launch_pv_t<2>(a, scores, part, p, s);
+    case 3: return launch_pv_t<3>(a, scores, part, p, s);
+    case 4: return launch_pv_t<4>(a, scores, part, p, s);
+    case 5: return launch_pv_t<5>(a, scores, part, p, s);
+    case 6: return launch_pv_t<6>(a, scores, part, p, s);
+    case 7: return launch_pv_t<7>(a, scores, part, p, s);
+    case 8: return launch_pv_t<8>(a, scores, part, p, s);
   }
   return fail(PALU_EUNSUPPORTED, "grouped-latent r_v %d (32 .. 512 in steps of 32)", a.rv);
 }
@@ -961,25 +674,16 @@ int dispatch_glrd(const DecodeArgs& a0, int cs_dtype, int out_dtype, hipStream_t
     return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_glrd_workspace_bytes), got %zu", need, a.ws_bytes);
   float* scores = reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(a.ws) + 255) & ~uintptr_t(255));
   float* part = scores + p.scores_floats;
-  // Scores: the whole-head form where its LDS fits (every shape but r_k > 416 with S > 40960), else the
-  // half-head form, whose partial scores the PV pass sums.
-  const bool full = glrd_full_lds(a.rk, a.S) <= 160 * 1024;
-  int rc;
-  if (full) {
-    const Plan pf = plan_splits(a.B * a.n_kv, a.S, 2 * G2_NW);
-    a.split_len = pf.split_len;
-    a.n_splits = pf.n_splits;
-    const int n_wg = ((a.B * n_groups * pf.n_splits + 7) / 8) * 8 * a.hpg;
-    rc = cs_dtype == PALU_DTYPE_F32 ? scores_full_kb<float>(a, scores, n_wg, s) : scores_full_kb<__bf16>(a, scores, n_wg, s);
-  } else {
-    a.split_len = p.split_len1;
-    a.n_splits = p.n_splits1;
-    rc = cs_dtype == PALU_DTYPE_F32 ? scores_kb<float>(a, scores, p.n_wg1, s) : scores_kb<__bf16>(a, scores, p.n_wg1, s);
-  }
+  const Plan pf = plan_splits(a.B * a.n_kv, a.S, 2 * G2_NW);
+  a.split_len = pf.split_len;
+  a.n_splits = pf.n_splits;
+  const int n_wg = ((a.B * n_groups * pf.n_splits + 7) / 8) * 8 * a.hpg;
+  const int rc = cs_dtype == PALU_DTYPE_F32 ? scores_full_kb<float>(a, scores, n_wg, s)
+                                            : scores_full_kb<__bf16>(a, scores, n_wg, s);
   if (rc) return rc;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent scores kernel launch: %s", hipGetErrorString(e));
-  if (int rc2 = launch_pv(a, scores, part, p, full ? 1 : 2, s)) return rc2;
+  if (int rc2 = launch_pv(a, scores, part, p, s)) return rc2;
   e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent PV kernel launch: %s", hipGetErrorString(e));
   const int out_lds = glrd_out_lds(a.rep, a.rv);

@@ -10,8 +10,12 @@ K-fast path), and the same decode data flow (attention.py:585-733):
            RoPE on q at current_pos (Meta-interleaved), read straight from the GEMM output
            latents (a head's first r columns, or a group's head slots concatenated) appended at
            current_pos from the GEMM output's latent columns (the strided latent-append kernel)
-           fused latent flash-decode (palu_sdpa_decode; u_v rebuilds V per head for grouped latents)
-           or, on the K-fast path (r_k == head_dim, per-head factors), flash-decode over the cached
+           with PaluRuntime.use_fused_k: fused latent flash-decode (palu_sdpa_decode; u_v rebuilds V
+           per head for grouped latents);
+           without it (the reference's default, attention.py:657-710): the naive path, which rebuilds
+           K = latent @ u_k for the first recon_len positions, rotates it (prefill-mode RoPE), rebuilds
+           grouped V with u_v, and runs the stock flash-decode over them;
+           on the K-fast path (r_k == head_dim, per-head factors), flash-decode over the cached
            rotated K
            absorbed-V output @ the r_v rows per head of wo_fused^T (the reference pads the output to
            head_dim and multiplies the full wo_fused; the padded rows contribute zero)
@@ -63,7 +67,11 @@ class PaluAttention(torch.nn.Module):
         # full-rank per-head factors collapse to stock K / V (reference attention.py:136-141)
         self.recon_k = self.gs > 1 or self.r_k < hd
         self.recon_v = self.gs > 1 or self.r_v < hd
+        # the fused op replaces the naive rebuild only where K really is a latent (reference
+        # attention.py:151); PaluRuntime() defaults to the naive path, as the reference's does
+        self.use_fused_k = self.recon_k and bool(self.palu.runtime.use_fused_k)
         self.cache_layout = cache_layout
+        self._naive_pos = {}
 
         ln = f"layers.{layer_num}.attention"
         P = f"{ln}.palu"
@@ -149,16 +157,57 @@ class PaluAttention(torch.nn.Module):
             decoder_ops.append_from(keys, k_rot.view(B, nkv * hd), hd, hd, pos)
         decoder_ops.append_from(values, vcols, self.gs * hd, self.r_v, pos)
         q4 = q[None]                                                         # [1, B, nh, hd]
-        if self.recon_k:
+        if self.use_fused_k:
             grouped = self.gs > 1
             attn = fused.palu_sdpa_decode(q4, keys, self.w_rot, self.cs_tab, values,
                                           self.head_dim if grouped else self.r_v, pos,
                                           u_v=self.u_v[None] if grouped else None, scale=self.scale,
                                           out_dtype=torch.bfloat16)
+        elif self.recon_k:
+            attn = self._naive_attention(q4, keys, values, pos)
         else:
             attn = fused.flash_multi_latent_attention_decode(q4, keys, values, self.r_v, pos, scale=self.scale)
         out = F.linear(attn[0].reshape(B, nh * self.out_width), self.wo_out)
         return out.reshape(*shape[:-1], self.hidden_size)
+
+    def _recon_len(self) -> int:
+        """Positions the naive path rebuilds: PaluRuntime.recon_len (the caller's bound on current_pos + 1)
+        rounded up to a multiple of 64, or the whole cache (reference attention.py:518-530)."""
+        S = self.palu.runtime.recon_len or self.max_seq_len
+        return min(-(-int(S) // 64) * 64, self.max_seq_len)
+
+    def _cache_rows(self, cache, S):
+        """[B, G, S, w] row-major bf16 view of the first S positions of a cache (tiled caches converted)."""
+        if isinstance(cache, LatentCache):
+            nb = -(-S // 32)
+            return LatentCache(cache.data[:, :, :nb], cache.role).to_rows()[:, :, :S]
+        return cache[:, :, :S]
+
+    def _naive_attention(self, q4, keys, values, pos):
+        """The reference's non-fused decode (attention.py:657-710) on the GPU: K = latent @ u_k for the
+        first recon_len positions (bf16 GEMM, fp32 accumulate), Meta RoPE at positions 0..S-1 (the HIP
+        rope kernel), grouped V rebuilt per head with u_v, then the stock flash-decode (the MLA op:
+        V of width r_v for per-head latents, 128 for grouped ones). Returns [1, B, nh, out_width]."""
+        S = self._recon_len()
+        if self.palu.runtime.check:
+            top = int(pos.max())
+            assert top < S, f"recon_len {S} does not cover current_pos max {top}"
+        B, nkv, hd, gs = self.max_batch_size, self.n_kv_heads, self.head_dim, self.gs
+        per_head = lambda lat: lat if gs == 1 else lat.repeat_interleave(gs, dim=1)     # group -> head latents
+        k_lat = per_head(self._cache_rows(keys, S)).contiguous()                          # [B, nkv, S, r_k]
+        k = torch.matmul(k_lat, self.u_k.contiguous())                                    # [B, nkv, S, hd] bf16
+        rows = B * nkv * S
+        rpos = self._naive_pos.get(rows)
+        if rpos is None:
+            rpos = torch.arange(S, dtype=torch.int32, device=self.device).repeat(B * nkv)
+            self._naive_pos[rows] = rpos
+        k_rot = decoder_ops.rope_rows(k.view(rows, hd), 1, rpos, self.cos, self.sin).view(B, nkv, S, hd)
+        v_lat = self._cache_rows(values, S)
+        if gs > 1:
+            v = torch.matmul(per_head(v_lat).contiguous(), self.u_v.contiguous())          # [B, nkv, S, hd]
+        else:
+            v = v_lat.contiguous()                                                         # absorbed V: [B, nkv, S, r_v]
+        return fused.flash_multi_latent_attention_decode(q4, k_rot, v, v.shape[-1], pos, scale=self.scale)
 
     def forward_prefill(self, x, rot_mats=None, user_id=0, page_table=None, chunk_page_table=None,
                         chunk_start_idx=None, kv_cache=None):

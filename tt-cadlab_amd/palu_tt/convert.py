@@ -16,14 +16,14 @@ State-dict keys are ``layers.{i}.attention.palu.{name}`` (reference convert.py:3
 """
 import hashlib
 import json
-import math
-import re
 from dataclasses import dataclass, field
 from pathlib import Path
-from typing import Dict, List, Optional
+from typing import Dict, List, Optional, Tuple
 
 import torch
+import torch.nn.functional as F
 from safetensors import safe_open
+from safetensors.torch import save_file
 
 from palu_tt import fused, hf
 
@@ -41,8 +41,12 @@ def reverse_permute(t: torch.Tensor, n_heads: int, dim1: int, dim2: int) -> torc
 
 @dataclass
 class PaluRuntime:
-    """Decode-path switches of the reference (convert.py:26-58). On MI355X the fused op always runs its
-    one schedule; use_fused_k selects it over the naive rebuild, the rest is accepted and recorded."""
+    """Decode-path switches of the reference (convert.py:26-58), same fields and defaults. use_fused_k
+    selects the fused latent decode over the naive path (K rebuilt and rotated for the first recon_len
+    positions, then the stock flash-decode; reference attention.py:657-710); check makes the naive path
+    verify that recon_len covers every row's position. The Tensix work-split switches (cs_recurrence,
+    fused_k_chunk, group_heads_per_core, rot_mode, table_mcast) and latent_quant_in_prefill are accepted
+    and recorded: the MI355X kernels have one schedule and bf16 caches."""
     recon_len: Optional[int] = None
     check: bool = False
     use_fused_k: bool = False
@@ -111,62 +115,124 @@ def identity_lowrank(hf_attn: Dict[str, torch.Tensor], n_kv_heads: int, head_dim
     return LowRank(heads(hf_attn["k"]), eye.clone(), heads(hf_attn["v"]), eye.clone())
 
 
-def _read_palu_layer(tensors, ranks, layer, proj, n_kv_heads, head_dim, rank_multiple):
-    """One projection of one layer -> (VT [n_kv, r_pad, hidden], U [n_kv, hd, r_pad], group size)."""
-    key = f"model.layers.{layer}.self_attn.{proj}"
-    r_list = [int(r) for r in ranks[key]]
-    n_groups = len(r_list)
-    assert n_kv_heads % n_groups == 0, f"{key}: {n_groups} groups do not divide {n_kv_heads} KV heads"
-    gs = n_kv_heads // n_groups
-    r_pad = int(math.ceil(max(r_list) / rank_multiple) * rank_multiple)
-    VT_all = tensors[f"{key}.VT.weight"]
-    VT = torch.zeros(n_kv_heads, r_pad, VT_all.shape[1])
-    U = torch.zeros(n_kv_heads, head_dim, r_pad)
-    offsets = [0] + list(torch.tensor(r_list).cumsum(0).tolist())
-    for g, r in enumerate(r_list):
-        U_g = tensors[f"{key}.U.{g}.weight"]
-        assert tuple(U_g.shape) == (gs * head_dim, r), f"{key}.U.{g}: {tuple(U_g.shape)} != {(gs * head_dim, r)}"
-        heads = slice(g * gs, (g + 1) * gs)
-        VT[heads, :r] = VT_all[offsets[g]:offsets[g] + r]
-        U[heads, :, :r] = U_g.reshape(gs, head_dim, r)
-    return VT, U, gs
+class _FactorDump:
+    """A Palu factor directory opened for reading: the group ranks of config.json and a name -> shard
+    index built from the safetensors headers alone; tensors are read one at a time when asked for, so a
+    multi-GB dump is never held in memory whole."""
+
+    def __init__(self, palu_dir: Path):
+        self.dir = Path(palu_dir)
+        cfg = json.loads((self.dir / "config.json").read_text())
+        if "head_wise_ranks" not in cfg:
+            raise ValueError(f"{self.dir / 'config.json'} has no 'head_wise_ranks' entry")
+        self.ranks = {name: [int(r) for r in rs] for name, rs in cfg["head_wise_ranks"].items()}
+        self.where: Dict[str, Path] = {}
+        for shard in sorted(self.dir.glob("*.safetensors")):
+            with safe_open(str(shard), framework="pt") as f:
+                self.where.update(dict.fromkeys(f.keys(), shard))
+
+    def tensor(self, name: str) -> torch.Tensor:
+        if name not in self.where:
+            raise KeyError(f"{self.dir}: no tensor {name!r} in any *.safetensors shard")
+        with safe_open(str(self.where[name]), framework="pt") as f:
+            return f.get_tensor(name).float()
+
+    def projection(self, layer: int, proj: str, n_kv_heads: int, head_dim: int, rank_multiple: int):
+        """(VT [n_kv, r_pad, hidden], U [n_kv, hd, r_pad], group size) of one projection. The stacked VT
+        is cut at the group ranks; every group is zero-padded to r_pad (the widest group rounded up to
+        rank_multiple) and handed to each of its heads, the head taking its hd rows of the group U."""
+        name = f"model.layers.{layer}.self_attn.{proj}"
+        if name not in self.ranks:
+            raise KeyError(f"{self.dir / 'config.json'}: head_wise_ranks has no entry for {name}")
+        group_ranks = self.ranks[name]
+        n_groups = len(group_ranks)
+        if n_groups == 0 or n_kv_heads % n_groups:
+            raise ValueError(f"{name}: {n_groups} rank groups do not divide {n_kv_heads} KV heads")
+        gs = n_kv_heads // n_groups
+        r_pad = -(-max(group_ranks) // rank_multiple) * rank_multiple
+        vt_groups = torch.split(self.tensor(f"{name}.VT.weight"), group_ranks, dim=0)
+        u_groups = [self.tensor(f"{name}.U.{g}.weight") for g in range(n_groups)]
+        for g, (u, r) in enumerate(zip(u_groups, group_ranks)):
+            if tuple(u.shape) != (gs * head_dim, r):
+                raise ValueError(f"{name}.U.{g}.weight is {tuple(u.shape)}, expected {(gs * head_dim, r)} "
+                                 f"(group of {gs} heads of width {head_dim}, rank {r})")
+        VT = torch.stack([F.pad(vt, (0, 0, 0, r_pad - vt.shape[0])) for vt in vt_groups])       # [G, r_pad, hidden]
+        U = torch.cat([F.pad(u, (0, r_pad - u.shape[1])).view(gs, head_dim, r_pad) for u in u_groups])
+        return VT.repeat_interleave(gs, dim=0).contiguous(), U.contiguous(), gs
 
 
 def load_palu_dir(palu_dir: Path, n_layers: int, n_kv_heads: int, head_dim: int, rank_multiple: int = 32,
                   latent_scale: str = "balanced") -> Dict[int, LowRank]:
-    """Factors of every layer, group ranks zero-padded to the layer's max rounded up to rank_multiple."""
-    assert latent_scale in ("balanced", "unit"), f"latent_scale must be 'balanced' or 'unit', got {latent_scale!r}"
-    palu_dir = Path(palu_dir)
-    ranks = json.loads((palu_dir / "config.json").read_text())["head_wise_ranks"]
-    tensors = {}
-    for f in sorted(palu_dir.glob("*.safetensors")):
-        with safe_open(str(f), framework="pt") as sf:
-            for k in sf.keys():
-                if ".k_proj." in k or ".v_proj." in k:
-                    tensors[k] = sf.get_tensor(k).float()
-    out = {}
+    """Per-layer factors of a Palu dump (a factors-only file or a full dump with the same key names),
+    group ranks zero-padded to the layer's widest group rounded up to rank_multiple (no change to any
+    product U @ VT). latent_scale "unit" rescales each latent component to unit scale
+    (unit_scale_lowrank); "balanced" keeps the dump's split."""
+    if latent_scale not in ("balanced", "unit"):
+        raise ValueError(f"latent_scale must be 'balanced' or 'unit', got {latent_scale!r}")
+    dump = _FactorDump(palu_dir)
+    layers = {}
     for i in range(n_layers):
-        k_VT, k_U, gs_k = _read_palu_layer(tensors, ranks, i, "k_proj", n_kv_heads, head_dim, rank_multiple)
-        v_VT, v_U, gs_v = _read_palu_layer(tensors, ranks, i, "v_proj", n_kv_heads, head_dim, rank_multiple)
-        assert gs_k == gs_v, f"layer {i}: K group size {gs_k} != V group size {gs_v}"
-        lr = LowRank(k_VT, k_U, v_VT, v_U, group_size=gs_k)
-        out[i] = unit_scale_lowrank(lr) if latent_scale == "unit" else lr
-    return out
+        k_VT, k_U, gs = dump.projection(i, "k_proj", n_kv_heads, head_dim, rank_multiple)
+        v_VT, v_U, gs_v = dump.projection(i, "v_proj", n_kv_heads, head_dim, rank_multiple)
+        if gs != gs_v:
+            raise ValueError(f"layer {i}: k_proj groups {gs} heads and v_proj {gs_v}; the group size must match")
+        lr = LowRank(k_VT, k_U, v_VT, v_U, group_size=gs)
+        layers[i] = unit_scale_lowrank(lr) if latent_scale == "unit" else lr
+    return layers
+
+
+def save_palu_dir(palu_dir: Path, layers: Dict[int, Dict[str, List[Tuple[torch.Tensor, torch.Tensor]]]],
+                  meta: Optional[dict] = None, shard: str = "palu_lowrank.safetensors") -> Path:
+    """Writes the on-disk format load_palu_dir reads. layers[i][proj] (proj "k_proj" / "v_proj") is the
+    list of per-group factors (U_g [group_size * hd, r_g], VT_g [r_g, hidden]); the group VTs are stacked
+    into one {proj}.VT.weight and config.json["head_wise_ranks"] records r_g per group."""
+    palu_dir = Path(palu_dir)
+    palu_dir.mkdir(parents=True, exist_ok=True)
+    tensors, ranks = {}, {}
+    for i, projs in sorted(layers.items()):
+        for proj, groups in projs.items():
+            name = f"model.layers.{i}.self_attn.{proj}"
+            ranks[name] = [int(vt.shape[0]) for _, vt in groups]
+            tensors[f"{name}.VT.weight"] = torch.cat([vt.float() for _, vt in groups]).contiguous()
+            tensors.update({f"{name}.U.{g}.weight": u.float().contiguous() for g, (u, _) in enumerate(groups)})
+    save_file(tensors, str(palu_dir / shard))
+    (palu_dir / "config.json").write_text(json.dumps({"head_wise_ranks": ranks, **(meta or {})}, indent=1))
+    return palu_dir
+
+
+def _sampled_digest(path: Path, windows: int = 16, width: int = 4096) -> bytes:
+    """sha256 of a safetensors shard's header plus `windows` evenly spaced `width`-byte windows of its data:
+    a content fingerprint that reads a few tens of KB however large the shard is."""
+    h = hashlib.sha256()
+    size = path.stat().st_size
+    with open(path, "rb") as f:
+        n = int.from_bytes(f.read(8), "little")
+        h.update(f.read(n))
+        lo = 8 + n
+        span = max(size - lo - width, 0)
+        for w in range(windows):
+            f.seek(lo + (span * w) // max(windows - 1, 1))
+            h.update(f.read(width))
+    h.update(str(size).encode())
+    return h.digest()
 
 
 def palu_dir_cache_id(palu_dir: Path) -> str:
-    """Directory name + 8 hex digits of a hash of config.json and every shard's name/size/mtime."""
+    """Id of a dump's weight set: the directory name (filesystem-safe) and 8 hex digits of a fingerprint
+    of config.json's bytes and every shard's header and sampled contents, so it changes when the ranks or
+    the tensors change and not when files are merely touched."""
     palu_dir = Path(palu_dir)
     h = hashlib.sha256((palu_dir / "config.json").read_bytes())
-    for f in sorted(palu_dir.glob("*.safetensors")):
-        st = f.stat()
-        h.update(f"{f.name}:{st.st_size}:{st.st_mtime_ns}\n".encode())
-    return f"{re.sub(r'[^A-Za-z0-9._-]', '_', palu_dir.resolve().name)}-{h.hexdigest()[:8]}"
+    for shard in sorted(palu_dir.glob("*.safetensors")):
+        h.update(shard.name.encode() + b"\0" + _sampled_digest(shard))
+    safe_name = "".join(c if (c.isalnum() or c in "._-") else "_" for c in palu_dir.resolve().name)
+    return f"{safe_name}-{h.hexdigest()[:8]}"
 
 
 def palu_cache_id_for(palu_dir: Path, latent_scale: str) -> str:
-    base = palu_dir_cache_id(palu_dir)
-    return base if latent_scale == "balanced" else f"{base}-{latent_scale}"
+    """The id under a latent scale: rescaled factors share shapes and dtypes with the balanced ones, so a
+    cache keyed by them must tell the two apart ("-unit" suffix)."""
+    return palu_dir_cache_id(palu_dir) + ("" if latent_scale == "balanced" else f"-{latent_scale}")
 
 
 def palu_layer_tensors(hf_attn: Dict[str, torch.Tensor], lr: LowRank, n_heads: int, n_kv_heads: int,
@@ -209,28 +275,37 @@ def palu_layer_tensors(hf_attn: Dict[str, torch.Tensor], lr: LowRank, n_heads: i
             "wo_fused": wo_fused, "w_rot": fused.w_rot_from_u_k(u_k.contiguous())}
 
 
+_ATTN_PROJ = {"q": "q_proj", "k": "k_proj", "v": "v_proj", "o": "o_proj"}
+
+
 def hf_attn_weights(hf_dir: Path, layer: int) -> Dict[str, torch.Tensor]:
-    p = f"model.layers.{layer}.self_attn."
-    t = hf.load_tensors(hf_dir, lambda k: k.startswith(p) and k.endswith("proj.weight"))
-    return {"q": t[p + "q_proj.weight"], "k": t[p + "k_proj.weight"], "v": t[p + "v_proj.weight"],
-            "o": t[p + "o_proj.weight"]}
+    """The four attention projection weights of one layer of an HF checkpoint, keyed q / k / v / o."""
+    names = {f"model.layers.{layer}.self_attn.{full}.weight": short for short, full in _ATTN_PROJ.items()}
+    found = hf.load_tensors(hf_dir, names.__contains__)
+    missing = sorted(set(names) - set(found))
+    if missing:
+        raise KeyError(f"{hf_dir}: missing {missing}")
+    return {names[k]: t for k, t in found.items()}
 
 
 def add_palu_to_state_dict(state_dict: dict, hf_dir: Path, palu_dir: Optional[Path], n_layers: int, n_heads: int,
                            n_kv_heads: int, head_dim: int, latent_scale: str = "balanced") -> PaluConfig:
-    """Adds layers.{i}.attention.palu.* for every layer; palu_dir None = identity factors (stock model)."""
-    lrs = None if palu_dir is None else load_palu_dir(palu_dir, n_layers, n_kv_heads, head_dim,
-                                                       latent_scale=latent_scale)
-    rank_k, rank_v = [], []
+    """Puts layers.{i}.attention.palu.{wk_lat_pad, wv_lat_pad, u_k, u_v, wo_fused, w_rot} into state_dict
+    for every layer and returns the PaluConfig describing them. palu_dir None runs the stock model through
+    the Palu path (identity factors, cache id "identity")."""
+    factors = (load_palu_dir(palu_dir, n_layers, n_kv_heads, head_dim, latent_scale=latent_scale)
+               if palu_dir is not None else None)
+    group_sizes = set()
+    per_layer_ranks = []
     for i in range(n_layers):
-        w = hf_attn_weights(hf_dir, i)
-        lr = identity_lowrank(w, n_kv_heads, head_dim) if lrs is None else lrs[i]
-        for name, t in palu_layer_tensors(w, lr, n_heads, n_kv_heads, head_dim).items():
-            state_dict[f"layers.{i}.attention.palu.{name}"] = t
-        rank_k.append(lr.r_k)
-        rank_v.append(lr.r_v)
-    cache_id = "identity" if palu_dir is None else palu_cache_id_for(palu_dir, latent_scale)
-    sizes = {lr.group_size for lr in lrs.values()} if lrs else {1}
-    assert len(sizes) == 1, f"mixed group sizes across layers: {sizes}"
-    return PaluConfig(rank_k=rank_k, rank_v=rank_v, cache_id=cache_id, group_size=sizes.pop(),
-                      latent_scale=latent_scale)
+        attn = hf_attn_weights(hf_dir, i)
+        lr = factors[i] if factors is not None else identity_lowrank(attn, n_kv_heads, head_dim)
+        tensors = palu_layer_tensors(attn, lr, n_heads, n_kv_heads, head_dim)
+        state_dict.update({f"layers.{i}.attention.palu.{k}": t for k, t in tensors.items()})
+        per_layer_ranks.append((lr.r_k, lr.r_v))
+        group_sizes.add(lr.group_size)
+    if len(group_sizes) > 1:
+        raise ValueError(f"layers use different group sizes {sorted(group_sizes)}; one model has one group size")
+    return PaluConfig(rank_k=[rk for rk, _ in per_layer_ranks], rank_v=[rv for _, rv in per_layer_ranks],
+                      cache_id="identity" if palu_dir is None else palu_cache_id_for(palu_dir, latent_scale),
+                      group_size=group_sizes.pop() if group_sizes else 1, latent_scale=latent_scale)

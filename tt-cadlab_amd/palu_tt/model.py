@@ -75,6 +75,16 @@ class Transformer(torch.nn.Module):
                 w2=t(f"{p}.feed_forward.w2.weight")))
         self._graph = None
 
+    def set_fused_k(self, use_fused_k: bool, recon_len: Optional[int] = None) -> None:
+        """Switches every layer between the fused latent decode and the naive path (PaluRuntime.use_fused_k,
+        recon_len), as the reference selects per built model; a captured decode graph is dropped."""
+        self.args.palu.runtime.use_fused_k = bool(use_fused_k)
+        self.args.palu.runtime.recon_len = recon_len
+        for L in self.layers:
+            att = L["attn"]
+            att.use_fused_k = att.recon_k and bool(use_fused_k)
+        self._graph = None
+
     def _ffn(self, L, h):
         gu = h @ L["w13_t"]
         g, u = gu.chunk(2, dim=-1)
@@ -138,12 +148,13 @@ def draw_ranks(n_layers: int, seed: int, lo: int = 32, hi: int = 128, step: int 
 
 
 def random_palu_state_dict(args: ModelArgs, ranks_k: List[int], ranks_v: List[int], device, seed: int = 0,
-                           std: float = 0.02, rank_multiple: int = 32, dense_out: Optional[list] = None) -> dict:
+                           std: float = 0.02, rank_multiple: int = 32, dense_out: Optional[list] = None,
+                           use_fused_k: bool = True) -> dict:
     """Random-init weights N(0, std) generated on `device`, and per-layer per-head SVD factors of the
     k / v projections at the given ranks (on `device` too), zero-padded to a multiple of rank_multiple
-    (convert.load_palu_dir's padding). Every tensor is left in bf16 on `device`. Sets args.palu. With
-    dense_out, every layer's fp32 projections (HF head order) and padded factors are appended to it as
-    (W, LowRank) on the host."""
+    (convert.load_palu_dir's padding). Every tensor is left in bf16 on `device`. Sets args.palu, whose
+    runtime takes the fused latent decode unless use_fused_k is False. With dense_out, every layer's fp32
+    projections (HF head order) and padded factors are appended to it as (W, LowRank) on the host."""
     g = torch.Generator(device=device).manual_seed(seed)
     bf = torch.bfloat16
     randn = lambda *s: torch.randn(*s, device=device, generator=g) * std
@@ -176,7 +187,8 @@ def random_palu_state_dict(args: ModelArgs, ranks_k: List[int], ranks_v: List[in
         sd[f"{p}.feed_forward.w1.weight"] = randn(args.ffn_dim, dim).to(bf)
         sd[f"{p}.feed_forward.w3.weight"] = randn(args.ffn_dim, dim).to(bf)
         sd[f"{p}.feed_forward.w2.weight"] = randn(dim, args.ffn_dim).to(bf)
-    args.palu = convert.PaluConfig(rank_k=rk_pad, rank_v=rv_pad, cache_id=f"random-seed{seed}")
+    args.palu = convert.PaluConfig(rank_k=rk_pad, rank_v=rv_pad, cache_id=f"random-seed{seed}",
+                                   runtime=convert.PaluRuntime(use_fused_k=use_fused_k))
     return sd
 
 
