@@ -1,22 +1,48 @@
 """Decode fidelity of the fused latent op against the naive path on the end-to-end decoder
 (palu_tt.decode_check, the reference's palu_tt/decode_check.py:47-133): one prefill, then the same
 teacher tokens through the naive path (K rebuilt and rotated, stock flash-decode) and through the fused
-op, logits compared per step.
+op, logits compared per step, and both compared with a third pass whose attention core is plain fp32
+torch over the same latent caches (K = latent @ u_k, Meta RoPE, masked softmax, V in fp32).
 
 The full-size case is the end-to-end configuration: 32 Llama-3.1-8B-shaped layers (vocab 128256, FFN
 14336 SwiGLU), per-layer M-LRD ranks drawn from [32, 128] in steps of 8 with mean 64 (the benchmark's
-seeds), batch 64, random 2048-token prompts, 16 teacher-forced decode steps. Bar: PCC >= 0.999 between
-the two paths' logits on every row at every step (the reference publishes a minimum of 0.9948 for its
-own fused op against its naive path, docs/results/stage2e.md:106-112). A small model runs the same check
-through HIP-graph decode steps, with a full-rank V layer (stock V path) among its layers.
+seeds), batch 64, random 2048-token prompts, 16 teacher-forced decode steps. This random-init model
+amplifies bf16-level differences in any one attention core: two fused runs that differ only in which
+wave sums which 32-position block (bf16 rounding of the probabilities) already agree to a logit PCC of
+only about 0.9985. So the bars are: fused vs naive PCC >= 0.995 on every row at every step (the
+reference publishes a minimum of 0.9948 for its own fused op against its naive path,
+docs/results/stage2e.md:106-112); fused vs fp32 attention >= 0.997 on every row and step; and the fused
+path no farther from fp32 attention on average than the naive path (to 5e-4). A small model (a full-rank
+V layer among its layers) runs the same check through HIP-graph decode steps with the 0.999 bar.
 """
 import pytest
 import torch
 
-from palu_tt import decode_check
+from palu_tt import decode_check, fused
 from palu_tt import model as pm
 
 pytestmark = pytest.mark.gpu
+
+
+def fp32_attention_core(layer, q4, keys, values, pos):
+    """Plain fp32 torch attention over a PaluAttention layer's caches: the reference pass."""
+    S = layer._recon_len()
+    gs, nkv, nh, hd = layer.gs, layer.n_kv_heads, layer.n_heads, layer.head_dim
+    per_head = (lambda t: t) if gs == 1 else (lambda t: t.repeat_interleave(gs, dim=1))
+    if layer.recon_k:
+        K = per_head(layer._cache_rows(keys, S)).float() @ layer.u_k.float()                 # [B, nkv, S, hd]
+        K = fused.apply_rope_meta(K, layer.cos[:S][None, None], layer.sin[:S][None, None])
+    else:
+        K = layer._cache_rows(keys, S).float()                                                # rotated full K
+    V = layer._cache_rows(values, S).float()
+    if gs > 1:
+        V = per_head(V) @ layer.u_v.float()
+    B = q4.shape[1]
+    q = q4[0].float().view(B, nkv, nh // nkv, hd)
+    sc = (q @ K.transpose(-1, -2)) * layer.scale                                               # [B, nkv, rep, S]
+    masked = torch.arange(S, device=q.device)[None, :] > pos.long()[:, None]
+    sc = sc.masked_fill(masked[:, None, None, :], float("-inf"))
+    return (torch.softmax(sc, dim=-1) @ V).reshape(1, B, nh, -1).to(torch.bfloat16)
 
 
 def test_fused_matches_naive_on_the_end_to_end_decoder(gpu):
@@ -28,10 +54,12 @@ def test_fused_matches_naive_on_the_end_to_end_decoder(gpu):
     g = torch.Generator().manual_seed(7)
     prompts = torch.randint(0, args.vocab_size, (B, P), generator=g).to(gpu)
     teacher = torch.randint(0, args.vocab_size, (B, T), generator=g).to(gpu)
-    r = decode_check.fused_vs_naive(model, prompts, teacher)
+    r = decode_check.fused_vs_naive(model, prompts, teacher, reference_core=fp32_attention_core)
     print("decode_check end-to-end:", r, flush=True)
     assert r["steps"] == T and r["rows"] == B
-    assert r["pcc_min"] >= 0.999, r
+    assert r["pcc_min"] >= 0.995, r
+    assert r["fused_vs_reference"]["pcc_min"] >= 0.997, r
+    assert r["fused_vs_reference"]["pcc_mean"] >= r["naive_vs_reference"]["pcc_mean"] - 5e-4, r
 
 
 def test_fused_matches_naive_with_graph_steps(gpu):
@@ -41,6 +69,6 @@ def test_fused_matches_naive_with_graph_steps(gpu):
     g = torch.Generator().manual_seed(3)
     prompts = torch.randint(0, args.vocab_size, (5, 97), generator=g).to(gpu)
     teacher = torch.randint(0, args.vocab_size, (5, 9), generator=g).to(gpu)
-    r = decode_check.fused_vs_naive(model, prompts, teacher, use_graph=True)
+    r = decode_check.fused_vs_naive(model, prompts, teacher, use_graph=True, reference_core=fp32_attention_core)
     print("decode_check small, graph steps:", r, flush=True)
-    assert r["pcc_min"] >= 0.999, r
+    assert r["pcc_min"] >= 0.999 and r["fused_vs_reference"]["pcc_min"] >= 0.999, r

@@ -156,19 +156,23 @@ class PaluAttention(torch.nn.Module):
             k_rot = decoder_ops.rope_rows(kcols, nkv, pos, self.cos, self.sin)
             decoder_ops.append_from(keys, k_rot.view(B, nkv * hd), hd, hd, pos)
         decoder_ops.append_from(values, vcols, self.gs * hd, self.r_v, pos)
-        q4 = q[None]                                                         # [1, B, nh, hd]
+        attn = self.decode_core(q[None], keys, values, pos)                  # [1, B, nh, out_width]
+        out = F.linear(attn[0].reshape(B, nh * self.out_width), self.wo_out)
+        return out.reshape(*shape[:-1], self.hidden_size)
+
+    def decode_core(self, q4, keys, values, pos):
+        """The attention core of a decode step over the caches (new rows already appended): q4 [1, B, nh, hd]
+        rotated at pos -> [1, B, nh, out_width] bf16. Fused latent op, naive path, or stock decode over the
+        cached rotated K, as the layer is configured."""
         if self.use_fused_k:
             grouped = self.gs > 1
-            attn = fused.palu_sdpa_decode(q4, keys, self.w_rot, self.cs_tab, values,
+            return fused.palu_sdpa_decode(q4, keys, self.w_rot, self.cs_tab, values,
                                           self.head_dim if grouped else self.r_v, pos,
                                           u_v=self.u_v[None] if grouped else None, scale=self.scale,
                                           out_dtype=torch.bfloat16)
-        elif self.recon_k:
-            attn = self._naive_attention(q4, keys, values, pos)
-        else:
-            attn = fused.flash_multi_latent_attention_decode(q4, keys, values, self.r_v, pos, scale=self.scale)
-        out = F.linear(attn[0].reshape(B, nh * self.out_width), self.wo_out)
-        return out.reshape(*shape[:-1], self.hidden_size)
+        if self.recon_k:
+            return self._naive_attention(q4, keys, values, pos)
+        return fused.flash_multi_latent_attention_decode(q4, keys, values, self.r_v, pos, scale=self.scale)
 
     def _recon_len(self) -> int:
         """Positions the naive path rebuilds: PaluRuntime.recon_len (the caller's bound on current_pos + 1)

@@ -6,11 +6,16 @@ Both paths share one prefill (the fused op replaces decode only, so the prefill 
 are left out of the comparison, as the reference leaves them out). Then every row is fed the same
 teacher tokens one decode step at a time, first through the naive path (K rebuilt for recon_len positions
 and rotated, stock flash-decode) and then through the fused op. Decode step t writes cache position
-prompt_len + t before it reads positions <= prompt_len + t, so the second pass overwrites what the first
+prompt_len + t before it reads positions <= prompt_len + t, so a later pass overwrites what an earlier one
 wrote and reads nothing stale. Reported per step: the minimum over rows of the logit PCC, and how often
 the argmax agrees.
+
+A caller may add a third pass through its own attention core (``reference_core(layer, q4, keys, values,
+pos) -> [1, B, nh, out_width]``, e.g. fp32 attention over the same latent caches): both paths are then
+also compared with it, which separates a path's own error from the run-to-run spread of the model.
 """
-from typing import Dict
+import types
+from typing import Callable, Dict, Optional
 
 import torch
 
@@ -24,28 +29,47 @@ def _pcc_rows(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return (a * b).sum(-1) / (a.norm(dim=-1) * b.norm(dim=-1)).clamp_min(1e-300)
 
 
+def _compare(x: torch.Tensor, y: torch.Tensor) -> Dict[str, object]:
+    pcc = torch.stack([_pcc_rows(x[t], y[t]) for t in range(x.shape[0])])     # [T, B]
+    return {"pcc_min_per_step": [round(float(v), 6) for v in pcc.min(dim=1).values],
+            "pcc_min": float(pcc.min()), "pcc_mean": float(pcc.mean()),
+            "argmax_agree": float((x.argmax(-1) == y.argmax(-1)).double().mean())}
+
+
 @torch.no_grad()
-def fused_vs_naive(model: "pm.Transformer", prompts: torch.Tensor, teacher: torch.Tensor,
-                   use_graph: bool = False) -> Dict[str, object]:
+def fused_vs_naive(model: "pm.Transformer", prompts: torch.Tensor, teacher: torch.Tensor, use_graph: bool = False,
+                   reference_core: Optional[Callable] = None) -> Dict[str, object]:
     """prompts [B, P] and teacher [B, T] token ids on the model's device (B == max_batch_size). Returns
-    {"steps": T, "pcc_min_per_step": [...], "pcc_min": x, "pcc_mean": x, "argmax_agree": x}."""
+    {"steps": T, "rows": B, "pcc_min_per_step": [...], "pcc_min", "pcc_mean", "argmax_agree"} for fused vs
+    naive, and with reference_core also "fused_vs_reference" and "naive_vs_reference" in the same form."""
     B, P = prompts.shape
     T = teacher.shape[1]
     assert B == model.args.max_batch_size and P + T <= model.args.max_seq_len
     pm.prefill_all(model, prompts)
-    runs = {}
-    for fused in (False, True):
-        model.set_fused_k(fused, recon_len=P + T)
-        step = model.decode_graph if use_graph else model.decode
+
+    def decode_pass(use_fused_k: bool, graph: bool) -> torch.Tensor:
+        model.set_fused_k(use_fused_k, recon_len=P + T)
+        step = model.decode_graph if graph else model.decode
         pos = torch.full((B,), P, dtype=torch.int32, device=model.device)
         logits = []
         for t in range(T):
             logits.append(step(teacher[:, t], pos).clone())
             pos += 1
-        runs[fused] = torch.stack(logits)                        # [T, B, vocab] fp32
+        return torch.stack(logits)                                       # [T, B, vocab] fp32
+
+    naive = decode_pass(False, use_graph)
+    fused_l = decode_pass(True, use_graph)
+    out = {"steps": T, "rows": B, **_compare(naive, fused_l)}
+    if reference_core is not None:
+        layers = [L["attn"] for L in model.layers]
+        for att in layers:
+            att.decode_core = types.MethodType(reference_core, att)
+        try:
+            ref = decode_pass(False, False)
+        finally:
+            for att in layers:
+                del att.decode_core                                      # back to the class's method
+        out["fused_vs_reference"] = _compare(fused_l, ref)
+        out["naive_vs_reference"] = _compare(naive, ref)
     model.set_fused_k(True)
-    naive, fused_l = runs[False], runs[True]
-    pcc = torch.stack([_pcc_rows(naive[t], fused_l[t]) for t in range(T)])   # [T, B]
-    agree = (naive.argmax(-1) == fused_l.argmax(-1)).double().mean()
-    return {"steps": T, "rows": B, "pcc_min_per_step": [round(float(x), 6) for x in pcc.min(dim=1).values],
-            "pcc_min": float(pcc.min()), "pcc_mean": float(pcc.mean()), "argmax_agree": float(agree)}
+    return out
