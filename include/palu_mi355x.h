@@ -2,7 +2,8 @@
  *
  * Every entry point takes raw device pointers, plain integer shapes and a hipStream_t, enqueues its
  * kernels on that stream and returns without synchronising. No entry point allocates device memory:
- * split-K partials go to a caller-provided workspace whose size palu_decode_workspace_bytes reports.
+ * split-K partials go to a caller-provided workspace whose size palu_decode_workspace_bytes reports
+ * (palu_sdpa_decode_noalloc keeps them in a static device array instead).
  * Tensors are dense row-major in the shapes given below; bf16 tensors must be 16-byte aligned.
  *
  * Return value: PALU_OK, or an error code with a message for palu_last_error() (thread-local, valid
@@ -20,7 +21,7 @@
 extern "C" {
 #endif
 
-#define PALU_ABI_VERSION 7
+#define PALU_ABI_VERSION 8
 
 #define PALU_OK 0
 #define PALU_EINVAL 1       /* arguments outside the op's envelope */
@@ -104,6 +105,27 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
                      int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width,
                      int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
                      void* workspace, size_t workspace_bytes, palu_stream_t stream);
+
+/* Bytes of the static device scratch array behind palu_sdpa_decode_noalloc (one per GPU). */
+#define PALU_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* palu_sdpa_decode without a workspace argument, allocating nothing. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The scratch memory the kernels need (split partials of the
+ * length-aware plan; the grouped-latent path's scores and PV partials) lives in a static device array of
+ * PALU_NOALLOC_SCRATCH_BYTES per GPU that the library holds until the process ends; the array of the
+ * current device (hipGetDevice) is used, so the stream must belong to that device. Shapes whose scratch
+ * need (palu_decode_workspace_bytes, or palu_glrd_workspace_bytes with u_v) exceeds it are rejected with
+ * PALU_EUNSUPPORTED before anything is launched. Every call on one GPU shares that GPU's array: calls
+ * ordered on one stream are safe; calls that overlap on one GPU (several streams or host threads) race.
+ * Every other argument, the envelope and the error messages are those of palu_sdpa_decode. */
+int palu_sdpa_decode_noalloc(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab,
+                             const void* v_latent, int head_dim_v, const int32_t* cur_pos, void* out,
+                             const float* rot_step, const void* trans_mat, const void* u_v, float scale,
+                             int heads_per_core, int rot_mode, int table_mcast, int k_chunk, int batch, int n_q,
+                             int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width, int cs_rows,
+                             int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
+                             palu_stream_t stream);
 
 /* Paged fused latent flash-decode: palu_sdpa_decode over caches held in fixed-size pages. The reference
  * keeps contiguous per-row caches (palu_tt/attention.py:86, 274-283); paging follows ttnn's paged decode

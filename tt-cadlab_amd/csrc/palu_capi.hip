@@ -3,6 +3,9 @@
 // translation units.
 #include "palu_kernel.h"
 
+#include <atomic>
+#include <mutex>
+
 namespace palu {
 
 thread_local char g_err[1024] = "";
@@ -245,6 +248,38 @@ int flash_setup(DecodeArgs& a, const void* q, const void* k, const void* v, cons
   return PALU_OK;
 }
 
+// Scratch of palu_sdpa_decode_noalloc: a static device array, one copy per GPU the library runs on. Host
+// code never uses the array's name as an address: its device address comes from hipGetSymbolAddress,
+// once per device with that device current, and is kept per device.
+__device__ __align__(256) unsigned char scratch[PALU_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int scratch_of_current_device(void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(PALU_EHIP, "palu_sdpa_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(PALU_EUNSUPPORTED, "palu_sdpa_decode_noalloc: device %d (this build keeps scratch for %d)", dev,
+                kMaxDevices);
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr)
+        return fail(PALU_EHIP, "palu_sdpa_decode_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                    hipGetErrorString(e));
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *addr = p;
+  return PALU_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -278,6 +313,39 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
                           w_rot_width, cs_rows, cs_cols, cs_dtype, out_dtype, cache_layout, deterministic, workspace,
                           workspace_bytes, "palu_sdpa_decode"))
     return rc;
+  a.k_sg = (long long)seq_len * r_k;
+  a.k_sb = a.k_sg * n_groups;
+  a.v_sg = (long long)seq_len * r_v;
+  a.v_sb = a.v_sg * n_groups;
+  return sdpa_dispatch(a, false, cache_layout, r_k, r_v, cs_dtype, out_dtype, stream);
+}
+
+int palu_sdpa_decode_noalloc(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab,
+                             const void* v_latent, int head_dim_v, const int32_t* cur_pos, void* out,
+                             const float* rot_step, const void* trans_mat, const void* u_v, float scale,
+                             int heads_per_core, int rot_mode, int table_mcast, int k_chunk, int batch, int n_q,
+                             int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width, int cs_rows,
+                             int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
+                             hipStream_t stream) {
+  palu::g_err[0] = 0;
+  (void)table_mcast;
+  DecodeArgs a;
+  // The envelope first (same checks and messages as palu_sdpa_decode), with the scratch size standing in
+  // for the workspace; nothing touches the HIP runtime before the shapes are known to fit.
+  if (int rc = sdpa_setup(a, q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos, out, rot_step, trans_mat, u_v,
+                          scale, heads_per_core, rot_mode, k_chunk, batch, n_q, n_kv, n_groups, seq_len, r_k, r_v,
+                          w_rot_width, cs_rows, cs_cols, cs_dtype, out_dtype, cache_layout, deterministic, nullptr,
+                          PALU_NOALLOC_SCRATCH_BYTES, "palu_sdpa_decode_noalloc"))
+    return rc;
+  const size_t need = u_v != nullptr ? glrd_workspace_bytes(batch, n_q, n_kv, n_groups, seq_len, r_v)
+                                     : decode_ws_bytes(batch * n_kv, head_dim_v);
+  if (need > PALU_NOALLOC_SCRATCH_BYTES)
+    return fail(PALU_EUNSUPPORTED, "palu_sdpa_decode_noalloc: these shapes need %zu bytes of scratch, more than the "
+                                   "%zu of the static array; call palu_sdpa_decode with a workspace", need,
+                (size_t)PALU_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (int rc = scratch_of_current_device(&ws)) return rc;
+  a.ws = static_cast<float*>(ws);
   a.k_sg = (long long)seq_len * r_k;
   a.k_sb = a.k_sg * n_groups;
   a.v_sg = (long long)seq_len * r_v;
