@@ -225,8 +225,9 @@ def measure_paged(dev, steps, warmup):
 
 def measure_glrd(dev, steps, warmup):
     """G-LRD group size 4: 8 KV heads in 2 groups sharing one K and one V latent, per-group ranks
-    drawn from {128, 192, 256, 384, 512} (seeded; a layer's latent is as wide as its widest group, the
-    narrower group zero-padded), V rebuilt per head in-kernel; batch 16, ctx 16384, tiled bf16.
+    drawn from {128, 192, 256, 384, 512} (seeded; the caches are as wide as the widest group, the
+    narrower group's columns padding the op never reads), V rebuilt per head in-kernel; batch 16, ctx
+    16384, tiled bf16.
     Also the widest layer (512, 512) and the stock full-KV decode at the same shape."""
     from palu_tt import fused
     from palu_tt.cache import LatentCache
@@ -252,7 +253,15 @@ def measure_glrd(dev, steps, warmup):
             v.data.normal_(generator=gd)
             layers.append((k, v))
         u_k = torch.randn(NKV, r_k, HD, generator=g) / r_k ** 0.5
-        u_v = (torch.randn(NKV, r_v, HD, generator=g) / r_v ** 0.5)[None].to(dev, torch.bfloat16).contiguous()
+        u_v = torch.randn(NKV, r_v, HD, generator=g) / r_v ** 0.5
+        # the drawn layer: each group at its own ranks, the narrower group zero-padded in the factors (as
+        # load_palu_dir pads it) and the op told the groups' ranks, so it reads only their own columns
+        group_ranks = (drawn_k, drawn_v) if note == "drawn" else None
+        if group_ranks is not None:
+            for gi in range(ng):
+                u_k[hpg * gi:hpg * (gi + 1), drawn_k[gi]:] = 0
+                u_v[hpg * gi:hpg * (gi + 1), drawn_v[gi]:] = 0
+        u_v = u_v[None].to(dev, torch.bfloat16).contiguous()
         w_rot = fused.w_rot_from_u_k(u_k)[None].to(dev, torch.bfloat16).contiguous()
         out = torch.empty(1, B, NQ, HD, dtype=torch.bfloat16, device=dev)
         ws = torch.empty(max(fused._native.load().palu_glrd_workspace_bytes(B, NQ, NKV, ng, S, r_v), 1),
@@ -260,7 +269,8 @@ def measure_glrd(dev, steps, warmup):
 
         def step(l):
             k, v = layers[l]
-            fused.palu_sdpa_decode(q, k, w_rot, cs, v, HD, cur, u_v=u_v, scale=HD ** -0.5, out=out, workspace=ws)
+            fused.palu_sdpa_decode(q, k, w_rot, cs, v, HD, cur, u_v=u_v, scale=HD ** -0.5, out=out, workspace=ws,
+                                   group_ranks=group_ranks)
 
         wall, kern, _ = time_calls(step, n_layers, steps, warmup)
         # algorithmic work counts each group at its own ranks (the drawn layer's narrower group is
@@ -271,7 +281,7 @@ def measure_glrd(dev, steps, warmup):
                     2 * B * hpg * NQ // NKV * rv_g * HD for rk_g, rv_g in zip(gk, gv))
         res.append({"ranks": note, "rank_k": r_k, "rank_v": r_v, "group_ranks": {"k": gk, "v": gv},
                     "us_per_layer": round(wall * 1e3, 2), "kernel_us": round(kern * 1e3, 2),
-                    "cache_bytes_read": B * ng * S * (r_k + r_v) * 2, **_roof(nbytes, flops, kern)})
+                    "cache_bytes": B * ng * S * (r_k + r_v) * 2, **_roof(nbytes, flops, kern)})
         del layers
         torch.cuda.empty_cache()
     kv = [(LatentCache.zeros(B, NKV, S, HD, dev, "k"), LatentCache.zeros(B, NKV, S, HD, dev, "v")) for _ in range(2)]

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define PALU_ABI_VERSION 8
+#define PALU_ABI_VERSION 9
 
 #define PALU_OK 0
 #define PALU_EINVAL 1       /* arguments outside the op's envelope */
@@ -93,6 +93,14 @@ size_t palu_glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int
  *                                    softmax(q K^T) (v_latent u_v[h]), 128 wide (head_dim_v == 128);
  *                                    needs PALU_LAYOUT_TILED, r_k and r_v in 32 .. 512 (multiples of
  *                                    32), and is not built for the paged entry point (PALU_EUNSUPPORTED)
+ *   group_ranks [2 * n_groups] int32 (host memory, may be NULL)
+ *                                    with u_v: each latent group's own ranks, K ranks then V ranks,
+ *                                    multiples of 32 up to r_k / r_v. The caches keep r_k / r_v columns
+ *                                    per group (the reference pads every group to the layer's widest);
+ *                                    the kernels read and multiply only a group's own columns, so the
+ *                                    padding is never touched. NULL: every group at r_k / r_v. Without
+ *                                    u_v every entry must equal r_k / r_v (PALU_EUNSUPPORTED otherwise).
+ *                                    No counterpart in the reference's op interface.
  *   scale                            softmax scale (the reference passes head_dim^-0.5)
  *   heads_per_core, rot_mode, table_mcast, k_chunk
  *                                    the reference's Tensix work-split switches; validated, and
@@ -101,7 +109,8 @@ size_t palu_glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int
  */
 int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab, const void* v_latent,
                      int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step, const void* trans_mat,
-                     const void* u_v, float scale, int heads_per_core, int rot_mode, int table_mcast, int k_chunk,
+                     const void* u_v, const int32_t* group_ranks, float scale, int heads_per_core, int rot_mode,
+                     int table_mcast, int k_chunk,
                      int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width,
                      int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
                      void* workspace, size_t workspace_bytes, palu_stream_t stream);
@@ -121,7 +130,8 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
  * Every other argument, the envelope and the error messages are those of palu_sdpa_decode. */
 int palu_sdpa_decode_noalloc(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab,
                              const void* v_latent, int head_dim_v, const int32_t* cur_pos, void* out,
-                             const float* rot_step, const void* trans_mat, const void* u_v, float scale,
+                             const float* rot_step, const void* trans_mat, const void* u_v,
+                             const int32_t* group_ranks, float scale,
                              int heads_per_core, int rot_mode, int table_mcast, int k_chunk, int batch, int n_q,
                              int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width, int cs_rows,
                              int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,

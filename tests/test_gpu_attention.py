@@ -32,22 +32,26 @@ class _Args:
         self.palu = palu
 
 
-def _group_svd(W, nkv, gs, rank):
+def _group_svd(W, nkv, gs, rank, group_ranks=None):
     """Per-group truncated SVD with Palu's balanced split; every head of a group gets the group's VT
-    and its hd-row slice of the group's U (reference compress.py:12-23, stage2b-design.md:80-86)."""
+    and its hd-row slice of the group's U (reference compress.py:12-23, stage2b-design.md:80-86). With
+    group_ranks, group g keeps its first group_ranks[g] components and is zero-padded to rank."""
     Wg = W.reshape(nkv // gs, gs * HD, -1)
     U, VT = ref.svd_per_head(Wg.reshape(-1, W.shape[1]), nkv // gs, rank)       # [G, gs*hd, r], [G, r, dim]
+    for g, r in enumerate(group_ranks or []):
+        U[g, :, r:] = 0
+        VT[g, r:] = 0
     U_h = U.reshape(nkv // gs, gs, HD, rank).reshape(nkv, HD, rank)
     VT_h = VT.repeat_interleave(gs, dim=0)
     return U_h.contiguous(), VT_h.contiguous()
 
 
-def _layer(dim, nh, nkv, r_k, r_v, gs, seed, use_fused_k=True, recon_len=None):
+def _layer(dim, nh, nkv, r_k, r_v, gs, seed, use_fused_k=True, recon_len=None, group_ranks=None):
     g = torch.Generator().manual_seed(seed)
     W = {"q": torch.randn(nh * HD, dim, generator=g) * 0.02, "k": torch.randn(nkv * HD, dim, generator=g) * 0.02,
          "v": torch.randn(nkv * HD, dim, generator=g) * 0.02, "o": torch.randn(dim, nh * HD, generator=g) * 0.02}
-    Uk, VTk = _group_svd(W["k"], nkv, gs, r_k)
-    Uv, VTv = _group_svd(W["v"], nkv, gs, r_v)
+    Uk, VTk = _group_svd(W["k"], nkv, gs, r_k, group_ranks and group_ranks[0])
+    Uv, VTv = _group_svd(W["v"], nkv, gs, r_v, group_ranks and group_ranks[1])
     lr = convert.LowRank(VTk, Uk, VTv, Uv, group_size=gs)
     # the model state dict holds wq in Meta (interleaved-pair) order, as the reference's checkpoint loader
     # leaves it; the converter's K tensors are Meta-ordered too
@@ -56,7 +60,8 @@ def _layer(dim, nh, nkv, r_k, r_v, gs, seed, use_fused_k=True, recon_len=None):
     for name, t in convert.palu_layer_tensors(W, lr, nh, nkv, HD).items():
         sd[f"layers.0.attention.palu.{name}"] = t
     palu = convert.PaluConfig(rank_k=[r_k], rank_v=[r_v], cache_id="test", group_size=gs,
-                              runtime=convert.PaluRuntime(use_fused_k=use_fused_k, recon_len=recon_len, check=True))
+                              runtime=convert.PaluRuntime(use_fused_k=use_fused_k, recon_len=recon_len, check=True),
+                              group_ranks=[group_ranks] if group_ranks else None)
     oracle = ref.PaluRefAttention(nh, nkv, HD, THETA, LLAMA3, W["q"], W["o"], ref.Factors(VTk, Uk, VTv, Uv))
     return sd, palu, oracle
 
@@ -77,6 +82,20 @@ def _close(out, exp, what):
 def test_attention_prefill_then_decode_matches_layer_oracle(gpu, r_k, r_v, gs, layout, fused, recon_len):
     dim, nh, nkv, B, S0, steps = 1024, 8, 2, 2, 40, 6
     sd, palu, oracle = _layer(dim, nh, nkv, r_k, r_v, gs, seed=r_k + r_v + gs, use_fused_k=fused, recon_len=recon_len)
+    _drive(gpu, sd, palu, oracle, dim, nh, nkv, B, S0, steps, layout, fused)
+
+
+def test_attention_grouped_latents_of_unequal_ranks(gpu):
+    """G-LRD with 2 groups of 2 KV heads whose ranks differ (K 96 / 192, V 256 / 64), padded to the
+    widest as load_palu_dir pads them; the layer passes the groups' own ranks to the fused op."""
+    dim, nh, nkv, B, S0, steps = 1024, 8, 4, 2, 40, 6
+    gr = ([96, 192], [256, 64])
+    sd, palu, oracle = _layer(dim, nh, nkv, 192, 256, 2, seed=7, group_ranks=gr)
+    att = _drive(gpu, sd, palu, oracle, dim, nh, nkv, B, S0, steps, "tiled", True)
+    assert att.group_ranks == ([96, 192], [256, 64])
+
+
+def _drive(gpu, sd, palu, oracle, dim, nh, nkv, B, S0, steps, layout, fused):
     att = PaluAttention(gpu, None, _Args(dim, nh, nkv, 128, B, palu), sd, None, 0, cache_layout=layout)
     assert att.use_fused_k == (fused and att.recon_k)
     g = torch.Generator().manual_seed(9)
@@ -89,6 +108,7 @@ def test_attention_prefill_then_decode_matches_layer_oracle(gpu, r_k, r_v, gs, l
         out = att.forward(x[:, t].to(gpu), torch.full((B,), t, dtype=torch.int32, device=gpu), mode="decode")
         torch.cuda.synchronize()
         _close(out, exp, f"decode step {t}")
+    return att
 
 
 def test_attention_kv_bytes_per_token(gpu):

@@ -129,6 +129,34 @@ def test_glrd_widest_ranks_at_long_context(gpu, S, pos):
     _check(_run(gpu, q, k, v, u_k, u_v, p, S), _oracle(q, k, v, u_k, u_v, p, S))
 
 
+@pytest.mark.parametrize("ranks_k,ranks_v,B,S", [([128, 512], [192, 384], 16, 16384), ([96, 32], [64, 160], 3, 1000),
+                                                  ([256, 256], [512, 128], 2, 4096)])
+def test_glrd_per_group_ranks_never_read_the_padding(gpu, ranks_k, ranks_v, B, S):
+    """Groups of unequal ranks in caches padded to the widest group: told each group's own ranks, the op
+    reads and multiplies only those columns. The padding columns of the latents and the padding rows of
+    u_k / u_v hold NaN on the GPU (zeros for the oracle), so a single read of them would show. The first
+    case is the configuration's drawn layer (B=16, ctx 16384, K ranks (128, 512), V ranks (192, 384))."""
+    S32 = (S + 31) // 32 * 32
+    r_k, r_v = max(ranks_k), max(ranks_v)
+    q, k, v, u_k, u_v, pos = _case(B, S32, r_k, r_v, hpg=4, seed=sum(ranks_k) + S)
+    pos.clamp_(max=S - 1)
+    for g, (rk, rv) in enumerate(zip(ranks_k, ranks_v)):
+        k[:, g, :, rk:] = 0
+        v[:, g, :, rv:] = 0
+        u_k[4 * g:4 * g + 4, rk:] = 0
+        u_v[4 * g:4 * g + 4, rv:] = 0
+    rows = [0, B - 1] if B > 2 else list(range(B))
+    exp = _oracle(q[:, rows], k[rows], v[rows], u_k, u_v, pos[rows], S32)
+    kn, vn, ukn, uvn = k.clone(), v.clone(), u_k.clone(), u_v.clone()
+    for g, (rk, rv) in enumerate(zip(ranks_k, ranks_v)):
+        kn[:, g, :, rk:] = float("nan")
+        vn[:, g, :, rv:] = float("nan")
+        ukn[4 * g:4 * g + 4, rk:] = float("nan")
+        uvn[4 * g:4 * g + 4, rv:] = float("nan")
+    out = _run(gpu, q, kn, vn, ukn, uvn, pos, S32, group_ranks=(ranks_k, ranks_v))
+    _check(out[:, rows], exp)
+
+
 def test_glrd_deterministic_repeat(gpu):
     args = _case(2, 2048, 256, 256, hpg=4, seed=8)
     a = _run(gpu, *args, 2048)

@@ -121,6 +121,7 @@ def test_load_palu_dir_mlrd_and_glrd(tmp_path):
     ranks, tensors = _write_palu_dir(tmp_path / "g", 2, hidden, hd, glrd, glrd)
     lr = convert.load_palu_dir(tmp_path / "g", 2, nkv, hd, rank_multiple=32)
     assert set(lr) == {0, 1} and lr[0].group_size == 2 and lr[0].r_k == 64     # 48 padded up to 64
+    assert lr[1].group_ranks_k == [48, 20] and lr[1].group_ranks_v == [48, 20]
     key = "model.layers.1.self_attn.k_proj"
     VT_all = tensors[f"{key}.VT.weight"]
     for h in range(nkv):
@@ -302,12 +303,13 @@ _FAKE = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced: validat
 
 def _sdpa(lib, **kw):
     a = dict(q=_FAKE, k=_FAKE, w=_FAKE, cs=_FAKE, v=_FAKE, head_dim_v=64, cur=_FAKE, out=_FAKE, rot_step=None,
-             trans_mat=None, u_v=None, scale=0.088, heads_per_core=0, rot_mode=2, table_mcast=1, k_chunk=0,
+             trans_mat=None, u_v=None, group_ranks=None, scale=0.088, heads_per_core=0, rot_mode=2, table_mcast=1, k_chunk=0,
              batch=2, n_q=8, n_kv=2, n_groups=2, seq_len=256, r_k=64, r_v=64, w_rot_width=256, cs_rows=256,
              cs_cols=256, cs_dtype=0, out_dtype=1, layout=0, det=0, ws=None, ws_bytes=0, stream=None)
     a.update(kw)
     rc = lib.palu_sdpa_decode(a["q"], a["k"], a["w"], a["cs"], a["v"], a["head_dim_v"], a["cur"], a["out"],
-                              a["rot_step"], a["trans_mat"], a["u_v"], a["scale"], a["heads_per_core"], a["rot_mode"],
+                              a["rot_step"], a["trans_mat"], a["u_v"], a["group_ranks"], a["scale"], a["heads_per_core"],
+                              a["rot_mode"],
                               a["table_mcast"], a["k_chunk"], a["batch"], a["n_q"], a["n_kv"], a["n_groups"],
                               a["seq_len"], a["r_k"], a["r_v"], a["w_rot_width"], a["cs_rows"], a["cs_cols"],
                               a["cs_dtype"], a["out_dtype"], a["layout"], a["det"], a["ws"], a["ws_bytes"], a["stream"])
@@ -336,6 +338,9 @@ def _sdpa(lib, **kw):
     (dict(seq_len=70000, cs_rows=70000), _native.PALU_EUNSUPPORTED, "65536"),
     (dict(q=ctypes.c_void_p((1 << 20) + 2)), _native.PALU_EINVAL, "aligned"),
     (dict(out=None), _native.PALU_EINVAL, "null"),
+    (dict(group_ranks=(ctypes.c_int32 * 4)(32, 64, 64, 64)), _native.PALU_EUNSUPPORTED, "group_ranks"),
+    (dict(group_ranks=(ctypes.c_int32 * 4)(48, 64, 64, 64)), _native.PALU_EINVAL, "multiple of 32"),
+    (dict(group_ranks=(ctypes.c_int32 * 4)(64, 64, 96, 64)), _native.PALU_EINVAL, "V rank"),
 ])
 def test_sdpa_decode_envelope_errors(lib, kw, code, needle):
     rc, msg = _sdpa(lib, **kw)

@@ -43,7 +43,7 @@ def _call(lib, d, dims, noalloc):
     out = torch.full((1, dims["B"], dims["nh"], dims["dv"]), float("nan"), dtype=torch.float32, device=dev)
     common = [_native.ptr(d["q"]), _native.ptr(d["k"]), _native.ptr(d["w_rot"]), _native.ptr(d["cs"]),
               _native.ptr(d["v"]), dims["dv"], _native.ptr(d["pos"]), _native.ptr(out), None, None,
-              _native.ptr(d["u_v"]), HD ** -0.5, 0, 2, 1, 0, dims["B"], dims["nh"], dims["nkv"], dims["n_groups"],
+              _native.ptr(d["u_v"]), None, HD ** -0.5, 0, 2, 1, 0, dims["B"], dims["nh"], dims["nkv"], dims["n_groups"],
               dims["S"], dims["r_k"], dims["r_v"], 2 * HD, dims["S"], 2 * HD, _native.DTYPE_F32, _native.DTYPE_F32,
               _native.LAYOUT_TILED, 1]
     stream = _native.stream_handle(dev)
@@ -91,7 +91,7 @@ def test_noalloc_rejects_shapes_beyond_the_scratch():
     fake = ctypes.c_void_p(1 << 20)
     B, S, nq, nkv, G, r = 64, 65536, 32, 8, 2, 512          # grouped-latent scores alone: 512 MiB
     assert lib.palu_glrd_workspace_bytes(B, nq, nkv, G, S, r) > _native.NOALLOC_SCRATCH_BYTES
-    rc = lib.palu_sdpa_decode_noalloc(fake, fake, fake, fake, fake, HD, fake, fake, None, None, fake, 0.088, 0, 2, 1,
+    rc = lib.palu_sdpa_decode_noalloc(fake, fake, fake, fake, fake, HD, fake, fake, None, None, fake, None, 0.088, 0, 2, 1,
                                       0, B, nq, nkv, G, S, r, r, 2 * HD, S, 2 * HD, 0, 1, _native.LAYOUT_TILED, 0,
                                       None)
     assert rc == _native.PALU_EUNSUPPORTED and "scratch" in lib.palu_last_error().decode()

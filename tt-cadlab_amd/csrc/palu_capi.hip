@@ -133,7 +133,8 @@ int check_append(void* cache, const void* new_rows, const int32_t* update_idxs, 
 // cache strides and the paging fields.
 int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w_rot, const void* cs_tab,
                const void* v_latent, int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step,
-               const void* trans_mat, const void* u_v, float scale, int heads_per_core, int rot_mode, int k_chunk,
+               const void* trans_mat, const void* u_v, const int32_t* group_ranks, float scale, int heads_per_core,
+               int rot_mode, int k_chunk,
                int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width, int cs_rows,
                int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic, void* workspace,
                size_t workspace_bytes, const char* who) {
@@ -188,8 +189,29 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
   if (!aligned16(q) || !aligned16(k_latent) || !aligned16(v_latent) || !aligned16(w_rot) || !aligned16(cs_tab))
     return fail(PALU_EINVAL, "q, k_latent, v_latent, w_rot and cs_tab must be 16-byte aligned");
   if ((long long)batch * n_kv > 65535) return fail(PALU_EUNSUPPORTED, "batch * n_kv = %d exceeds the grid limit", batch * n_kv);
+  if (group_ranks != nullptr) {
+    if (n_groups > MAX_GROUPS)
+      return fail(PALU_EUNSUPPORTED, "group_ranks: %d latent groups (this build takes per-group ranks for up to %d)",
+                  n_groups, MAX_GROUPS);
+    for (int g = 0; g < 2 * n_groups; ++g) {
+      const int r = group_ranks[g], top = g < n_groups ? r_k : r_v;
+      if (r < 32 || r > top || r % 32 != 0)
+        return fail(PALU_EINVAL, "group_ranks[%d] = %d: a group's %s rank must be a multiple of 32 in 32..%d", g, r,
+                    g < n_groups ? "K" : "V", top);
+      if (u_v == nullptr && r != top)
+        return fail(PALU_EUNSUPPORTED, "group_ranks below the cache width need grouped latents with u_v; the "
+                                       "per-head (absorbed-V) kernels read whole latent rows");
+    }
+  }
 
   memset(&a, 0, sizeof(a));
+  for (int g = 0; g < MAX_GROUPS; ++g) {
+    a.grk[g] = (short)(group_ranks != nullptr && g < n_groups ? group_ranks[g] : r_k);
+    a.grv[g] = (short)(group_ranks != nullptr && g < n_groups ? group_ranks[n_groups + g] : r_v);
+  }
+  a.grp_lo = 0;
+  a.grp_cnt = n_groups;
+  a.rk_eff = r_k;
   a.q = static_cast<const __bf16*>(q);
   a.k = static_cast<const __bf16*>(k_latent);
   a.v = static_cast<const __bf16*>(v_latent);
@@ -301,7 +323,8 @@ size_t palu_glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int
 
 int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab, const void* v_latent,
                      int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step, const void* trans_mat,
-                     const void* u_v, float scale, int heads_per_core, int rot_mode, int table_mcast, int k_chunk,
+                     const void* u_v, const int32_t* group_ranks, float scale, int heads_per_core, int rot_mode,
+                     int table_mcast, int k_chunk,
                      int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width,
                      int cs_rows, int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -309,7 +332,7 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
   (void)table_mcast;
   DecodeArgs a;
   if (int rc = sdpa_setup(a, q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos, out, rot_step, trans_mat, u_v,
-                          scale, heads_per_core, rot_mode, k_chunk, batch, n_q, n_kv, n_groups, seq_len, r_k, r_v,
+                          group_ranks, scale, heads_per_core, rot_mode, k_chunk, batch, n_q, n_kv, n_groups, seq_len, r_k, r_v,
                           w_rot_width, cs_rows, cs_cols, cs_dtype, out_dtype, cache_layout, deterministic, workspace,
                           workspace_bytes, "palu_sdpa_decode"))
     return rc;
@@ -322,7 +345,8 @@ int palu_sdpa_decode(const void* q, const void* k_latent, const void* w_rot, con
 
 int palu_sdpa_decode_noalloc(const void* q, const void* k_latent, const void* w_rot, const void* cs_tab,
                              const void* v_latent, int head_dim_v, const int32_t* cur_pos, void* out,
-                             const float* rot_step, const void* trans_mat, const void* u_v, float scale,
+                             const float* rot_step, const void* trans_mat, const void* u_v,
+                             const int32_t* group_ranks, float scale,
                              int heads_per_core, int rot_mode, int table_mcast, int k_chunk, int batch, int n_q,
                              int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width, int cs_rows,
                              int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic,
@@ -333,7 +357,7 @@ int palu_sdpa_decode_noalloc(const void* q, const void* k_latent, const void* w_
   // The envelope first (same checks and messages as palu_sdpa_decode), with the scratch size standing in
   // for the workspace; nothing touches the HIP runtime before the shapes are known to fit.
   if (int rc = sdpa_setup(a, q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos, out, rot_step, trans_mat, u_v,
-                          scale, heads_per_core, rot_mode, k_chunk, batch, n_q, n_kv, n_groups, seq_len, r_k, r_v,
+                          group_ranks, scale, heads_per_core, rot_mode, k_chunk, batch, n_q, n_kv, n_groups, seq_len, r_k, r_v,
                           w_rot_width, cs_rows, cs_cols, cs_dtype, out_dtype, cache_layout, deterministic, nullptr,
                           PALU_NOALLOC_SCRATCH_BYTES, "palu_sdpa_decode_noalloc"))
     return rc;
@@ -368,7 +392,7 @@ int palu_sdpa_decode_paged(const void* q, const void* k_pages, const void* w_rot
   const int seq_len = max_pages_per_seq * page_size;
   DecodeArgs a;
   if (int rc = sdpa_setup(a, q, k_pages, w_rot, cs_tab, v_pages, head_dim_v, cur_pos, out, rot_step, trans_mat, u_v,
-                          scale, heads_per_core, rot_mode, k_chunk, batch, n_q, n_kv, n_groups, seq_len, r_k, r_v,
+                          nullptr, scale, heads_per_core, rot_mode, k_chunk, batch, n_q, n_kv, n_groups, seq_len, r_k, r_v,
                           w_rot_width, cs_rows, cs_cols, cs_dtype, out_dtype, cache_layout, deterministic, workspace,
                           workspace_bytes, "palu_sdpa_decode_paged"))
     return rc;

@@ -67,7 +67,8 @@ inline GlrdPlan glrd_plan(int B, int n_q, int n_kv, int n_groups, int S, int rv)
 // head's score is complete here; the PV pass reads one score per (head, position).
 //
 // LDS map (KBP = rank blocks rounded up to even), at most 150.3 KB (r_k 512) at every length:
-//   ukt   u_k^T as A tiles [row tile 8][rank block KBP][lane] bf16x8 (zero past r_k); at least 32 KB,
+//   ukt   u_k^T as A tiles [row tile 8][rank block KBP][lane] bf16x8 (zero past the group's r_k); at
+//         least 32 KB,
 //         because the prologue stages cs_tab rows 0..63 ([t][f] float2) in the same place
 //   tl    (cos, sin) of angle 64*Lo*f, Lo < 16                                              8 KB
 //   tm    (cos, sin) of angle 1024*Mi*f, Mi < 16                                            8 KB
@@ -102,15 +103,16 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
 
   // Workgroup id -> (latent stream, KV head in group): ids 8*q + x with the same x share an XCD, and the
   // hpg workgroups of one stream (same row, group and split) get consecutive q, so they meet in one L2.
+  // The launch covers groups grp_lo .. grp_lo + grp_cnt - 1, all of K rank rk_eff.
   const int n_groups = a.n_kv / a.hpg;
   const int L = blockIdx.x;
   const int x8 = L & 7, q8 = L >> 3;
   const int hig = q8 % a.hpg;
   const int sigma = (q8 / a.hpg) * 8 + x8;
-  if (sigma >= a.B * n_groups * a.n_splits) return;   // padding workgroup (uniform)
+  if (sigma >= a.B * a.grp_cnt * a.n_splits) return;  // padding workgroup (uniform)
   const int split = sigma % a.n_splits;
   const int bg = sigma / a.n_splits;
-  const int b = bg / n_groups, grp = bg - b * n_groups;
+  const int b = bg / a.grp_cnt, grp = a.grp_lo + (bg - b * a.grp_cnt);
   const int kvh = grp * a.hpg + hig;
   const int QH = a.hpg * a.rep;
   const int NB = a.S / BLK;
@@ -119,7 +121,8 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int KB = a.rk >> 5;
+  const int KB = a.rk >> 5;                       // rank blocks of the cache (tile addressing)
+  const int KBe = a.rk_eff >> 5;                  // rank blocks of this group (the rest is never read)
 
   int len = a.cur_pos[b] + 1;
   len = len < 0 ? 0 : (len > a.S ? a.S : len);
@@ -182,7 +185,7 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
     // w stages rank blocks kb = w, w + G2_NW, ...; its lane (gg, mh, rt) reads ranks 32 kb + 8 gg .. +7 at
     // dims 16 rt + 8 mh .. +7 (8 rows of 16 bytes; the wave reads 4 rows x 256 contiguous bytes per
     // step), transposes the 8 x 8 block in registers and writes 8 whole 16-byte tile slots. Rank blocks
-    // past r_k (r_k is a multiple of 32, so the test is uniform) are zero.
+    // past the group's r_k (a multiple of 32, so the test is uniform) are zero.
     {
       const int gg = lane & 3, mh = (lane >> 2) & 1, rt = lane >> 3;
       const __bf16* ukp = a.w_rot + (long long)kvh * a.rk * (2 * HD) + 16 * rt + 8 * mh;
@@ -191,7 +194,7 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int r = 32 * kb + 8 * gg + j;
-          v[j] = kb < KB ? *reinterpret_cast<const bf16x8*>(ukp + (long long)r * (2 * HD)) : bf16x8{};
+          v[j] = kb < KBe ? *reinterpret_cast<const bf16x8*>(ukp + (long long)r * (2 * HD)) : bf16x8{};
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -206,7 +209,8 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   }
 
   // Tile loads of a pair of blocks: tile (kb, hb, c) of pair pp is block 2 pp + hb, K-tile c * KB + kb.
-  // Rank blocks past r_k read the same tile order's kb 0 (the matching u_k^T tiles are zero); blocks past
+  // Rank blocks past the group's r_k read the same tile order's kb 0 (the matching u_k^T tiles are zero,
+  // and the cache columns past the group's rank are never touched); blocks past
   // the split's data read the split's first block. Every path issues the same loads.
   // The block and tile offsets are uniform (scalar registers), the lane's 16 bytes the only vector part.
   auto load_kb = [&](int pp, int kb, bf16x8 (&t)[4]) {
@@ -214,7 +218,7 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
     for (int hb = 0; hb < 2; ++hb) {
       const int blk = 2 * pp + hb;
       const bool live = pp < npairs && blk < nblk;
-      const int kbr = kb < KB ? kb : 0;
+      const int kbr = kb < KBe ? kb : 0;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const long long off = __builtin_amdgcn_readfirstlane((int)(((s_lo >> 5) + (live ? blk : 0)) * (32 * a.rk) +
@@ -352,8 +356,9 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int VT = a.rv >> 4;
-  const int TG = glrd_pv_tg(VT), PG = G_NW / TG;
+  const int TG = glrd_pv_tg(a.rv >> 4), PG = G_NW / TG;   // tile groups from the cache width (TPW's basis)
+  const int rv_g = a.grv[grp];                            // this group's rank: V tiles past it are never read
+  const int VT = rv_g >> 4;
   const int tg = w % TG, pg = w / TG;
   const int head = ht * 16 + n;                       // head of this lane column inside the group
   const bool head_live = head < QH;
@@ -382,11 +387,13 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
     x.s[0] = *reinterpret_cast<const float4*>(p0);
     x.s[1] = *reinterpret_cast<const float4*>(p0 + 4);
     // The V latent is read once per decode step (one workgroup per row, group and split): nontemporal.
+    // Tiles past the group's rank are not loaded (their products are skipped below).
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int mt = tg * TPW + i;
-      x.v[i] = __builtin_nontemporal_load(
-          reinterpret_cast<const bf16x8*>(vbase + (long long)jj * (32 * a.rv) + (mt < VT ? mt : 0) * 512));
+      if (mt < VT)
+        x.v[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const bf16x8*>(vbase + (long long)jj * (32 * a.rv) + mt * 512));
     }
   };
 
@@ -425,6 +432,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
     l_run += lsum;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
+      if (tg * TPW + i >= VT) continue;              // past the group's rank (uniform)
       bf16x8 vA = x.v[i];
       if constexpr (partial) {
 #pragma unroll
@@ -468,7 +476,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
   for (int e = tid; e < 16 * ncols; e += G_NW * 64) {
     const int hh = e / ncols, col = e - hh * ncols;
     const int t = col / (TPW * 16), c = col - t * (TPW * 16);
-    if (ht * 16 + hh >= QH || col >= a.rv) continue;
+    if (ht * 16 + hh >= QH || col >= rv_g) continue;
     float M = NEG_INF;
     for (int q = 0; q < PG; ++q) M = fmaxf(M, reinterpret_cast<const float*>(smem)[(q * TG + t) * (16 * TPW * 16 + 32) + 16 * TPW * 16 + hh]);
     float acc = 0.f, Ls = 0.f;
@@ -500,14 +508,15 @@ __host__ __device__ inline int glrd_out_lds(int rep, int rv) { return (16 * 4 * 
 template <typename OutT>
 __global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, const float* part, int n_splits2) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int rv = a.rv, rep = a.rep;
-  float* red = reinterpret_cast<float*>(smem);
-  float* olat = red + 16 * 4 * HD;
-  float* wsplit = olat + rep * rv;
-  float* lsum = wsplit + rep * G_MAX_SPLITS2;
+  const int rep = a.rep;
   const int item = blockIdx.x;
   const int b = item / a.n_kv, kvh = item - b * a.n_kv;
-  const int stride = rv + G_PSTRIDE_PAD;
+  const int rv = a.grv[kvh / a.hpg];                  // the group's rank: partial columns past it are unset
+  float* red = reinterpret_cast<float*>(smem);
+  float* olat = red + 16 * 4 * HD;
+  float* wsplit = olat + rep * a.rv;
+  float* lsum = wsplit + rep * G_MAX_SPLITS2;
+  const int stride = a.rv + G_PSTRIDE_PAD;
   const int tid = threadIdx.x;
   const float* p0 = part + (long long)(b * a.n_q + kvh * rep) * n_splits2 * stride;
   // split weights: wsplit[h][s] = 2^(m_s - M_h); lsum[h] = sum_s l_s 2^(m_s - M_h). Wave w handles heads
@@ -517,14 +526,14 @@ __global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, 
     for (int h = w; h < rep; h += 4) {
       const float* ph = p0 + (long long)h * n_splits2 * stride;
       float M = NEG_INF;
-      for (int s = lane; s < n_splits2; s += 64) M = fmaxf(M, ph[(long long)s * stride + rv]);
+      for (int s = lane; s < n_splits2; s += 64) M = fmaxf(M, ph[(long long)s * stride + a.rv]);
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
       float Ls = 0.f;
       for (int s = lane; s < n_splits2; s += 64) {
-        const float f = (M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(ph[(long long)s * stride + rv] - M);
+        const float f = (M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(ph[(long long)s * stride + a.rv] - M);
         wsplit[h * G_MAX_SPLITS2 + s] = f;
-        Ls += ph[(long long)s * stride + rv + 1] * f;
+        Ls += ph[(long long)s * stride + a.rv + 1] * f;
       }
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) Ls += __shfl_xor(Ls, o, 64);
@@ -544,7 +553,7 @@ __global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, 
   __syncthreads();
   const int dg = tid & 15, rs = tid >> 4;             // 8 output dims, one of 16 rank slices
   const int per = rv / 16;                              // rv is a multiple of 32
-  const __bf16* uv = a.u_v + (long long)kvh * rv * HD + 8 * dg;
+  const __bf16* uv = a.u_v + (long long)kvh * a.rv * HD + 8 * dg;
   for (int hg = 0; hg < rep; hg += 4) {                 // heads hg .. hg + 3 of this KV head
     float acc[4][8];
 #pragma unroll
@@ -597,7 +606,7 @@ int launch_scores_full(const DecodeArgs& a, float* scores, int n_wg, hipStream_t
 
 template <typename TabT>
 int scores_full_kb(const DecodeArgs& a, float* scores, int n_wg, hipStream_t s) {
-  switch ((a.rk / 32 + 1) / 2) {                  // rank blocks rounded up to even
+  switch ((a.rk_eff / 32 + 1) / 2) {              // the launch's rank blocks rounded up to even
     case 1: return launch_scores_full<2, TabT>(a, scores, n_wg, s);
     case 2: return launch_scores_full<4, TabT>(a, scores, n_wg, s);
     case 3: return launch_scores_full<6, TabT>(a, scores, n_wg, s);
@@ -607,7 +616,7 @@ int scores_full_kb(const DecodeArgs& a, float* scores, int n_wg, hipStream_t s) 
     case 7: return launch_scores_full<14, TabT>(a, scores, n_wg, s);
     case 8: return launch_scores_full<16, TabT>(a, scores, n_wg, s);
   }
-  return fail(PALU_EUNSUPPORTED, "grouped-latent r_k %d (32 .. 512 in steps of 32)", a.rk);
+  return fail(PALU_EUNSUPPORTED, "grouped-latent r_k %d (32 .. 512 in steps of 32)", a.rk_eff);
 }
 
 template <typename K>
@@ -674,15 +683,26 @@ int dispatch_glrd(const DecodeArgs& a0, int cs_dtype, int out_dtype, hipStream_t
     return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_glrd_workspace_bytes), got %zu", need, a.ws_bytes);
   float* scores = reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(a.ws) + 255) & ~uintptr_t(255));
   float* part = scores + p.scores_floats;
-  const Plan pf = plan_splits(a.B * a.n_kv, a.S, 2 * G2_NW);
-  a.split_len = pf.split_len;
-  a.n_splits = pf.n_splits;
-  const int n_wg = ((a.B * n_groups * pf.n_splits + 7) / 8) * 8 * a.hpg;
-  const int rc = cs_dtype == PALU_DTYPE_F32 ? scores_full_kb<float>(a, scores, n_wg, s)
-                                            : scores_full_kb<__bf16>(a, scores, n_wg, s);
-  if (rc) return rc;
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent scores kernel launch: %s", hipGetErrorString(e));
+  // Scores: one launch over every group when they share a K rank, else one launch per group at its own
+  // rank (the kernel's rank loop is unrolled per width).
+  bool uniform_k = true;
+  for (int g = 0; g < n_groups; ++g) uniform_k = uniform_k && a.grk[g] == a.rk;
+  hipError_t e = hipSuccess;
+  for (int g0 = 0; g0 < n_groups; g0 += uniform_k ? n_groups : 1) {
+    DecodeArgs ag = a;
+    ag.grp_lo = g0;
+    ag.grp_cnt = uniform_k ? n_groups : 1;
+    ag.rk_eff = a.grk[g0];
+    const Plan pf = plan_splits(a.B * ag.grp_cnt * a.hpg, a.S, 2 * G2_NW);
+    ag.split_len = pf.split_len;
+    ag.n_splits = pf.n_splits;
+    const int n_wg = ((a.B * ag.grp_cnt * pf.n_splits + 7) / 8) * 8 * a.hpg;
+    const int rc = cs_dtype == PALU_DTYPE_F32 ? scores_full_kb<float>(ag, scores, n_wg, s)
+                                              : scores_full_kb<__bf16>(ag, scores, n_wg, s);
+    if (rc) return rc;
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent scores kernel launch: %s", hipGetErrorString(e));
+  }
   if (int rc2 = launch_pv(a, scores, part, p, s)) return rc2;
   e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent PV kernel launch: %s", hipGetErrorString(e));

@@ -62,6 +62,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int HD = 128;     // head dim
+constexpr int MAX_GROUPS = 16;  // latent groups per layer with per-group ranks
 constexpr int BLK = 32;     // positions per block: two 16-position MFMA tiles, also the rotation chunk
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LAZY_RESCALE_LOG2 = 8.0f;  // running max is refreshed when a score exceeds it by > 2^8
@@ -92,7 +93,12 @@ struct DecodeArgs {
   // Grouped latents with in-kernel V (u_v given): [n_kv, RV, HD] per KV head; k/v are then the group
   // latents [B, n_groups, S, RK / RV] in the tiled layout, and the output is HD wide.
   const __bf16* u_v;
-  int rk, rv;             // latent widths of the grouped-latent kernel (runtime there)
+  int rk, rv;             // latent widths of the caches (the grouped-latent kernels take them at run time)
+  // Grouped latents: each group's own ranks (<= rk / rv, multiples of 32; the cache columns past them
+  // are never read), and the groups one scores launch covers (grp_lo .. grp_lo + grp_cnt - 1, whose
+  // K rank is rk_eff).
+  short grk[MAX_GROUPS], grv[MAX_GROUPS];
+  int grp_lo, grp_cnt, rk_eff;
 };
 
 // Error reporting (defined in palu_capi.hip): formats the message for palu_last_error, returns code.

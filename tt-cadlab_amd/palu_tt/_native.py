@@ -14,7 +14,7 @@ from palu_tt._build import library_path
 
 PALU_OK, PALU_EINVAL, PALU_EUNSUPPORTED, PALU_EHIP = 0, 1, 2, 3
 DTYPE_F32, DTYPE_BF16 = 0, 1
-ABI_VERSION = 8
+ABI_VERSION = 9
 LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_TILED_V = 0, 1, 2
 
 _vp, _i, _f, _sz, _ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_longlong
@@ -24,10 +24,10 @@ _SIGNATURES = {
     "palu_abi_version": (_i, []),
     "palu_decode_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "palu_glrd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
-    "palu_sdpa_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i,
+    "palu_sdpa_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i,
                               _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
-    "palu_sdpa_decode_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i,
-                                      _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "palu_sdpa_decode_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i,
+                                      _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "palu_flash_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "palu_latent_append": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "palu_sdpa_decode_paged": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i,

@@ -70,6 +70,10 @@ class PaluAttention(torch.nn.Module):
         # the fused op replaces the naive rebuild only where K really is a latent (reference
         # attention.py:151); PaluRuntime() defaults to the naive path, as the reference's does
         self.use_fused_k = self.recon_k and bool(self.palu.runtime.use_fused_k)
+        # grouped latents of unequal ranks (padded to rank_k / rank_v): the fused op reads only each
+        # group's own columns when it is given the groups' ranks
+        gr = self.palu.group_ranks[layer_num] if self.palu.group_ranks else None
+        self.group_ranks = (list(gr[0]), list(gr[1])) if (gr is not None and self.gs > 1) else None
         self.cache_layout = cache_layout
         self._naive_pos = {}
 
@@ -169,7 +173,7 @@ class PaluAttention(torch.nn.Module):
             return fused.palu_sdpa_decode(q4, keys, self.w_rot, self.cs_tab, values,
                                           self.head_dim if grouped else self.r_v, pos,
                                           u_v=self.u_v[None] if grouped else None, scale=self.scale,
-                                          out_dtype=torch.bfloat16)
+                                          out_dtype=torch.bfloat16, group_ranks=self.group_ranks)
         if self.recon_k:
             return self._naive_attention(q4, keys, values, pos)
         return fused.flash_multi_latent_attention_decode(q4, keys, values, self.r_v, pos, scale=self.scale)

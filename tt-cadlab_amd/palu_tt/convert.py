@@ -70,6 +70,9 @@ class PaluConfig:
     group_size: int = 1
     latent_scale: str = "balanced"
     device_tables: dict = field(default_factory=dict, repr=False, compare=False)
+    # Per layer, the latent groups' own ranks (K ranks, V ranks) before the padding to rank_k / rank_v, or
+    # None. With grouped latents the fused op then reads only each group's own cache columns.
+    group_ranks: Optional[List[Optional[Tuple[List[int], List[int]]]]] = None
 
 
 @dataclass
@@ -81,6 +84,8 @@ class LowRank:
     v_VT: torch.Tensor
     v_U: torch.Tensor
     group_size: int = 1
+    group_ranks_k: Optional[List[int]] = None    # each group's rank before padding (load_palu_dir fills them)
+    group_ranks_v: Optional[List[int]] = None
 
     @property
     def r_k(self) -> int:
@@ -105,7 +110,8 @@ def unit_scale_lowrank(lr: LowRank) -> LowRank:
         return VT2, U2
     k_VT, k_U = rescale(lr.k_VT, lr.k_U, lr.group_size)
     v_VT, v_U = rescale(lr.v_VT, lr.v_U, lr.group_size)
-    return LowRank(k_VT, k_U, v_VT, v_U, group_size=lr.group_size)
+    return LowRank(k_VT, k_U, v_VT, v_U, group_size=lr.group_size, group_ranks_k=lr.group_ranks_k,
+                   group_ranks_v=lr.group_ranks_v)
 
 
 def identity_lowrank(hf_attn: Dict[str, torch.Tensor], n_kv_heads: int, head_dim: int) -> LowRank:
@@ -138,7 +144,7 @@ class _FactorDump:
             return f.get_tensor(name).float()
 
     def projection(self, layer: int, proj: str, n_kv_heads: int, head_dim: int, rank_multiple: int):
-        """(VT [n_kv, r_pad, hidden], U [n_kv, hd, r_pad], group size) of one projection. The stacked VT
+        """(VT [n_kv, r_pad, hidden], U [n_kv, hd, r_pad], group size, group ranks) of one projection. The stacked VT
         is cut at the group ranks; every group is zero-padded to r_pad (the widest group rounded up to
         rank_multiple) and handed to each of its heads, the head taking its hd rows of the group U."""
         name = f"model.layers.{layer}.self_attn.{proj}"
@@ -158,7 +164,7 @@ class _FactorDump:
                                  f"(group of {gs} heads of width {head_dim}, rank {r})")
         VT = torch.stack([F.pad(vt, (0, 0, 0, r_pad - vt.shape[0])) for vt in vt_groups])       # [G, r_pad, hidden]
         U = torch.cat([F.pad(u, (0, r_pad - u.shape[1])).view(gs, head_dim, r_pad) for u in u_groups])
-        return VT.repeat_interleave(gs, dim=0).contiguous(), U.contiguous(), gs
+        return VT.repeat_interleave(gs, dim=0).contiguous(), U.contiguous(), gs, list(group_ranks)
 
 
 def load_palu_dir(palu_dir: Path, n_layers: int, n_kv_heads: int, head_dim: int, rank_multiple: int = 32,
@@ -172,11 +178,11 @@ def load_palu_dir(palu_dir: Path, n_layers: int, n_kv_heads: int, head_dim: int,
     dump = _FactorDump(palu_dir)
     layers = {}
     for i in range(n_layers):
-        k_VT, k_U, gs = dump.projection(i, "k_proj", n_kv_heads, head_dim, rank_multiple)
-        v_VT, v_U, gs_v = dump.projection(i, "v_proj", n_kv_heads, head_dim, rank_multiple)
+        k_VT, k_U, gs, rk = dump.projection(i, "k_proj", n_kv_heads, head_dim, rank_multiple)
+        v_VT, v_U, gs_v, rv = dump.projection(i, "v_proj", n_kv_heads, head_dim, rank_multiple)
         if gs != gs_v:
             raise ValueError(f"layer {i}: k_proj groups {gs} heads and v_proj {gs_v}; the group size must match")
-        lr = LowRank(k_VT, k_U, v_VT, v_U, group_size=gs)
+        lr = LowRank(k_VT, k_U, v_VT, v_U, group_size=gs, group_ranks_k=rk, group_ranks_v=rv)
         layers[i] = unit_scale_lowrank(lr) if latent_scale == "unit" else lr
     return layers
 
@@ -296,16 +302,18 @@ def add_palu_to_state_dict(state_dict: dict, hf_dir: Path, palu_dir: Optional[Pa
     factors = (load_palu_dir(palu_dir, n_layers, n_kv_heads, head_dim, latent_scale=latent_scale)
                if palu_dir is not None else None)
     group_sizes = set()
-    per_layer_ranks = []
+    per_layer_ranks, group_ranks = [], []
     for i in range(n_layers):
         attn = hf_attn_weights(hf_dir, i)
         lr = factors[i] if factors is not None else identity_lowrank(attn, n_kv_heads, head_dim)
         tensors = palu_layer_tensors(attn, lr, n_heads, n_kv_heads, head_dim)
         state_dict.update({f"layers.{i}.attention.palu.{k}": t for k, t in tensors.items()})
         per_layer_ranks.append((lr.r_k, lr.r_v))
+        group_ranks.append(None if lr.group_ranks_k is None else (lr.group_ranks_k, lr.group_ranks_v))
         group_sizes.add(lr.group_size)
     if len(group_sizes) > 1:
         raise ValueError(f"layers use different group sizes {sorted(group_sizes)}; one model has one group size")
     return PaluConfig(rank_k=[rk for rk, _ in per_layer_ranks], rank_v=[rv for _, rv in per_layer_ranks],
                       cache_id="identity" if palu_dir is None else palu_cache_id_for(palu_dir, latent_scale),
-                      group_size=group_sizes.pop() if group_sizes else 1, latent_scale=latent_scale)
+                      group_size=group_sizes.pop() if group_sizes else 1, latent_scale=latent_scale,
+                      group_ranks=group_ranks if factors is not None else None)

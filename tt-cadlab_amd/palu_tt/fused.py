@@ -21,6 +21,7 @@ MI355X kernel has one schedule: K rows are rotated by their offset inside a 32-p
 an LDS-resident table and the query is rotated back by the block base, which is the reference's Phase 2
 identity (fused.py:1-24) with a fixed chunk; results do not depend on those switches.
 """
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import Optional, Tuple
@@ -239,7 +240,7 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
                      trans_mat=None, u_v=None, scale=None, heads_per_core=None, rot_mode="dst", table_mcast=True,
                      program_config=None, compute_kernel_config=None, memory_config=None,
                      out_dtype=torch.bfloat16, out=None, workspace=None, deterministic=False,
-                     page_table_tensor=None, noalloc=False) -> torch.Tensor:
+                     page_table_tensor=None, noalloc=False, group_ranks=None) -> torch.Tensor:
     """Fused latent flash-decode (ttnn.transformer.palu_sdpa_decode). Returns [1, B, n_q, head_dim_v].
 
     For every p <= cur_pos[b]: K[p] = RoPE_p(k_latent[p] @ u_k) with u_k = w_rot[..., :128], then
@@ -254,6 +255,9 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
     deterministic=True fixes which wave of a workgroup sums which 32-position block, so repeated calls
     are bit-identical; the default hands blocks out from a counter (faster; calls differ at the bf16
     rounding of the softmax probabilities, well inside the parity tolerance).
+    group_ranks=(ranks_k, ranks_v), one rank per latent group (with u_v): each group's own widths, the
+    cache columns past them being padding that the kernels never read (the reference pads every group to
+    the layer's widest and reads the padding).
     noalloc=True (contiguous caches only, no workspace) calls palu_sdpa_decode_noalloc, which keeps the
     kernels' scratch in the library's static per-GPU array: with ``out`` given, the call allocates no
     device memory at all (for HIP graph capture and serving loops); calls overlapping on one GPU race.
@@ -302,13 +306,20 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
     else:
         _as_dev(out, "out", out_dtype, dev)
         _require(tuple(out.shape) == (1, B, n_q, width), f"out must be [1, {B}, {n_q}, {width}]")
+    gr = None
+    if group_ranks is not None:
+        gk, gv = (list(x) for x in group_ranks)
+        _require(len(gk) == n_groups and len(gv) == n_groups,
+                 f"group_ranks must give {n_groups} K ranks and {n_groups} V ranks")
+        _require(pt is None, "group_ranks: per-group ranks are built for contiguous caches")
+        gr = (ctypes.c_int32 * (2 * n_groups))(*[int(r) for r in gk + gv])
     lib = _native.load()
     sc = float(HEAD_DIM ** -0.5 if scale is None else scale)
     if noalloc:
         _require(pt is None and workspace is None, "noalloc takes contiguous caches and no workspace")
         _native.check(lib.palu_sdpa_decode_noalloc(
             _native.ptr(q), _native.ptr(k_store), _native.ptr(w), _native.ptr(cs), _native.ptr(v_store), width,
-            _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv), sc,
+            _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv), gr, sc,
             int(heads_per_core or 0), rot, int(bool(table_mcast)), _k_chunk(program_config), B, n_q, n_kv, n_groups,
             S, r_k, r_v, w_width, cs.shape[0], cs.shape[1], _DTYPES[cs.dtype], _DTYPES[out_dtype], layout,
             int(bool(deterministic)), _native.stream_handle(dev)))
@@ -320,7 +331,7 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
     if pt is None:
         _native.check(lib.palu_sdpa_decode(
             _native.ptr(q), _native.ptr(k_store), _native.ptr(w), _native.ptr(cs), _native.ptr(v_store), width,
-            _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv), sc,
+            _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv), gr, sc,
             int(heads_per_core or 0), rot, int(bool(table_mcast)), _k_chunk(program_config), B, n_q, n_kv, n_groups,
             S, r_k, r_v, w_width, cs.shape[0], cs.shape[1], _DTYPES[cs.dtype], _DTYPES[out_dtype], layout,
             int(bool(deterministic)), _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
