@@ -932,6 +932,9 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
   a.n_wg = decode_workgroups(items);
   a.balanced = a.n_wg > items ? 1 : 0;
   if (!a.balanced) a.n_wg = items;
+  // Chunks of the length-aware plan are short: there the fixed block order (no round trip to the
+  // shared counter per pair) is the faster one, and it is reproducible as well.
+  if (a.balanced) a.deterministic = 1;
   const size_t need = decode_ws_bytes(items, RV);
   if (need > 0 && (a.ws == nullptr || a.ws_bytes < need))
     return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_decode_workspace_bytes), got %zu", need, a.ws_bytes);
