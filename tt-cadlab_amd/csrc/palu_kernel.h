@@ -287,7 +287,7 @@ __device__ int plan_chunk_pairs(const DecodeArgs& a) {
 //         besides the latent prefetch                                                 [16][128] bf16
 //   ctr   the block counter
 //   th    (cos, sin) of angle 1024*H*f, H < ceil(S / 1024): the high part             [nH][64] float2
-//   kc    staging of rows 0..63 of cs_tab ([t][f] float2) while rtab is built, overlaying qx
+//   kc    staging of cs_tab rows 0..7 and 8, 16, .., 56 ([row][f] float2) while rtab is built, overlaying qx
 // The wave-merge buffer of the epilogue overlays the front.
 template <int RK, int RV, bool KFULL, int NW>
 struct Smem {
@@ -350,9 +350,11 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
   // Latent mode: the angle-table rows are the same for every workgroup and depend on nothing below, so
   // their loads are issued first, ahead of the plan's scalar reads of cur_pos. Rows t < 64 serve the K
   // rotation, 64*Lo (Lo < 16) and 1024*H the query's pair base; one coalesced row per wave load.
-  const int n_rows = KFULL ? 0 : 80 + (a.S + 1023) / 1024;
-  constexpr int RPW = (80 + 64 + NW - 1) / NW;  // rows per wave, enough for S <= 65536
-  auto row_t = [](int r) { return r < 64 ? r : (r < 80 ? 64 * (r - 64) : 1024 * (r - 80)); };
+  // Rows: t0 < 8 and 8 t1 (t1 = 1..7) for the K rotation (t = 8 t1 + t0 by angle addition), 64 Lo
+  // (Lo < 16) and 1024 H (H < ceil(S / 1024)) for the query's pair base.
+  const int n_rows = KFULL ? 0 : 31 + (a.S + 1023) / 1024;
+  constexpr int RPW = (31 + 64 + NW - 1) / NW;  // rows per wave, enough for S <= 65536
+  auto row_t = [](int r) { return r < 8 ? r : (r < 15 ? 8 * (r - 7) : (r < 31 ? 64 * (r - 15) : 1024 * (r - 31))); };
   float4 rowv[KFULL ? 1 : RPW];
   if constexpr (!KFULL) {
     const TabT* cs = static_cast<const TabT*>(a.cs);
@@ -541,7 +543,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       if (r < n_rows) {
         const int t = row_t(r);
         const bool ok = t < a.cs_rows;
-        float2* dst = r < 64 ? kc + r * 64 : (r < 80 ? tl + (r - 64) * 64 : th + (r - 80) * 64);
+        float2* dst = r < 15 ? kc + r * 64 : (r < 31 ? tl + (r - 15) * 64 : th + (r - 31) * 64);
         const int f = 2 * (lane & 31);
         float* d0 = reinterpret_cast<float*>(dst + f) + (lane >> 5);
         d0[0] = ok ? rowv[i].x : (lane < 32 ? 1.f : 0.f);
@@ -559,13 +561,21 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
     }
     load_first(1, kln, vln);
     __syncthreads();
-    // K rotation table in lane order from the staged rows 0..63
+    // K rotation table in lane order: (cos, sin) of t f for t = 8 t1 + t0 < 64 by angle addition of the
+    // staged rows t0 and 8 t1 in fp32 (within fp32 rounding of the table's own values, far below the
+    // fp16 the table is stored in)
     for (int e = tid; e < 2 * 2 * 8 * 64; e += NW * 64) {
       const int l = e & 63, rt = (e >> 6) & 7, c = (e >> 9) & 1, hb = e >> 10;
       const int nn = l & 15, gg = l >> 4;
       const int t = 32 * hb + 8 * (nn >> 2) + 4 * c + (nn & 3);
+      const int t0 = t & 7, t1 = t >> 3;
       const int f = 8 * rt + 2 * gg;
-      const float2 x = kc[t * 64 + f], y = kc[t * 64 + f + 1];   // (cos, sin) of frequencies f, f + 1
+      float2 x = kc[t0 * 64 + f], y = kc[t0 * 64 + f + 1];       // (cos, sin) of t0 f and t0 (f + 1)
+      if (t1 > 0) {
+        const float2 u = kc[(7 + t1) * 64 + f], v = kc[(7 + t1) * 64 + f + 1];
+        x = make_float2(x.x * u.x - x.y * u.y, x.y * u.x + x.x * u.y);
+        y = make_float2(y.x * v.x - y.y * v.y, y.y * v.x + y.x * v.y);
+      }
       rtab[e] = f16x8{(_Float16)x.x, (_Float16)x.x, (_Float16)-x.y, (_Float16)x.y,
                       (_Float16)y.x, (_Float16)y.x, (_Float16)-y.y, (_Float16)y.y};
     }
