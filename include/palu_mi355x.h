@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define PALU_ABI_VERSION 9
+#define PALU_ABI_VERSION 10
 
 #define PALU_OK 0
 #define PALU_EINVAL 1       /* arguments outside the op's envelope */
@@ -208,13 +208,30 @@ int palu_latent_append_strided(void* cache, const void* src, long long src_batch
                                const int32_t* update_idxs, int batch, int n_groups, int seq_len, int width,
                                int cache_layout, palu_stream_t stream);
 
-/* Per row of [rows, dim]: h = x + res (res may be NULL: h = x), rounded to bf16 and stored to h_out when
- * h_out is not NULL; y_out = h * rsqrt(mean(h^2) + eps) * weight. dim a multiple of 8, at most 8192. */
-int palu_rmsnorm(const void* x, const void* res, void* h_out, void* y_out, const void* weight, int rows, int dim,
-                 float eps, palu_stream_t stream);
+/* The decode step's QKV epilogue in one launch, from the fp32 split partials [ks, batch, ncols] of the
+ * QKV projection (palu_linear_tiled with PALU_LINEAR_F32_PARTIALS), summed in slice order: q_out
+ * [batch, n_heads, 128] = the first n_heads 128-wide heads rotated at pos[b] (as palu_rope_rows), and for
+ * every latent group g the K slice (columns k_col_offset + g * k_group_stride, k_width wide; rotated as
+ * well when k_rope, then k_width must be 128) and the V slice (v_col_offset + g * v_group_stride, v_width
+ * wide) appended at pos[b] to k_cache / v_cache (as palu_latent_append_strided; K caches ROWS or TILED,
+ * V caches ROWS or TILED_V). Column offsets and strides multiples of 8. */
+int palu_qkv_post(const float* qkv_part, int ks, int batch, int ncols, const int32_t* pos, const float* cos_table,
+                  const float* sin_table, int table_rows, int n_heads, void* q_out, void* k_cache, int k_layout,
+                  int k_col_offset, int k_group_stride, int k_width, int k_rope, void* v_cache, int v_layout,
+                  int v_col_offset, int v_group_stride, int v_width, int n_groups, int seq_len, palu_stream_t stream);
 
-/* out[r][f] = silu(gu[r][f]) * gu[r][ffn + f] for gu [rows, 2 ffn], out [rows, ffn]; ffn a multiple of 8. */
-int palu_swiglu(const void* gu, void* out, int rows, int ffn, palu_stream_t stream);
+/* Per row of [rows, dim]: h = x + res, rounded to bf16 and stored to h_out when h_out is not NULL;
+ * y_out = h * rsqrt(mean(h^2) + eps) * weight. dim a multiple of 8, at most 8192. The residual input is
+ * res (bf16 [rows, dim]), or res_part (fp32 [res_ks, rows, dim]: the split partials of a projection's
+ * PALU_LINEAR_F32_PARTIALS output, summed here), or neither (h = x). y_tiled = 1 writes y_out in the
+ * 64-row tiled activation layout that palu_linear_tiled reads with x_tiled = 1 (rows <= 64, dim a
+ * multiple of 32; the buffer holds 64 rows, those past `rows` untouched). */
+int palu_rmsnorm(const void* x, const void* res, const float* res_part, int res_ks, void* h_out, void* y_out,
+                 const void* weight, int rows, int dim, float eps, int y_tiled, palu_stream_t stream);
+
+/* out[r][f] = silu(gu[r][f]) * gu[r][ffn + f] for gu [rows, 2 ffn], out [rows, ffn]; ffn a multiple of 8.
+ * out_tiled = 1 writes out in the 64-row tiled activation layout (rows <= 64, ffn a multiple of 32). */
+int palu_swiglu(const void* gu, void* out, int rows, int ffn, int out_tiled, palu_stream_t stream);
 
 /* Meta-interleaved RoPE of `heads` 128-wide heads per row at the row's position:
  * dst[b, h, :] = rotate(src[b * src_row_stride + h * 128 .. +127], pos[b]), pairs (2i, 2i+1) ->
@@ -222,6 +239,37 @@ int palu_swiglu(const void* gu, void* out, int rows, int ffn, palu_stream_t stre
  * fused.cos_sin_tables). Positions outside the table are clamped into it. dst is [rows, heads, 128]. */
 int palu_rope_rows(const void* src, long long src_row_stride, void* dst, const int32_t* pos, const float* cos_table,
                    const float* sin_table, int table_rows, int rows, int heads, palu_stream_t stream);
+
+/* Output modes of palu_linear_tiled. */
+#define PALU_LINEAR_BF16 0          /* y: bf16 [rows, n], rows ldy apart */
+#define PALU_LINEAR_F32_PARTIALS 1  /* y: fp32 [ks, rows, n], the k slices' partial sums, not added up */
+#define PALU_LINEAR_SWIGLU_TILED 2  /* y: bf16 [64, n / 2] tiled activations, silu(gate) * up (ks = 1) */
+
+/* Decode-step projection: y[r][c] = sum_k x[r][k] w[c][k] for rows = 1..64 (bf16 in, fp32 accumulate),
+ * with w [n, k] given tiled for groups of rtw row tiles (palu_tt.decoder_ops.tile_weight: 16 x 32 tiles
+ * of 1 KB, lane 16 g + i of tile (rt, kt) holding w[16 rt + i][32 kt + 8 g .. +7]; row tiles in groups of
+ * rtw, the last group possibly shorter, each group's tiles stored [kt][rt in group]). x is row-major with
+ * rows ldx apart (x_tiled = 0; ldx >= k, a multiple of 8) or in the 64-row tiled activation layout
+ * (x_tiled = 1: the same 1 KB tiles over 64 rows, stored [kt][row tile], rows past `rows` ignored;
+ * palu_rmsnorm and palu_swiglu write it). n a multiple of 16, k of 32, x 16-byte aligned. rtw (1..8)
+ * must be the one the weight was tiled with; ks (1..64) k slices. y_mode PALU_LINEAR_BF16: y rows ldy
+ * apart (>= n, a multiple of 4); with ks > 1 the slices' fp32 partials go through a caller workspace of
+ * palu_linear_workspace_bytes(rows, n, k, ks) bytes and a second launch adds them. PALU_LINEAR_F32_PARTIALS:
+ * y receives the ks partial sums (no workspace, no second launch). PALU_LINEAR_SWIGLU_TILED: w holds
+ * gate and up rows interleaved eight at a time (rows 16 j .. 16 j + 7 gate outputs 8 j .. 8 j + 7, rows
+ * 16 j + 8 .. 16 j + 15 the up rows of the same outputs; n a multiple of 64, ks = 1) and y receives
+ * silu(gate) * up as the [64, n / 2] tiled activations of the next projection.
+ * palu_linear_plan suggests (rtw, ks) for a shape. The reference's counterpart is the ttnn.linear of
+ * each projection of its decode step. */
+int palu_linear_tiled(const void* x, long long ldx, int x_tiled, int rows, const void* w_tiled, int n, int k, void* y,
+                      long long ldy, int y_mode, int rtw, int ks, void* workspace, size_t workspace_bytes,
+                      palu_stream_t stream);
+
+/* A work split (rtw, ks) for palu_linear_tiled at this shape, from a model of the busiest CU's bytes. */
+int palu_linear_plan(int rows, int n, int k, int* rtw, int* ks);
+
+/* Workspace bytes of palu_linear_tiled with ks k slices (0 for ks == 1 or invalid shapes). */
+size_t palu_linear_workspace_bytes(int rows, int n, int k, int ks);
 
 #ifdef __cplusplus
 }

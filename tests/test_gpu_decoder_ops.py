@@ -80,3 +80,210 @@ def test_strided_append_equals_contiguous_append(gpu, layout, role, gs, width):
     ta = a.data if layout == "tiled" else a
     tb = b.data if layout == "tiled" else b
     assert torch.equal(ta, tb)
+
+
+def _linear_ref(x, w):
+    return x.float() @ w.float().T
+
+
+def _check_linear(y, ref):
+    y = y.float()
+    scale = ref.abs().max().item()
+    err = (y - ref).abs().max().item()
+    cos = F.cosine_similarity(y.flatten(), ref.flatten(), dim=0).item()
+    # bf16 output of an fp32 sum: one rounding of the result (2^-8 relative) plus summation order
+    assert err <= scale * 2 ** -7 and cos >= 0.99999, f"max-abs {err:.3e} of scale {scale:.3e}, cosine {cos:.7f}"
+
+
+@pytest.mark.parametrize("rows,n,k", [(64, 4096, 4096), (64, 5120, 4096), (64, 4096, 2432), (64, 28672, 4096),
+                                      (64, 4096, 14336), (17, 6144, 4096), (1, 256, 1024), (5, 48, 96)])
+def test_linear_tiled_matches_fp32(gpu, rows, n, k):
+    """The decode projections at the 32-layer decoder's shapes (QKV, output, gate/up, down) and small,
+    ragged ones, with the plan's work split, against fp32 torch on the same bf16 inputs."""
+    g = torch.Generator().manual_seed(n + k + rows)
+    x = torch.randn(rows, k, generator=g).to(gpu, torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(gpu, torch.bfloat16)
+    rtw, ks = decoder_ops.linear_plan(rows, n, k)
+    y = decoder_ops.linear_tiled(x, decoder_ops.tile_weight(w, rtw), rtw, ks)
+    torch.cuda.synchronize()
+    _check_linear(y, _linear_ref(x, w))
+
+
+@pytest.mark.parametrize("rtw,ks", [(1, 1), (2, 4), (3, 2), (5, 1), (7, 8), (8, 3), (8, 16), (4, 64)])
+def test_linear_tiled_every_work_split(gpu, rtw, ks):
+    """Every row-tile grouping and k-slice count, including ones that leave the last group short (n = 400:
+    25 row tiles), slices with an odd step count per wave, and more slices than k tiles can fill."""
+    g = torch.Generator().manual_seed(rtw * 100 + ks)
+    x = torch.randn(40, 1344, generator=g).to(gpu, torch.bfloat16)
+    w = (torch.randn(400, 1344, generator=g) * 0.05).to(gpu, torch.bfloat16)
+    y = decoder_ops.linear_tiled(x, decoder_ops.tile_weight(w, rtw), rtw, ks)
+    torch.cuda.synchronize()
+    _check_linear(y, _linear_ref(x, w))
+
+
+def test_linear_tiled_strided_views_and_repeat(gpu):
+    """x and out as column slices of wider rows (the QKV output layout), a caller workspace, and a
+    bit-identical repeat (the k-slice sums and the wave tree run in a fixed order)."""
+    g = torch.Generator().manual_seed(11)
+    xw = torch.randn(64, 4096 + 64, generator=g).to(gpu, torch.bfloat16)
+    x = xw[:, 32:32 + 4096]
+    w = (torch.randn(1024, 4096, generator=g) * 0.02).to(gpu, torch.bfloat16)
+    wt = decoder_ops.tile_weight(w, 2)
+    ow = torch.zeros(64, 1024 + 16, dtype=torch.bfloat16, device=gpu)
+    out = ow[:, 8:8 + 1024]
+    ws = torch.empty(4 * 64 * 1024 * 4, dtype=torch.uint8, device=gpu)
+    decoder_ops.linear_tiled(x, wt, 2, 4, out=out, workspace=ws)
+    again = decoder_ops.linear_tiled(x, wt, 2, 4)
+    torch.cuda.synchronize()
+    _check_linear(out, _linear_ref(x, w))
+    assert torch.equal(out, again)
+    assert (ow[:, :8] == 0).all() and (ow[:, 8 + 1024:] == 0).all()
+
+
+def test_linear_tiled_rejects_bad_shapes(gpu):
+    x = torch.zeros(65, 64, dtype=torch.bfloat16, device=gpu)
+    wt = torch.zeros(32, 64, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError, match="1..64"):
+        decoder_ops.linear_tiled(x, wt, 1, 1)
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        decoder_ops.linear_tiled(x[:8], torch.zeros(24, 64, dtype=torch.bfloat16, device=gpu), 1, 1)
+    with pytest.raises(RuntimeError, match="rtw"):
+        decoder_ops.linear_tiled(x[:8], wt, 9, 1)
+
+
+@pytest.mark.parametrize("rows,n,k,rtw,ks", [(64, 28672, 4096, 7, 1), (64, 4096, 14336, 4, 4), (23, 4096, 2432, 1, 1),
+                                             (64, 400, 1344, 3, 2)])
+def test_linear_tiled_activations(gpu, rows, n, k, rtw, ks):
+    """Activations in the 64-row tiled layout (tile_rows) give the same result as row-major ones, bit for
+    bit (same products, same order), and match fp32; the pad rows past the live count hold NaN and are
+    ignored."""
+    g = torch.Generator().manual_seed(rows * 7 + rtw)
+    x = torch.randn(rows, k, generator=g).to(gpu, torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(gpu, torch.bfloat16)
+    wt = decoder_ops.tile_weight(w, rtw)
+    padded = torch.full((64, k), float("nan"), dtype=torch.bfloat16, device=gpu)
+    padded[:rows] = x
+    xt = decoder_ops.tile_weight(padded, 4)
+    a = decoder_ops.linear_tiled(xt, wt, rtw, ks, x_tiled=True, rows=rows)
+    b = decoder_ops.linear_tiled(x, wt, rtw, ks)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    _check_linear(a, _linear_ref(x, w))
+
+
+@pytest.mark.parametrize("rows", [64, 9])
+def test_rmsnorm_and_swiglu_write_the_tiled_layout(gpu, rows):
+    """rmsnorm / swiglu with tiled_out write exactly tile_rows of their row-major outputs."""
+    g = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, 4096, generator=g).to(gpu, torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(4096, generator=g)).to(gpu, torch.bfloat16)
+    gu = torch.randn(rows, 2 * 1024, generator=g).to(gpu, torch.bfloat16)
+    y = decoder_ops.rmsnorm(x, w, 1e-5)
+    yt = torch.zeros(64, 4096, dtype=torch.bfloat16, device=gpu)
+    decoder_ops.rmsnorm(x, w, 1e-5, out=yt, tiled_out=True)
+    s = decoder_ops.swiglu(gu)
+    st = torch.zeros(64, 1024, dtype=torch.bfloat16, device=gpu)
+    decoder_ops.swiglu(gu, out=st, tiled_out=True)
+    torch.cuda.synchronize()
+    assert torch.equal(yt, decoder_ops.tile_rows(y))
+    assert torch.equal(st, decoder_ops.tile_rows(s))
+    with pytest.raises(RuntimeError, match="tiled output"):
+        decoder_ops.rmsnorm(torch.zeros(65, 64, dtype=torch.bfloat16, device=gpu), w[:64], 1e-5,
+                            out=torch.zeros(64, 64, dtype=torch.bfloat16, device=gpu), tiled_out=True)
+
+
+@pytest.mark.parametrize("rtw,ks", [(4, 4), (3, 2), (7, 1)])
+def test_linear_partials_mode(gpu, rtw, ks):
+    """mode="partials" returns the k slices' fp32 sums; added up in slice order they are what the bf16
+    mode rounds (bit for bit once rounded), and they match fp32."""
+    g = torch.Generator().manual_seed(rtw * 10 + ks)
+    x = torch.randn(64, 2048, generator=g).to(gpu, torch.bfloat16)
+    w = (torch.randn(1024, 2048, generator=g) * 0.02).to(gpu, torch.bfloat16)
+    wt = decoder_ops.tile_weight(w, rtw)
+    part = decoder_ops.linear_tiled(x, wt, rtw, ks, mode="partials")
+    y = decoder_ops.linear_tiled(x, wt, rtw, ks)
+    torch.cuda.synchronize()
+    assert part.shape == (ks, 64, 1024) and part.dtype == torch.float32
+    s = part[0].clone()
+    for k in range(1, ks):
+        s += part[k]
+    assert torch.equal(s.to(torch.bfloat16), y)
+    _check_linear(s, _linear_ref(x, w))
+
+
+@pytest.mark.parametrize("rows,x_tiled", [(64, True), (64, False), (13, True)])
+def test_linear_swiglu_mode(gpu, rows, x_tiled):
+    """The gate / up projection with SwiGLU in its epilogue (interleave_gate_up weight, tiled output)
+    equals silu(x w_gate^T) * (x w_up^T) from fp32 products, one bf16 rounding at the end."""
+    g = torch.Generator().manual_seed(rows + x_tiled)
+    k, f = 1024, 1536
+    x = torch.randn(rows, k, generator=g).to(gpu, torch.bfloat16)
+    wg = (torch.randn(f, k, generator=g) * 0.05).to(gpu, torch.bfloat16)
+    wu = (torch.randn(f, k, generator=g) * 0.05).to(gpu, torch.bfloat16)
+    lin = decoder_ops.DecodeLinear(None, 64, gate_up=(wg, wu))
+    assert lin.tiled and lin.ks == 1
+    xa = decoder_ops.tile_rows(x) if x_tiled else x
+    out = lin(xa, x_tiled=x_tiled, rows=rows)
+    torch.cuda.synchronize()
+    gate, up = _linear_ref(x, wg), _linear_ref(x, wu)
+    ref = gate / (1 + torch.exp(-gate)) * up
+    got = decoder_ops.untile_rows(out, rows)
+    _check_linear(got, ref)
+    assert torch.equal(lin.plain(), torch.cat([wg, wu], 0))
+
+
+def test_rmsnorm_residual_from_partials(gpu):
+    """res_part (a projection's fp32 split partials) gives h = bf16(x + sum of the slices) and the norm of it."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(64, 4096, generator=g).to(gpu, torch.bfloat16)
+    part = torch.randn(4, 64, 4096, generator=g).to(gpu)
+    w = (1 + 0.1 * torch.randn(4096, generator=g)).to(gpu, torch.bfloat16)
+    h = x.clone()
+    y = decoder_ops.rmsnorm(h, w, 1e-5, res_part=part, h_out=h)
+    torch.cuda.synchronize()
+    s = part[0] + part[1] + part[2] + part[3]
+    h_ref = (x.float() + s).to(torch.bfloat16)
+    assert torch.equal(h, h_ref)
+    hf = h_ref.float()
+    y_ref = (hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-5) * w.float())
+    assert (y.float() - y_ref).abs().max() <= 2e-2 * y_ref.abs().max()
+
+
+@pytest.mark.parametrize("layout,gs,r_k,r_v,k_rope", [("tiled", 1, 64, 96, False), ("rows", 1, 32, 128, False),
+                                                      ("tiled", 4, 256, 192, False), ("tiled", 1, 128, 64, True)])
+def test_qkv_post_equals_rope_and_appends(gpu, layout, gs, r_k, r_v, k_rope):
+    """The fused QKV epilogue: q rotated at each row's position, every group's K and V slices appended at
+    that position (rotated K for the stock path), from fp32 split partials; against rope of the summed
+    projection and the strided appends of its bf16 rounding."""
+    g = torch.Generator().manual_seed(r_k + r_v + gs)
+    B, nh, nkv, hd, S, ks = 6, 8, 4, 128, 256, 3
+    G = nkv // gs
+    ncols = (nh + 2 * nkv) * hd
+    part = torch.randn(ks, B, ncols, generator=g).to(gpu)
+    pos = torch.tensor([0, 5, 31, 32, 200, 255], dtype=torch.int32, device=gpu)
+    cos, sin = fused.cos_sin_tables(hd, S, 500000.0, None)
+    cos, sin = cos.to(gpu).contiguous(), sin.to(gpu).contiguous()
+    k_w = hd if k_rope else r_k
+    mk = (lambda w, role: LatentCache.zeros(B, G, S, w, gpu, role)) if layout == "tiled" else \
+        (lambda w, role: torch.zeros(B, G, S, w, dtype=torch.bfloat16, device=gpu))
+    keys, values, keys2, values2 = mk(k_w, "k"), mk(r_v, "v"), mk(k_w, "k"), mk(r_v, "v")
+    q = decoder_ops.qkv_post(part, pos, cos, sin, nh, keys, nh * hd, gs * hd, k_w, values, (nh + nkv) * hd, gs * hd, r_v,
+                             k_rope=k_rope)
+    s = part[0] + part[1] + part[2]
+    xqkv = s.to(torch.bfloat16)
+    if k_rope:
+        krot = fused.apply_rope_meta(s[:, nh * hd:(nh + nkv) * hd].view(B, nkv, hd), cos[pos.long()][:, None],
+                                     sin[pos.long()][:, None]).to(torch.bfloat16)
+        decoder_ops.append_from(keys2, krot.reshape(B, nkv * hd), hd, hd, pos)
+    else:
+        decoder_ops.append_from(keys2, xqkv[:, nh * hd:], gs * hd, k_w, pos)
+    decoder_ops.append_from(values2, xqkv[:, (nh + nkv) * hd:], gs * hd, r_v, pos)
+    torch.cuda.synchronize()
+    q_ref = fused.apply_rope_meta(s[:, :nh * hd].view(B, nh, hd), cos[pos.long()][:, None], sin[pos.long()][:, None])
+    assert (q.float() - q_ref).abs().max() <= 1e-2 * q_ref.abs().max()
+    kt = (lambda c: c.to_rows()) if layout == "tiled" else (lambda c: c)
+    if k_rope:
+        assert (kt(keys).float() - kt(keys2).float()).abs().max() <= 1e-2 * krot.float().abs().max()
+    else:
+        assert torch.equal(kt(keys), kt(keys2))
+    assert torch.equal(kt(values), kt(values2))

@@ -430,3 +430,27 @@ def test_bench_refuses_more_than_one_gpu():
                          timeout=300)
     assert res.returncode == 2
     assert "exactly one GPU" in json.loads(res.stdout.strip().splitlines()[-1])["error"]
+
+
+def test_tile_weight_layout_and_inverse():
+    """tile_weight puts w[16 rt + i][32 kt + 8 g + e] at lane 16 g + i, element e of tile (rt, kt) (the A
+    operand of one 16x16x32 MFMA per 1 KB tile); row tiles form groups of rtw (the last one shorter when
+    rtw does not divide them) stored [kt][rt in group]; untile_weight undoes it."""
+    from palu_tt import decoder_ops
+    n, k = 80, 96                                    # 5 row tiles, 3 k tiles
+    w = torch.arange(n * k, dtype=torch.float32).reshape(n, k)
+    n16, kt_n = n // 16, k // 32
+    for rtw in (1, 2, 3, 5, 8):
+        t = decoder_ops.tile_weight(w, rtw).reshape(-1)
+        for rt in range(n16):
+            grp, r = divmod(rt, rtw)
+            cnt = min(rtw, n16 - grp * rtw)
+            for kt in range(kt_n):
+                for g, i, e in [(0, 0, 0), (3, 15, 7), (1, 4, 5), (2, 9, 2)]:
+                    tile = grp * rtw * kt_n + kt * cnt + r
+                    assert t[(tile * 64 + 16 * g + i) * 8 + e] == w[16 * rt + i, 32 * kt + 8 * g + e], (rtw, rt, kt)
+        assert torch.equal(decoder_ops.untile_weight(decoder_ops.tile_weight(w, rtw), rtw), w)
+    with pytest.raises(RuntimeError, match="n % 16"):
+        decoder_ops.tile_weight(torch.zeros(40, 64), 1)
+    with pytest.raises(RuntimeError, match="rtw"):
+        decoder_ops.tile_weight(torch.zeros(32, 64), 9)

@@ -9,13 +9,21 @@ namespace {
 
 __device__ __forceinline__ float bf(const __bf16 x) { return (float)x; }
 
+// Element offset of (row, col .. col + 7) in the 64-row tiled activation layout of the decode projection
+// (palu_linear_tiled with x_tiled): tile (col / 32, row / 16) of 1 KB, lane 16 ((col % 32) / 8) + row % 16.
+__device__ __forceinline__ long long tiled_row_offset(int row, int col) {
+  return ((long long)((col >> 5) * 4 + (row >> 4)) * 64 + 16 * ((col & 31) >> 3) + (row & 15)) * 8;
+}
+
 // One workgroup per row: h = x (+ res), stored when h_out is given; y = h * rsqrt(mean(h^2) + eps) * w.
 // Each thread holds up to RMS_VEC vectors of 8 elements in registers between the two passes.
 constexpr int RMS_THREADS = 256;
 constexpr int RMS_VEC = 4;               // dim <= 256 * 8 * 4 = 8192
 
-__global__ __launch_bounds__(RMS_THREADS) void palu_rmsnorm_kernel(const __bf16* x, const __bf16* res, __bf16* h_out,
-                                                                   __bf16* y_out, const __bf16* w, int dim, float eps) {
+__global__ __launch_bounds__(RMS_THREADS) void palu_rmsnorm_kernel(const __bf16* x, const __bf16* res,
+                                                                   const float* res_part, int res_ks, long long part_stride,
+                                                                   __bf16* h_out, __bf16* y_out, const __bf16* w, int dim,
+                                                                   float eps, int y_tiled) {
   const int row = blockIdx.x, tid = threadIdx.x;
   const __bf16* xr = x + (long long)row * dim;
   const __bf16* rr = res ? res + (long long)row * dim : nullptr;
@@ -31,6 +39,19 @@ __global__ __launch_bounds__(RMS_THREADS) void palu_rmsnorm_kernel(const __bf16*
         const bf16x8 c = *reinterpret_cast<const bf16x8*>(rr + e);
 #pragma unroll
         for (int j = 0; j < 8; ++j) hv[j] = (__bf16)(bf(a[j]) + bf(c[j]));   // bf16 residual stream
+      } else if (res_part) {
+        // the sublayer output as the fp32 k-slice partials of its projection: summed here, in slice order
+        const float* pp = res_part + (long long)row * dim + e;
+        f32x4 s0 = *reinterpret_cast<const f32x4*>(pp), s1 = *reinterpret_cast<const f32x4*>(pp + 4);
+        for (int k = 1; k < res_ks; ++k) {
+          s0 += *reinterpret_cast<const f32x4*>(pp + k * part_stride);
+          s1 += *reinterpret_cast<const f32x4*>(pp + k * part_stride + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          hv[j] = (__bf16)(bf(a[j]) + s0[j]);
+          hv[4 + j] = (__bf16)(bf(a[4 + j]) + s1[j]);
+        }
       } else {
         hv = a;
       }
@@ -59,13 +80,14 @@ __global__ __launch_bounds__(RMS_THREADS) void palu_rmsnorm_kernel(const __bf16*
       bf16x8 o;
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[j] = (__bf16)((v[i][j] * r) * bf(wv[j]));
-      *reinterpret_cast<bf16x8*>(y_out + (long long)row * dim + e) = o;
+      *reinterpret_cast<bf16x8*>(y_out + (y_tiled ? tiled_row_offset(row, e) : (long long)row * dim + e)) = o;
     }
   }
 }
 
 // out[r][f] = silu(g) * u with g = gu[r][f], u = gu[r][ffn + f]; 8 elements per thread.
-__global__ __launch_bounds__(256) void palu_swiglu_kernel(const __bf16* gu, __bf16* out, int rows, int ffn) {
+__global__ __launch_bounds__(256) void palu_swiglu_kernel(const __bf16* gu, __bf16* out, int rows, int ffn,
+                                                          int out_tiled) {
   const long long vecs = (long long)rows * (ffn / 8);
   for (long long e = blockIdx.x * 256LL + threadIdx.x; e < vecs; e += (long long)gridDim.x * 256) {
     const int r = (int)(e / (ffn / 8)), f = (int)(e % (ffn / 8)) * 8;
@@ -77,7 +99,7 @@ __global__ __launch_bounds__(256) void palu_swiglu_kernel(const __bf16* gu, __bf
       const float gv = bf(g[j]);
       o[j] = (__bf16)((gv / (1.f + __expf(-gv))) * bf(u[j]));
     }
-    *reinterpret_cast<bf16x8*>(out + (long long)r * ffn + f) = o;
+    *reinterpret_cast<bf16x8*>(out + (out_tiled ? tiled_row_offset(r, f) : (long long)r * ffn + f)) = o;
   }
 }
 
@@ -127,27 +149,35 @@ int launched(const char* what) {
 
 extern "C" {
 
-int palu_rmsnorm(const void* x, const void* res, void* h_out, void* y_out, const void* weight, int rows, int dim,
-                 float eps, hipStream_t stream) {
+int palu_rmsnorm(const void* x, const void* res, const float* res_part, int res_ks, void* h_out, void* y_out,
+                 const void* weight, int rows, int dim, float eps, int y_tiled, hipStream_t stream) {
   palu::g_err[0] = 0;
   if (!x || !y_out || !weight) return fail(PALU_EINVAL, "palu_rmsnorm: a required pointer is null");
   if (rows <= 0 || dim <= 0 || dim % 8 != 0 || dim > RMS_THREADS * 8 * RMS_VEC)
     return fail(PALU_EINVAL, "palu_rmsnorm: dim must be a multiple of 8 up to %d, got %d", RMS_THREADS * 8 * RMS_VEC, dim);
-  if (!a16(x) || !a16(y_out) || !a16(weight) || (res && !a16(res)) || (h_out && !a16(h_out)))
+  if (y_tiled && (rows > 64 || dim % 32 != 0))
+    return fail(PALU_EINVAL, "palu_rmsnorm: a tiled output needs rows <= 64 and dim a multiple of 32, got %d x %d", rows, dim);
+  if (res && res_part) return fail(PALU_EINVAL, "palu_rmsnorm: res and res_part are exclusive");
+  if (res_part && (res_ks < 1 || res_ks > 64))
+    return fail(PALU_EINVAL, "palu_rmsnorm: res_ks = %d partial slices (1..64)", res_ks);
+  if (!a16(x) || !a16(y_out) || !a16(weight) || (res && !a16(res)) || (h_out && !a16(h_out)) ||
+      (res_part && !a16(res_part)))
     return fail(PALU_EINVAL, "palu_rmsnorm: 16-byte alignment required");
   hipLaunchKernelGGL(palu_rmsnorm_kernel, dim3(rows), dim3(RMS_THREADS), 0, stream, static_cast<const __bf16*>(x),
-                     static_cast<const __bf16*>(res), static_cast<__bf16*>(h_out), static_cast<__bf16*>(y_out),
-                     static_cast<const __bf16*>(weight), dim, eps);
+                     static_cast<const __bf16*>(res), res_part, res_part ? res_ks : 0, (long long)rows * dim,
+                     static_cast<__bf16*>(h_out), static_cast<__bf16*>(y_out), static_cast<const __bf16*>(weight), dim,
+                     eps, y_tiled ? 1 : 0);
   return launched("palu_rmsnorm");
 }
-
-int palu_swiglu(const void* gu, void* out, int rows, int ffn, hipStream_t stream) {
+int palu_swiglu(const void* gu, void* out, int rows, int ffn, int out_tiled, hipStream_t stream) {
   palu::g_err[0] = 0;
   if (!gu || !out) return fail(PALU_EINVAL, "palu_swiglu: a required pointer is null");
   if (rows <= 0 || ffn <= 0 || ffn % 8 != 0) return fail(PALU_EINVAL, "palu_swiglu: ffn must be a multiple of 8, got %d", ffn);
+  if (out_tiled && (rows > 64 || ffn % 32 != 0))
+    return fail(PALU_EINVAL, "palu_swiglu: a tiled output needs rows <= 64 and ffn a multiple of 32, got %d x %d", rows, ffn);
   if (!a16(gu) || !a16(out)) return fail(PALU_EINVAL, "palu_swiglu: 16-byte alignment required");
   hipLaunchKernelGGL(palu_swiglu_kernel, dim3(grid_for((long long)rows * (ffn / 8))), dim3(256), 0, stream,
-                     static_cast<const __bf16*>(gu), static_cast<__bf16*>(out), rows, ffn);
+                     static_cast<const __bf16*>(gu), static_cast<__bf16*>(out), rows, ffn, out_tiled ? 1 : 0);
   return launched("palu_swiglu");
 }
 

@@ -19,7 +19,7 @@ INCLUDE = REPO / "include"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_NAME = "libpalu_mi355x.so"
 SOURCES = ["palu_capi.hip", "palu_decode_rows.hip", "palu_decode_tiled.hip", "palu_decode_rows_paged.hip",
-           "palu_decode_tiled_paged.hip", "palu_decode_full.hip", "palu_glrd.hip", "palu_decoder.hip"]
+           "palu_decode_tiled_paged.hip", "palu_decode_full.hip", "palu_glrd.hip", "palu_decoder.hip", "palu_linear.hip"]
 HEADERS = ["palu_kernel.h"]
 
 HIPCC_FLAGS = [

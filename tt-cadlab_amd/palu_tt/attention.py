@@ -83,15 +83,18 @@ class PaluAttention(torch.nn.Module):
         wq = state_dict[f"{ln}.wq.weight"]
         wk = state_dict[f"{P}.wk_lat_pad"]
         wv = state_dict[f"{P}.wv_lat_pad"]
-        # weights in the nn.Linear layout [out, in]: the M=B GEMMs of decode stream them fastest that way
-        self.wqkv = torch.cat([wq, wk, wv], dim=0).to(dev, bf).contiguous()          # [(nh + 2 nkv) hd, dim]
+        # [(nh + 2 nkv) hd, dim]: held in the decode projection's tiled order (decoder_ops.DecodeLinear);
+        # the prefill multiplies by its nn.Linear-layout copy
+        self.wqkv = decoder_ops.DecodeLinear(torch.cat([wq, wk, wv], dim=0).to(dev, bf).contiguous(),
+                                             self.max_batch_size)
         self.wo = state_dict[f"{ln}.wo.weight"].to(dev, bf).contiguous()
         wo_fused = (state_dict[f"{P}.wo_fused"].to(dev, bf) if (self.recon_v and self.gs == 1) else self.wo)
         # decode output width per head: the absorbed-V latent (r_v) or, with u_v / stock V, head_dim; the
         # output projection keeps only those rows of wo_fused (the rest multiply the zero padding)
         self.out_width = self.head_dim if (self.gs > 1 or not self.recon_v) else self.r_v
-        self.wo_out = (wo_fused.view(-1, self.n_heads, self.head_dim)[:, :, :self.out_width]
-                       .reshape(-1, self.n_heads * self.out_width).contiguous())
+        self.wo_out = decoder_ops.DecodeLinear(wo_fused.view(-1, self.n_heads, self.head_dim)[:, :, :self.out_width]
+                                               .reshape(-1, self.n_heads * self.out_width).contiguous(),
+                                               self.max_batch_size)
         self.u_k = state_dict[f"{P}.u_k"].to(dev, bf).contiguous() if self.recon_k else None   # [nkv, r_k, hd]
         self.w_rot = state_dict[f"{P}.w_rot"].to(dev, bf)[None].contiguous() if self.recon_k else None
         self.u_v = state_dict[f"{P}.u_v"].to(dev, bf).contiguous() if self.recon_v else None   # [nkv, r_v, hd]
@@ -137,32 +140,49 @@ class PaluAttention(torch.nn.Module):
         return fused.apply_rope_meta(x, self.cos[pos][..., None, :], self.sin[pos][..., None, :])
 
     # ------------------------------------------------------------------------------------------------
-    def forward_decode(self, x, current_pos, rot_mats=None, page_table=None, kv_cache=None):
+    def forward_decode(self, x, current_pos, rot_mats=None, page_table=None, kv_cache=None, x_tiled=False,
+                       out_partials=False):
         """One decode step for all max_batch_size rows: QKV projection; RoPE of q (and of K on the K-fast
-        path) read straight from the projection; latent append from its latent columns; the fused op
-        (or the stock decode over rotated K); output projection over the out_width rows per head."""
+        path) and the latent appends from the projection's columns (one fused launch over its split
+        partials when the projection is tiled); the fused op (or the naive path, or the stock decode over
+        rotated K); output projection over the out_width rows per head. With x_tiled, x is the [64, dim]
+        tiled activation buffer (decoder_ops.rmsnorm(..., tiled_out=True)) holding the max_batch_size rows,
+        and the output is [max_batch_size, dim]; with out_partials it is the output projection's fp32 split
+        partials [ks, B, dim] (decoder_ops.rmsnorm's res_part)."""
         assert page_table is None and kv_cache is None
-        shape = x.shape
-        x2 = x.reshape(-1, self.hidden_size).to(torch.bfloat16)
-        B = x2.shape[0]
+        if x_tiled:
+            B = self.max_batch_size
+            shape, x2 = (B, self.hidden_size), x
+        else:
+            shape = x.shape
+            x2 = x.reshape(-1, self.hidden_size).to(torch.bfloat16)
+            B = x2.shape[0]
         if B != self.max_batch_size:
             raise ValueError(f"decode batch {B} != max_batch_size {self.max_batch_size}")
         pos = current_pos.reshape(-1).to(self.device, torch.int32)
         assert pos.numel() == B
         nh, nkv, hd = self.n_heads, self.n_kv_heads, self.head_dim
-        xqkv = F.linear(x2, self.wqkv)                                      # [B, (nh + 2 nkv) hd]
-        q = decoder_ops.rope_rows(xqkv, nh, pos, self.cos, self.sin)         # [B, nh, hd]
         keys, values = self.layer_past
-        kcols, vcols = xqkv[:, nh * hd:], xqkv[:, (nh + nkv) * hd:]
-        if self.recon_k:
-            decoder_ops.append_from(keys, kcols, self.gs * hd, self.r_k, pos)
-        else:                                                                # stock K path: rotated full K
-            k_rot = decoder_ops.rope_rows(kcols, nkv, pos, self.cos, self.sin)
-            decoder_ops.append_from(keys, k_rot.view(B, nkv * hd), hd, hd, pos)
-        decoder_ops.append_from(values, vcols, self.gs * hd, self.r_v, pos)
+        k_width = self.r_k if self.recon_k else hd
+        if self.wqkv.tiled:
+            part = self.wqkv(x2, x_tiled=x_tiled, rows=B, mode="partials")  # [ks, B, (nh + 2 nkv) hd] fp32
+            q = decoder_ops.qkv_post(part, pos, self.cos, self.sin, nh, keys, nh * hd, self.gs * hd, k_width,
+                                     values, (nh + nkv) * hd, self.gs * hd, self.r_v, k_rope=not self.recon_k)
+        else:
+            xqkv = self.wqkv(x2)                                            # [B, (nh + 2 nkv) hd]
+            q = decoder_ops.rope_rows(xqkv, nh, pos, self.cos, self.sin)     # [B, nh, hd]
+            kcols, vcols = xqkv[:, nh * hd:], xqkv[:, (nh + nkv) * hd:]
+            if self.recon_k:
+                decoder_ops.append_from(keys, kcols, self.gs * hd, self.r_k, pos)
+            else:                                                            # stock K path: rotated full K
+                k_rot = decoder_ops.rope_rows(kcols, nkv, pos, self.cos, self.sin)
+                decoder_ops.append_from(keys, k_rot.view(B, nkv * hd), hd, hd, pos)
+            decoder_ops.append_from(values, vcols, self.gs * hd, self.r_v, pos)
         attn = self.decode_core(q[None], keys, values, pos)                  # [1, B, nh, out_width]
-        out = F.linear(attn[0].reshape(B, nh * self.out_width), self.wo_out)
-        return out.reshape(*shape[:-1], self.hidden_size)
+        a2 = attn[0].reshape(B, nh * self.out_width)
+        if out_partials:
+            return self.wo_out(a2, mode="partials")
+        return self.wo_out(a2).reshape(*shape[:-1], self.hidden_size)
 
     def decode_core(self, q4, keys, values, pos):
         """The attention core of a decode step over the caches (new rows already appended): q4 [1, B, nh, hd]
@@ -233,7 +253,7 @@ class PaluAttention(torch.nn.Module):
 
     def _prefill_one(self, x2, user):
         S = x2.shape[0]
-        q_pre, k_slots, v_slots = self._split(F.linear(x2, self.wqkv))      # [S, nh | nkv, hd]
+        q_pre, k_slots, v_slots = self._split(F.linear(x2, self.wqkv.plain()))   # [S, nh | nkv, hd]
         pos = torch.arange(S, device=self.device)
         k_lat = self._group_latent(k_slots, self.r_k) if self.recon_k else None    # [S, n_groups, r_k]
         v_lat = self._group_latent(v_slots, self.r_v)

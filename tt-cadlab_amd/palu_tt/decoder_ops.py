@@ -6,6 +6,7 @@ projection's latent columns. Every op writes into tensors the caller passes or a
 are bf16 on the GPU except the fp32 RoPE tables and int32 positions. No CPU fallback: a missing library
 raises RuntimeError.
 """
+import ctypes
 from typing import Optional
 
 import torch
@@ -20,36 +21,52 @@ def _check(t: torch.Tensor, name: str, dtype=torch.bfloat16) -> None:
 
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, res: Optional[torch.Tensor] = None,
-            h_out: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+            h_out: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+            tiled_out: bool = False, res_part: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y = h * rsqrt(mean(h^2) + eps) * weight per row with h = x + res (bf16 residual stream; res may be
-    None). When h_out is given, h is written there (it may alias x). x, res, h_out, out: [rows, dim]."""
+    None), or h = x + the sum of res_part (fp32 [ks, rows, dim], a projection's split partials, from
+    linear_tiled(..., mode="partials")). When h_out is given, h is written there (it may alias x). x, res,
+    h_out: [rows, dim]; out: [rows, dim], or with tiled_out a [64, dim] buffer in the tiled activation
+    layout (tile_rows) that linear_tiled(..., x_tiled=True) reads (rows <= 64)."""
     _check(x, "x")
     _check(weight, "weight")
     rows, dim = x.reshape(-1, x.shape[-1]).shape
-    out = torch.empty_like(x) if out is None else out
-    for t, n in ((res, "res"), (h_out, "h_out"), (out, "out")):
+    ks = 0
+    if res_part is not None:
+        _check(res_part, "res_part", torch.float32)
+        if res_part.dim() != 3 or res_part.shape[1:] != (rows, dim) or not res_part.is_contiguous():
+            raise RuntimeError(f"res_part must be a contiguous [ks, {rows}, {dim}] fp32 tensor")
+        ks = res_part.shape[0]
+    if out is None:
+        out = (torch.empty(64, dim, dtype=torch.bfloat16, device=x.device) if tiled_out else torch.empty_like(x))
+    for t, n in ((res, "res"), (h_out, "h_out")):
         if t is not None:
             _check(t, n)
             if t.numel() != x.numel() or not t.is_contiguous():
                 raise RuntimeError(f"{n} must be contiguous with the shape of x")
+    _check(out, "out")
+    if not out.is_contiguous() or out.numel() != (64 * dim if tiled_out else x.numel()):
+        raise RuntimeError("out must be contiguous with the shape of x ([64, dim] when tiled)")
     if not x.is_contiguous():
         raise RuntimeError("x must be contiguous")
     _native.check(_native.load().palu_rmsnorm(
-        _native.ptr(x), _native.ptr(res), _native.ptr(h_out), _native.ptr(out), _native.ptr(weight), rows, dim,
-        float(eps), _native.stream_handle(x.device)))
+        _native.ptr(x), _native.ptr(res), _native.ptr(res_part), ks, _native.ptr(h_out), _native.ptr(out),
+        _native.ptr(weight), rows, dim, float(eps), int(tiled_out), _native.stream_handle(x.device)))
     return out
 
 
-def swiglu(gu: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """silu(g) * u for gu = [g | u] of shape [rows, 2 ffn]; returns [rows, ffn]."""
+def swiglu(gu: torch.Tensor, out: Optional[torch.Tensor] = None, tiled_out: bool = False) -> torch.Tensor:
+    """silu(g) * u for gu = [g | u] of shape [rows, 2 ffn]; returns [rows, ffn], or with tiled_out a
+    [64, ffn] buffer in the tiled activation layout (rows <= 64)."""
     _check(gu, "gu")
     if not gu.is_contiguous():
         raise RuntimeError("gu must be contiguous")
     rows, two_f = gu.reshape(-1, gu.shape[-1]).shape
     ffn = two_f // 2
     if out is None:
-        out = torch.empty(*gu.shape[:-1], ffn, dtype=torch.bfloat16, device=gu.device)
-    _native.check(_native.load().palu_swiglu(_native.ptr(gu), _native.ptr(out), rows, ffn,
+        out = (torch.empty(64, ffn, dtype=torch.bfloat16, device=gu.device) if tiled_out
+               else torch.empty(*gu.shape[:-1], ffn, dtype=torch.bfloat16, device=gu.device))
+    _native.check(_native.load().palu_swiglu(_native.ptr(gu), _native.ptr(out), rows, ffn, int(tiled_out),
                                              _native.stream_handle(gu.device)))
     return out
 
@@ -97,3 +114,231 @@ def append_from(cache, src: torch.Tensor, group_stride: int, width: int, pos: to
     _native.check(_native.load().palu_latent_append_strided(
         _native.ptr(store), _native.ptr(src), src.stride(0), int(group_stride), _native.ptr(p), B, G, S, width, layout,
         _native.stream_handle(src.device)))
+
+
+def tile_weight(w: torch.Tensor, rtw: int) -> torch.Tensor:
+    """The [n, k] nn.Linear weight in the decode projection's tiled order for workgroups of rtw row tiles
+    (a new contiguous tensor of the same bytes). Tile (rt, kt) of 16 output columns x 32 inputs is 1 KB,
+    lane 16 g + i holding w[16 rt + i][32 kt + 8 g .. +7]. Row tiles form groups of rtw (the last group
+    may be shorter); inside a group the tiles are stored k tile by k tile, [kt][rt in group], so the
+    workgroup that owns a group reads it as one sequential stream. n a multiple of 16, k of 32."""
+    n, k = w.shape
+    if n % 16 or k % 32:
+        raise RuntimeError(f"tile_weight: shape [{n}, {k}] needs n % 16 == 0 and k % 32 == 0")
+    if not 1 <= rtw <= 8:
+        raise RuntimeError(f"tile_weight: rtw = {rtw} must be in 1..8")
+    n16, kt = n // 16, k // 32
+    t = w.reshape(n16, 16, kt, 4, 8).permute(0, 2, 3, 1, 4)               # [rt, kt, g, i, e]
+    full = (n16 // rtw) * rtw
+    parts = [t[:full].reshape(n16 // rtw, rtw, kt, 4, 16, 8).transpose(1, 2).reshape(-1)]
+    if full < n16:
+        parts.append(t[full:].transpose(0, 1).reshape(-1))
+    return torch.cat(parts).reshape(n, k)
+
+
+def untile_weight(wt: torch.Tensor, rtw: int) -> torch.Tensor:
+    """Inverse of tile_weight: the [n, k] nn.Linear layout."""
+    n, k = wt.shape
+    n16, kt = n // 16, k // 32
+    full = (n16 // rtw) * rtw
+    flat = wt.reshape(-1)
+    t = flat[:full * kt * 512].reshape(n16 // rtw, kt, rtw, 4, 16, 8).transpose(1, 2).reshape(full, kt, 4, 16, 8)
+    if full < n16:
+        rest = flat[full * kt * 512:].reshape(kt, n16 - full, 4, 16, 8).transpose(0, 1)
+        t = torch.cat([t, rest])
+    return t.permute(0, 3, 1, 2, 4).reshape(n, k).contiguous()
+
+
+def tile_rows(x: torch.Tensor) -> torch.Tensor:
+    """Activations [rows <= 64, k] in the 64-row tiled layout that linear_tiled reads with x_tiled=True
+    (rows padded with zeros to 64, then tile_weight's order with the four 16-row tiles as one group)."""
+    rows, k = x.shape
+    if rows > 64:
+        raise RuntimeError(f"tile_rows: {rows} rows (at most 64)")
+    pad = torch.zeros(64, k, dtype=x.dtype, device=x.device)
+    pad[:rows] = x
+    return tile_weight(pad, 4)
+
+
+def untile_rows(xt: torch.Tensor, rows: int) -> torch.Tensor:
+    """Inverse of tile_rows: the first `rows` rows of a [64, k] tiled activation buffer, row-major."""
+    return untile_weight(xt, 4)[:rows]
+
+
+def linear_plan(rows: int, n: int, k: int):
+    """(row tiles per workgroup, k slices) suggested for this shape: tile the weight with that rtw."""
+    rtw, ks = ctypes.c_int(0), ctypes.c_int(0)
+    _native.check(_native.load().palu_linear_plan(rows, n, k, ctypes.byref(rtw), ctypes.byref(ks)))
+    return rtw.value, ks.value
+
+
+_LINEAR_MODES = {"bf16": 0, "partials": 1, "swiglu": 2}
+
+
+def linear_tiled(x: torch.Tensor, w_tiled: torch.Tensor, rtw: int, ks: int, out: Optional[torch.Tensor] = None,
+                 workspace: Optional[torch.Tensor] = None, x_tiled: bool = False, rows: Optional[int] = None,
+                 mode: str = "bf16") -> torch.Tensor:
+    """x @ w.T for the decode step's rows (at most 64) with w given by tile_weight(w, rtw) ([n, k]), split
+    into ks k slices. x: a row-strided [rows, k] view, or with x_tiled a [64, k] buffer in the tiled
+    activation layout (tile_rows; rmsnorm / swiglu with tiled_out) and `rows` the live row count.
+    mode "bf16": returns [rows, n] bf16 (or writes `out`, a row-strided [rows, n] view); split partials
+    go to `workspace` (a uint8 GPU tensor of at least palu_linear_workspace_bytes, else a fresh one from
+    torch's caching allocator) and a second launch adds them. mode "partials": returns the fp32 split
+    partials [ks, rows, n] for a consumer that sums them (rmsnorm's res_part, qkv_post). mode "swiglu": w
+    is interleave_gate_up's gate / up weight (ks = 1) and the result is silu(gate) * up as [64, n / 2]
+    tiled activations. linear_plan(rows, n, k) suggests (rtw, ks)."""
+    _check(x, "x")
+    _check(w_tiled, "w_tiled")
+    if x.dim() != 2 or x.stride(1) != 1 or w_tiled.dim() != 2 or not w_tiled.is_contiguous():
+        raise RuntimeError("x must be a row-strided [rows, k] view and w_tiled a contiguous [n, k] tensor")
+    if mode not in _LINEAR_MODES:
+        raise RuntimeError(f"mode must be one of {sorted(_LINEAR_MODES)}")
+    k = x.shape[1]
+    if x_tiled:
+        if x.shape[0] != 64 or not x.is_contiguous() or rows is None:
+            raise RuntimeError("a tiled x is a contiguous [64, k] buffer and needs the live row count `rows`")
+    else:
+        rows = x.shape[0]
+    n = w_tiled.shape[0]
+    if w_tiled.shape[1] != k:
+        raise RuntimeError(f"x has k = {k}, w_tiled has {w_tiled.shape[1]}")
+    if mode == "partials":
+        if out is None:
+            out = torch.empty(ks, rows, n, dtype=torch.float32, device=x.device)
+        _check(out, "out", torch.float32)
+        if out.shape != (ks, rows, n) or not out.is_contiguous():
+            raise RuntimeError(f"out must be a contiguous [{ks}, {rows}, {n}] fp32 tensor")
+    elif mode == "swiglu":
+        if out is None:
+            out = torch.empty(64, n // 2, dtype=torch.bfloat16, device=x.device)
+        _check(out, "out")
+        if out.shape != (64, n // 2) or not out.is_contiguous():
+            raise RuntimeError(f"out must be a contiguous [64, {n // 2}] bf16 tensor")
+    else:
+        if out is None:
+            out = torch.empty(rows, n, dtype=torch.bfloat16, device=x.device)
+        _check(out, "out")
+        if out.dim() != 2 or out.shape != (rows, n) or out.stride(1) != 1:
+            raise RuntimeError(f"out must be a row-strided [{rows}, {n}] view")
+    lib = _native.load()
+    need = lib.palu_linear_workspace_bytes(rows, n, k, ks) if mode == "bf16" else 0
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _native.check(lib.palu_linear_tiled(
+        _native.ptr(x), x.stride(0), int(x_tiled), rows, _native.ptr(w_tiled), n, k, _native.ptr(out),
+        out.stride(0) if mode == "bf16" else n, _LINEAR_MODES[mode], rtw, ks,
+        _native.ptr(workspace) if need else None, need, _native.stream_handle(x.device)))
+    return out
+
+
+def interleave_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """[2 ffn, k] with gate and up rows interleaved eight at a time (rows 16 j .. 16 j + 7: gate rows
+    8 j .. 8 j + 7, then the up rows of the same outputs), the weight linear_tiled's "swiglu" mode takes."""
+    f, k = w_gate.shape
+    if w_up.shape != (f, k) or f % 8:
+        raise RuntimeError("gate and up weights must share a shape [ffn, k] with ffn a multiple of 8")
+    return torch.stack([w_gate.reshape(f // 8, 8, k), w_up.reshape(f // 8, 8, k)], 1).reshape(2 * f, k)
+
+
+def deinterleave_gate_up(w: torch.Tensor) -> torch.Tensor:
+    """Inverse of interleave_gate_up, as one [2 ffn, k] tensor: the gate rows, then the up rows."""
+    f2, k = w.shape
+    t = w.reshape(f2 // 16, 2, 8, k)
+    return torch.cat([t[:, 0].reshape(f2 // 2, k), t[:, 1].reshape(f2 // 2, k)], 0)
+
+
+def qkv_post(part: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_heads: int,
+             keys, k_col_offset: int, k_group_stride: int, k_width: int, values, v_col_offset: int,
+             v_group_stride: int, v_width: int, k_rope: bool = False,
+             q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The QKV epilogue of a decode step in one launch, from the projection's fp32 split partials part
+    [ks, B, ncols]: returns q [B, n_heads, 128], the first n_heads heads rotated at pos (as rope_rows), and
+    appends every latent group's K and V slices (columns k_col_offset + g * k_group_stride, k_width wide,
+    rotated too when k_rope; v_col_offset + g * v_group_stride, v_width wide) to keys / values at pos (as
+    append_from). keys / values: LatentCache (tiled) or row-major [B, G, S, width] bf16 tensors."""
+    _check(part, "part", torch.float32)
+    _check(cos, "cos", torch.float32)
+    _check(sin, "sin", torch.float32)
+    if part.dim() != 3 or not part.is_contiguous():
+        raise RuntimeError("part must be a contiguous [ks, B, ncols] fp32 tensor")
+    ks, B, ncols = part.shape
+    p = pos.reshape(-1).to(device=part.device, dtype=torch.int32).contiguous()
+    if p.numel() != B:
+        raise RuntimeError(f"pos has {p.numel()} entries for {B} rows")
+    if q_out is None:
+        q_out = torch.empty(B, n_heads, 128, dtype=torch.bfloat16, device=part.device)
+
+    def cache_args(cache, role):
+        if isinstance(cache, LatentCache):
+            layout = _native.LAYOUT_TILED if cache.role == "k" else _native.LAYOUT_TILED_V
+            return cache.data, layout, cache.shape
+        return cache, _native.LAYOUT_ROWS, cache.shape
+
+    kd, kl, (kb, G, S, kw) = cache_args(keys, "k")
+    vd, vl, (vb, vG, vS, vw) = cache_args(values, "v")
+    if (kb, G, S, kw) != (B, G, S, k_width) or (vb, vG, vS, vw) != (B, G, S, v_width):
+        raise RuntimeError("cache shapes must be [B, G, S, k_width] and [B, G, S, v_width]")
+    _native.check(_native.load().palu_qkv_post(
+        _native.ptr(part), ks, B, ncols, _native.ptr(p), _native.ptr(cos), _native.ptr(sin), cos.shape[0], n_heads,
+        _native.ptr(q_out), _native.ptr(kd), kl, k_col_offset, k_group_stride, k_width, int(k_rope), _native.ptr(vd),
+        vl, v_col_offset, v_group_stride, v_width, G, S, _native.stream_handle(part.device)))
+    return q_out
+
+
+class DecodeLinear:
+    """One projection of the decode step, y = x @ w.T, for w [n, k] in the nn.Linear layout (for a gate /
+    up pair, gate_up=(w_gate, w_up) instead: y = silu(x @ w_gate.T) * (x @ w_up.T)). For up to 64 rows
+    (and n % 16 == 0, k % 32 == 0) the weight is held only in the tiled order of linear_tiled, with the
+    work split linear_plan suggests (or rtw / ks) and a workspace for its split partials; otherwise it
+    stays as it is and the call is torch's F.linear. plain() returns the weight in the nn.Linear layout
+    ([gate; up] for a pair; a fresh copy when tiled), for the prefill's many-row products."""
+
+    def __init__(self, w: Optional[torch.Tensor], rows: int, gate_up=None, rtw: int = 0, ks: int = 0):
+        self.gate_up = gate_up is not None
+        if self.gate_up:
+            w = torch.cat(list(gate_up), 0)
+        n, k = w.shape
+        self.n, self.k = n, k
+        self.tiled = (rows <= 64 and n % (64 if self.gate_up else 16) == 0 and k % 32 == 0 and w.is_cuda
+                      and w.dtype == torch.bfloat16)
+        if self.tiled:
+            self.rtw, self.ks = (rtw, ks) if rtw else linear_plan(rows, n, k)
+            if self.gate_up:
+                self.ks = 1
+                w = interleave_gate_up(*gate_up)
+            self.weight = tile_weight(w, self.rtw)
+            need = _native.load().palu_linear_workspace_bytes(rows, n, k, self.ks)
+            self.workspace = torch.empty(need, dtype=torch.uint8, device=w.device) if need else None
+        else:
+            self.ks = 1
+            self.weight = w.contiguous()
+
+    def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, x_tiled: bool = False,
+                 rows: Optional[int] = None, mode: Optional[str] = None) -> torch.Tensor:
+        """x: [rows, k] (row-strided), or with x_tiled the [64, k] tiled activation buffer and `rows`.
+        mode (linear_tiled's): "bf16" (the default of a plain projection), "partials" (fp32 [ks, rows, n]),
+        "swiglu" (the default and only mode of a gate / up pair: [64, n / 2] tiled activations when tiled,
+        else [rows, n / 2] bf16)."""
+        mode = mode or ("swiglu" if self.gate_up else "bf16")
+        if (mode == "swiglu") != self.gate_up:
+            raise RuntimeError("the swiglu mode is the gate / up pair's only mode")
+        if self.tiled:
+            return linear_tiled(x, self.weight, self.rtw, self.ks, out=out, workspace=self.workspace,
+                                x_tiled=x_tiled, rows=rows, mode=mode)
+        if x_tiled:
+            raise RuntimeError("tiled activations need a tiled projection (at most 64 rows)")
+        y = torch.nn.functional.linear(x, self.weight)
+        if mode == "swiglu":
+            return swiglu(y)
+        if mode == "partials":
+            return y.float()[None]
+        if out is not None:
+            out.copy_(y)
+            return out
+        return y
+
+    def plain(self) -> torch.Tensor:
+        if not self.tiled:
+            return self.weight
+        w = untile_weight(self.weight, self.rtw)
+        return deinterleave_gate_up(w) if self.gate_up else w

@@ -61,7 +61,10 @@ class Transformer(torch.nn.Module):
         t = lambda k: state_dict.pop(k).to(dev, bf)
         self.tok_embeddings = t("tok_embeddings.weight")
         self.norm_w = t("norm.weight")
-        self.output = t("output.weight")                                 # [vocab, dim] (nn.Linear layout)
+        # projections of the decode step, held in its tiled order (decoder_ops.DecodeLinear); the prefill
+        # multiplies by nn.Linear-layout copies made per call
+        rows = args.max_batch_size
+        self.output = decoder_ops.DecodeLinear(t("output.weight"), rows)         # [vocab, dim]
         self.layers = []
         for i in range(args.n_layers):
             p = f"layers.{i}"
@@ -71,8 +74,12 @@ class Transformer(torch.nn.Module):
                 state_dict.pop(k)
             self.layers.append(dict(
                 attn=attn, attn_norm=t(f"{p}.attention_norm.weight"), ffn_norm=t(f"{p}.ffn_norm.weight"),
-                w13_t=torch.cat([t(f"{p}.feed_forward.w1.weight"), t(f"{p}.feed_forward.w3.weight")], 0).T.contiguous(),
-                w2=t(f"{p}.feed_forward.w2.weight")))
+                w13=decoder_ops.DecodeLinear(None, rows, gate_up=(t(f"{p}.feed_forward.w1.weight"),
+                                                                  t(f"{p}.feed_forward.w3.weight"))),
+                w2=decoder_ops.DecodeLinear(t(f"{p}.feed_forward.w2.weight"), rows)))
+        # tiled activations between the decode step's kernels where every projection that reads them is tiled
+        self._tiled_acts = self.output.tiled and all(
+            L["w13"].tiled and L["w2"].tiled and L["attn"].wqkv.tiled for L in self.layers)
         self._graph = None
 
     def set_fused_k(self, use_fused_k: bool, recon_len: Optional[int] = None) -> None:
@@ -86,9 +93,9 @@ class Transformer(torch.nn.Module):
         self._graph = None
 
     def _ffn(self, L, h):
-        gu = h @ L["w13_t"]
+        gu = F.linear(h, L["w13"].plain())
         g, u = gu.chunk(2, dim=-1)
-        return F.linear((F.silu(g.float()) * u.float()).to(h.dtype), L["w2"])
+        return F.linear((F.silu(g.float()) * u.float()).to(h.dtype), L["w2"].plain())
 
     @torch.no_grad()
     def prefill(self, tokens: torch.Tensor, user_id: int = 0) -> torch.Tensor:
@@ -99,23 +106,31 @@ class Transformer(torch.nn.Module):
         for L in self.layers:
             h = h + L["attn"].forward_prefill(rms_norm(h, L["attn_norm"], eps), user_id=user_id)
             h = h + self._ffn(L, rms_norm(h, L["ffn_norm"], eps))
-        return F.linear(rms_norm(h[:, -1], self.norm_w, eps), self.output).float()
+        return F.linear(rms_norm(h[:, -1], self.norm_w, eps), self.output.plain()).float()
 
     @torch.no_grad()
     def decode(self, tokens: torch.Tensor, current_pos: torch.Tensor) -> torch.Tensor:
         """One decode step for all max_batch_size rows: tokens [B] at positions current_pos [B] (int32,
         device); returns logits [B, vocab] fp32. The residual stream h is updated in place: each RMSNorm
-        kernel first adds the previous sublayer's output to it."""
+        kernel first adds the previous sublayer's output to it, as the fp32 split partials of its output
+        projection. For up to 64 rows the RMSNorm kernels and the gate / up projection (SwiGLU in its
+        epilogue) write their outputs in the tiled activation layout that the next projections read."""
         eps = self.args.norm_eps
+        B = tokens.shape[0]
+        xt = self._tiled_acts
         h = self.tok_embeddings[tokens]                                  # [B, dim]
-        f = None
+        f = None                                                         # fp32 split partials [ks, B, dim]
         for L in self.layers:
-            y = decoder_ops.rmsnorm(h, L["attn_norm"], eps, res=f, h_out=h)
-            o = L["attn"].forward_decode(y, current_pos)
-            y = decoder_ops.rmsnorm(h, L["ffn_norm"], eps, res=o, h_out=h)
-            f = F.linear(decoder_ops.swiglu(y @ L["w13_t"]), L["w2"])
-        y = decoder_ops.rmsnorm(h, self.norm_w, eps, res=f)
-        return F.linear(y, self.output).float()
+            y = decoder_ops.rmsnorm(h, L["attn_norm"], eps, res_part=f, h_out=h, tiled_out=xt)
+            o = L["attn"].forward_decode(y, current_pos, x_tiled=xt, out_partials=True)
+            y = decoder_ops.rmsnorm(h, L["ffn_norm"], eps, res_part=o, h_out=h, tiled_out=xt)
+            a = L["w13"](y, x_tiled=xt, rows=B)                           # silu(gate) * up
+            at = L["w13"].tiled                                          # a tiled gate / up writes tiled rows
+            if at and not L["w2"].tiled:
+                a, at = decoder_ops.untile_rows(a, B), False
+            f = L["w2"](a, x_tiled=at, rows=B, mode="partials")
+        y = decoder_ops.rmsnorm(h, self.norm_w, eps, res_part=f, tiled_out=xt)
+        return self.output(y, x_tiled=xt, rows=B).float()
 
     @torch.no_grad()
     def decode_graph(self, tokens: torch.Tensor, current_pos: torch.Tensor) -> torch.Tensor:
