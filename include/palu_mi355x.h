@@ -30,6 +30,10 @@ extern "C" {
 
 #define PALU_DTYPE_F32 0
 #define PALU_DTYPE_BF16 1
+/* OR'ed into palu_sdpa_decode's out_dtype (bf16, batch <= 64): the output [batch, n_q * head_dim_v] is
+ * written in the 64-row tiled activation layout that palu_linear_tiled reads with x_tiled = 1 (the next
+ * projection of the decode step) instead of row-major. No counterpart in the reference op. */
+#define PALU_OUT_TILED_ROWS 0x100
 
 /* Cache layouts. ROWS: the reference's logical [B, G, S, width] row-major tensor. The tiled layouts
  * hold the same values with every 32-position block stored as (width / 16) tiles of 1 KB (64 slots of

@@ -287,3 +287,29 @@ def test_qkv_post_equals_rope_and_appends(gpu, layout, gs, r_k, r_v, k_rope):
     else:
         assert torch.equal(kt(keys), kt(keys2))
     assert torch.equal(kt(values), kt(values2))
+
+
+@pytest.mark.parametrize("B,S,r_k,r_v,hpg", [(32, 512, 64, 64, 1), (3, 1024, 96, 32, 1), (16, 256, 128, 256, 4)])
+def test_sdpa_decode_tiled_rows_output(gpu, B, S, r_k, r_v, hpg):
+    """palu_sdpa_decode with tiled_rows writes tile_rows of its row-major output, bit for bit (fixed
+    block order): items in one chunk (B = 32: 256 items), items merged from chunks (B = 3), and the
+    grouped-latent path (u_v, 128-wide output)."""
+    g = torch.Generator().manual_seed(B * 100 + r_k)
+    nh, nkv, hd = 32, 8, 128
+    ng = nkv // hpg
+    q = torch.randn(1, B, nh, hd, generator=g).to(gpu, torch.bfloat16)
+    k = torch.randn(B, ng, S, r_k, generator=g).to(gpu, torch.bfloat16)
+    v = torch.randn(B, ng, S, r_v, generator=g).to(gpu, torch.bfloat16)
+    u_k = (torch.randn(nkv, r_k, hd, generator=g) / r_k ** 0.5).to(torch.bfloat16)
+    u_v = (torch.randn(1, nkv, r_v, hd, generator=g) / r_v ** 0.5).to(gpu, torch.bfloat16) if hpg > 1 else None
+    pos = torch.randint(0, S, (B,), generator=g).to(gpu, torch.int32)
+    cos, sin = fused.cos_sin_tables(hd, S, 500000.0, None)
+    w_rot = fused.w_rot_from_u_k(u_k).to(gpu, torch.bfloat16)[None]
+    cs = fused.cs_table(cos, sin, S)[None, None].to(gpu)
+    kc, vc = LatentCache.from_rows(k, "k"), LatentCache.from_rows(v, "v")
+    width = hd if hpg > 1 else r_v
+    a = fused.palu_sdpa_decode(q, kc, w_rot, cs, vc, width, pos, u_v=u_v, deterministic=True)
+    t = fused.palu_sdpa_decode(q, kc, w_rot, cs, vc, width, pos, u_v=u_v, deterministic=True, tiled_rows=True)
+    torch.cuda.synchronize()
+    assert t.shape == (64, nh * width)
+    assert torch.equal(decoder_ops.untile_rows(t, B), a[0].reshape(B, nh * width))

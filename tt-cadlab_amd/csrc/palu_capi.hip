@@ -210,7 +210,7 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
                const void* trans_mat, const void* u_v, const int32_t* group_ranks, float scale, int heads_per_core,
                int rot_mode, int k_chunk,
                int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_k, int r_v, int w_rot_width, int cs_rows,
-               int cs_cols, int cs_dtype, int out_dtype, int cache_layout, int deterministic, void* workspace,
+               int cs_cols, int cs_dtype, int& out_dtype, int cache_layout, int deterministic, void* workspace,
                size_t workspace_bytes, const char* who) {
   if (!q || !k_latent || !w_rot || !cs_tab || !v_latent || !cur_pos || !out)
     return fail(PALU_EINVAL, "%s: a required tensor pointer is null", who);
@@ -258,7 +258,11 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
       return fail(PALU_EINVAL, "head_dim_v %d must equal the V latent width %d on the absorbed-V path", head_dim_v, r_v);
   }
   if (cs_dtype != PALU_DTYPE_F32 && cs_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "cs_tab dtype must be fp32 or bf16");
+  const int out_tiled = (out_dtype & PALU_OUT_TILED_ROWS) ? 1 : 0;
+  out_dtype &= ~PALU_OUT_TILED_ROWS;
   if (out_dtype != PALU_DTYPE_F32 && out_dtype != PALU_DTYPE_BF16) return fail(PALU_EINVAL, "output dtype must be fp32 or bf16");
+  if (out_tiled && (batch > 64 || out_dtype != PALU_DTYPE_BF16 || ((long long)n_q * head_dim_v) % 32 != 0))
+    return fail(PALU_EINVAL, "a tiled-rows output needs batch <= 64, bf16 and n_q * head_dim_v a multiple of 32");
   if (int rc = check_layout(cache_layout, seq_len, who)) return rc;
   if (!aligned16(q) || !aligned16(k_latent) || !aligned16(v_latent) || !aligned16(w_rot) || !aligned16(cs_tab))
     return fail(PALU_EINVAL, "q, k_latent, v_latent, w_rot and cs_tab must be 16-byte aligned");
@@ -297,6 +301,7 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
   a.ws_bytes = workspace_bytes;
   a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = hpg; a.S = seq_len; a.cs_rows = cs_rows;
   a.deterministic = deterministic ? 1 : 0;
+  a.out_tiled = out_tiled;
   a.qscale = scale * 1.4426950408889634f;
   a.u_v = static_cast<const __bf16*>(u_v);
   a.rk = r_k;
@@ -339,6 +344,7 @@ int flash_setup(DecodeArgs& a, const void* q, const void* k, const void* v, cons
   a.ws = static_cast<float*>(workspace);
   a.ws_bytes = workspace_bytes;
   a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = 1; a.S = seq_len; a.cs_rows = 0;
+  a.out_tiled = 0;
   a.deterministic = deterministic ? 1 : 0;
   a.qscale = scale * 1.4426950408889634f;
   return PALU_OK;

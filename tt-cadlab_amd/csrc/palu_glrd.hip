@@ -582,7 +582,7 @@ __global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, 
 #pragma unroll
         for (int q = 0; q < 16; ++q) sum += red[(q * 4 + i) * HD + d];
         const float Ls = lsum[h];
-        OutT* o = static_cast<OutT*>(a.out) + ((long long)b * a.n_q + (long long)kvh * rep + h) * HD + d;
+        OutT* o = static_cast<OutT*>(a.out) + out_index(a, b, ((long long)kvh * rep + h) * HD + d, (long long)a.n_q * HD);
         store_out(o, Ls > 0.f ? sum / Ls : 0.f);
       }
     }

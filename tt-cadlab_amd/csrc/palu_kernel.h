@@ -85,6 +85,7 @@ struct DecodeArgs {
   int n_wg;               // M-LRD / stock decode: workgroups launched; n_wg > B * n_kv splits items by length
   int balanced;           // 1 when n_wg > B * n_kv (length-aware chunks, merged through ws)
   int deterministic;      // 1: wave w takes blocks w, w + NW, ... (reproducible); 0: blocks from a counter
+  int out_tiled;          // 1: out in the 64-row tiled activation layout of the next projection (B <= 64)
   float qscale;           // softmax scale * log2(e)
   // Paged caches: k/v are page pools [n_pages, G, page_size, width] (rows or tiled) and k_sb / v_sb are
   // page strides; the page of block J of row b is page_table[b * pt_stride + (J >> page_shift)].
@@ -201,6 +202,14 @@ __device__ __forceinline__ float max8(f32x4 a, f32x4 b) {
 
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(__bf16 x) { return (float)x; }
+
+// Element index of output (row b, column col) of [B, row_len]: row-major, or the 64-row tiled activation
+// layout that palu_linear_tiled reads (tile (col / 32, b / 16) of 1 KB, lane 16 ((col % 32) / 8) + b % 16).
+__device__ __forceinline__ long long out_index(const DecodeArgs& a, int b, long long col, long long row_len) {
+  if (a.out_tiled)
+    return ((long long)((col >> 5) * 4 + (b >> 4)) * 64 + 16 * ((col & 31) >> 3) + (b & 15)) * 8 + (col & 7);
+  return (long long)b * row_len + col;
+}
 
 __device__ __forceinline__ void store_out(float* p, float v) { *p = v; }
 __device__ __forceinline__ void store_out(__bf16* p, float v) { *p = (__bf16)v; }
@@ -894,7 +903,7 @@ __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a
       }
     }
     if (n_chunks == 1) {
-      OutT* o = static_cast<OutT*>(a.out) + ((long long)b * a.n_q + (long long)kvh * a.rep + h) * RV + r;
+      OutT* o = static_cast<OutT*>(a.out) + out_index(a, b, ((long long)kvh * a.rep + h) * RV + r, (long long)a.n_q * RV);
       store_out(o, L > 0.f ? acc / L : 0.f);
     } else {
       float* wrow = a.ws + ((long long)blockIdx.x * 16 + h) * (RV + 2);
@@ -929,7 +938,7 @@ __global__ __launch_bounds__(RV) void palu_merge_kernel(const DecodeArgs a) {
       acc += row[r] * f;
     }
   }
-  OutT* o = static_cast<OutT*>(a.out) + ((long long)b * a.n_q + (long long)kvh * a.rep + h) * RV + r;
+  OutT* o = static_cast<OutT*>(a.out) + out_index(a, b, ((long long)kvh * a.rep + h) * RV + r, (long long)a.n_q * RV);
   store_out(o, L > 0.f ? acc / L : 0.f);
 }
 

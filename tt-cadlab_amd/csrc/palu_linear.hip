@@ -24,9 +24,8 @@
 // use the whole 512-entry register file) take the slice's k tiles in turn (wave w: kt0 + w, kt0 + w + 4,
 // ...). Per k tile a wave loads RTW weight tiles (nontemporal: read once per step) and the four 16-row
 // activation tiles (cached), and issues RTW x 4 MFMAs into RTW x 4 accumulators; the loads of the next
-// NB - 1 k tiles are in flight meanwhile. The waves' partial sums meet in LDS (a tree: 4 -> 2 -> 1) and
-// wave 0 stores the result: bf16 y when KS == 1, else fp32 partials [KS][m][n] that
-// palu_linear_reduce_kernel sums.
+// NB - 1 k tiles are in flight meanwhile. The waves' partial sums meet in LDS, and each wave adds up and
+// stores a quarter of the output tiles (bf16 y, fp32 split partials, or the SwiGLU activations).
 //
 // Measured on MI355X (64 rows, weights rotated past the MALL, HIP-graph launches): the tiled activations
 // take the gate/up projection (28672 x 4096) from 51.9 to 43.4 us, against 52.5 us for hipBLASLt; a
@@ -43,7 +42,7 @@ constexpr int LIN_MAX_RTW = 8;
 template <int RTW>
 struct LinSmem {
   static constexpr int SLOT = RTW * LIN_MT * 64;          // f32x4 per wave partial
-  static constexpr int BYTES = (LIN_NW / 2) * SLOT * 16;  // first tree round: NW / 2 slots
+  static constexpr int BYTES = LIN_NW * SLOT * 16;        // every wave's partial
 };
 
 // NB register buffers per wave, so each step's loads are issued NB - 1 steps before its MFMAs. Weight
@@ -126,71 +125,51 @@ __global__ __launch_bounds__(LIN_NW * 64) void palu_linear_kernel(const __bf16* 
     }
   }
 
-  // Tree reduction of the wave partials: slot layout [slot][r][mt][lane] of f32x4.
+  // The waves' partials meet in LDS (slot layout [wave][r][mt][lane] of f32x4); each wave then sums
+  // the four slots of every fourth (r, mt) tile and stores that tile, so the epilogue's arithmetic and
+  // stores are spread over the four SIMDs.
 #pragma unroll
-  for (int half = LIN_NW / 2; half >= 1; half >>= 1) {
-    if (w >= half && w < 2 * half) {
+  for (int r = 0; r < RTW; ++r)
 #pragma unroll
-      for (int r = 0; r < RTW; ++r)
-#pragma unroll
-        for (int mt = 0; mt < LIN_MT; ++mt) red[(w - half) * SM::SLOT + (r * LIN_MT + mt) * 64 + lane] = acc[r][mt];
-    }
-    __syncthreads();
-    if (w < half) {
-#pragma unroll
-      for (int r = 0; r < RTW; ++r)
-#pragma unroll
-        for (int mt = 0; mt < LIN_MT; ++mt) acc[r][mt] += red[w * SM::SLOT + (r * LIN_MT + mt) * 64 + lane];
-    }
-    __syncthreads();
-  }
-  if (w != 0) return;
+    for (int mt = 0; mt < LIN_MT; ++mt) red[w * SM::SLOT + (r * LIN_MT + mt) * 64 + lane] = acc[r][mt];
+  __syncthreads();
 
   // Lane (g, mm) of tile (r, mt) holds y^T[16 (rt0 + r) + 4 g + i][16 mt + mm], i < 4: four consecutive
   // output columns of activation row 16 mt + mm.
-  if constexpr (SWIGLU) {
-    // Gate / up pairs: rows 0-7 of row tile rt are gate columns 8 rt .. 8 rt + 7 and rows 8-15 the up
-    // columns of the same outputs (tile_weight of the interleaved weight), so lane (g, mm) with g < 2
-    // holds gate columns 8 rt + 4 g + i and lane (g + 2, mm), 32 lanes on, the matching up values.
-    // out = silu(gate) * up, stored in the tiled activation layout (64 rows x n / 2) the next
-    // projection reads.
 #pragma unroll
-    for (int mt = 0; mt < LIN_MT; ++mt) {
-      const int row = 16 * mt + mm;
+  for (int t = 0; t < RTW * LIN_MT; ++t) {
+    if (t % LIN_NW != w) continue;                         // uniform per wave
+    const int r = t / LIN_MT, mt = t % LIN_MT;
+    f32x4 v = red[(r * LIN_MT + mt) * 64 + lane];
 #pragma unroll
-      for (int r = 0; r < RTW; ++r) {
-        f32x4 up;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(acc[r][mt][i], 32, 64);
-        if (g >= 2 || row >= m || r >= rt_cnt) continue;
-        const int col = 8 * (rt0 + r) + 4 * g;
-        bf16x4 o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float gv = acc[r][mt][i];
-          o[i] = (__bf16)((gv / (1.f + __expf(-gv))) * up[i]);
-        }
-        const long long off = ((long long)((col >> 5) * 4 + (row >> 4)) * 64 + 16 * ((col & 31) >> 3) + (row & 15)) * 8
-                              + (col & 7);
-        *reinterpret_cast<bf16x4*>(y + off) = o;
-      }
-    }
-    return;
-  }
-#pragma unroll
-  for (int mt = 0; mt < LIN_MT; ++mt) {
+    for (int q = 1; q < LIN_NW; ++q) v += red[q * SM::SLOT + (r * LIN_MT + mt) * 64 + lane];
     const int row = 16 * mt + mm;
-    if (row >= m) continue;
+    if constexpr (SWIGLU) {
+      // Gate / up pairs: rows 0-7 of row tile rt are gate columns 8 rt .. 8 rt + 7 and rows 8-15 the up
+      // columns of the same outputs (tile_weight of the interleaved weight), so lane (g, mm) with g < 2
+      // holds gate columns 8 rt + 4 g + i and lane (g + 2, mm), 32 lanes on, the matching up values.
+      // out = silu(gate) * up, stored in the tiled activation layout (64 rows x n / 2) the next
+      // projection reads.
+      f32x4 up;
 #pragma unroll
-    for (int r = 0; r < RTW; ++r) {
-      if (r >= rt_cnt) continue;
+      for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(v[i], 32, 64);
+      if (g >= 2 || row >= m || r >= rt_cnt) continue;
+      const int col = 8 * (rt0 + r) + 4 * g;
+      bf16x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = (__bf16)((v[i] / (1.f + __expf(-v[i]))) * up[i]);
+      const long long off = ((long long)((col >> 5) * 4 + (row >> 4)) * 64 + 16 * ((col & 31) >> 3) + (row & 15)) * 8
+                            + (col & 7);
+      *reinterpret_cast<bf16x4*>(y + off) = o;
+    } else {
+      if (row >= m || r >= rt_cnt) continue;
       const long long col = 16LL * (rt0 + r) + 4 * g;
       if (part) {
-        *reinterpret_cast<f32x4*>(part + ((long long)ks * m + row) * (16LL * n16) + col) = acc[r][mt];
+        *reinterpret_cast<f32x4*>(part + ((long long)ks * m + row) * (16LL * n16) + col) = v;
       } else {
         bf16x4 o;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = (__bf16)acc[r][mt][i];
+        for (int i = 0; i < 4; ++i) o[i] = (__bf16)v[i];
         *reinterpret_cast<bf16x4*>(y + row * ldy + col) = o;
       }
     }

@@ -14,6 +14,7 @@ from palu_tt._build import library_path
 
 PALU_OK, PALU_EINVAL, PALU_EUNSUPPORTED, PALU_EHIP = 0, 1, 2, 3
 DTYPE_F32, DTYPE_BF16 = 0, 1
+OUT_TILED_ROWS = 0x100      # PALU_OUT_TILED_ROWS, OR'ed into palu_sdpa_decode's out_dtype
 ABI_VERSION = 10
 LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_TILED_V = 0, 1, 2
 

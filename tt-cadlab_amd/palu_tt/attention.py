@@ -178,22 +178,27 @@ class PaluAttention(torch.nn.Module):
                 k_rot = decoder_ops.rope_rows(kcols, nkv, pos, self.cos, self.sin)
                 decoder_ops.append_from(keys, k_rot.view(B, nkv * hd), hd, hd, pos)
             decoder_ops.append_from(values, vcols, self.gs * hd, self.r_v, pos)
-        attn = self.decode_core(q[None], keys, values, pos)                  # [1, B, nh, out_width]
-        a2 = attn[0].reshape(B, nh * self.out_width)
+        # the fused op writes its output straight in the tiled activation layout the output projection reads
+        tiled_attn = self.wo_out.tiled and self.use_fused_k and B <= 64
+        attn = self.decode_core(q[None], keys, values, pos, tiled_rows=tiled_attn)
+        tiled_attn = attn.dim() == 2                                          # a core may answer row-major
+        a2 = attn if tiled_attn else attn[0].reshape(B, nh * self.out_width)   # [64 | B, nh * out_width]
         if out_partials:
-            return self.wo_out(a2, mode="partials")
-        return self.wo_out(a2).reshape(*shape[:-1], self.hidden_size)
+            return self.wo_out(a2, x_tiled=tiled_attn, rows=B, mode="partials")
+        return self.wo_out(a2, x_tiled=tiled_attn, rows=B).reshape(*shape[:-1], self.hidden_size)
 
-    def decode_core(self, q4, keys, values, pos):
+    def decode_core(self, q4, keys, values, pos, tiled_rows=False):
         """The attention core of a decode step over the caches (new rows already appended): q4 [1, B, nh, hd]
         rotated at pos -> [1, B, nh, out_width] bf16. Fused latent op, naive path, or stock decode over the
-        cached rotated K, as the layer is configured."""
+        cached rotated K, as the layer is configured. With tiled_rows the fused op answers in the tiled
+        activation layout, [64, nh * out_width]; the other cores answer row-major regardless."""
         if self.use_fused_k:
             grouped = self.gs > 1
             return fused.palu_sdpa_decode(q4, keys, self.w_rot, self.cs_tab, values,
                                           self.head_dim if grouped else self.r_v, pos,
                                           u_v=self.u_v[None] if grouped else None, scale=self.scale,
-                                          out_dtype=torch.bfloat16, group_ranks=self.group_ranks)
+                                          out_dtype=torch.bfloat16, group_ranks=self.group_ranks,
+                                          tiled_rows=tiled_rows)
         if self.recon_k:
             return self._naive_attention(q4, keys, values, pos)
         return fused.flash_multi_latent_attention_decode(q4, keys, values, self.r_v, pos, scale=self.scale)

@@ -62,8 +62,9 @@ def fused_vs_naive(model: "pm.Transformer", prompts: torch.Tensor, teacher: torc
     out = {"steps": T, "rows": B, **_compare(naive, fused_l)}
     if reference_core is not None:
         layers = [L["attn"] for L in model.layers]
-        for att in layers:
-            att.decode_core = types.MethodType(reference_core, att)
+        for att in layers:   # the reference core answers row-major whatever layout the layer asks for
+            att.decode_core = types.MethodType(
+                lambda self, q4, keys, values, pos, tiled_rows=False: reference_core(self, q4, keys, values, pos), att)
         try:
             ref = decode_pass(False, False)
         finally:

@@ -240,8 +240,11 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
                      trans_mat=None, u_v=None, scale=None, heads_per_core=None, rot_mode="dst", table_mcast=True,
                      program_config=None, compute_kernel_config=None, memory_config=None,
                      out_dtype=torch.bfloat16, out=None, workspace=None, deterministic=False,
-                     page_table_tensor=None, noalloc=False, group_ranks=None) -> torch.Tensor:
-    """Fused latent flash-decode (ttnn.transformer.palu_sdpa_decode). Returns [1, B, n_q, head_dim_v].
+                     page_table_tensor=None, noalloc=False, group_ranks=None, tiled_rows=False) -> torch.Tensor:
+    """Fused latent flash-decode (ttnn.transformer.palu_sdpa_decode). Returns [1, B, n_q, head_dim_v], or
+    with tiled_rows (bf16, B <= 64; no counterpart in the reference op) a [64, n_q * head_dim_v] buffer in
+    the tiled activation layout that the decode step's output projection reads
+    (decoder_ops.linear_tiled(..., x_tiled=True)).
 
     For every p <= cur_pos[b]: K[p] = RoPE_p(k_latent[p] @ u_k) with u_k = w_rot[..., :128], then
     softmax(q K^T * scale) over the attended rows of v_latent (absorbed V). Query head h reads KV head
@@ -301,7 +304,15 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
     tm = None if trans_mat is None else _as_dev(trans_mat.contiguous(), "trans_mat", None, dev)
     uv = None if u_v is None else _as_dev(u_v.reshape(-1, *u_v.shape[-2:]).contiguous(), "u_v", torch.bfloat16, dev)
     width = int(head_dim_v)
-    if out is None:
+    od = _DTYPES[out_dtype]
+    if tiled_rows:
+        _require(out_dtype == torch.bfloat16 and B <= 64, "a tiled-rows output is bf16 for at most 64 rows")
+        od |= _native.OUT_TILED_ROWS
+        if out is None:
+            out = torch.empty(64, n_q * width, dtype=out_dtype, device=dev)
+        _as_dev(out, "out", out_dtype, dev)
+        _require(tuple(out.shape) == (64, n_q * width) and out.is_contiguous(), f"out must be [64, {n_q * width}]")
+    elif out is None:
         out = torch.empty(1, B, n_q, width, dtype=out_dtype, device=dev)
     else:
         _as_dev(out, "out", out_dtype, dev)
@@ -321,7 +332,7 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
             _native.ptr(q), _native.ptr(k_store), _native.ptr(w), _native.ptr(cs), _native.ptr(v_store), width,
             _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv), gr, sc,
             int(heads_per_core or 0), rot, int(bool(table_mcast)), _k_chunk(program_config), B, n_q, n_kv, n_groups,
-            S, r_k, r_v, w_width, cs.shape[0], cs.shape[1], _DTYPES[cs.dtype], _DTYPES[out_dtype], layout,
+            S, r_k, r_v, w_width, cs.shape[0], cs.shape[1], _DTYPES[cs.dtype], od, layout,
             int(bool(deterministic)), _native.stream_handle(dev)))
         return out
     if uv is not None and pt is None:
@@ -333,7 +344,7 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
             _native.ptr(q), _native.ptr(k_store), _native.ptr(w), _native.ptr(cs), _native.ptr(v_store), width,
             _native.ptr(cp), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv), gr, sc,
             int(heads_per_core or 0), rot, int(bool(table_mcast)), _k_chunk(program_config), B, n_q, n_kv, n_groups,
-            S, r_k, r_v, w_width, cs.shape[0], cs.shape[1], _DTYPES[cs.dtype], _DTYPES[out_dtype], layout,
+            S, r_k, r_v, w_width, cs.shape[0], cs.shape[1], _DTYPES[cs.dtype], od, layout,
             int(bool(deterministic)), _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
     else:
         _native.check(lib.palu_sdpa_decode_paged(
@@ -341,7 +352,7 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
             _native.ptr(cp), _native.ptr(pt), _native.ptr(out), _native.ptr(rs), _native.ptr(tm), _native.ptr(uv), sc,
             int(heads_per_core or 0), rot, int(bool(table_mcast)), _k_chunk(program_config), B, n_q, n_kv, n_groups,
             n_pages, page_size, pt.shape[1], r_k, r_v, w_width, cs.shape[0], cs.shape[1], _DTYPES[cs.dtype],
-            _DTYPES[out_dtype], layout, int(bool(deterministic)), _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
+            od, layout, int(bool(deterministic)), _native.ptr(ws), ws_bytes, _native.stream_handle(dev)))
     return out
 
 
