@@ -6,10 +6,11 @@ Same construction inputs and state-dict keys as the reference (``layers.{i}.atte
 same cache contents (latent rows of width r_k / r_v per head or per group, or rotated full K on the
 K-fast path), and the same decode data flow (attention.py:585-733):
 
-  decode:  x @ [wq | wk_lat_pad | wv_lat_pad]^T -> q, latent slots (one GEMM)
-           RoPE on q at current_pos (Meta-interleaved), read straight from the GEMM output
-           latents (a head's first r columns, or a group's head slots concatenated) appended at
-           current_pos from the GEMM output's latent columns (the strided latent-append kernel)
+  decode:  x @ [wq | wk_lat | wv_lat]^T -> q, latents (one GEMM; wk_lat / wv_lat are the latent rows of
+           the converter's wk_lat_pad / wv_lat_pad, a head's first r rows or a group's, without the
+           zero padding to head_dim)
+           RoPE on q at current_pos (Meta-interleaved) and the latents appended at current_pos, both
+           straight from the GEMM output (one fused launch over the projection's split partials)
            with PaluRuntime.use_fused_k: fused latent flash-decode (palu_sdpa_decode; u_v rebuilds V
            per head for grouped latents);
            without it (the reference's default, attention.py:657-710): the naive path, which rebuilds
@@ -81,10 +82,14 @@ class PaluAttention(torch.nn.Module):
         P = f"{ln}.palu"
         dev, bf = self.device, torch.bfloat16
         wq = state_dict[f"{ln}.wq.weight"]
-        wk = state_dict[f"{P}.wk_lat_pad"]
-        wv = state_dict[f"{P}.wv_lat_pad"]
-        # [(nh + 2 nkv) hd, dim]: held in the decode projection's tiled order (decoder_ops.DecodeLinear);
-        # the prefill multiplies by its nn.Linear-layout copy
+        # the latent rows of wk_lat_pad / wv_lat_pad: group g's rows g * gs * hd .. + width (a head's
+        # first r rows for group size 1, the whole head on the full-rank paths); the rest is zero padding
+        self.k_width = self.r_k if self.recon_k else hd
+        gw = lambda w, width: w.reshape(self.n_groups, self.gs * hd, -1)[:, :width].reshape(-1, w.shape[-1])
+        wk = gw(state_dict[f"{P}.wk_lat_pad"], self.k_width)
+        wv = gw(state_dict[f"{P}.wv_lat_pad"], self.r_v)
+        # [nh hd + n_groups (k_width + r_v), dim]: held in the decode projection's tiled order
+        # (decoder_ops.DecodeLinear); the prefill multiplies by its nn.Linear-layout copy
         self.wqkv = decoder_ops.DecodeLinear(torch.cat([wq, wk, wv], dim=0).to(dev, bf).contiguous(),
                                              self.max_batch_size)
         self.wo = state_dict[f"{ln}.wo.weight"].to(dev, bf).contiguous()
@@ -123,17 +128,14 @@ class PaluAttention(torch.nn.Module):
         return self.n_groups * (k_width + self.r_v) * 2.0
 
     def _split(self, xqkv):
-        nh, nkv, hd = self.n_heads, self.n_kv_heads, self.head_dim
-        q = xqkv[..., :nh * hd].unflatten(-1, (nh, hd))
-        k = xqkv[..., nh * hd:(nh + nkv) * hd].unflatten(-1, (nkv, hd))
-        v = xqkv[..., (nh + nkv) * hd:].unflatten(-1, (nkv, hd))
+        """[..., nh hd + G (k_width + r_v)] projection output -> q [..., nh, hd], K latents [..., G, k_width]
+        (the rotated-later full K heads on the full-rank path), V latents [..., G, r_v]."""
+        nh, hd, G = self.n_heads, self.head_dim, self.n_groups
+        k0, v0 = nh * hd, nh * hd + G * self.k_width
+        q = xqkv[..., :k0].unflatten(-1, (nh, hd))
+        k = xqkv[..., k0:v0].unflatten(-1, (G, self.k_width))
+        v = xqkv[..., v0:].unflatten(-1, (G, self.r_v))
         return q, k, v
-
-    def _group_latent(self, slots, r):
-        """[..., nkv, hd] head slots -> [..., n_groups, r]: a head's first r columns (group size 1), or a
-        group's head slots concatenated (reference attention.py:545-565)."""
-        g = slots.unflatten(-2, (self.n_groups, self.gs)).flatten(-2)     # [..., n_groups, gs * hd]
-        return g[..., :r]
 
     def _rope(self, x, pos):
         """Meta-interleaved RoPE of x [..., heads, hd] at positions pos (broadcast over heads)."""
@@ -163,21 +165,22 @@ class PaluAttention(torch.nn.Module):
         assert pos.numel() == B
         nh, nkv, hd = self.n_heads, self.n_kv_heads, self.head_dim
         keys, values = self.layer_past
-        k_width = self.r_k if self.recon_k else hd
+        kw, G = self.k_width, self.n_groups
+        k0, v0 = nh * hd, nh * hd + G * kw                                  # column offsets of K and V latents
         if self.wqkv.tiled:
-            part = self.wqkv(x2, x_tiled=x_tiled, rows=B, mode="partials")  # [ks, B, (nh + 2 nkv) hd] fp32
-            q = decoder_ops.qkv_post(part, pos, self.cos, self.sin, nh, keys, nh * hd, self.gs * hd, k_width,
-                                     values, (nh + nkv) * hd, self.gs * hd, self.r_v, k_rope=not self.recon_k)
+            part = self.wqkv(x2, x_tiled=x_tiled, rows=B, mode="partials")  # [ks, B, nh hd + G (kw + r_v)] fp32
+            q = decoder_ops.qkv_post(part, pos, self.cos, self.sin, nh, keys, k0, kw, kw, values, v0, self.r_v,
+                                     self.r_v, k_rope=not self.recon_k)
         else:
-            xqkv = self.wqkv(x2)                                            # [B, (nh + 2 nkv) hd]
+            xqkv = self.wqkv(x2)                                            # [B, nh hd + G (kw + r_v)]
             q = decoder_ops.rope_rows(xqkv, nh, pos, self.cos, self.sin)     # [B, nh, hd]
-            kcols, vcols = xqkv[:, nh * hd:], xqkv[:, (nh + nkv) * hd:]
+            kcols, vcols = xqkv[:, k0:], xqkv[:, v0:]
             if self.recon_k:
-                decoder_ops.append_from(keys, kcols, self.gs * hd, self.r_k, pos)
+                decoder_ops.append_from(keys, kcols, kw, kw, pos)
             else:                                                            # stock K path: rotated full K
                 k_rot = decoder_ops.rope_rows(kcols, nkv, pos, self.cos, self.sin)
                 decoder_ops.append_from(keys, k_rot.view(B, nkv * hd), hd, hd, pos)
-            decoder_ops.append_from(values, vcols, self.gs * hd, self.r_v, pos)
+            decoder_ops.append_from(values, vcols, self.r_v, self.r_v, pos)
         # the fused op writes its output straight in the tiled activation layout the output projection reads
         tiled_attn = self.wo_out.tiled and self.use_fused_k and B <= 64
         attn = self.decode_core(q[None], keys, values, pos, tiled_rows=tiled_attn)
@@ -258,13 +261,11 @@ class PaluAttention(torch.nn.Module):
 
     def _prefill_one(self, x2, user):
         S = x2.shape[0]
-        q_pre, k_slots, v_slots = self._split(F.linear(x2, self.wqkv.plain()))   # [S, nh | nkv, hd]
+        q_pre, k_lat, v_lat = self._split(F.linear(x2, self.wqkv.plain()))   # [S, nh, hd], [S, G, kw], [S, G, r_v]
         pos = torch.arange(S, device=self.device)
-        k_lat = self._group_latent(k_slots, self.r_k) if self.recon_k else None    # [S, n_groups, r_k]
-        v_lat = self._group_latent(v_slots, self.r_v)
         rep_g = lambda t: t.repeat_interleave(self.gs, dim=1)                       # group latent per head
-        K = torch.einsum("sgr,grd->sgd", rep_g(k_lat).float(), self.u_k.float()) if self.recon_k else k_slots.float()
-        V = torch.einsum("sgr,grd->sgd", rep_g(v_lat).float(), self.u_v.float()) if self.recon_v else v_slots.float()
+        K = torch.einsum("sgr,grd->sgd", rep_g(k_lat).float(), self.u_k.float()) if self.recon_k else k_lat.float()
+        V = torch.einsum("sgr,grd->sgd", rep_g(v_lat).float(), self.u_v.float()) if self.recon_v else v_lat.float()
         q = self._rope(q_pre.float(), pos)
         K = self._rope(K, pos)
         keys, values = self.layer_past
