@@ -345,3 +345,47 @@ def test_stock_tiled_is_bit_identical_to_rows(gpu, B, S, dv):
                            out_dtype=torch.float32, deterministic=True)
     torch.cuda.synchronize()
     assert torch.equal(a.cpu(), b.cpu())
+
+
+@pytest.mark.parametrize("B,S,r_k,r_v", [(4, 1024, 64, 48), (32, 256, 32, 80), (3, 640, 128, 112), (1, 4096, 96, 48)])
+def test_tiled_v_widths_in_16s(gpu, B, S, r_k, r_v):
+    """Tiled V caches also take V latent widths that are multiples of 16 (V tiles are 16 wide): the fused
+    op with one item per workgroup (B = 32) and with merged chunks, and the append in V-tile order."""
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(B, S, r_k, r_v)
+    w_rot = ref.w_rot_from_u_k(u_k)[None].to(gpu, torch.bfloat16)
+    cs = ref.cs_table(cos, sin, S)[None, None].to(gpu)
+    kc = LatentCache.from_rows(k_lat.to(gpu, torch.bfloat16), "k")
+    vc = LatentCache.from_rows(v.to(gpu, torch.bfloat16), "v")
+    new_v = _bf(torch.randn(1, B, 8, r_v))
+    dpos = pos.to(gpu, torch.int32)
+    fused.paged_update_cache(vc, new_v.to(gpu, torch.bfloat16), dpos)
+    v_full = v.clone()
+    for b in range(B):
+        v_full[b, :, pos[b]] = new_v[0, b]
+    out = fused.palu_sdpa_decode(q.to(gpu, torch.bfloat16), kc, w_rot, cs, vc, r_v, dpos, scale=HD ** -0.5,
+                                 out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(vc.to_rows().float().cpu(), v_full)
+    _check(out.cpu(), ref.reference_decode(q, k_lat, u_k, v_full, pos, cos, sin, HD ** -0.5))
+
+
+@pytest.mark.parametrize("dv", [48, 80, 112])
+def test_stock_flash_decode_tiled_v_widths_in_16s(gpu, dv):
+    """The stock flash-decode (the naive path's core) over full K and a tiled V of width 48 / 80 / 112."""
+    B, S = 5, 512
+    g = torch.Generator().manual_seed(dv)
+    q = _bf(torch.randn(1, B, 32, HD, generator=g))
+    k = _bf(torch.randn(B, 8, S, HD, generator=g))
+    v = _bf(torch.randn(B, 8, S, dv, generator=g))
+    pos = torch.randint(0, S, (B,), generator=g)
+    out = fused.flash_decode(q.to(gpu, torch.bfloat16), LatentCache.from_rows(k.to(gpu, torch.bfloat16), "k"),
+                             LatentCache.from_rows(v.to(gpu, torch.bfloat16), "v"), pos.to(gpu, torch.int32),
+                             scale=HD ** -0.5, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _check(out.cpu(), ref.full_kv_decode(q, k, v, pos, HD ** -0.5))
+
+
+def test_row_major_v_width_in_16s_is_refused(gpu):
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(2, 256, 64, 48)
+    with pytest.raises(RuntimeError, match="r_v must be a multiple of 32"):
+        _run_fused(gpu, q, k_lat, u_k, v, pos, cos, sin, 256)

@@ -6,7 +6,8 @@ torch over the same latent caches (K = latent @ u_k, Meta RoPE, masked softmax, 
 
 The full-size case is the end-to-end configuration: 32 Llama-3.1-8B-shaped layers (vocab 128256, FFN
 14336 SwiGLU), per-layer M-LRD ranks drawn from [32, 128] in steps of 8 with mean 64 (the benchmark's
-seeds), batch 64, random 2048-token prompts, 16 teacher-forced decode steps. This random-init model
+seeds; V ranks padded to 16 as the benchmark pads them), batch 64, random 2048-token prompts, 16
+teacher-forced decode steps. This random-init model
 amplifies bf16-level differences in any one attention core: two fused runs that differ only in which
 wave sums which 32-position block (bf16 rounding of the probabilities) already agree to a logit PCC of
 only about 0.9985. So the bars are: fused vs naive PCC >= 0.995 on every row at every step (the
@@ -48,7 +49,8 @@ def fp32_attention_core(layer, q4, keys, values, pos):
 def test_fused_matches_naive_on_the_end_to_end_decoder(gpu):
     B, P, T, L = 64, 2048, 16, 32
     args = pm.ModelArgs(n_layers=L, max_batch_size=B, max_seq_len=P + 32)
-    sd = pm.random_palu_state_dict(args, pm.draw_ranks(L, seed=1), pm.draw_ranks(L, seed=2), gpu, seed=0)
+    sd = pm.random_palu_state_dict(args, pm.draw_ranks(L, seed=1), pm.draw_ranks(L, seed=2), gpu, seed=0,
+                                   rank_multiple_v=16)
     model = pm.Transformer(args, sd, gpu)
     del sd
     g = torch.Generator().manual_seed(7)

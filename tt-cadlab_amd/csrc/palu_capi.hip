@@ -123,8 +123,10 @@ int check_append(void* cache, const void* new_rows, const int32_t* update_idxs, 
   if (batch <= 0 || n_groups <= 0 || S <= 0 || width <= 0 || width % 8 != 0)
     return fail(PALU_EINVAL, "%s: width must be a positive multiple of 8, got %d", who, width);
   if (int rc = check_layout(layout == PALU_LAYOUT_TILED_V ? PALU_LAYOUT_TILED : layout, S, who)) return rc;
-  if (layout != PALU_LAYOUT_ROWS && width % 32 != 0)
-    return fail(PALU_EINVAL, "%s: a tiled cache row is a multiple of 32 wide, got %d", who, width);
+  if (layout == PALU_LAYOUT_TILED && width % 32 != 0)
+    return fail(PALU_EINVAL, "%s: a tiled K cache row is a multiple of 32 wide, got %d", who, width);
+  if (layout == PALU_LAYOUT_TILED_V && width % 16 != 0)
+    return fail(PALU_EINVAL, "%s: a tiled V cache row is a multiple of 16 wide, got %d", who, width);
   if (!aligned16(cache) || !aligned16(new_rows)) return fail(PALU_EINVAL, "%s: 16-byte alignment required", who);
   return PALU_OK;
 }
@@ -225,8 +227,12 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
     return fail(PALU_EINVAL, "%s: batch, head counts and seq_len must be positive", who);
   if (r_k <= 0 || r_k % 32 != 0 || r_k > 512)
     return fail(PALU_EINVAL, "r_k must be a multiple of 32 in 32..512 (the latent width of k_latent), got %d", r_k);
-  if (r_v <= 0 || r_v % 32 != 0 || r_v > 512)
-    return fail(PALU_EINVAL, "r_v must be a multiple of 32 in 32..512 (the latent width of v_latent), got %d", r_v);
+  // V latents are 16-wide tiles in the tiled layout: per-head (absorbed-V) tiled caches also take widths
+  // that are multiples of 16; row-major caches and grouped latents (u_v) keep multiples of 32
+  const int rv_step = (cache_layout == PALU_LAYOUT_TILED && u_v == nullptr) ? 16 : 32;
+  if (r_v <= 0 || r_v % rv_step != 0 || r_v > 512)
+    return fail(PALU_EINVAL, "r_v must be a multiple of %d in %d..512 (the latent width of v_latent), got %d", rv_step,
+                rv_step, r_v);
   if (n_kv % n_groups != 0)
     return fail(PALU_EINVAL, "heads_per_group: %d latent heads do not divide the %d KV heads of w_rot", n_groups, n_kv);
   const int hpg = n_kv / n_groups;

@@ -1,5 +1,5 @@
 // Stock flash-decode kernels over full, already-rotated K (the non-fused decode path and the full-KV
-// comparator): every V width, both cache layouts, contiguous or paged, fp32 or bf16 output.
+// comparator): every V width (multiples of 32; of 16 for tiled caches), both cache layouts, contiguous or paged, fp32 or bf16 output.
 #include "palu_kernel.h"
 
 namespace {
@@ -13,7 +13,15 @@ int dispatch_full_dv(const palu::DecodeArgs& a, int dv, bool f32o, hipStream_t s
     case 96: return f32o ? launch<HD, 96, true, TILED, PAGED, float, float>(a, s) : launch<HD, 96, true, TILED, PAGED, float, B16>(a, s);
     case 128: return f32o ? launch<HD, 128, true, TILED, PAGED, float, float>(a, s) : launch<HD, 128, true, TILED, PAGED, float, B16>(a, s);
   }
-  return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128", dv);
+  if constexpr (TILED) {   // 16-wide V tiles: the widths in between as well
+    switch (dv) {
+      case 48: return f32o ? launch<HD, 48, true, TILED, PAGED, float, float>(a, s) : launch<HD, 48, true, TILED, PAGED, float, B16>(a, s);
+      case 80: return f32o ? launch<HD, 80, true, TILED, PAGED, float, float>(a, s) : launch<HD, 80, true, TILED, PAGED, float, B16>(a, s);
+      case 112: return f32o ? launch<HD, 112, true, TILED, PAGED, float, float>(a, s) : launch<HD, 112, true, TILED, PAGED, float, B16>(a, s);
+    }
+  }
+  return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128 (and 48, 80, 112 for "
+                                 "tiled caches)", dv);
 }
 
 }  // namespace

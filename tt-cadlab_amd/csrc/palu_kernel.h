@@ -333,7 +333,7 @@ __device__ __forceinline__ float4 load4f<__bf16>(const __bf16* p) {
 template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, int NW, typename TabT, typename OutT>
 __global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a) {
   static_assert(RK % 32 == 0 && RK <= 128, "RK");
-  static_assert(RV % 32 == 0 && RV <= 128, "RV");
+  static_assert(RV % 16 == 0 && RV <= 128 && (TILED || RV % 32 == 0), "RV: 16-wide V tiles (tiled), 32-wide rows");
   static_assert(!KFULL || RK == HD, "full K has the head dim");
   constexpr int KB = RK / 32;   // 32-wide contraction blocks of the K operand
   constexpr int VB = RV / 32;   // 32-wide blocks of a V row
@@ -986,7 +986,16 @@ int dispatch_rv(const DecodeArgs& a, int rv, hipStream_t s) {
     case 96: return launch<RK, 96, KFULL, TILED, PAGED, TabT, OutT>(a, s);
     case 128: return launch<RK, 128, KFULL, TILED, PAGED, TabT, OutT>(a, s);
   }
-  return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128", rv);
+  // V tiles are 16 wide, so tiled V caches also take the widths in between (row-major ones do not)
+  if constexpr (TILED) {
+    switch (rv) {
+      case 48: return launch<RK, 48, KFULL, TILED, PAGED, TabT, OutT>(a, s);
+      case 80: return launch<RK, 80, KFULL, TILED, PAGED, TabT, OutT>(a, s);
+      case 112: return launch<RK, 112, KFULL, TILED, PAGED, TabT, OutT>(a, s);
+    }
+  }
+  return fail(PALU_EUNSUPPORTED, "head_dim_v %d: this build supports V widths 32, 64, 96, 128 (and 48, 80, 112 for "
+                                 "tiled caches)", rv);
 }
 
 template <bool TILED, bool PAGED, typename TabT, typename OutT>

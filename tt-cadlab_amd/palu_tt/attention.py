@@ -64,7 +64,10 @@ class PaluAttention(torch.nn.Module):
         self.r_k = int(self.palu.rank_k[layer_num])
         self.r_v = int(self.palu.rank_v[layer_num])
         hd = self.head_dim
-        assert self.r_k % 32 == 0 and self.r_v % 32 == 0 and self.r_k <= self.gs * hd and self.r_v <= self.gs * hd
+        # V latents are 16-wide tiles in a tiled cache (per-head latents); everything else is in 32s
+        v_step = 16 if (cache_layout == "tiled" and self.gs == 1) else 32
+        assert self.r_k % 32 == 0 and self.r_v % v_step == 0 and self.r_k <= self.gs * hd and self.r_v <= self.gs * hd, \
+            f"ranks r_k = {self.r_k} (a multiple of 32), r_v = {self.r_v} (a multiple of {v_step})"
         # full-rank per-head factors collapse to stock K / V (reference attention.py:136-141)
         self.recon_k = self.gs > 1 or self.r_k < hd
         self.recon_v = self.gs > 1 or self.r_v < hd
@@ -243,7 +246,9 @@ class PaluAttention(torch.nn.Module):
             v = torch.matmul(per_head(v_lat).contiguous(), self.u_v.contiguous())          # [B, nkv, S, hd]
         else:
             v = v_lat.contiguous()                                                         # absorbed V: [B, nkv, S, r_v]
-        return fused.flash_multi_latent_attention_decode(q4, k_rot, v, v.shape[-1], pos, scale=self.scale)
+        if v.shape[-1] % 32:   # V widths in 16s exist only as tiled caches (16-wide V tiles): hand both over tiled
+            k_rot, v = LatentCache.from_rows(k_rot, "k"), LatentCache.from_rows(v, "v")
+        return fused.flash_multi_latent_attention_decode(q4, k_rot, v, self.out_width, pos, scale=self.scale)
 
     def forward_prefill(self, x, rot_mats=None, user_id=0, page_table=None, chunk_page_table=None,
                         chunk_start_idx=None, kv_cache=None):

@@ -30,7 +30,8 @@ def rows_to_tiled(rows: torch.Tensor, role: str = "k") -> torch.Tensor:
     """[B, G, S, r] -> tiled storage [B, G, S/32, r/16, 64, 8] in the role's tile order."""
     B, G, S, r = rows.shape
     assert role in ROLES, f"role must be 'k' or 'v', got {role!r}"
-    assert S % BLOCK == 0 and r % 32 == 0, f"tiled layout needs S % 32 == 0 and r % 32 == 0, got S={S}, r={r}"
+    step = 32 if role == "k" else 16            # K tiles pair 32-wide rank blocks; V tiles are 16 wide
+    assert S % BLOCK == 0 and r % step == 0, f"tiled {role} layout needs S % 32 == 0 and r % {step} == 0, got S={S}, r={r}"
     if role == "k":
         # position 32*blk + 8*tb + 4*c + i, r-index 32*kb + 8*g + j  ->  [blk][c][kb][g][tb][i][j]
         x = rows.reshape(B, G, S // BLOCK, 4, 2, 4, r // 32, 4, 8).permute(0, 1, 2, 4, 6, 7, 3, 5, 8)
@@ -66,7 +67,8 @@ class LatentCache:
     def zeros(batch: int, n_groups: int, max_seq: int, width: int, device, role: str = "k",
               dtype=torch.bfloat16) -> "LatentCache":
         assert max_seq % BLOCK == 0, f"max_seq must be a multiple of {BLOCK}, got {max_seq}"
-        assert width % 32 == 0, f"width must be a multiple of 32, got {width}"
+        step = 32 if role == "k" else 16
+        assert width % step == 0, f"a tiled {role} cache's width must be a multiple of {step}, got {width}"
         return LatentCache(torch.zeros(batch, n_groups, max_seq // BLOCK, width // 16, 64, 8, dtype=dtype,
                                        device=device), role)
 

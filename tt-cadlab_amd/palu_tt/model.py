@@ -6,14 +6,14 @@ Weights follow the tt_transformers state-dict names the reference loads (tok_emb
 attention_norm / attention.wq|wk|wv|wo / ffn_norm / feed_forward.w1|w2|w3, norm, output) plus the
 converter's layers.{i}.attention.palu.*. ``random_palu_state_dict`` builds a random-init model with
 per-layer M-LRD ranks (per-head SVD of random k/v projections, ranks padded up to a multiple of 32 as
-convert.load_palu_dir does), which is what the end-to-end benchmark uses.
+convert.load_palu_dir does, or V ranks to a multiple of 16 for tiled caches), which is what the
+end-to-end benchmark uses.
 
-Decode runs every layer's projections as plain GEMMs (hipBLASLt through torch; the gate/up weight
-input-major, the others in the nn.Linear layout, whichever streams faster at M = batch), the attention
-core and
-the elementwise work around it (RMSNorm with the residual add, RoPE, latent append, SwiGLU) through the
-HIP library; ``Transformer.decode_graph`` captures a whole decode step in a HIP graph so a step is one
-graph launch.
+Decode runs every projection on the library's M <= 64 projection kernel over weights held tiled
+(decoder_ops.DecodeLinear), and the attention core and the elementwise work around it (RMSNorm with the
+residual add, RoPE and the latent appends fused into one QKV epilogue, SwiGLU in the gate/up epilogue)
+through the HIP library; ``Transformer.decode_graph`` captures a whole decode step in a HIP graph so a
+step is one graph launch.
 """
 import math
 from dataclasses import dataclass, field
@@ -164,10 +164,11 @@ def draw_ranks(n_layers: int, seed: int, lo: int = 32, hi: int = 128, step: int 
 
 def random_palu_state_dict(args: ModelArgs, ranks_k: List[int], ranks_v: List[int], device, seed: int = 0,
                            std: float = 0.02, rank_multiple: int = 32, dense_out: Optional[list] = None,
-                           use_fused_k: bool = True) -> dict:
+                           use_fused_k: bool = True, rank_multiple_v: Optional[int] = None) -> dict:
     """Random-init weights N(0, std) generated on `device`, and per-layer per-head SVD factors of the
     k / v projections at the given ranks (on `device` too), zero-padded to a multiple of rank_multiple
-    (convert.load_palu_dir's padding). Every tensor is left in bf16 on `device`. Sets args.palu, whose
+    (convert.load_palu_dir's padding; V ranks to a multiple of rank_multiple_v when given: 16 suits tiled
+    caches, whose V tiles are 16 wide). Every tensor is left in bf16 on `device`. Sets args.palu, whose
     runtime takes the fused latent decode unless use_fused_k is False. With dense_out, every layer's fp32
     projections (HF head order) and padded factors are appended to it as (W, LowRank) on the host."""
     g = torch.Generator(device=device).manual_seed(seed)
@@ -176,14 +177,14 @@ def random_palu_state_dict(args: ModelArgs, ranks_k: List[int], ranks_v: List[in
     hd, nh, nkv, dim = args.head_dim, args.n_heads, args.n_kv_heads, args.dim
     sd = {"tok_embeddings.weight": randn(args.vocab_size, dim).to(bf), "output.weight": randn(args.vocab_size, dim).to(bf),
           "norm.weight": torch.ones(dim, dtype=bf, device=device)}
-    pad = lambda r: int(math.ceil(r / rank_multiple) * rank_multiple)
+    pad = lambda r, m: int(math.ceil(r / m) * m)
     rk_pad, rv_pad = [], []
     for i in range(args.n_layers):
         W = {"q": randn(nh * hd, dim), "k": randn(nkv * hd, dim), "v": randn(nkv * hd, dim), "o": randn(dim, nh * hd)}
         fac = []
-        for w, r in ((W["k"], ranks_k[i]), (W["v"], ranks_v[i])):
+        for w, r, m in ((W["k"], ranks_k[i], rank_multiple), (W["v"], ranks_v[i], rank_multiple_v or rank_multiple)):
             U, VT = compress.svd_per_head(w, nkv, r)
-            rp = min(pad(r), hd)
+            rp = min(pad(r, m), hd)
             fac += [F.pad(VT, (0, 0, 0, rp - r)), F.pad(U, (0, rp - r))]
         lr = convert.LowRank(*fac)
         rk_pad.append(lr.r_k)
