@@ -302,7 +302,7 @@ template <int RK, int RV, bool KFULL, int NW>
 struct Smem {
   static constexpr int UKT_STRIDE = RK + 8;
   static constexpr int RTAB_BYTES = KFULL ? 0 : 2 * 2 * 8 * 64 * 16;
-  static constexpr int KC_BYTES = 64 * 64 * 8;
+  static constexpr int KC_BYTES = 15 * 64 * 8;   // the 15 staged cs_tab rows of the K rotation table
   static constexpr int UKT_BYTES = KFULL ? 0 : HD * UKT_STRIDE * 2;
   static constexpr int QX_WAVE_BYTES = 16 * 4 * 8 * 4 * 2;   // [head 16][g 4][row tile 8][4 dims] fp16
   static constexpr int QX_BYTES = KFULL ? 0 : (NW * QX_WAVE_BYTES > KC_BYTES ? NW * QX_WAVE_BYTES : KC_BYTES);
@@ -331,7 +331,10 @@ __device__ __forceinline__ float4 load4f<__bf16>(const __bf16* p) {
 }
 
 template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, int NW, typename TabT, typename OutT>
-__global__ __launch_bounds__(NW * 64) void palu_decode_kernel(const DecodeArgs a) {
+// At least two waves per SIMD (256 registers) wherever the width pair's default is 8 waves per workgroup,
+// so that its 4-wave variant fits two workgroups per CU.
+__global__ __launch_bounds__(NW * 64, (NW == 8 || pick_nw<RK, RV, KFULL, TILED>() == 8) ? 2 : 1)
+void palu_decode_kernel(const DecodeArgs a) {
   static_assert(RK % 32 == 0 && RK <= 128, "RK");
   static_assert(RV % 16 == 0 && RV <= 128 && (TILED || RV % 32 == 0), "RV: 16-wide V tiles (tiled), 32-wide rows");
   static_assert(!KFULL || RK == HD, "full K has the head dim");
@@ -943,20 +946,8 @@ __global__ __launch_bounds__(RV) void palu_merge_kernel(const DecodeArgs a) {
 }
 
 
-template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, typename TabT, typename OutT>
-int launch(const DecodeArgs& a0, hipStream_t stream) {
-  constexpr int NW = pick_nw<RK, RV, KFULL, TILED>();
-  DecodeArgs a = a0;
-  const int items = a.B * a.n_kv;
-  a.n_wg = decode_workgroups(items);
-  a.balanced = a.n_wg > items ? 1 : 0;
-  if (!a.balanced) a.n_wg = items;
-  // Chunks of the length-aware plan are short: there the fixed block order (no round trip to the
-  // shared counter per pair) is the faster one, and it is reproducible as well.
-  if (a.balanced) a.deterministic = 1;
-  const size_t need = decode_ws_bytes(items, RV);
-  if (need > 0 && (a.ws == nullptr || a.ws_bytes < need))
-    return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_decode_workspace_bytes), got %zu", need, a.ws_bytes);
+template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, typename TabT, typename OutT, int NW>
+int launch_nw(const DecodeArgs& a, int items, hipStream_t stream) {
   using SM = Smem<RK, RV, KFULL, NW>;
   auto kern = palu_decode_kernel<RK, RV, KFULL, TILED, PAGED, NW, TabT, OutT>;
   const int lds = SM::bytes(a.S) + (PAGED ? ((a.S >> 5 >> a.page_shift) + 2) * 4 : 0);
@@ -976,6 +967,33 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
     if (e != hipSuccess) return fail(PALU_EHIP, "merge kernel launch: %s", hipGetErrorString(e));
   }
   return PALU_OK;
+}
+
+template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, typename TabT, typename OutT>
+int launch(const DecodeArgs& a0, hipStream_t stream) {
+  constexpr int NW = pick_nw<RK, RV, KFULL, TILED>();
+  DecodeArgs a = a0;
+  const int items = a.B * a.n_kv;
+  a.n_wg = decode_workgroups(items);
+  a.balanced = a.n_wg > items ? 1 : 0;
+  if (!a.balanced) a.n_wg = items;
+  // Chunks of the length-aware plan are short: there the fixed block order (no round trip to the
+  // shared counter per pair) is the faster one, and it is reproducible as well.
+  if (a.balanced) a.deterministic = 1;
+  const size_t need = decode_ws_bytes(items, RV);
+  if (need > 0 && (a.ws == nullptr || a.ws_bytes < need))
+    return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_decode_workspace_bytes), got %zu", need, a.ws_bytes);
+  // Two or more whole items per CU (e.g. batch 64 x 8 KV heads): an 8-wave workgroup fills a CU's
+  // registers, so the CU's second item would start, prologue and all, only when its first ended. Two
+  // 4-wave workgroups fit a CU together (256 registers per wave, LDS for two), and one's prologue then
+  // runs while the other streams. Built for the tiled contiguous caches with fp32 tables and bf16
+  // output, the decoder's configuration.
+  if constexpr (NW == 8 && TILED && !PAGED && !KFULL && std::is_same<TabT, float>::value &&
+                std::is_same<OutT, __bf16>::value) {
+    if (!a.balanced && items >= 2 * TARGET_WGS && 2 * Smem<RK, RV, KFULL, 4>::bytes(a.S) <= 160 * 1024)
+      return launch_nw<RK, RV, KFULL, TILED, PAGED, TabT, OutT, 4>(a, items, stream);
+  }
+  return launch_nw<RK, RV, KFULL, TILED, PAGED, TabT, OutT, NW>(a, items, stream);
 }
 
 template <int RK, bool KFULL, bool TILED, bool PAGED, typename TabT, typename OutT>
