@@ -286,9 +286,9 @@ __device__ int plan_chunk_pairs(const DecodeArgs& a) {
 }
 
 // LDS map of one workgroup (latent mode; full-K mode keeps only the merge buffer and the counter):
-//   rtab  pair-relative K rotation (offset t < 64 inside a pair of blocks), fp16 x 8 {cos f, cos f,
-//         -sin f, sin f, cos f+1, cos f+1, -sin f+1, sin f+1} per (block of the pair, tile, 16-dim row
-//         tile, lane), i.e. exactly the operand order of the rebuilt K^T accumulators  32 KB
+//   rtab  pair-relative K rotation (offset t < 64 inside a pair of blocks), fp16 x 4 {cos f, sin f,
+//         cos f+1, sin f+1} per (block of the pair, tile, 16-dim row tile, lane); the packed fp16
+//         multiplies take (cos, cos) and (-sin, sin) through operand selects and the negate modifier  16 KB
 //   ukT   u_k^T, rows padded by 16 bytes (bank spread)                               HD x (RK + 8) bf16
 //   qx    per wave, the rotated query (fp16) regrouped into its MFMA operand layout  NW x 4 KB
 //   tl    (cos, sin) of angle 64*Lo*f, Lo < 16: the low part of a pair base           [16][64] float2
@@ -301,7 +301,7 @@ __device__ int plan_chunk_pairs(const DecodeArgs& a) {
 template <int RK, int RV, bool KFULL, int NW>
 struct Smem {
   static constexpr int UKT_STRIDE = RK + 8;
-  static constexpr int RTAB_BYTES = KFULL ? 0 : 2 * 2 * 8 * 64 * 16;
+  static constexpr int RTAB_BYTES = KFULL ? 0 : 2 * 2 * 8 * 64 * 8;
   static constexpr int KC_BYTES = 15 * 64 * 8;   // the 15 staged cs_tab rows of the K rotation table
   static constexpr int UKT_BYTES = KFULL ? 0 : HD * UKT_STRIDE * 2;
   static constexpr int QX_WAVE_BYTES = 16 * 4 * 8 * 4 * 2;   // [head 16][g 4][row tile 8][4 dims] fp16
@@ -344,7 +344,7 @@ void palu_decode_kernel(const DecodeArgs a) {
   using SM = Smem<RK, RV, KFULL, NW>;
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  f16x8* rtab = reinterpret_cast<f16x8*>(smem);
+  f16x4* rtab = reinterpret_cast<f16x4*>(smem);
   __bf16* ukT = reinterpret_cast<__bf16*>(smem + SM::UKT_OFFSET);
   float2* tl = reinterpret_cast<float2*>(smem + SM::TL_OFFSET);
   float2* th = reinterpret_cast<float2*>(smem + SM::TH_OFFSET);
@@ -588,8 +588,7 @@ void palu_decode_kernel(const DecodeArgs a) {
         x = make_float2(x.x * u.x - x.y * u.y, x.y * u.x + x.x * u.y);
         y = make_float2(y.x * v.x - y.y * v.y, y.y * v.x + y.x * v.y);
       }
-      rtab[e] = f16x8{(_Float16)x.x, (_Float16)x.x, (_Float16)-x.y, (_Float16)x.y,
-                      (_Float16)y.x, (_Float16)y.x, (_Float16)-y.y, (_Float16)y.y};
+      rtab[e] = f16x4{(_Float16)x.x, (_Float16)x.y, (_Float16)y.x, (_Float16)y.y};
     }
   } else {
     load_first(0, kl, vl);
@@ -752,8 +751,9 @@ void palu_decode_kernel(const DecodeArgs a) {
           f16x2 r[2][2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const f16x8 t = rtab[((hb * 2 + c) * 8 + 2 * kq + h) * 64 + lane];
-            const f16x2 c0 = {t[0], t[1]}, s0 = {t[2], t[3]}, c1 = {t[4], t[5]}, s1 = {t[6], t[7]};
+            // (c, s) pairs: (c, c) and (-s, s) are the packed ops' operand selects and negate modifier
+            const f16x4 t = rtab[((hb * 2 + c) * 8 + 2 * kq + h) * 64 + lane];
+            const f16x2 c0 = {t[0], t[0]}, s0 = {-t[1], t[1]}, c1 = {t[2], t[2]}, s1 = {-t[3], t[3]};
             const f16x2 x01 = to_f16x2(acc[c][h][0], acc[c][h][1]);
             const f16x2 x23 = to_f16x2(acc[c][h][2], acc[c][h][3]);
             r[h][0] = x01 * c0 + x01.yx * s0;
