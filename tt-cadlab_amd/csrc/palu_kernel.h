@@ -919,9 +919,11 @@ void palu_decode_kernel(const DecodeArgs a) {
 // Merge the chunk partials of every split item: out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)
 // over the item's chunks. One workgroup per (item, query head), one thread per output column; the
 // item's first chunk left (first slot, chunk count) after the partial slots. Items in one chunk were
-// written by the decode kernel itself.
+// written by the decode kernel itself. The partials of MC chunks are loaded together (one round trip
+// to memory per MC chunks, not one per load); the chunks past MC are folded in with a running rescale.
 template <int RV, typename OutT>
 __global__ __launch_bounds__(RV) void palu_merge_kernel(const DecodeArgs a) {
+  constexpr int MC = 8;
   const int item = blockIdx.x / a.rep, h = blockIdx.x - item * a.rep;
   const int b = item / a.n_kv, kvh = item - b * a.n_kv;
   const int* ent = reinterpret_cast<const int*>(a.ws + (long long)a.n_wg * 16 * (RV + 2)) + 2 * item;
@@ -930,16 +932,33 @@ __global__ __launch_bounds__(RV) void palu_merge_kernel(const DecodeArgs a) {
   const int r = threadIdx.x;
   const float* ws = a.ws + ((long long)first * 16 + h) * (RV + 2);
   constexpr long long SLOT = 16 * (RV + 2);
-  float M = NEG_INF;
-  for (int s = 0; s < nc; ++s) M = fmaxf(M, ws[s * SLOT + RV]);
-  float L = 0.f, acc = 0.f;
-  if (M != NEG_INF) {
-    for (int s = 0; s < nc; ++s) {
-      const float* row = ws + s * SLOT;
-      const float f = __builtin_amdgcn_exp2f(row[RV] - M);
-      L += row[RV + 1] * f;
-      acc += row[r] * f;
+  float M = NEG_INF, L = 0.f, acc = 0.f;
+  for (int s0 = 0; s0 < nc; s0 += MC) {
+    float mv[MC], lv[MC], ov[MC];
+#pragma unroll
+    for (int i = 0; i < MC; ++i) {
+      const float* row = ws + min(s0 + i, nc - 1) * SLOT;   // clamped into the item's slots
+      mv[i] = row[RV];
+      lv[i] = row[RV + 1];
+      ov[i] = row[r];
     }
+    float Mn = M;
+#pragma unroll
+    for (int i = 0; i < MC; ++i)
+      if (s0 + i < nc) Mn = fmaxf(Mn, mv[i]);
+    if (Mn == NEG_INF) continue;            // every chunk so far empty
+    const float c = __builtin_amdgcn_exp2f(M - Mn);   // 0 while M is -inf
+    L *= c;
+    acc *= c;
+#pragma unroll
+    for (int i = 0; i < MC; ++i) {
+      if (s0 + i < nc) {
+        const float f = __builtin_amdgcn_exp2f(mv[i] - Mn);
+        L += lv[i] * f;
+        acc += ov[i] * f;
+      }
+    }
+    M = Mn;
   }
   OutT* o = static_cast<OutT*>(a.out) + out_index(a, b, ((long long)kvh * a.rep + h) * RV + r, (long long)a.n_q * RV);
   store_out(o, L > 0.f ? acc / L : 0.f);
