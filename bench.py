@@ -303,8 +303,8 @@ def measure_glrd(dev, steps, warmup):
 def measure_e2e(a, dev):
     """Llama-3.1-8B-shaped decoder (32 layers, vocab 128256, FFN 14336 SwiGLU, RMSNorm eps 1e-5), random-init
     bf16 weights; per-layer M-LRD ranks drawn from [32, 128] in steps of 8 with mean 64 (K and V drawn
-    separately, seeded), K padded to a multiple of 32 and V to a multiple of 16 (the tiled V cache's tile
-    width). Batch rows get random-id prompts, are prefilled, then
+    separately, seeded), both padded to a multiple of 16 (the tiled caches' granularity: 16-wide V tiles, K
+    rows ending in a 16-wide half tile). Batch rows get random-id prompts, are prefilled, then
     decode greedily; decode tokens/s = batch x timed decode steps / decode wall time (the first generated
     token comes from prefill and is not timed). Then the same model shape with full-rank (128) K and V: the
     stock bf16 full-KV decode through the same engine."""
@@ -317,7 +317,7 @@ def measure_e2e(a, dev):
     for kind, rk, rv in (("palu", ranks_k, ranks_v), ("stock", [HD] * L, [HD] * L)):
         args = pm.ModelArgs(n_layers=L, max_batch_size=B, max_seq_len=(P + n_new + 31) // 32 * 32)
         t0 = time.perf_counter()
-        model = pm.Transformer(args, pm.random_palu_state_dict(args, rk, rv, dev, seed=0, rank_multiple_v=16), dev)
+        model = pm.Transformer(args, pm.random_palu_state_dict(args, rk, rv, dev, seed=0, rank_multiple=16), dev)
         torch.cuda.synchronize()
         t_build = time.perf_counter() - t0
         prompts = torch.randint(0, args.vocab_size, (B, P), generator=torch.Generator().manual_seed(7)).to(dev)

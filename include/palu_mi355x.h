@@ -39,7 +39,9 @@ extern "C" {
  * hold the same values with every 32-position block stored as (width / 16) tiles of 1 KB (64 slots of
  * 8 bf16) in the operand order of the kernel's MFMAs (g < 4, n < 16, c < 2):
  *   K-tile order (K latents, full K): tile c * (width/32) + kb, slot 16*g + n holds width-index
- *     32*kb + 8*g .. +7 of block position 8*(n/4) + 4*c + n%4;
+ *     32*kb + 8*g .. +7 of block position 8*(n/4) + 4*c + n%4. A width that is an odd multiple of 16
+ *     (K latents of the per-head path) ends each half-block c (16 * width elements from c * 16 * width)
+ *     in a 512-byte half tile: slot 16*g + n holds the 4 width-indices 32*(width/32) + 4*g .. +3;
  *   V-tile order (V latents, full V): tile mt, slot 16*g + m holds block positions 8*g .. 8*g+7 of
  *     width-index 16*mt + m.
  * A decode call with PALU_LAYOUT_TILED reads K caches in K-tile order and V caches in V-tile order;
@@ -82,6 +84,8 @@ size_t palu_glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int
  *   w_rot    [n_kv, r_k, 256] bf16   [u_k | u_k T] per KV head, u_k in Meta head order
  *   cs_tab   [cs_rows, 256]          [cos | sin] per position, Meta-interleaved; fp32 or bf16
  *   v_latent [B, n_groups, S, r_v]   bf16 V latent cache (absorbed V: attended over directly)
+ *   r_k, r_v                         multiples of 32 (ROWS), or of 16 with PALU_LAYOUT_TILED on the
+ *                                    per-head path (no u_v); the kernels are built for 32 .. 128
  *   cur_pos  [B] int32 (device)      inclusive last valid position of each row
  *   out      [B, n_q, head_dim_v]    fp32 or bf16
  *   cache_layout                     PALU_LAYOUT_ROWS or PALU_LAYOUT_TILED for both latent caches

@@ -6,7 +6,7 @@ from palu_tt.cache import LatentCache, rows_to_tiled, tiled_to_rows
 
 
 @pytest.mark.parametrize("role", ["k", "v"])
-@pytest.mark.parametrize("S,r", [(32, 32), (64, 64), (256, 96), (96, 128)])
+@pytest.mark.parametrize("S,r", [(32, 32), (64, 64), (256, 96), (96, 128), (64, 48), (32, 80), (96, 112), (32, 16)])
 def test_round_trip_is_exact(S, r, role):
     rows = torch.randn(2, 3, S, r).to(torch.bfloat16)
     tiled = rows_to_tiled(rows, role)
@@ -29,6 +29,28 @@ def test_slot_mapping_matches_the_documented_operand_order():
                     p = 32 * blk + 8 * (n // 4) + 4 * c + n % 4
                     for j in range(8):
                         assert tiled[0, 0, blk, c * (r // 32) + kb, l, j] == p * 1000 + 32 * kb + 8 * g + j
+
+
+@pytest.mark.parametrize("r", [48, 80])
+def test_k_half_tile_slot_mapping(r):
+    """K width an odd multiple of 16: half-block c of a block is 16 r elements from c * 16 r; its full tiles
+    keep the 32-deep order and its last 256 elements hold r-indices 32 (r // 32) + 4 g + j (j < 4) of
+    position 8 (n // 4) + 4 c + n % 4 in slot 16 g + n."""
+    S = 64
+    kbf = r // 32
+    pos = torch.arange(S)[:, None].expand(S, r)
+    col = torch.arange(r)[None, :].expand(S, r)
+    flat = rows_to_tiled((pos * 1000 + col).float()[None, None], "k").reshape(S // 32, 32 * r)
+    for blk in range(S // 32):
+        for c in range(2):
+            for l in range(64):
+                g, n = divmod(l, 16)
+                p = 32 * blk + 8 * (n // 4) + 4 * c + n % 4
+                for kb in range(kbf):
+                    for j in range(8):
+                        assert flat[blk, c * 16 * r + kb * 512 + 8 * l + j] == p * 1000 + 32 * kb + 8 * g + j
+                for j in range(4):
+                    assert flat[blk, c * 16 * r + kbf * 512 + 4 * l + j] == p * 1000 + 32 * kbf + 4 * g + j
 
 
 def test_v_slot_mapping_matches_the_documented_operand_order():

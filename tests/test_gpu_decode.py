@@ -385,6 +385,38 @@ def test_stock_flash_decode_tiled_v_widths_in_16s(gpu, dv):
     _check(out.cpu(), ref.full_kv_decode(q, k, v, pos, HD ** -0.5))
 
 
+@pytest.mark.parametrize("B,S,r_k,r_v,out_dtype,det", [
+    (4, 1024, 48, 64, torch.float32, False), (32, 256, 80, 48, torch.float32, True),
+    (3, 640, 112, 112, torch.float32, False), (64, 256, 80, 64, torch.bfloat16, False),
+    (1, 4096, 48, 128, torch.float32, False), (2, 512, 112, 32, torch.bfloat16, True)])
+def test_tiled_k_widths_in_16s(gpu, B, S, r_k, r_v, out_dtype, det):
+    """Tiled K caches also take K latent widths that are odd multiples of 16 (each half-block of K ends in
+    a 16-wide half tile, 4 values per lane): one item per workgroup (B = 32), two co-resident
+    4-wave workgroups per CU (B = 64), merged chunks (B < 32), and the K append in K-tile order."""
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(B, S, r_k, r_v, seed=r_k + r_v)
+    w_rot = ref.w_rot_from_u_k(u_k)[None].to(gpu, torch.bfloat16)
+    cs = ref.cs_table(cos, sin, S)[None, None].to(gpu)
+    kc = LatentCache.from_rows(k_lat.to(gpu, torch.bfloat16), "k")
+    vc = LatentCache.from_rows(v.to(gpu, torch.bfloat16), "v")
+    new_k = _bf(torch.randn(1, B, 8, r_k))
+    dpos = pos.to(gpu, torch.int32)
+    fused.paged_update_cache(kc, new_k.to(gpu, torch.bfloat16), dpos)
+    k_full = k_lat.clone()
+    for b in range(B):
+        k_full[b, :, pos[b]] = new_k[0, b]
+    out = fused.palu_sdpa_decode(q.to(gpu, torch.bfloat16), kc, w_rot, cs, vc, r_v, dpos, scale=HD ** -0.5,
+                                 out_dtype=out_dtype, deterministic=det)
+    torch.cuda.synchronize()
+    assert torch.equal(kc.to_rows().float().cpu(), k_full)
+    _check(out.float().cpu(), ref.reference_decode(q, k_full, u_k, v, pos, cos, sin, HD ** -0.5))
+
+
+def test_row_major_k_width_in_16s_is_refused(gpu):
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(2, 256, 48, 64)
+    with pytest.raises(RuntimeError, match="r_k must be a multiple of 32"):
+        _run_fused(gpu, q, k_lat, u_k, v, pos, cos, sin, 256)
+
+
 def test_row_major_v_width_in_16s_is_refused(gpu):
     q, k_lat, u_k, v, pos, cos, sin = _inputs(2, 256, 64, 48)
     with pytest.raises(RuntimeError, match="r_v must be a multiple of 32"):

@@ -50,7 +50,7 @@ def test_fused_matches_naive_on_the_end_to_end_decoder(gpu):
     B, P, T, L = 64, 2048, 16, 32
     args = pm.ModelArgs(n_layers=L, max_batch_size=B, max_seq_len=P + 32)
     sd = pm.random_palu_state_dict(args, pm.draw_ranks(L, seed=1), pm.draw_ranks(L, seed=2), gpu, seed=0,
-                                   rank_multiple_v=16)
+                                   rank_multiple=16)
     model = pm.Transformer(args, sd, gpu)
     del sd
     g = torch.Generator().manual_seed(7)

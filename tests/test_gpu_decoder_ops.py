@@ -63,7 +63,8 @@ def test_rope_rows_matches_apply_rope_meta(gpu):
 
 
 @pytest.mark.parametrize("layout,role,gs,width", [("tiled", "k", 1, 64), ("tiled", "v", 1, 96), ("rows", "k", 1, 32),
-                                                   ("tiled", "k", 4, 384), ("tiled", "v", 2, 256), ("rows", "v", 4, 512)])
+                                                   ("tiled", "k", 4, 384), ("tiled", "v", 2, 256), ("rows", "v", 4, 512),
+                                                   ("tiled", "k", 1, 112)])
 def test_strided_append_equals_contiguous_append(gpu, layout, role, gs, width):
     g = torch.Generator().manual_seed(width + gs)
     B, nkv, S = 5, 8, 96
@@ -232,16 +233,21 @@ def test_linear_swiglu_mode(gpu, rows, x_tiled):
     assert torch.equal(lin.plain(), torch.cat([wg, wu], 0))
 
 
-def test_rmsnorm_residual_from_partials(gpu):
-    """res_part (a projection's fp32 split partials) gives h = bf16(x + sum of the slices) and the norm of it."""
-    g = torch.Generator().manual_seed(5)
-    x = torch.randn(64, 4096, generator=g).to(gpu, torch.bfloat16)
-    part = torch.randn(4, 64, 4096, generator=g).to(gpu)
-    w = (1 + 0.1 * torch.randn(4096, generator=g)).to(gpu, torch.bfloat16)
+@pytest.mark.parametrize("ks,rows,dim", [(4, 64, 4096), (1, 64, 4096), (3, 5, 4096), (5, 64, 4096), (9, 2, 1000)])
+def test_rmsnorm_residual_from_partials(gpu, ks, rows, dim):
+    """res_part (a projection's fp32 split partials) gives h = bf16(x + sum of the slices, in slice order)
+    and the norm of it; more than four slices take the kernel's extra load rounds, dim 1000 has lanes past
+    the row's end."""
+    g = torch.Generator().manual_seed(5 + ks)
+    x = torch.randn(rows, dim, generator=g).to(gpu, torch.bfloat16)
+    part = torch.randn(ks, rows, dim, generator=g).to(gpu)
+    w = (1 + 0.1 * torch.randn(dim, generator=g)).to(gpu, torch.bfloat16)
     h = x.clone()
     y = decoder_ops.rmsnorm(h, w, 1e-5, res_part=part, h_out=h)
     torch.cuda.synchronize()
-    s = part[0] + part[1] + part[2] + part[3]
+    s = part[0].clone()
+    for k in range(1, ks):
+        s += part[k]
     h_ref = (x.float() + s).to(torch.bfloat16)
     assert torch.equal(h, h_ref)
     hf = h_ref.float()
@@ -250,7 +256,8 @@ def test_rmsnorm_residual_from_partials(gpu):
 
 
 @pytest.mark.parametrize("layout,gs,r_k,r_v,k_rope", [("tiled", 1, 64, 96, False), ("rows", 1, 32, 128, False),
-                                                      ("tiled", 4, 256, 192, False), ("tiled", 1, 128, 64, True)])
+                                                      ("tiled", 4, 256, 192, False), ("tiled", 1, 128, 64, True),
+                                                      ("tiled", 1, 80, 48, False)])
 def test_qkv_post_equals_rope_and_appends(gpu, layout, gs, r_k, r_v, k_rope):
     """The fused QKV epilogue: q rotated at each row's position, every group's K and V slices appended at
     that position (rotated K for the stock path), from fp32 split partials; against rope of the summed

@@ -80,10 +80,10 @@ def _check(out, exp):
 
 @pytest.mark.parametrize("layout", ["rows", "tiled"])
 @pytest.mark.parametrize("r_k,r_v,page_size", [(64, 64, 64), (32, 128, 64), (128, 64, 64), (64, 32, 32), (96, 96, 128),
-                                               (64, 80, 64)])
+                                               (64, 80, 64), (80, 64, 64), (48, 112, 32)])
 def test_paged_decode_matches_oracle(gpu, layout, r_k, r_v, page_size):
-    if layout == "rows" and r_v % 32:
-        pytest.skip("row-major caches take V widths in 32s")
+    if layout == "rows" and (r_k % 32 or r_v % 32):
+        pytest.skip("row-major caches take latent widths in 32s")
     B, S = 4, 2048
     q, k, v, u_k, pos, kp, vp, pt = _case(B, S, r_k, r_v, page_size, seed=r_k + r_v + page_size)
     assert torch.equal(ref.gather_pages(kp, pt), k) and torch.equal(ref.gather_pages(vp, pt), v)

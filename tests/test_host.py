@@ -318,6 +318,7 @@ def _sdpa(lib, **kw):
 
 @pytest.mark.parametrize("kw,code,needle", [
     (dict(r_k=48), _native.PALU_EINVAL, "r_k"),
+    (dict(r_k=40, layout=1), _native.PALU_EINVAL, "r_k must be a multiple of 16"),
     (dict(cs_cols=128), _native.PALU_EINVAL, "cs_tab"),
     (dict(cs_rows=100), _native.PALU_EINVAL, "cs_tab"),
     (dict(w_rot_width=128), _native.PALU_EINVAL, "w_rot"),
@@ -354,8 +355,8 @@ def test_flash_decode_and_append_envelope_errors(lib):
     assert rc == _native.PALU_EINVAL and "multiple of 32" in lib.palu_last_error().decode()
     rc = lib.palu_latent_append(_FAKE, _FAKE, _FAKE, 2, 2, 256, 12, 0, None)
     assert rc == _native.PALU_EINVAL and "multiple of 8" in lib.palu_last_error().decode()
-    rc = lib.palu_latent_append(_FAKE, _FAKE, _FAKE, 2, 2, 256, 48, 1, None)
-    assert rc == _native.PALU_EINVAL and "multiple of 32" in lib.palu_last_error().decode()
+    rc = lib.palu_latent_append(_FAKE, _FAKE, _FAKE, 2, 2, 256, 40, 1, None)
+    assert rc == _native.PALU_EINVAL and "multiple of 16" in lib.palu_last_error().decode()
 
 
 def test_paged_envelope_errors(lib):
@@ -388,8 +389,10 @@ def test_paged_envelope_errors(lib):
     assert rc == _native.PALU_EINVAL and "page_table" in lib.palu_last_error().decode()
     rc = lib.palu_latent_append_paged(_FAKE, _FAKE, _FAKE, _FAKE, 2, 2, 16, 96, 4, 64, 0, None)
     assert rc == _native.PALU_EINVAL and "power of two" in lib.palu_last_error().decode()
-    rc = lib.palu_latent_append_paged(_FAKE, _FAKE, _FAKE, _FAKE, 2, 2, 16, 64, 4, 48, 1, None)
-    assert rc == _native.PALU_EINVAL and "multiple of 32" in lib.palu_last_error().decode()
+    rc = lib.palu_latent_append_paged(_FAKE, _FAKE, _FAKE, _FAKE, 2, 2, 16, 64, 4, 40, 1, None)
+    assert rc == _native.PALU_EINVAL and "multiple of 16" in lib.palu_last_error().decode()
+    rc, msg = sdpa_paged(r_k=40, layout=1)         # tiled caches: K widths in 16s
+    assert rc == _native.PALU_EINVAL and "r_k must be a multiple of 16" in msg
 
 
 def test_glrd_envelope_errors(lib):

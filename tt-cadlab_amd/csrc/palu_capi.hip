@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void palu_append_kernel(__bf16* cache, const _
     if constexpr (LAYOUT == PALU_LAYOUT_ROWS) {
       *reinterpret_cast<bf16x8*>(stream + (long long)p * width + 8 * v) = x;
     } else if constexpr (LAYOUT == PALU_LAYOUT_TILED) {
-      *reinterpret_cast<bf16x8*>(stream + tiled_k_offset(p, 8 * v, width)) = x;
+      store_k8(stream, p, 8 * v, width, x);
     } else {
       const long long o = tiled_v_offset(p, 8 * v, width);   // 8 slots 16 bytes apart
 #pragma unroll
@@ -123,8 +123,8 @@ int check_append(void* cache, const void* new_rows, const int32_t* update_idxs, 
   if (batch <= 0 || n_groups <= 0 || S <= 0 || width <= 0 || width % 8 != 0)
     return fail(PALU_EINVAL, "%s: width must be a positive multiple of 8, got %d", who, width);
   if (int rc = check_layout(layout == PALU_LAYOUT_TILED_V ? PALU_LAYOUT_TILED : layout, S, who)) return rc;
-  if (layout == PALU_LAYOUT_TILED && width % 32 != 0)
-    return fail(PALU_EINVAL, "%s: a tiled K cache row is a multiple of 32 wide, got %d", who, width);
+  if (layout == PALU_LAYOUT_TILED && width % 16 != 0)
+    return fail(PALU_EINVAL, "%s: a tiled K cache row is a multiple of 16 wide, got %d", who, width);
   if (layout == PALU_LAYOUT_TILED_V && width % 16 != 0)
     return fail(PALU_EINVAL, "%s: a tiled V cache row is a multiple of 16 wide, got %d", who, width);
   if (!aligned16(cache) || !aligned16(new_rows)) return fail(PALU_EINVAL, "%s: 16-byte alignment required", who);
@@ -137,6 +137,8 @@ int check_append(void* cache, const void* new_rows, const int32_t* update_idxs, 
 // full-rank K path, one head per group) and V slice (v_off + g * v_gs, v_w wide) appended to the caches
 // at position pos[b], as palu_rope_rows and palu_latent_append_strided do over a bf16 projection output.
 // One thread per 8 consecutive columns; the partials are summed in slice order in fp32 and rounded once.
+constexpr int QP_PK = 4;   // partial slices loaded together
+
 __global__ __launch_bounds__(256) void palu_qkv_post_kernel(const float* part, int ks, int B, int ncols,
                                                             const int32_t* pos, const float* cos_t, const float* sin_t,
                                                             int table_rows, int nh, __bf16* q_out, __bf16* kc,
@@ -165,14 +167,31 @@ __global__ __launch_bounds__(256) void palu_qkv_post_kernel(const float* part, i
       c8 = ((t - qv - kv) % (v_w / 8)) * 8;
       col = v_off + gi * v_gs + c8;
     }
+    // The row's position and the first QP_PK partial slices are loaded together (the kernel is bound by
+    // memory latency); slices past ks re-read the last one and are not added.
+    const int p = pos[b];
     const float* pp = part + (long long)b * ncols + col;
-    f32x4 s0 = *reinterpret_cast<const f32x4*>(pp), s1 = *reinterpret_cast<const f32x4*>(pp + 4);
-    for (int k = 1; k < ks; ++k) {
-      s0 += *reinterpret_cast<const f32x4*>(pp + (long long)k * B * ncols);
-      s1 += *reinterpret_cast<const f32x4*>(pp + (long long)k * B * ncols + 4);
+    const long long pstride = (long long)B * ncols;
+    f32x4 pa[QP_PK][2];
+#pragma unroll
+    for (int k = 0; k < QP_PK; ++k) {
+      const float* pk = pp + min(k, ks - 1) * pstride;
+      pa[k][0] = *reinterpret_cast<const f32x4*>(pk);
+      pa[k][1] = *reinterpret_cast<const f32x4*>(pk + 4);
+    }
+    f32x4 s0 = pa[0][0], s1 = pa[0][1];
+#pragma unroll
+    for (int k = 1; k < QP_PK; ++k) {
+      if (k < ks) {
+        s0 += pa[k][0];
+        s1 += pa[k][1];
+      }
+    }
+    for (int k = QP_PK; k < ks; ++k) {
+      s0 += *reinterpret_cast<const f32x4*>(pp + k * pstride);
+      s1 += *reinterpret_cast<const f32x4*>(pp + k * pstride + 4);
     }
     float v[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-    const int p = pos[b];
     if (kind == 0 || (kind == 1 && k_rope)) {
       const int pr = p < 0 ? 0 : (p >= table_rows ? table_rows - 1 : p);
 #pragma unroll
@@ -196,7 +215,7 @@ __global__ __launch_bounds__(256) void palu_qkv_post_kernel(const float* part, i
     if (layout == PALU_LAYOUT_ROWS) {
       *reinterpret_cast<bf16x8*>(stream + (long long)p * width + c8) = o;
     } else if (layout == PALU_LAYOUT_TILED) {
-      *reinterpret_cast<bf16x8*>(stream + tiled_k_offset(p, c8, width)) = o;
+      store_k8(stream, p, c8, width, o);
     } else {
       const long long off = tiled_v_offset(p, c8, width);   // 8 slots 16 bytes apart
 #pragma unroll
@@ -225,11 +244,13 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
     return fail(PALU_EINVAL, "k_chunk_size must be 0 or a power of two multiple of 32, got %d", k_chunk);
   if (batch <= 0 || n_q <= 0 || n_kv <= 0 || n_groups <= 0 || seq_len <= 0)
     return fail(PALU_EINVAL, "%s: batch, head counts and seq_len must be positive", who);
-  if (r_k <= 0 || r_k % 32 != 0 || r_k > 512)
-    return fail(PALU_EINVAL, "r_k must be a multiple of 32 in 32..512 (the latent width of k_latent), got %d", r_k);
-  // V latents are 16-wide tiles in the tiled layout: per-head (absorbed-V) tiled caches also take widths
-  // that are multiples of 16; row-major caches and grouped latents (u_v) keep multiples of 32
-  const int rv_step = (cache_layout == PALU_LAYOUT_TILED && u_v == nullptr) ? 16 : 32;
+  // Per-head (absorbed-V) tiled caches take latent widths in multiples of 16: V tiles are 16 wide and a K
+  // row's last 16 columns form a half tile. Row-major caches and grouped latents (u_v) keep multiples of 32.
+  const int r_step = (cache_layout == PALU_LAYOUT_TILED && u_v == nullptr) ? 16 : 32;
+  if (r_k <= 0 || r_k % r_step != 0 || r_k > 512)
+    return fail(PALU_EINVAL, "r_k must be a multiple of %d in %d..512 (the latent width of k_latent), got %d", r_step,
+                r_step, r_k);
+  const int rv_step = r_step;
   if (r_v <= 0 || r_v % rv_step != 0 || r_v > 512)
     return fail(PALU_EINVAL, "r_v must be a multiple of %d in %d..512 (the latent width of v_latent), got %d", rv_step,
                 rv_step, r_v);
@@ -322,6 +343,9 @@ int sdpa_dispatch(const DecodeArgs& a, bool paged, int cache_layout, int r_k, in
     if (paged) return fail(PALU_EUNSUPPORTED, "u_v: the in-kernel V rebuild is not built for paged caches");
     return dispatch_glrd(a, cs_dtype, out_dtype, stream);
   }
+  if (tiled && r_k % 32 != 0)   // K rows ending in a half tile: their own translation units
+    return paged ? dispatch_latent_tiled_paged_k16(a, r_k, r_v, cs_dtype, out_dtype, stream)
+                 : dispatch_latent_tiled_k16(a, r_k, r_v, cs_dtype, out_dtype, stream);
   if (paged)
     return tiled ? dispatch_latent_tiled_paged(a, r_k, r_v, cs_dtype, out_dtype, stream)
                  : dispatch_latent_rows_paged(a, r_k, r_v, cs_dtype, out_dtype, stream);

@@ -16,9 +16,16 @@ __device__ __forceinline__ long long tiled_row_offset(int row, int col) {
 }
 
 // One workgroup per row: h = x (+ res), stored when h_out is given; y = h * rsqrt(mean(h^2) + eps) * w.
-// Each thread holds up to RMS_VEC vectors of 8 elements in registers between the two passes.
-constexpr int RMS_THREADS = 256;
-constexpr int RMS_VEC = 4;               // dim <= 256 * 8 * 4 = 8192
+// Each thread holds up to RMS_VEC vectors of 8 elements in registers between the two passes. The kernel
+// is tiny and bound by memory latency, so every load of the row (x, the residual or the first RMS_PK
+// partial slices, the weight) is issued before the first is used: one round trip to memory, plus one
+// per further RMS_PK slices.
+constexpr int RMS_THREADS = 512;
+constexpr int RMS_VEC = 2;               // dim <= 512 * 8 * 2 = 8192
+constexpr int RMS_PK = 4;                // fp32 partial slices loaded together
+
+__device__ __forceinline__ bf16x8 ld8(const __bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
 __global__ __launch_bounds__(RMS_THREADS) void palu_rmsnorm_kernel(const __bf16* x, const __bf16* res,
                                                                    const float* res_part, int res_ks, long long part_stride,
@@ -27,40 +34,77 @@ __global__ __launch_bounds__(RMS_THREADS) void palu_rmsnorm_kernel(const __bf16*
   const int row = blockIdx.x, tid = threadIdx.x;
   const __bf16* xr = x + (long long)row * dim;
   const __bf16* rr = res ? res + (long long)row * dim : nullptr;
+  const float* pr = res_part ? res_part + (long long)row * dim : nullptr;
+
+  // Loads; a lane past the row's end reads its last vector (in bounds) and never uses it.
+  bf16x8 xa[RMS_VEC], ra[RMS_VEC], wa[RMS_VEC];
+  f32x4 pa[RMS_VEC][RMS_PK][2];
+#pragma unroll
+  for (int i = 0; i < RMS_VEC; ++i) {
+    const int e = min((tid + i * RMS_THREADS) * 8, dim - 8);
+    xa[i] = ld8(xr + e);
+    wa[i] = ld8(w + e);
+    if (rr) ra[i] = ld8(rr + e);
+    if (pr) {
+#pragma unroll
+      for (int k = 0; k < RMS_PK; ++k) {
+        const float* pp = pr + min(k, res_ks - 1) * part_stride + e;
+        pa[i][k][0] = ld4(pp);
+        pa[i][k][1] = ld4(pp + 4);
+      }
+    }
+  }
+
   float v[RMS_VEC][8];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < RMS_VEC; ++i) {
     const int e = (tid + i * RMS_THREADS) * 8;
-    if (e < dim) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(xr + e);
-      bf16x8 hv;
-      if (rr) {
-        const bf16x8 c = *reinterpret_cast<const bf16x8*>(rr + e);
+    bf16x8 hv;
+    if (rr) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) hv[j] = (__bf16)(bf(a[j]) + bf(c[j]));   // bf16 residual stream
-      } else if (res_part) {
-        // the sublayer output as the fp32 k-slice partials of its projection: summed here, in slice order
-        const float* pp = res_part + (long long)row * dim + e;
-        f32x4 s0 = *reinterpret_cast<const f32x4*>(pp), s1 = *reinterpret_cast<const f32x4*>(pp + 4);
-        for (int k = 1; k < res_ks; ++k) {
-          s0 += *reinterpret_cast<const f32x4*>(pp + k * part_stride);
-          s1 += *reinterpret_cast<const f32x4*>(pp + k * part_stride + 4);
+      for (int j = 0; j < 8; ++j) hv[j] = (__bf16)(bf(xa[i][j]) + bf(ra[i][j]));   // bf16 residual stream
+    } else if (pr) {
+      // the sublayer output as the fp32 k-slice partials of its projection: summed here, in slice order
+      f32x4 s0 = pa[i][0][0], s1 = pa[i][0][1];
+#pragma unroll
+      for (int k = 1; k < RMS_PK; ++k) {
+        if (k < res_ks) {
+          s0 += pa[i][k][0];
+          s1 += pa[i][k][1];
+        }
+      }
+      for (int k0 = RMS_PK; k0 < res_ks; k0 += RMS_PK) {
+        const int ec = min(e, dim - 8);
+        f32x4 q[RMS_PK][2];
+#pragma unroll
+        for (int k = 0; k < RMS_PK; ++k) {
+          const float* pp = pr + min(k0 + k, res_ks - 1) * part_stride + ec;
+          q[k][0] = ld4(pp);
+          q[k][1] = ld4(pp + 4);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          hv[j] = (__bf16)(bf(a[j]) + s0[j]);
-          hv[4 + j] = (__bf16)(bf(a[4 + j]) + s1[j]);
+        for (int k = 0; k < RMS_PK; ++k) {
+          if (k0 + k < res_ks) {
+            s0 += q[k][0];
+            s1 += q[k][1];
+          }
         }
-      } else {
-        hv = a;
       }
-      if (h_out) *reinterpret_cast<bf16x8*>(h_out + (long long)row * dim + e) = hv;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        v[i][j] = bf(hv[j]);
-        ss += v[i][j] * v[i][j];
+      for (int j = 0; j < 4; ++j) {
+        hv[j] = (__bf16)(bf(xa[i][j]) + s0[j]);
+        hv[4 + j] = (__bf16)(bf(xa[i][4 + j]) + s1[j]);
       }
+    } else {
+      hv = xa[i];
+    }
+    const bool live = e < dim;
+    if (live && h_out) *reinterpret_cast<bf16x8*>(h_out + (long long)row * dim + e) = hv;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[i][j] = live ? bf(hv[j]) : 0.f;
+      ss += v[i][j] * v[i][j];
     }
   }
   __shared__ float part[RMS_THREADS / 64];
@@ -76,10 +120,9 @@ __global__ __launch_bounds__(RMS_THREADS) void palu_rmsnorm_kernel(const __bf16*
   for (int i = 0; i < RMS_VEC; ++i) {
     const int e = (tid + i * RMS_THREADS) * 8;
     if (e < dim) {
-      const bf16x8 wv = *reinterpret_cast<const bf16x8*>(w + e);
       bf16x8 o;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = (__bf16)((v[i][j] * r) * bf(wv[j]));
+      for (int j = 0; j < 8; ++j) o[j] = (__bf16)((v[i][j] * r) * bf(wa[i][j]));
       *reinterpret_cast<bf16x8*>(y_out + (y_tiled ? tiled_row_offset(row, e) : (long long)row * dim + e)) = o;
     }
   }

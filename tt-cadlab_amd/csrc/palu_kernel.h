@@ -114,7 +114,7 @@ constexpr int pick_nw() {
   // -Rpass-analysis=kernel-resource-usage: every latent width pair but r_k 64 / r_v 128 does), else 4
   // waves with the 512-register budget.
   if (KFULL) return 8;
-  return (RK == 64 && RV == 128) ? 4 : 8;
+  return ((RK + 31) / 32 == 2 && RV == 128) ? 4 : 8;   // r_k 48 holds the registers of r_k 64
 }
 constexpr int MIN_NW = 4;
 constexpr int TARGET_WGS = 256;  // one workgroup per CU at full occupancy of the chip
@@ -155,6 +155,9 @@ int dispatch_latent_rows(const DecodeArgs& a, int rk, int rv, int cs_dtype, int 
 int dispatch_latent_tiled(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
 int dispatch_latent_rows_paged(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
 int dispatch_latent_tiled_paged(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
+// tiled caches whose K width is an odd multiple of 16 (48, 80, 112)
+int dispatch_latent_tiled_k16(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
+int dispatch_latent_tiled_paged_k16(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
 int dispatch_full(const DecodeArgs& a, bool tiled, bool paged, int dv, bool f32_out, hipStream_t s);
 int dispatch_glrd(const DecodeArgs& a, int cs_dtype, int out_dtype, hipStream_t s);
 size_t glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_v);
@@ -167,10 +170,28 @@ namespace {
 using namespace palu;
 
 // Offset (elements) of width-index k of position p inside one (b, g) stream of width R, K-tile order.
+// A block's positions t = p % 32 with (t / 4) % 2 == c form half-block c, 16 R elements from c * 16 R:
+// R / 32 full tiles of 512 (lane 16 gg + nn holds width-indices 32 kb + 8 gg .. +7), then, when R is an
+// odd multiple of 16, one half tile of 256 (lane 16 gg + nn holds width-indices 32 (R / 32) + 4 gg .. +3,
+// the low half of its 32-deep MFMA operand); nn = 4 (t / 8) + t % 4 is the position's operand column.
 __device__ __forceinline__ long long tiled_k_offset(int p, int k, int R) {
   const int t = p & 31, c = (t >> 2) & 1, nn = ((t >> 3) << 2) | (t & 3);
-  const int kb = k >> 5, gg = (k >> 3) & 3;
-  return (long long)(p >> 5) * (32 * R) + ((c * (R >> 5) + kb) * 64 + 16 * gg + nn) * 8 + (k & 7);
+  const int kb = k >> 5, kbf = R >> 5;
+  const long long half = (long long)(p >> 5) * (32 * R) + c * 16 * R;
+  if (kb < kbf) return half + (kb * 64 + 16 * ((k >> 3) & 3) + nn) * 8 + (k & 7);
+  return half + kbf * 512 + (16 * ((k & 15) >> 2) + nn) * 4 + (k & 3);
+}
+
+// Stores width-indices k .. k + 7 (k a multiple of 8) of position p in K-tile order: one 16-byte store
+// in a full tile, two 8-byte stores 16 lanes apart in the half tile.
+__device__ __forceinline__ void store_k8(__bf16* stream, int p, int k, int R, const bf16x8 x) {
+  const long long o = tiled_k_offset(p, k, R);
+  if ((k >> 5) < (R >> 5)) {
+    *reinterpret_cast<bf16x8*>(stream + o) = x;
+  } else {
+    *reinterpret_cast<bf16x4*>(stream + o) = bf16x4{x[0], x[1], x[2], x[3]};
+    *reinterpret_cast<bf16x4*>(stream + o + 64) = bf16x4{x[4], x[5], x[6], x[7]};
+  }
 }
 
 // V-tile order: tile mt = k / 16, slot 16 * (t / 8) + k % 16, element t % 8 (t = p % 32).
@@ -184,6 +205,12 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// Four bf16 in the low half of an MFMA operand, zeros above: a half K tile's 4 values per lane on the
+// 32-deep product, whose upper k slots then contribute exactly 0 (both operands zero there).
+__device__ __forceinline__ bf16x8 low4(const bf16x4 h) {
+  const bf16x4 z = {};
+  return __builtin_shufflevector(h, z, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 // fp32 pair -> fp16 pair, rounded toward zero: finite inputs beyond the fp16 range saturate to
@@ -335,10 +362,12 @@ template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, int NW, typename T
 // so that its 4-wave variant fits two workgroups per CU.
 __global__ __launch_bounds__(NW * 64, (NW == 8 || pick_nw<RK, RV, KFULL, TILED>() == 8) ? 2 : 1)
 void palu_decode_kernel(const DecodeArgs a) {
-  static_assert(RK % 32 == 0 && RK <= 128, "RK");
+  static_assert(RK % 16 == 0 && RK <= 128 && (TILED || RK % 32 == 0), "RK: 16-wide half tiles (tiled), 32-wide rows");
   static_assert(RV % 16 == 0 && RV <= 128 && (TILED || RV % 32 == 0), "RV: 16-wide V tiles (tiled), 32-wide rows");
   static_assert(!KFULL || RK == HD, "full K has the head dim");
-  constexpr int KB = RK / 32;   // 32-wide contraction blocks of the K operand
+  constexpr int KBF = RK / 32;              // 32-wide contraction blocks of the K operand
+  constexpr bool KH = RK % 32 != 0;         // and a 16-wide one (tiled caches)
+  constexpr int KB = KBF + (KH ? 1 : 0);    // register blocks; a half block holds 4 values, zeros above
   constexpr int VB = RV / 32;   // 32-wide blocks of a V row
   constexpr int VT = RV / 16;   // 16-wide V tiles = PV M-tiles
   using SM = Smem<RK, RV, KFULL, NW>;
@@ -459,12 +488,17 @@ void palu_decode_kernel(const DecodeArgs a) {
   };
   auto load_k = [&](int base, bool live, int pid, bf16x8 (&kd)[2][KB]) {
     if constexpr (TILED) {
-      const __bf16* kt = kbase + blk_off(base, pid, a.k_sb, RK) + (live ? lane * 8 : 0);
+      const __bf16* kt = kbase + blk_off(base, pid, a.k_sb, RK);
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
+      for (int c = 0; c < 2; ++c) {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-          kd[c][kb] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(kt + (c * KB + kb) * 512));
+        for (int kb = 0; kb < KBF; ++kb)
+          kd[c][kb] = __builtin_nontemporal_load(
+              reinterpret_cast<const bf16x8*>(kt + c * 16 * RK + kb * 512 + (live ? lane * 8 : 0)));
+        if constexpr (KH)
+          kd[c][KBF] = low4(__builtin_nontemporal_load(
+              reinterpret_cast<const bf16x4*>(kt + c * 16 * RK + KBF * 512 + (live ? lane * 4 : 0))));
+      }
     } else {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -614,10 +648,13 @@ void palu_decode_kernel(const DecodeArgs a) {
   bf16x8 ukA[UK_LDS ? 1 : 8][UK_LDS ? 1 : KB];
   if constexpr (!KFULL && !UK_LDS) {
 #pragma unroll
-    for (int rt = 0; rt < 8; ++rt)
+    for (int rt = 0; rt < 8; ++rt) {
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+      for (int kb = 0; kb < KBF; ++kb)
         ukA[rt][kb] = *reinterpret_cast<const bf16x8*>(ukT + (16 * rt + n) * SM::UKT_STRIDE + 32 * kb + 8 * g);
+      if constexpr (KH)
+        ukA[rt][KBF] = low4(*reinterpret_cast<const bf16x4*>(ukT + (16 * rt + n) * SM::UKT_STRIDE + 32 * KBF + 4 * g));
+    }
   }
 
   // ROWS: identity B operands that move one 16-column slice of a 32-wide V block into the PV layout.
@@ -731,7 +768,7 @@ void palu_decode_kernel(const DecodeArgs a) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) acc[c][h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+        for (int kb = 0; kb < KBF; ++kb)
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const int rt = 2 * kq + h;
@@ -743,6 +780,22 @@ void palu_decode_kernel(const DecodeArgs a) {
 #pragma unroll
             for (int c = 0; c < 2; ++c) acc[c][h] = mfma16(ua, kc[c][kb], acc[c][h]);
           }
+        if constexpr (KH) {
+          // the last 16 ranks: lane (n, g) holds ranks 32 KBF + 4 g .. +3 of its u_k^T row and latent
+          // column in the low half of both operands and zeros above, so the same 32-deep product (one
+          // opcode on the whole accumulation chain) adds exactly their contribution
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int rt = 2 * kq + h;
+            bf16x8 ua;
+            if constexpr (UK_LDS)
+              ua = low4(*reinterpret_cast<const bf16x4*>(ukT + uk_off - 4 * g + 16 * rt * SM::UKT_STRIDE + 32 * KBF));
+            else
+              ua = ukA[rt][KBF];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) acc[c][h] = mfma16(ua, kc[c][KBF], acc[c][h]);
+          }
+        }
         // RoPE by the block offset of this lane's position, (x0, x1) -> (x0 c - x1 s, x1 c + x0 s), in
         // packed fp16: (x0, x1) * (c, c) + (x1, x0) * (-s, s) is one multiply and one fma per pair. The
         // rotated slice is the fp16 A operand of the QK product as it stands.
@@ -835,7 +888,7 @@ void palu_decode_kernel(const DecodeArgs a) {
   // The early K refill keeps one more K buffer live through the softmax and PV; it is used where
   // that still fits the register budget without spilling (full K, r_k <= 64, r_k + r_v <= 192; the
   // rest refill K together with V after the PV product).
-  constexpr bool EARLY_K = KFULL || RK <= 64 || RK + RV <= 192;
+  constexpr bool EARLY_K = KFULL || KB * 32 <= 64 || KB * 32 + RV <= 192;
   int p = w;
   while (p < npairs) {
     int pn = p + NW;
@@ -1035,27 +1088,38 @@ int dispatch_rv(const DecodeArgs& a, int rv, hipStream_t s) {
                                  "tiled caches)", rv);
 }
 
-template <bool TILED, bool PAGED, typename TabT, typename OutT>
+// K16: the widths that end in a half tile (tiled caches only), built in translation units of their own.
+template <bool TILED, bool PAGED, bool K16, typename TabT, typename OutT>
 int dispatch_latent(const DecodeArgs& a, int rk, int rv, hipStream_t s) {
-  switch (rk) {
-    case 32: return dispatch_rv<32, false, TILED, PAGED, TabT, OutT>(a, rv, s);
-    case 64: return dispatch_rv<64, false, TILED, PAGED, TabT, OutT>(a, rv, s);
-    case 96: return dispatch_rv<96, false, TILED, PAGED, TabT, OutT>(a, rv, s);
-    case 128: return dispatch_rv<128, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+  if constexpr (K16) {
+    static_assert(TILED, "half K tiles exist in the tiled layout only");
+    switch (rk) {
+      case 48: return dispatch_rv<48, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+      case 80: return dispatch_rv<80, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+      case 112: return dispatch_rv<112, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+    }
+  } else {
+    switch (rk) {
+      case 32: return dispatch_rv<32, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+      case 64: return dispatch_rv<64, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+      case 96: return dispatch_rv<96, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+      case 128: return dispatch_rv<128, false, TILED, PAGED, TabT, OutT>(a, rv, s);
+    }
   }
-  return fail(PALU_EUNSUPPORTED, "r_k %d: this build rebuilds K from latents of width 32, 64, 96 or 128", rk);
+  return fail(PALU_EUNSUPPORTED, "r_k %d: this build rebuilds K from latents of width 32, 64, 96 or 128 (and 48, 80, "
+                                 "112 for tiled caches)", rk);
 }
 
 
 // The four (table dtype, output dtype) instantiations of one cache layout.
-template <bool TILED, bool PAGED>
+template <bool TILED, bool PAGED, bool K16 = false>
 int dispatch_dtypes(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s) {
   const bool f32o = out_dtype == PALU_DTYPE_F32;
   if (cs_dtype == PALU_DTYPE_F32)
-    return f32o ? dispatch_latent<TILED, PAGED, float, float>(a, rk, rv, s)
-                : dispatch_latent<TILED, PAGED, float, __bf16>(a, rk, rv, s);
-  return f32o ? dispatch_latent<TILED, PAGED, __bf16, float>(a, rk, rv, s)
-              : dispatch_latent<TILED, PAGED, __bf16, __bf16>(a, rk, rv, s);
+    return f32o ? dispatch_latent<TILED, PAGED, K16, float, float>(a, rk, rv, s)
+                : dispatch_latent<TILED, PAGED, K16, float, __bf16>(a, rk, rv, s);
+  return f32o ? dispatch_latent<TILED, PAGED, K16, __bf16, float>(a, rk, rv, s)
+              : dispatch_latent<TILED, PAGED, K16, __bf16, __bf16>(a, rk, rv, s);
 }
 
 }  // namespace

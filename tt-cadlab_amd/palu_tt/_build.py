@@ -19,7 +19,8 @@ INCLUDE = REPO / "include"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_NAME = "libpalu_mi355x.so"
 SOURCES = ["palu_capi.hip", "palu_decode_rows.hip", "palu_decode_tiled.hip", "palu_decode_rows_paged.hip",
-           "palu_decode_tiled_paged.hip", "palu_decode_full.hip", "palu_glrd.hip", "palu_decoder.hip", "palu_linear.hip"]
+           "palu_decode_tiled_paged.hip", "palu_decode_tiled_k16.hip", "palu_decode_tiled_paged_k16.hip",
+           "palu_decode_full.hip", "palu_glrd.hip", "palu_decoder.hip", "palu_linear.hip"]
 HEADERS = ["palu_kernel.h"]
 
 HIPCC_FLAGS = [

@@ -64,10 +64,11 @@ class PaluAttention(torch.nn.Module):
         self.r_k = int(self.palu.rank_k[layer_num])
         self.r_v = int(self.palu.rank_v[layer_num])
         hd = self.head_dim
-        # V latents are 16-wide tiles in a tiled cache (per-head latents); everything else is in 32s
-        v_step = 16 if (cache_layout == "tiled" and self.gs == 1) else 32
-        assert self.r_k % 32 == 0 and self.r_v % v_step == 0 and self.r_k <= self.gs * hd and self.r_v <= self.gs * hd, \
-            f"ranks r_k = {self.r_k} (a multiple of 32), r_v = {self.r_v} (a multiple of {v_step})"
+        # tiled caches of per-head latents take ranks in multiples of 16 (16-wide V tiles, K rows ending in a
+        # half tile); row-major caches and grouped latents keep multiples of 32
+        step = 16 if (cache_layout == "tiled" and self.gs == 1) else 32
+        assert self.r_k % step == 0 and self.r_v % step == 0 and self.r_k <= self.gs * hd and self.r_v <= self.gs * hd, \
+            f"ranks r_k = {self.r_k}, r_v = {self.r_v} must be multiples of {step}"
         # full-rank per-head factors collapse to stock K / V (reference attention.py:136-141)
         self.recon_k = self.gs > 1 or self.r_k < hd
         self.recon_v = self.gs > 1 or self.r_v < hd

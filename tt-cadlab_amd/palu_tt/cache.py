@@ -8,12 +8,15 @@ order of the kernel's MFMAs, so a wave reads one contiguous KB per load instruct
 the matrix cores without any regrouping. The order depends on the cache's role:
 
   K caches ("k"): tile c * (r/32) + kb, slot l = 16*g + n (g < 4, n < 16) holds r-index 32*kb + 8*g
-    .. +7 of block position 8*(n//4) + 4*c + n%4 (the operand of the K rebuild);
+    .. +7 of block position 8*(n//4) + 4*c + n%4 (the operand of the K rebuild). When r is an odd
+    multiple of 16, each half-block c (its 16 * r elements start at c * 16 * r) ends in a 512-byte half
+    tile: slot l = 16*g + n holds the 4 r-indices 32*(r//32) + 4*g .. +3 (the low half of the lane's
+    operand, zeros above);
   V caches ("v"): tile mt, slot l = 16*g + m holds block positions 8*g .. 8*g + 7 of r-index 16*mt + m
     (the operand of the probability-times-V product).
 
-The storage tensor is [B, G, S/32, r/16, 64, 8] bf16; ``from_rows`` / ``to_rows`` convert to and from
-the logical row-major tensor.
+The storage tensor is [B, G, S/32, r/16, 64, 8] bf16 (one 32-position block is 32 * r elements in that
+order); ``from_rows`` / ``to_rows`` convert to and from the logical row-major tensor.
 """
 from dataclasses import dataclass
 from typing import Tuple
@@ -30,24 +33,36 @@ def rows_to_tiled(rows: torch.Tensor, role: str = "k") -> torch.Tensor:
     """[B, G, S, r] -> tiled storage [B, G, S/32, r/16, 64, 8] in the role's tile order."""
     B, G, S, r = rows.shape
     assert role in ROLES, f"role must be 'k' or 'v', got {role!r}"
-    step = 32 if role == "k" else 16            # K tiles pair 32-wide rank blocks; V tiles are 16 wide
-    assert S % BLOCK == 0 and r % step == 0, f"tiled {role} layout needs S % 32 == 0 and r % {step} == 0, got S={S}, r={r}"
+    assert S % BLOCK == 0 and r % 16 == 0, f"tiled {role} layout needs S % 32 == 0 and r % 16 == 0, got S={S}, r={r}"
+    nb, kbf = S // BLOCK, r // 32
     if role == "k":
         # position 32*blk + 8*tb + 4*c + i, r-index 32*kb + 8*g + j  ->  [blk][c][kb][g][tb][i][j]
-        x = rows.reshape(B, G, S // BLOCK, 4, 2, 4, r // 32, 4, 8).permute(0, 1, 2, 4, 6, 7, 3, 5, 8)
+        blk = rows.reshape(B, G, nb, 4, 2, 4, r)
+        x = blk[..., :32 * kbf].reshape(B, G, nb, 4, 2, 4, kbf, 4, 8).permute(0, 1, 2, 4, 6, 7, 3, 5, 8)
+        x = x.reshape(B, G, nb, 2, kbf * 512)
+        if r % 32:
+            # half tile: r-index 32*kbf + 4*g + j  ->  [blk][c][g][tb][i][j]
+            h = blk[..., 32 * kbf:].reshape(B, G, nb, 4, 2, 4, 4, 4).permute(0, 1, 2, 4, 6, 3, 5, 7)
+            x = torch.cat([x, h.reshape(B, G, nb, 2, 256)], dim=-1)
     else:
         # position 32*blk + 8*g + j, r-index 16*mt + m  ->  [blk][mt][g][m][j]
-        x = rows.reshape(B, G, S // BLOCK, 4, 8, r // 16, 16).permute(0, 1, 2, 5, 3, 6, 4)
-    return x.reshape(B, G, S // BLOCK, r // 16, 64, 8).contiguous()
+        x = rows.reshape(B, G, nb, 4, 8, r // 16, 16).permute(0, 1, 2, 5, 3, 6, 4)
+    return x.reshape(B, G, nb, r // 16, 64, 8).contiguous()
 
 
 def tiled_to_rows(tiled: torch.Tensor, role: str = "k") -> torch.Tensor:
     """Inverse of rows_to_tiled."""
     B, G, nblk, ntile, _, _ = tiled.shape
     r = ntile * 16
+    kbf = r // 32
     if role == "k":
-        x = tiled.reshape(B, G, nblk, 2, r // 32, 4, 4, 4, 8)     # [blk][c][kb][g][tb][i][j]
-        x = x.permute(0, 1, 2, 6, 3, 7, 4, 5, 8)                 # [blk][tb][c][i][kb][g][j]
+        flat = tiled.reshape(B, G, nblk, 2, 16 * r)               # the two half-blocks c
+        x = flat[..., :kbf * 512].reshape(B, G, nblk, 2, kbf, 4, 4, 4, 8)   # [blk][c][kb][g][tb][i][j]
+        x = x.permute(0, 1, 2, 6, 3, 7, 4, 5, 8).reshape(B, G, nblk, 4, 2, 4, 32 * kbf)  # [blk][tb][c][i][kb g j]
+        if r % 32:
+            h = flat[..., kbf * 512:].reshape(B, G, nblk, 2, 4, 4, 4, 4)     # [blk][c][g][tb][i][j]
+            h = h.permute(0, 1, 2, 5, 3, 6, 4, 7).reshape(B, G, nblk, 4, 2, 4, 16)  # [blk][tb][c][i][g j]
+            x = torch.cat([x, h], dim=-1)
     else:
         x = tiled.reshape(B, G, nblk, r // 16, 4, 16, 8)         # [blk][mt][g][m][j]
         x = x.permute(0, 1, 2, 4, 6, 3, 5)                       # [blk][g][j][mt][m]
@@ -67,8 +82,7 @@ class LatentCache:
     def zeros(batch: int, n_groups: int, max_seq: int, width: int, device, role: str = "k",
               dtype=torch.bfloat16) -> "LatentCache":
         assert max_seq % BLOCK == 0, f"max_seq must be a multiple of {BLOCK}, got {max_seq}"
-        step = 32 if role == "k" else 16
-        assert width % step == 0, f"a tiled {role} cache's width must be a multiple of {step}, got {width}"
+        assert width % 16 == 0, f"a tiled {role} cache's width must be a multiple of 16, got {width}"
         return LatentCache(torch.zeros(batch, n_groups, max_seq // BLOCK, width // 16, 64, 8, dtype=dtype,
                                        device=device), role)
 
