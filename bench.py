@@ -327,12 +327,12 @@ def measure_e2e(a, dev):
         t_pre = time.perf_counter() - t0
         step = model.decode if a.e2e_no_graph else model.decode_graph
         pos = torch.full((B,), P, dtype=torch.int32, device=dev)
-        step(tok, pos)                                    # capture / warm-up at position P (rewritten below)
+        step(tok, pos, greedy=True)                       # capture / warm-up at position P (rewritten below)
         torch.cuda.synchronize()
         toks = [tok]
         t0 = time.perf_counter()
         for _ in range(n_new - 1):
-            tok = step(tok, pos).argmax(-1)
+            tok = step(tok, pos, greedy=True).clone()     # the step's argmax ids (the graph's buffer is reused)
             toks.append(tok)
             pos += 1
         torch.cuda.synchronize()

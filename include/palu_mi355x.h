@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define PALU_ABI_VERSION 10
+#define PALU_ABI_VERSION 11
 
 #define PALU_OK 0
 #define PALU_EINVAL 1       /* arguments outside the op's envelope */
@@ -240,6 +240,13 @@ int palu_rmsnorm(const void* x, const void* res, const float* res_part, int res_
 /* out[r][f] = silu(gu[r][f]) * gu[r][ffn + f] for gu [rows, 2 ffn], out [rows, ffn]; ffn a multiple of 8.
  * out_tiled = 1 writes out in the 64-row tiled activation layout (rows <= 64, ffn a multiple of 32). */
 int palu_swiglu(const void* gu, void* out, int rows, int ffn, int out_tiled, palu_stream_t stream);
+
+/* Greedy sampling: out[r] = index of the largest value of row r of x (bf16, rows of n values, row stride
+ * ld elements: ld >= n, a multiple of 8), the first one among equal maxima and NaN above every number
+ * (torch.argmax's result). No counterpart in the reference's op interface: its generation loop takes
+ * the argmax of the host-side logits (generate.py:53-62); this keeps the decode step's greedy pick in
+ * the same HIP graph as the step. */
+int palu_argmax_rows(const void* x, long long ld, int rows, int n, int64_t* out, palu_stream_t stream);
 
 /* Meta-interleaved RoPE of `heads` 128-wide heads per row at the row's position:
  * dst[b, h, :] = rotate(src[b * src_row_stride + h * 128 .. +127], pos[b]), pairs (2i, 2i+1) ->

@@ -172,6 +172,24 @@ def test_linear_tiled_activations(gpu, rows, n, k, rtw, ks):
     _check_linear(a, _linear_ref(x, w))
 
 
+@pytest.mark.parametrize("rows,n,stride", [(64, 128256, 128256), (3, 1000, 1008), (1, 7, 8), (5, 4099, 4104)])
+def test_argmax_rows_matches_torch(gpu, rows, n, stride):
+    """First index among equal maxima (planted ties, a row of equal values), NaN above every number."""
+    g = torch.Generator().manual_seed(n)
+    buf = torch.randn(rows, stride, generator=g).to(torch.bfloat16)
+    x = buf[:, :n]
+    x[0, n // 3] = x[0, n - 1] = 9.0                        # tie: the first index wins
+    if rows > 1:
+        x[1] = 0.5                                           # all equal: index 0
+    if rows > 2:
+        x[2, n // 2] = float("nan")                          # NaN wins over every number
+        x[2, n - 2] = float("nan")
+    xd = buf.to(gpu)[:, :n]
+    got = decoder_ops.argmax_rows(xd)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), torch.argmax(x.float(), dim=-1))
+
+
 @pytest.mark.parametrize("rows", [64, 9])
 def test_rmsnorm_and_swiglu_write_the_tiled_layout(gpu, rows):
     """rmsnorm / swiglu with tiled_out write exactly tile_rows of their row-major outputs."""

@@ -69,9 +69,13 @@ def test_decoder_teacher_forced_matches_lowrank_llama(gpu, layout):
         pos = torch.full((B,), S + t, dtype=torch.int32, device=gpu)
         eager = model.decode(tok, pos)
         graph = model.decode_graph(tok, pos).clone()                      # rewrites the same cache rows
+        greedy = model.decode_graph(tok, pos, greedy=True).clone()
         torch.cuda.synchronize()
         _check(eager, exp[:, S + t], f"decode step {t}")
         assert ref.cosine(graph.cpu(), eager.cpu()) >= 0.99999, f"graph replay differs at step {t}"
+        # the greedy graph's ids pick a maximal logit of the step (up to the steps' own differences)
+        e = eager.cpu()
+        assert (e.max(-1).values - e.gather(1, greedy.cpu()[:, None])[:, 0]).abs().max() <= 1e-2 * e.abs().max()
 
 
 def test_generate_greedy_is_consistent_with_decode(gpu):

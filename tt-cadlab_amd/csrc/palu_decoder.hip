@@ -128,6 +128,63 @@ __global__ __launch_bounds__(RMS_THREADS) void palu_rmsnorm_kernel(const __bf16*
   }
 }
 
+// Greedy sampling's argmax: out[r] = the index of the largest value of row r, the first one among equal
+// maxima, NaN above every number (torch.argmax's order). One workgroup per row; each thread scans every
+// ARG_THREADS-th 8-element vector in index order, ARG_UNROLL loads at a time, then the workgroup reduces
+// the (value, index) pairs.
+constexpr int ARG_THREADS = 1024;
+constexpr int ARG_UNROLL = 8;
+
+__device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na != nb) return na;
+  if (!na && a != b) return a > b;
+  return ia < ib;
+}
+
+__global__ __launch_bounds__(ARG_THREADS) void palu_argmax_kernel(const __bf16* x, long long ld, int n,
+                                                                  int64_t* out) {
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const __bf16* xr = x + (long long)row * ld;
+  float best = -__builtin_huge_valf();
+  int bi = 0x7fffffff;
+  const int nv = n / 8;                               // whole vectors; the tail is scanned below
+  for (int v0 = tid; v0 < nv; v0 += ARG_THREADS * ARG_UNROLL) {
+    bf16x8 buf[ARG_UNROLL];
+#pragma unroll
+    for (int u = 0; u < ARG_UNROLL; ++u) {
+      const int v = min(v0 + u * ARG_THREADS, nv - 1);   // in bounds; duplicates are skipped below
+      buf[u] = *reinterpret_cast<const bf16x8*>(xr + 8LL * v);
+    }
+#pragma unroll
+    for (int u = 0; u < ARG_UNROLL; ++u) {
+      const int v = v0 + u * ARG_THREADS;
+      if (v < nv) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (arg_better(bf(buf[u][j]), 8 * v + j, best, bi)) { best = bf(buf[u][j]); bi = 8 * v + j; }
+      }
+    }
+  }
+  for (int e = 8 * nv + tid; e < n; e += ARG_THREADS)
+    if (arg_better(bf(xr[e]), e, best, bi)) { best = bf(xr[e]); bi = e; }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (arg_better(ob, oi, best, bi)) { best = ob; bi = oi; }
+  }
+  __shared__ float sv[ARG_THREADS / 64];
+  __shared__ int si[ARG_THREADS / 64];
+  if ((tid & 63) == 0) { sv[tid >> 6] = best; si[tid >> 6] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < ARG_THREADS / 64; ++w)
+      if (arg_better(sv[w], si[w], best, bi)) { best = sv[w]; bi = si[w]; }
+    out[row] = bi;
+  }
+}
+
 // out[r][f] = silu(g) * u with g = gu[r][f], u = gu[r][ffn + f]; 8 elements per thread.
 __global__ __launch_bounds__(256) void palu_swiglu_kernel(const __bf16* gu, __bf16* out, int rows, int ffn,
                                                           int out_tiled) {
@@ -212,6 +269,18 @@ int palu_rmsnorm(const void* x, const void* res, const float* res_part, int res_
                      eps, y_tiled ? 1 : 0);
   return launched("palu_rmsnorm");
 }
+int palu_argmax_rows(const void* x, long long ld, int rows, int n, int64_t* out, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  if (!x || !out) return fail(PALU_EINVAL, "palu_argmax_rows: a required pointer is null");
+  if (rows <= 0 || rows > 65535 || n <= 0 || ld < n || ld % 8 != 0)
+    return fail(PALU_EINVAL, "palu_argmax_rows: rows %d (1..65535), n %d and a row stride %lld >= n, a multiple of 8",
+                rows, n, ld);
+  if (!a16(x)) return fail(PALU_EINVAL, "palu_argmax_rows: 16-byte alignment required");
+  hipLaunchKernelGGL(palu_argmax_kernel, dim3(rows), dim3(ARG_THREADS), 0, stream, static_cast<const __bf16*>(x), ld, n,
+                     out);
+  return launched("palu_argmax_rows");
+}
+
 int palu_swiglu(const void* gu, void* out, int rows, int ffn, int out_tiled, hipStream_t stream) {
   palu::g_err[0] = 0;
   if (!gu || !out) return fail(PALU_EINVAL, "palu_swiglu: a required pointer is null");

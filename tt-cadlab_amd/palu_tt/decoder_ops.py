@@ -55,6 +55,22 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, res: Optional[tor
     return out
 
 
+def argmax_rows(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """torch.argmax(x, dim=-1) of a bf16 [rows, n] tensor (row-strided, stride a multiple of 8) as int64
+    [rows]: the first index among equal maxima, NaN above every number."""
+    _check(x, "x")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise RuntimeError("x must be a row-strided [rows, n] bf16 view")
+    rows, n = x.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=x.device)
+    if out.dtype != torch.int64 or out.shape != (rows,) or not out.is_contiguous() or out.device != x.device:
+        raise RuntimeError(f"out must be a contiguous int64 [{rows}] tensor on {x.device}")
+    _native.check(_native.load().palu_argmax_rows(_native.ptr(x), x.stride(0), rows, n, _native.ptr(out),
+                                                  _native.stream_handle(x.device)))
+    return out
+
+
 def swiglu(gu: torch.Tensor, out: Optional[torch.Tensor] = None, tiled_out: bool = False) -> torch.Tensor:
     """silu(g) * u for gu = [g | u] of shape [rows, 2 ffn]; returns [rows, ffn], or with tiled_out a
     [64, ffn] buffer in the tiled activation layout (rows <= 64)."""

@@ -109,9 +109,10 @@ class Transformer(torch.nn.Module):
         return F.linear(rms_norm(h[:, -1], self.norm_w, eps), self.output.plain()).float()
 
     @torch.no_grad()
-    def decode(self, tokens: torch.Tensor, current_pos: torch.Tensor) -> torch.Tensor:
+    def decode(self, tokens: torch.Tensor, current_pos: torch.Tensor, greedy: bool = False) -> torch.Tensor:
         """One decode step for all max_batch_size rows: tokens [B] at positions current_pos [B] (int32,
-        device); returns logits [B, vocab] fp32. The residual stream h is updated in place: each RMSNorm
+        device); returns logits [B, vocab] fp32, or with greedy the argmax token ids [B] int64 taken from
+        the bf16 logits (the same ids as argmax of the fp32 ones). The residual stream h is updated in place: each RMSNorm
         kernel first adds the previous sublayer's output to it, as the fp32 split partials of its output
         projection. For up to 64 rows the RMSNorm kernels and the gate / up projection (SwiGLU in its
         epilogue) write their outputs in the tiled activation layout that the next projections read."""
@@ -130,27 +131,34 @@ class Transformer(torch.nn.Module):
                 a, at = decoder_ops.untile_rows(a, B), False
             f = L["w2"](a, x_tiled=at, rows=B, mode="partials")
         y = decoder_ops.rmsnorm(h, self.norm_w, eps, res_part=f, tiled_out=xt)
-        return self.output(y, x_tiled=xt, rows=B).float()
+        logits = self.output(y, x_tiled=xt, rows=B)
+        return decoder_ops.argmax_rows(logits) if greedy else logits.float()
 
     @torch.no_grad()
-    def decode_graph(self, tokens: torch.Tensor, current_pos: torch.Tensor) -> torch.Tensor:
-        """decode() replayed from a HIP graph captured on first use; tokens and current_pos are copied into
-        the graph's static inputs (the caller's tensors may change between steps)."""
+    def decode_graph(self, tokens: torch.Tensor, current_pos: torch.Tensor, greedy: bool = False) -> torch.Tensor:
+        """decode() replayed from a HIP graph captured on first use (one graph per value of greedy); tokens
+        and current_pos are copied into the graph's static inputs (the caller's tensors may change between
+        steps). The returned tensor is the graph's output buffer, rewritten by the next replay."""
         if self._graph is None:
-            self._tok = tokens.clone()
-            self._pos = current_pos.clone()
+            self._graph = {}
+        if greedy not in self._graph:
+            if not hasattr(self, "_tok"):
+                self._tok = tokens.clone()
+                self._pos = current_pos.clone()
             s = torch.cuda.Stream(self.device)
             s.wait_stream(torch.cuda.current_stream(self.device))
             with torch.cuda.stream(s):
-                self._graph_warm = self.decode(self._tok, self._pos)     # sets kernel attributes outside capture
+                self.decode(self._tok, self._pos, greedy)                # sets kernel attributes outside capture
             torch.cuda.current_stream(self.device).wait_stream(s)
-            self._graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self._graph):
-                self._logits = self.decode(self._tok, self._pos)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                out = self.decode(self._tok, self._pos, greedy)
+            self._graph[greedy] = (g, out)
+        g, out = self._graph[greedy]
         self._tok.copy_(tokens)
         self._pos.copy_(current_pos)
-        self._graph.replay()
-        return self._logits
+        g.replay()
+        return out
 
 
 def draw_ranks(n_layers: int, seed: int, lo: int = 32, hi: int = 128, step: int = 8, mean: float = 64.0) -> List[int]:
@@ -228,8 +236,7 @@ def generate(model: Transformer, prompts: torch.Tensor, n_new: int, use_graph: b
     pos = torch.full((B,), S, dtype=torch.int32, device=model.device)
     step = model.decode_graph if use_graph else model.decode
     for t in range(n_new - 1):
-        logits = step(tok, pos)
-        tok = logits.argmax(-1)
+        tok = step(tok, pos, greedy=True).clone()                    # argmax of the step's logits
         out.append(tok)
         pos += 1
     return torch.stack(out, dim=1)
