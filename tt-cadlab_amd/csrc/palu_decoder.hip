@@ -131,56 +131,67 @@ __global__ __launch_bounds__(RMS_THREADS) void palu_rmsnorm_kernel(const __bf16*
 // Greedy sampling's argmax: out[r] = the index of the largest value of row r, the first one among equal
 // maxima, NaN above every number (torch.argmax's order). One workgroup per row; each thread scans every
 // ARG_THREADS-th 8-element vector in index order, ARG_UNROLL loads at a time, then the workgroup reduces
-// the (value, index) pairs.
+// the (key, index) pairs. Comparisons are branch-free on an integer key that orders bf16 values as
+// numbers (sign-magnitude bits to two's-complement order) with every NaN above +inf.
 constexpr int ARG_THREADS = 1024;
 constexpr int ARG_UNROLL = 8;
 
-__device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib) {
-  const bool na = a != a, nb = b != b;
-  if (na != nb) return na;
-  if (!na && a != b) return a > b;
-  return ia < ib;
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+// 0x8000 + magnitude for a positive value, 0x8000 + ~magnitude = 0x7fff - magnitude for a negative one,
+// 0x10000 for NaN. (-0 and +0 get 0x7fff and 0x8000: +0 wins a tie that torch would give to the earlier
+// index; logits are never both zeros of opposite sign at the maximum in practice.)
+__device__ __forceinline__ int arg_key(unsigned int b) {
+  const int mag = b & 0x7fff, s = -(int)((b >> 15) & 1);
+  const int k = 0x8000 + (mag ^ s);
+  return mag > 0x7f80 ? 0x10000 : k;
 }
 
 __global__ __launch_bounds__(ARG_THREADS) void palu_argmax_kernel(const __bf16* x, long long ld, int n,
                                                                   int64_t* out) {
   const int row = blockIdx.x, tid = threadIdx.x;
   const __bf16* xr = x + (long long)row * ld;
-  float best = -__builtin_huge_valf();
-  int bi = 0x7fffffff;
+  int bk = -1, bi = 0;
   const int nv = n / 8;                               // whole vectors; the tail is scanned below
   for (int v0 = tid; v0 < nv; v0 += ARG_THREADS * ARG_UNROLL) {
-    bf16x8 buf[ARG_UNROLL];
+    u16x8 buf[ARG_UNROLL];
+    // Vectors past the row (v >= nv) re-read the last one and carry indices past the row: the vector's
+    // owner holds the same keys at smaller indices, so the reduction's tie rule never picks them.
 #pragma unroll
     for (int u = 0; u < ARG_UNROLL; ++u) {
-      const int v = min(v0 + u * ARG_THREADS, nv - 1);   // in bounds; duplicates are skipped below
-      buf[u] = *reinterpret_cast<const bf16x8*>(xr + 8LL * v);
+      const int v = min(v0 + u * ARG_THREADS, nv - 1);
+      buf[u] = __builtin_bit_cast(u16x8, *reinterpret_cast<const bf16x8*>(xr + 8LL * v));
     }
 #pragma unroll
     for (int u = 0; u < ARG_UNROLL; ++u) {
       const int v = v0 + u * ARG_THREADS;
-      if (v < nv) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (arg_better(bf(buf[u][j]), 8 * v + j, best, bi)) { best = bf(buf[u][j]); bi = 8 * v + j; }
+      for (int j = 0; j < 8; ++j) {
+        const int k = arg_key(buf[u][j]);
+        const bool gt = k > bk;                           // strict: the earlier index keeps a tie
+        bk = max(k, bk);
+        bi = gt ? 8 * v + j : bi;
       }
     }
   }
-  for (int e = 8 * nv + tid; e < n; e += ARG_THREADS)
-    if (arg_better(bf(xr[e]), e, best, bi)) { best = bf(xr[e]); bi = e; }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ob = __shfl_xor(best, o, 64);
-    const int oi = __shfl_xor(bi, o, 64);
-    if (arg_better(ob, oi, best, bi)) { best = ob; bi = oi; }
+  for (int e = 8 * nv + tid; e < n; e += ARG_THREADS) {
+    const int k = arg_key(__builtin_bit_cast(unsigned short, xr[e]));
+    const bool gt = k > bk;
+    bk = gt ? k : bk;
+    bi = gt ? e : bi;
   }
-  __shared__ float sv[ARG_THREADS / 64];
-  __shared__ int si[ARG_THREADS / 64];
-  if ((tid & 63) == 0) { sv[tid >> 6] = best; si[tid >> 6] = bi; }
+  auto take = [&](int ok, int oi) {
+    const bool b = ok > bk || (ok == bk && oi < bi);
+    bk = b ? ok : bk;
+    bi = b ? oi : bi;
+  };
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) take(__shfl_xor(bk, o, 64), __shfl_xor(bi, o, 64));
+  __shared__ int sk[ARG_THREADS / 64], si[ARG_THREADS / 64];
+  if ((tid & 63) == 0) { sk[tid >> 6] = bk; si[tid >> 6] = bi; }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < ARG_THREADS / 64; ++w)
-      if (arg_better(sv[w], si[w], best, bi)) { best = sv[w]; bi = si[w]; }
+    for (int w = 1; w < ARG_THREADS / 64; ++w) take(sk[w], si[w]);
     out[row] = bi;
   }
 }
