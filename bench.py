@@ -225,12 +225,11 @@ def measure_paged(dev, steps, warmup):
 
 def measure_glrd(dev, steps, warmup):
     """G-LRD group size 4: 8 KV heads in 2 groups sharing one K and one V latent, per-group ranks
-    drawn from {128, 192, 256, 384, 512} (seeded; the caches are as wide as the widest group, the
-    narrower group's columns padding the op never reads), V rebuilt per head in-kernel; batch 16, ctx
-    16384, tiled bf16.
+    drawn from {128, 192, 256, 384, 512} (seeded; each group's latents stored at its own ranks,
+    GroupedLatentCache), V rebuilt per head in-kernel; batch 16, ctx 16384, tiled bf16.
     Also the widest layer (512, 512) and the stock full-KV decode at the same shape."""
     from palu_tt import fused
-    from palu_tt.cache import LatentCache
+    from palu_tt.cache import GroupedLatentCache, LatentCache
     B, S, hpg = 16, 16384, 4
     ng = NKV // hpg
     g = torch.Generator().manual_seed(4)
@@ -247,15 +246,19 @@ def measure_glrd(dev, steps, warmup):
         gd = torch.Generator(device=dev).manual_seed(r_k + r_v)
         layers = []
         for _ in range(n_layers):
-            k = LatentCache.zeros(B, ng, S, r_k, dev, "k")
-            v = LatentCache.zeros(B, ng, S, r_v, dev, "v")
+            if note == "drawn":
+                k = GroupedLatentCache.zeros(B, drawn_k, S, dev, "k")
+                v = GroupedLatentCache.zeros(B, drawn_v, S, dev, "v")
+            else:
+                k = LatentCache.zeros(B, ng, S, r_k, dev, "k")
+                v = LatentCache.zeros(B, ng, S, r_v, dev, "v")
             k.data.normal_(generator=gd)
             v.data.normal_(generator=gd)
             layers.append((k, v))
         u_k = torch.randn(NKV, r_k, HD, generator=g) / r_k ** 0.5
         u_v = torch.randn(NKV, r_v, HD, generator=g) / r_v ** 0.5
-        # the drawn layer: each group at its own ranks, the narrower group zero-padded in the factors (as
-        # load_palu_dir pads it) and the op told the groups' ranks, so it reads only their own columns
+        # the drawn layer: each group's latents at its own ranks (compact caches), the narrower group
+        # zero-padded in the factors (as load_palu_dir pads it); the op reads only each group's columns
         group_ranks = (drawn_k, drawn_v) if note == "drawn" else None
         if group_ranks is not None:
             for gi in range(ng):
@@ -281,7 +284,7 @@ def measure_glrd(dev, steps, warmup):
                     2 * B * hpg * NQ // NKV * rv_g * HD for rk_g, rv_g in zip(gk, gv))
         res.append({"ranks": note, "rank_k": r_k, "rank_v": r_v, "group_ranks": {"k": gk, "v": gv},
                     "us_per_layer": round(wall * 1e3, 2), "kernel_us": round(kern * 1e3, 2),
-                    "cache_bytes": B * ng * S * (r_k + r_v) * 2, **_roof(nbytes, flops, kern)})
+                    "cache_bytes": layers[0][0].nbytes() + layers[0][1].nbytes(), **_roof(nbytes, flops, kern)})
         del layers
         torch.cuda.empty_cache()
     kv = [(LatentCache.zeros(B, NKV, S, HD, dev, "k"), LatentCache.zeros(B, NKV, S, HD, dev, "v")) for _ in range(2)]

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define PALU_ABI_VERSION 11
+#define PALU_ABI_VERSION 12
 
 #define PALU_OK 0
 #define PALU_EINVAL 1       /* arguments outside the op's envelope */
@@ -49,6 +49,11 @@ extern "C" {
 #define PALU_LAYOUT_ROWS 0
 #define PALU_LAYOUT_TILED 1   /* decode: K-tile K, V-tile V; append: K-tile order */
 #define PALU_LAYOUT_TILED_V 2 /* append: V-tile order */
+/* decode with u_v and group_ranks: grouped latents stored compactly, every group at its own ranks (K-tile
+ * order for K, V-tile order for V); row b's group streams lie one after another, group g starting at
+ * element b * S * sum(ranks) + S * (sum of the ranks of groups 0 .. g-1). No counterpart in the
+ * reference, which pads every group to the layer's widest (convert.py:178). */
+#define PALU_LAYOUT_TILED_GROUPED 3
 
 #define PALU_ROT_LEGACY 0
 #define PALU_ROT_PACK 1
@@ -215,6 +220,15 @@ int palu_latent_append_paged(void* cache_pages, const void* new_rows, const int3
 int palu_latent_append_strided(void* cache, const void* src, long long src_batch_stride, long long src_group_stride,
                                const int32_t* update_idxs, int batch, int n_groups, int seq_len, int width,
                                int cache_layout, palu_stream_t stream);
+
+/* Latent append into grouped latents stored compactly (PALU_LAYOUT_TILED_GROUPED): group g's stream of
+ * row b (offsets as that layout says, widths[g] wide: host memory, multiples of 16 up to 512) gets at
+ * position update_idxs[b] the first widths[g] values of src[b * src_batch_stride + g * src_group_stride
+ * ..], in K-tile (order = PALU_LAYOUT_TILED) or V-tile order (PALU_LAYOUT_TILED_V). seq_len a multiple of
+ * 32, at most 16 groups. No counterpart in the reference (its caches are padded to the widest group). */
+int palu_latent_append_grouped(void* cache, const void* src, long long src_batch_stride, long long src_group_stride,
+                               const int32_t* update_idxs, int batch, int n_groups, int seq_len, const int32_t* widths,
+                               int order, palu_stream_t stream);
 
 /* The decode step's QKV epilogue in one launch, from the fp32 split partials [ks, batch, ncols] of the
  * QKV projection (palu_linear_tiled with PALU_LINEAR_F32_PARTIALS), summed in slice order: q_out

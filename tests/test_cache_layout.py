@@ -2,7 +2,7 @@
 import pytest
 import torch
 
-from palu_tt.cache import LatentCache, rows_to_tiled, tiled_to_rows
+from palu_tt.cache import GroupedLatentCache, LatentCache, rows_to_tiled, tiled_to_rows
 
 
 @pytest.mark.parametrize("role", ["k", "v"])
@@ -74,3 +74,28 @@ def test_latent_cache_reports_logical_shape():
     rows = torch.randn(2, 8, 128, 64).to(torch.bfloat16)
     for role in ("k", "v"):
         assert torch.equal(LatentCache.from_rows(rows, role).to_rows(), rows)
+
+
+@pytest.mark.parametrize("role", ["k", "v"])
+def test_grouped_cache_stores_each_group_at_its_own_ranks(role):
+    """Row b's group streams lie one after another, group g from S * (ranks before it), each the tiled
+    storage of that group's first ranks[g] columns; to_rows pads with zeros; write_rows touches only
+    each group's own columns."""
+    B, S, ranks = 2, 64, (32, 96, 64)
+    rows = torch.randn(B, 3, S, 96).to(torch.bfloat16)
+    c = GroupedLatentCache.from_rows(rows, ranks, role)
+    assert c.data.shape == (B, S * sum(ranks)) and c.shape == (B, 3, S, 96)
+    off = 0
+    for g, r in enumerate(ranks):
+        for b in range(B):
+            assert torch.equal(c.data[b, off:off + S * r], rows_to_tiled(rows[b:b + 1, g:g + 1, :, :r].contiguous(), role).flatten())
+        off += S * r
+    exp = rows.clone()
+    for g, r in enumerate(ranks):
+        exp[:, g, :, r:] = 0
+    assert torch.equal(c.to_rows(), exp)
+    new = torch.randn(3, 5, 96).to(torch.bfloat16)
+    c.write_rows(1, 30, new)
+    for g, r in enumerate(ranks):
+        exp[1, g, 30:35, :r] = new[g, :, :r]
+    assert torch.equal(c.to_rows(), exp)

@@ -15,6 +15,7 @@ import torch
 from oracle import palu_oracle as ref
 from palu_tt import convert
 from palu_tt.attention import PaluAttention
+from palu_tt.cache import GroupedLatentCache
 
 pytestmark = pytest.mark.gpu
 
@@ -87,12 +88,15 @@ def test_attention_prefill_then_decode_matches_layer_oracle(gpu, r_k, r_v, gs, l
 
 def test_attention_grouped_latents_of_unequal_ranks(gpu):
     """G-LRD with 2 groups of 2 KV heads whose ranks differ (K 96 / 192, V 256 / 64), padded to the
-    widest as load_palu_dir pads them; the layer passes the groups' own ranks to the fused op."""
+    widest in the factors as load_palu_dir pads them; the layer keeps each group's latents at its own
+    ranks (compact caches) and passes the groups' ranks to the fused op."""
     dim, nh, nkv, B, S0, steps = 1024, 8, 4, 2, 40, 6
     gr = ([96, 192], [256, 64])
     sd, palu, oracle = _layer(dim, nh, nkv, 192, 256, 2, seed=7, group_ranks=gr)
     att = _drive(gpu, sd, palu, oracle, dim, nh, nkv, B, S0, steps, "tiled", True)
     assert att.group_ranks == ([96, 192], [256, 64])
+    assert all(isinstance(c, GroupedLatentCache) for c in att.layer_past)
+    assert att.kv_bytes_per_token() == (96 + 192 + 256 + 64) * 2.0
 
 
 def _drive(gpu, sd, palu, oracle, dim, nh, nkv, B, S0, steps, layout, fused):

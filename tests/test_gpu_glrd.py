@@ -8,8 +8,8 @@ import pytest
 import torch
 
 from oracle import palu_oracle as ref
-from palu_tt import fused
-from palu_tt.cache import LatentCache
+from palu_tt import decoder_ops, fused
+from palu_tt.cache import GroupedLatentCache, LatentCache
 
 pytestmark = pytest.mark.gpu
 
@@ -155,6 +155,49 @@ def test_glrd_per_group_ranks_never_read_the_padding(gpu, ranks_k, ranks_v, B, S
         uvn[4 * g:4 * g + 4, rv:] = float("nan")
     out = _run(gpu, q, kn, vn, ukn, uvn, pos, S32, group_ranks=(ranks_k, ranks_v))
     _check(out[:, rows], exp)
+
+
+@pytest.mark.parametrize("ranks_k,ranks_v,B,S", [([128, 512], [192, 384], 4, 4096), ([96, 32], [64, 160], 3, 1000),
+                                                  ([256, 256], [512, 128], 2, 2048)])
+def test_glrd_compact_group_caches(gpu, ranks_k, ranks_v, B, S):
+    """Every group stored at its own ranks (GroupedLatentCache, PALU_LAYOUT_TILED_GROUPED): the decode
+    equals, bit for bit, the one over caches padded to the widest group and told the group ranks, and
+    matches the oracle; appends land in each group's own stream (checked through to_rows); the storage
+    is the groups' own bytes."""
+    S32 = (S + 31) // 32 * 32
+    r_k, r_v = max(ranks_k), max(ranks_v)
+    q, k, v, u_k, u_v, pos = _case(B, S32, r_k, r_v, hpg=4, seed=sum(ranks_v) + S)
+    pos.clamp_(max=S - 1)
+    for g, (rk, rv) in enumerate(zip(ranks_k, ranks_v)):
+        k[:, g, :, rk:] = 0
+        v[:, g, :, rv:] = 0
+        u_k[4 * g:4 * g + 4, rk:] = 0
+        u_v[4 * g:4 * g + 4, rv:] = 0
+    gk = GroupedLatentCache.from_rows(k.to(gpu, torch.bfloat16), ranks_k, "k")
+    gv = GroupedLatentCache.from_rows(v.to(gpu, torch.bfloat16), ranks_v, "v")
+    assert gk.nbytes() + gv.nbytes() == B * S32 * (sum(ranks_k) + sum(ranks_v)) * 2
+    # append one new row per batch row at its position, from a strided source wider than every rank
+    new_k = _bf(torch.randn(B, 2, r_k + 32))
+    new_v = _bf(torch.randn(B, 2, r_v + 32))
+    dpos = pos.to(gpu, torch.int32)
+    decoder_ops.append_from(gk, new_k.to(gpu, torch.bfloat16).reshape(B, -1), r_k + 32, r_k + 32, dpos)
+    decoder_ops.append_from(gv, new_v.to(gpu, torch.bfloat16).reshape(B, -1), r_v + 32, r_v + 32, dpos)
+    for b in range(B):
+        for g, (rk, rv) in enumerate(zip(ranks_k, ranks_v)):
+            k[b, g, pos[b], :rk] = new_k[b, g, :rk]
+            v[b, g, pos[b], :rv] = new_v[b, g, :rv]
+    torch.cuda.synchronize()
+    assert torch.equal(gk.to_rows().float().cpu(), k) and torch.equal(gv.to_rows().float().cpu(), v)
+    cos, sin = fused.cos_sin_tables(HD, S32, THETA, LLAMA3)
+    compact = fused.palu_sdpa_decode(
+        q.to(gpu, torch.bfloat16), gk, fused.w_rot_from_u_k(u_k).to(gpu, torch.bfloat16)[None],
+        fused.cs_table(cos, sin, S32)[None, None].to(gpu), gv, HD, dpos, u_v=u_v.to(gpu, torch.bfloat16)[None],
+        scale=HD ** -0.5, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    padded = _run(gpu, q, k, v, u_k, u_v, pos, S32, group_ranks=(ranks_k, ranks_v))
+    assert torch.equal(compact.cpu(), padded)
+    rows = [0, B - 1]
+    _check(padded[:, rows], _oracle(q[:, rows], k[rows], v[rows], u_k, u_v, pos[rows], S32))
 
 
 def test_glrd_deterministic_repeat(gpu):

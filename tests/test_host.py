@@ -328,6 +328,7 @@ def _sdpa(lib, **kw):
     (dict(n_groups=3, n_kv=4), _native.PALU_EINVAL, "heads_per_group"),
     (dict(u_v=_FAKE, head_dim_v=64), _native.PALU_EINVAL, "head_dim_v"),
     (dict(u_v=_FAKE, head_dim_v=128), _native.PALU_EUNSUPPORTED, "u_v"),
+    (dict(layout=3), _native.PALU_EINVAL, "needs u_v and group_ranks"),
     (dict(head_dim_v=128), _native.PALU_EINVAL, "head_dim_v"),
     (dict(heads_per_core=4), _native.PALU_EINVAL, "heads_per_core"),
     (dict(n_q=6, n_kv=4, n_groups=4), _native.PALU_EINVAL, "KV head count"),
@@ -357,6 +358,14 @@ def test_flash_decode_and_append_envelope_errors(lib):
     assert rc == _native.PALU_EINVAL and "multiple of 8" in lib.palu_last_error().decode()
     rc = lib.palu_latent_append(_FAKE, _FAKE, _FAKE, 2, 2, 256, 40, 1, None)
     assert rc == _native.PALU_EINVAL and "multiple of 16" in lib.palu_last_error().decode()
+    widths = (ctypes.c_int32 * 2)(64, 40)
+    rc = lib.palu_latent_append_grouped(_FAKE, _FAKE, 256, 128, _FAKE, 2, 2, 256, widths, 1, None)
+    assert rc == _native.PALU_EINVAL and "group 1 width 40" in lib.palu_last_error().decode()
+    widths = (ctypes.c_int32 * 2)(64, 32)
+    rc = lib.palu_latent_append_grouped(_FAKE, _FAKE, 256, 128, _FAKE, 2, 2, 256, widths, 0, None)
+    assert rc == _native.PALU_EINVAL and "order must be" in lib.palu_last_error().decode()
+    rc = lib.palu_latent_append_grouped(_FAKE, _FAKE, 256, 128, _FAKE, 2, 17, 256, widths, 1, None)
+    assert rc == _native.PALU_EINVAL and "1..16 groups" in lib.palu_last_error().decode()
 
 
 def test_paged_envelope_errors(lib):

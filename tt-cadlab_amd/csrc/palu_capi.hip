@@ -117,6 +117,41 @@ int launch_append(void* cache, const void* new_rows, const int32_t* update_idxs,
   return PALU_OK;
 }
 
+// Append into grouped latents stored compactly (PALU_LAYOUT_TILED_GROUPED): row b's group streams lie one
+// after another, group g at element offset off[g] of the row (row_elems elements per row) and width[g]
+// wide; the source holds group g's row at rows + b * sb + g * sg (its first width[g] values). One
+// thread per 8 values; vec0 are the groups' first vector indices within a row.
+struct GroupTable {
+  long long off[MAX_GROUPS];
+  int width[MAX_GROUPS];
+  int vec0[MAX_GROUPS + 1];
+};
+
+template <int LAYOUT>
+__global__ __launch_bounds__(256) void palu_append_grouped_kernel(__bf16* cache, const __bf16* rows, long long sb,
+                                                                  long long sg, const int32_t* idx, int B, int G, int S,
+                                                                  long long row_elems, const GroupTable t) {
+  const int vec = t.vec0[G];
+  const long long total = (long long)B * vec;
+  for (long long e = blockIdx.x * 256LL + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
+    const int b = (int)(e / vec), u = (int)(e - (long long)b * vec);
+    int gi = 0;
+    while (gi + 1 < G && u >= t.vec0[gi + 1]) ++gi;
+    const int v = u - t.vec0[gi];
+    const int p = idx[b];
+    if (p < 0 || p >= S) continue;
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(rows + b * sb + gi * sg + 8 * v);
+    __bf16* stream = cache + b * row_elems + t.off[gi];
+    if constexpr (LAYOUT == PALU_LAYOUT_TILED) {
+      store_k8(stream, p, 8 * v, t.width[gi], x);
+    } else {
+      const long long o = tiled_v_offset(p, 8 * v, t.width[gi]);   // 8 slots 16 bytes apart
+#pragma unroll
+      for (int j = 0; j < 8; ++j) stream[o + 8 * j] = x[j];
+    }
+  }
+}
+
 int check_append(void* cache, const void* new_rows, const int32_t* update_idxs, int batch, int n_groups, int S,
                  int width, int layout, const char* who) {
   if (!cache || !new_rows || !update_idxs) return fail(PALU_EINVAL, "%s: a required pointer is null", who);
@@ -235,6 +270,7 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
                size_t workspace_bytes, const char* who) {
   if (!q || !k_latent || !w_rot || !cs_tab || !v_latent || !cur_pos || !out)
     return fail(PALU_EINVAL, "%s: a required tensor pointer is null", who);
+  int grouped_streams = 0;
   if (rot_mode < 0 || rot_mode > 2) return fail(PALU_EINVAL, "rot_mode must be 'legacy', 'pack' or 'dst'");
   if ((rot_step == nullptr) != (trans_mat == nullptr))
     return fail(PALU_EINVAL, "rot_step and trans_mat are optional together: pass both (Phase 2) or neither (Phase 1)");
@@ -272,6 +308,13 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
     if (hpg == 1) return fail(PALU_EINVAL, "heads_per_core > 1 shares a latent between heads and needs grouped latents");
     if (hpg % heads_per_core != 0)
       return fail(PALU_EINVAL, "heads_per_core %d must divide heads_per_group %d", heads_per_core, hpg);
+  }
+  if (cache_layout == PALU_LAYOUT_TILED_GROUPED) {
+    if (u_v == nullptr || group_ranks == nullptr)
+      return fail(PALU_EINVAL, "PALU_LAYOUT_TILED_GROUPED stores grouped latents at the groups' own ranks: it needs "
+                               "u_v and group_ranks");
+    cache_layout = PALU_LAYOUT_TILED;   // same tile orders, per-group streams (set at dispatch)
+    grouped_streams = 1;
   }
   if (u_v != nullptr) {
     if (head_dim_v != HD) return fail(PALU_EINVAL, "head_dim_v must be %d when u_v rebuilds V in-kernel, got %d", HD, head_dim_v);
@@ -329,6 +372,7 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
   a.B = batch; a.n_q = n_q; a.n_kv = n_kv; a.rep = n_q / n_kv; a.hpg = hpg; a.S = seq_len; a.cs_rows = cs_rows;
   a.deterministic = deterministic ? 1 : 0;
   a.out_tiled = out_tiled;
+  a.grouped_streams = grouped_streams;
   a.qscale = scale * 1.4426950408889634f;
   a.u_v = static_cast<const __bf16*>(u_v);
   a.rk = r_k;
@@ -341,7 +385,22 @@ int sdpa_dispatch(const DecodeArgs& a, bool paged, int cache_layout, int r_k, in
   const bool tiled = cache_layout == PALU_LAYOUT_TILED;
   if (a.u_v != nullptr) {
     if (paged) return fail(PALU_EUNSUPPORTED, "u_v: the in-kernel V rebuild is not built for paged caches");
-    return dispatch_glrd(a, cs_dtype, out_dtype, stream);
+    // Each group's stream: padded caches hold every group at r_k / r_v columns, compact ones at the
+    // group's own ranks, one group after another within a row.
+    DecodeArgs ag = a;
+    const int n_groups = a.n_kv / a.hpg;
+    long long ok = 0, ov = 0;
+    for (int g = 0; g < n_groups; ++g) {
+      ag.gkw[g] = (short)(a.grouped_streams ? a.grk[g] : r_k);
+      ag.gvw[g] = (short)(a.grouped_streams ? a.grv[g] : r_v);
+      ag.gko[g] = ok;
+      ag.gvo[g] = ov;
+      ok += (long long)a.S * ag.gkw[g];
+      ov += (long long)a.S * ag.gvw[g];
+    }
+    ag.k_sb = ok;
+    ag.v_sb = ov;
+    return dispatch_glrd(ag, cs_dtype, out_dtype, stream);
   }
   if (tiled && r_k % 32 != 0)   // K rows ending in a half tile: their own translation units
     return paged ? dispatch_latent_tiled_paged_k16(a, r_k, r_v, cs_dtype, out_dtype, stream)
@@ -613,6 +672,50 @@ int palu_latent_append_strided(void* cache, const void* src, long long src_batch
                              "and %lld", src_batch_stride, src_group_stride);
   return launch_append<false>(cache, src, update_idxs, nullptr, 0, 0, batch, n_groups, seq_len, width, cache_layout,
                               stream, src_batch_stride, src_group_stride);
+}
+
+int palu_latent_append_grouped(void* cache, const void* src, long long src_batch_stride, long long src_group_stride,
+                               const int32_t* update_idxs, int batch, int n_groups, int seq_len, const int32_t* widths,
+                               int order, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  if (!cache || !src || !update_idxs || !widths)
+    return fail(PALU_EINVAL, "palu_latent_append_grouped: a required pointer is null");
+  if (batch <= 0 || n_groups <= 0 || n_groups > MAX_GROUPS || seq_len <= 0 || seq_len % 32 != 0)
+    return fail(PALU_EINVAL, "palu_latent_append_grouped: batch, 1..%d groups and seq_len (a multiple of 32) must be "
+                             "positive, got %d, %d, %d", MAX_GROUPS, batch, n_groups, seq_len);
+  if (order != PALU_LAYOUT_TILED && order != PALU_LAYOUT_TILED_V)
+    return fail(PALU_EINVAL, "palu_latent_append_grouped: order must be PALU_LAYOUT_TILED (K tiles) or "
+                             "PALU_LAYOUT_TILED_V (V tiles), got %d", order);
+  if (src_batch_stride < 0 || src_group_stride < 0 || src_batch_stride % 8 || src_group_stride % 8)
+    return fail(PALU_EINVAL, "palu_latent_append_grouped: source strides must be non-negative multiples of 8, got %lld "
+                             "and %lld", src_batch_stride, src_group_stride);
+  if (!aligned16(cache) || !aligned16(src)) return fail(PALU_EINVAL, "palu_latent_append_grouped: 16-byte alignment required");
+  GroupTable t;
+  long long off = 0;
+  t.vec0[0] = 0;
+  for (int g = 0; g < n_groups; ++g) {
+    const int w = widths[g];
+    if (w <= 0 || w % 16 != 0 || w > 512)
+      return fail(PALU_EINVAL, "palu_latent_append_grouped: group %d width %d (a multiple of 16 up to 512)", g, w);
+    t.off[g] = off;
+    t.width[g] = w;
+    t.vec0[g + 1] = t.vec0[g] + w / 8;
+    off += (long long)seq_len * w;
+  }
+  const long long total = (long long)batch * t.vec0[n_groups];
+  int blocks = (int)((total + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  auto* c = static_cast<__bf16*>(cache);
+  auto* r = static_cast<const __bf16*>(src);
+  if (order == PALU_LAYOUT_TILED)
+    hipLaunchKernelGGL((palu_append_grouped_kernel<PALU_LAYOUT_TILED>), dim3(blocks), dim3(256), 0, stream, c, r,
+                       src_batch_stride, src_group_stride, update_idxs, batch, n_groups, seq_len, off, t);
+  else
+    hipLaunchKernelGGL((palu_append_grouped_kernel<PALU_LAYOUT_TILED_V>), dim3(blocks), dim3(256), 0, stream, c, r,
+                       src_batch_stride, src_group_stride, update_idxs, batch, n_groups, seq_len, off, t);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PALU_EHIP, "grouped append launch: %s", hipGetErrorString(e));
+  return PALU_OK;
 }
 
 int palu_latent_append_paged(void* cache_pages, const void* new_rows, const int32_t* update_idxs,

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int KB = a.rk >> 5;                       // rank blocks of the cache (tile addressing)
+  const int KB = a.gkw[grp] >> 5;                 // rank blocks of the group's stream (tile addressing)
   const int KBe = a.rk_eff >> 5;                  // rank blocks of this group (the rest is never read)
 
   int len = a.cur_pos[b] + 1;
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   const int s_hi = min(len, s_lo + a.split_len);
   const int nblk = s_hi > s_lo ? (s_hi - s_lo + BLK - 1) / BLK : 0;
   const int npairs = (nblk + 1) >> 1;
-  const __bf16* kbase = a.k + b * a.k_sb + grp * a.k_sg;
+  const __bf16* kbase = a.k + b * a.k_sb + a.gko[grp];
 
   // ---- prologue -----------------------------------------------------------------------------------
   // rot[cc][rt] = fp16 {cos f, sin f, cos f+1, sin f+1} at offset t = 32 hb + 8(n/4) + 4c + n%4 inside a
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
       const int kbr = kb < KBe ? kb : 0;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const long long off = __builtin_amdgcn_readfirstlane((int)(((s_lo >> 5) + (live ? blk : 0)) * (32 * a.rk) +
+        const long long off = __builtin_amdgcn_readfirstlane((int)(((s_lo >> 5) + (live ? blk : 0)) * (32 * KB * 32) +
                                                                     (c * KB + kbr) * 512));
         t[2 * hb + c] = *reinterpret_cast<const bf16x8*>(kbase + off + lane * 8);
       }
@@ -374,7 +374,8 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
   const float* sc0 = scores + ((long long)(b * n_groups + grp) * NB + (s_lo >> 5)) * QH * BLK +
                      (long long)head_c * BLK + 8 * g;
   const long long blk_stride = (long long)QH * BLK;
-  const __bf16* vbase = a.v + b * a.v_sb + grp * a.v_sg + (long long)(s_lo >> 5) * (32 * a.rv) + lane * 8;
+  const int vw = a.gvw[grp];                              // the group's stream width
+  const __bf16* vbase = a.v + b * a.v_sb + a.gvo[grp] + (long long)(s_lo >> 5) * (32 * vw) + lane * 8;
 
   struct Blk {
     float4 s[2];             // positions 8g .. 8g+7 of this lane's head
@@ -393,7 +394,7 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
       const int mt = tg * TPW + i;
       if (mt < VT)
         x.v[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const bf16x8*>(vbase + (long long)jj * (32 * a.rv) + mt * 512));
+            reinterpret_cast<const bf16x8*>(vbase + (long long)jj * (32 * vw) + mt * 512));
     }
   };
 

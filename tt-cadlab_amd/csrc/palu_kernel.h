@@ -86,6 +86,7 @@ struct DecodeArgs {
   int balanced;           // 1 when n_wg > B * n_kv (length-aware chunks, merged through ws)
   int deterministic;      // 1: wave w takes blocks w, w + NW, ... (reproducible); 0: blocks from a counter
   int out_tiled;          // 1: out in the 64-row tiled activation layout of the next projection (B <= 64)
+  int grouped_streams;    // grouped latents stored compactly, each group at its own ranks (PALU_LAYOUT_TILED_GROUPED)
   float qscale;           // softmax scale * log2(e)
   // Paged caches: k/v are page pools [n_pages, G, page_size, width] (rows or tiled) and k_sb / v_sb are
   // page strides; the page of block J of row b is page_table[b * pt_stride + (J >> page_shift)].
@@ -100,6 +101,11 @@ struct DecodeArgs {
   // K rank is rk_eff).
   short grk[MAX_GROUPS], grv[MAX_GROUPS];
   int grp_lo, grp_cnt, rk_eff;
+  // Grouped-latent streams: group g of row b starts at element b * k_sb + gko[g] and is gkw[g] wide (the
+  // padded layout: g * k_sg and rk; the compact one: S times the widths of the groups before it, and
+  // the group's own rank). Same for V.
+  long long gko[MAX_GROUPS], gvo[MAX_GROUPS];
+  short gkw[MAX_GROUPS], gvw[MAX_GROUPS];
 };
 
 // Error reporting (defined in palu_capi.hip): formats the message for palu_last_error, returns code.

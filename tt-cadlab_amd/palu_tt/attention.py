@@ -33,7 +33,7 @@ import torch
 import torch.nn.functional as F
 
 from palu_tt import decoder_ops, fused
-from palu_tt.cache import LatentCache
+from palu_tt.cache import GroupedLatentCache, LatentCache
 
 
 class PaluAttention(torch.nn.Module):
@@ -116,7 +116,13 @@ class PaluAttention(torch.nn.Module):
 
         B, S = self.max_batch_size, self.max_seq_len
         k_width = self.r_k if self.recon_k else hd
-        if cache_layout == "tiled":
+        if cache_layout == "tiled" and self.group_ranks is not None:
+            # grouped latents of unequal ranks: every group stored at its own ranks (the reference pads
+            # each to the widest, attention.py:274-283 with convert.py:178)
+            assert S % 32 == 0, "the tiled cache holds whole 32-position blocks"
+            keys = GroupedLatentCache.zeros(B, self.group_ranks[0], S, dev, "k")
+            values = GroupedLatentCache.zeros(B, self.group_ranks[1], S, dev, "v")
+        elif cache_layout == "tiled":
             assert S % 32 == 0, "the tiled cache holds whole 32-position blocks"
             keys = LatentCache.zeros(B, self.n_groups, S, k_width, dev, "k")
             values = LatentCache.zeros(B, self.n_groups, S, self.r_v, dev, "v")
@@ -127,7 +133,11 @@ class PaluAttention(torch.nn.Module):
 
     # ------------------------------------------------------------------------------------------------
     def kv_bytes_per_token(self) -> float:
-        """Cache bytes per token per layer (bf16 latents), reference attention.py:352-358."""
+        """Cache bytes per token per layer (bf16 latents), reference attention.py:352-358; compact grouped
+        caches count each group at its own ranks."""
+        keys, values = self.layer_past
+        if isinstance(keys, GroupedLatentCache):
+            return (sum(keys.ranks) + sum(values.ranks)) * 2.0
         k_width = self.r_k if self.recon_k else self.head_dim
         return self.n_groups * (k_width + self.r_v) * 2.0
 
@@ -171,12 +181,13 @@ class PaluAttention(torch.nn.Module):
         keys, values = self.layer_past
         kw, G = self.k_width, self.n_groups
         k0, v0 = nh * hd, nh * hd + G * kw                                  # column offsets of K and V latents
-        if self.wqkv.tiled:
+        if self.wqkv.tiled and not isinstance(keys, GroupedLatentCache):
             part = self.wqkv(x2, x_tiled=x_tiled, rows=B, mode="partials")  # [ks, B, nh hd + G (kw + r_v)] fp32
             q = decoder_ops.qkv_post(part, pos, self.cos, self.sin, nh, keys, k0, kw, kw, values, v0, self.r_v,
                                      self.r_v, k_rope=not self.recon_k)
         else:
-            xqkv = self.wqkv(x2)                                            # [B, nh hd + G (kw + r_v)]
+            # bf16 projection output; compact grouped caches take their appends from its columns
+            xqkv = self.wqkv(x2, x_tiled=x_tiled, rows=B) if x_tiled else self.wqkv(x2)   # [B, nh hd + G (kw + r_v)]
             q = decoder_ops.rope_rows(xqkv, nh, pos, self.cos, self.sin)     # [B, nh, hd]
             kcols, vcols = xqkv[:, k0:], xqkv[:, v0:]
             if self.recon_k:
@@ -218,6 +229,8 @@ class PaluAttention(torch.nn.Module):
 
     def _cache_rows(self, cache, S):
         """[B, G, S, w] row-major bf16 view of the first S positions of a cache (tiled caches converted)."""
+        if isinstance(cache, GroupedLatentCache):
+            return cache.to_rows()[:, :, :S]
         if isinstance(cache, LatentCache):
             nb = -(-S // 32)
             return LatentCache(cache.data[:, :, :nb], cache.role).to_rows()[:, :, :S]
@@ -288,7 +301,7 @@ class PaluAttention(torch.nn.Module):
     def _fill(self, cache, rows, user_id):
         """Rows [S, G, w] into cache row user_id at positions 0..S-1 (reference ttnn.fill_cache)."""
         r = rows.to(torch.bfloat16).transpose(0, 1)                       # [G, S, w]
-        if isinstance(cache, LatentCache):
+        if isinstance(cache, (LatentCache, GroupedLatentCache)):
             cache.write_rows(user_id, 0, r)
         else:
             cache[user_id, :, :r.shape[1]] = r

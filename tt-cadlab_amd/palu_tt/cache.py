@@ -119,3 +119,81 @@ class LatentCache:
 
     def nbytes(self) -> int:
         return self.data.numel() * self.data.element_size()
+
+
+@dataclass
+class GroupedLatentCache:
+    """Grouped latents (G-LRD) whose groups have unequal ranks, stored compactly: group g of every row at
+    its own width ranks[g], in the role's tile order, instead of padded to the layer's widest group as
+    the reference keeps them (palu_tt/convert.py:178). Row b's group streams lie one after another: the
+    storage is [B, S * sum(ranks)] bf16 and group g starts at S * (ranks[0] + .. + ranks[g-1]). The
+    logical tensor is the padded [B, n_groups, max_seq, max(ranks)] one, its columns past a group's rank
+    zero (``to_rows``); ``from_rows`` keeps each group's first ranks[g] columns."""
+    data: torch.Tensor
+    ranks: Tuple[int, ...]
+    max_seq: int
+    role: str = "k"
+
+    def __post_init__(self):
+        assert self.role in ROLES, f"role must be 'k' or 'v', got {self.role!r}"
+        self.ranks = tuple(int(r) for r in self.ranks)
+        assert self.max_seq % BLOCK == 0 and all(r > 0 and r % 16 == 0 for r in self.ranks), \
+            f"max_seq a multiple of {BLOCK} and ranks multiples of 16, got {self.max_seq}, {self.ranks}"
+        assert self.data.dim() == 2 and self.data.shape[1] == self.max_seq * sum(self.ranks)
+
+    @staticmethod
+    def zeros(batch: int, ranks, max_seq: int, device, role: str = "k", dtype=torch.bfloat16) -> "GroupedLatentCache":
+        return GroupedLatentCache(torch.zeros(batch, max_seq * sum(int(r) for r in ranks), dtype=dtype, device=device),
+                                  tuple(ranks), max_seq, role)
+
+    def _offset(self, g: int) -> int:
+        return self.max_seq * sum(self.ranks[:g])
+
+    def group(self, g: int) -> torch.Tensor:
+        """Group g's tiled storage as a [B, 1, S/32, ranks[g]/16, 64, 8] view (rows are not contiguous)."""
+        B, S, r = self.data.shape[0], self.max_seq, self.ranks[g]
+        return self.data[:, self._offset(g):self._offset(g) + S * r].view(B, 1, S // BLOCK, r // 16, 64, 8)
+
+    @staticmethod
+    def from_rows(rows: torch.Tensor, ranks, role: str = "k") -> "GroupedLatentCache":
+        B, G, S, w = rows.shape
+        assert len(ranks) == G and max(ranks) <= w, f"{G} groups of ranks <= {w}, got {ranks}"
+        c = GroupedLatentCache.zeros(B, ranks, S, rows.device, role, rows.dtype)
+        for g, r in enumerate(c.ranks):
+            c.group(g).copy_(rows_to_tiled(rows[:, g:g + 1, :, :r].contiguous(), role))
+        return c
+
+    def to_rows(self) -> torch.Tensor:
+        B, S, w = self.data.shape[0], self.max_seq, max(self.ranks)
+        out = torch.zeros(B, len(self.ranks), S, w, dtype=self.data.dtype, device=self.data.device)
+        for g, r in enumerate(self.ranks):
+            out[:, g, :, :r] = tiled_to_rows(self.group(g).contiguous(), self.role)[:, 0]
+        return out
+
+    def write_rows(self, b: int, start: int, rows: torch.Tensor) -> None:
+        """cache[b, :, start:start + n, :] = rows ([G, n, >= max(ranks)], each group's first ranks[g] columns)."""
+        G, n, _ = rows.shape
+        b0, b1 = start // BLOCK, (start + n + BLOCK - 1) // BLOCK
+        for g, r in enumerate(self.ranks):
+            blk = self.group(g)[b:b + 1, :, b0:b1]
+            cur = tiled_to_rows(blk.contiguous(), self.role)                        # [1, 1, (b1 - b0) * 32, r]
+            cur[0, 0, start - b0 * BLOCK:start - b0 * BLOCK + n] = rows[g, :, :r].to(cur.dtype)
+            blk.copy_(rows_to_tiled(cur, self.role))
+
+    @property
+    def shape(self) -> Tuple[int, int, int, int]:
+        return (self.data.shape[0], len(self.ranks), self.max_seq, max(self.ranks))
+
+    @property
+    def device(self):
+        return self.data.device
+
+    @property
+    def dtype(self):
+        return self.data.dtype
+
+    def data_ptr(self) -> int:
+        return self.data.data_ptr()
+
+    def nbytes(self) -> int:
+        return self.data.numel() * self.data.element_size()

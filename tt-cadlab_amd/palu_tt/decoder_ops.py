@@ -12,7 +12,7 @@ from typing import Optional
 import torch
 
 from palu_tt import _native
-from palu_tt.cache import LatentCache
+from palu_tt.cache import GroupedLatentCache, LatentCache
 
 
 def _check(t: torch.Tensor, name: str, dtype=torch.bfloat16) -> None:
@@ -111,11 +111,23 @@ def rope_rows(src: torch.Tensor, heads: int, pos: torch.Tensor, cos: torch.Tenso
 
 def append_from(cache, src: torch.Tensor, group_stride: int, width: int, pos: torch.Tensor) -> None:
     """cache[b, g, pos[b], :] = src[b, g * group_stride : g * group_stride + width] for a row-strided
-    src [B, >= ...] (the latent columns of the QKV output). cache: LatentCache (tiled) or a row-major
-    [B, G, S, width] bf16 tensor."""
+    src [B, >= ...] (the latent columns of the QKV output). cache: LatentCache (tiled), a row-major
+    [B, G, S, width] bf16 tensor, or a GroupedLatentCache (each group takes its first ranks[g] columns)."""
     _check(src, "src")
     if src.dim() != 2 or src.stride(1) != 1:
         raise RuntimeError("src must be a row-strided [rows, width] view")
+    p = pos.reshape(-1).to(device=src.device, dtype=torch.int32).contiguous()
+    if isinstance(cache, GroupedLatentCache):
+        # each group's first ranks[g] columns of its width-wide source slice
+        B, G, S, w = cache.shape
+        if w > width:
+            raise RuntimeError(f"cache ranks up to {w} exceed the append width {width}")
+        widths = (ctypes.c_int32 * G)(*cache.ranks)
+        order = _native.LAYOUT_TILED if cache.role == "k" else _native.LAYOUT_TILED_V
+        _native.check(_native.load().palu_latent_append_grouped(
+            _native.ptr(cache.data), _native.ptr(src), src.stride(0), int(group_stride), _native.ptr(p), B, G, S, widths,
+            order, _native.stream_handle(src.device)))
+        return
     if isinstance(cache, LatentCache):
         store = cache.data
         B, G, S, w = cache.shape
@@ -126,7 +138,6 @@ def append_from(cache, src: torch.Tensor, group_stride: int, width: int, pos: to
         layout = _native.LAYOUT_ROWS
     if w != width:
         raise RuntimeError(f"cache width {w} != append width {width}")
-    p = pos.reshape(-1).to(device=src.device, dtype=torch.int32).contiguous()
     _native.check(_native.load().palu_latent_append_strided(
         _native.ptr(store), _native.ptr(src), src.stride(0), int(group_stride), _native.ptr(p), B, G, S, width, layout,
         _native.stream_handle(src.device)))

@@ -28,8 +28,8 @@ from typing import Optional, Tuple
 
 import torch
 
-from palu_tt import _native
-from palu_tt.cache import LatentCache
+from palu_tt import _native, decoder_ops
+from palu_tt.cache import GroupedLatentCache, LatentCache
 
 MAX_CHUNK = 512          # the reference's cap on the static K chunk (ttnn sdpa_decode)
 HEAD_DIM = 128
@@ -169,6 +169,11 @@ def _as_dev(t: torch.Tensor, name: str, dtype=None, device=None) -> torch.Tensor
 def _cache_arg(t, name: str, device, role: Optional[str] = None):
     """(storage tensor, logical shape, layout id) of a row-major tensor or a LatentCache; a tiled cache
     passed where the op reads K (role "k") or V (role "v") must be stored in that role's tile order."""
+    if isinstance(t, GroupedLatentCache):
+        _as_dev(t.data, name, torch.bfloat16, device)
+        _require(role is not None and t.role == role,
+                 f"{name} is a GroupedLatentCache in {t.role!r} tile order; this argument reads a {role!r} cache")
+        return t.data, tuple(t.shape), _native.LAYOUT_TILED_GROUPED
     if isinstance(t, LatentCache):
         _as_dev(t.data, name, torch.bfloat16, device)
         _require(role is None or t.role == role,
@@ -260,7 +265,8 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
     rounding of the softmax probabilities, well inside the parity tolerance).
     group_ranks=(ranks_k, ranks_v), one rank per latent group (with u_v): each group's own widths, the
     cache columns past them being padding that the kernels never read (the reference pads every group to
-    the layer's widest and reads the padding).
+    the layer's widest and reads the padding). k_latent / v_latent may also be GroupedLatentCache pairs,
+    each group stored at its own ranks (no padding in memory either); their ranks are the group ranks.
     noalloc=True (contiguous caches only, no workspace) calls palu_sdpa_decode_noalloc, which keeps the
     kernels' scratch in the library's static per-GPU array: with ``out`` given, the call allocates no
     device memory at all (for HIP graph capture and serving loops); calls overlapping on one GPU race.
@@ -318,6 +324,12 @@ def palu_sdpa_decode(q, k_latent, w_rot, cs_tab, v_latent, head_dim_v, cur_pos_t
         _as_dev(out, "out", out_dtype, dev)
         _require(tuple(out.shape) == (1, B, n_q, width), f"out must be [1, {B}, {n_q}, {width}]")
     gr = None
+    if layout == _native.LAYOUT_TILED_GROUPED:
+        # compact grouped caches carry their groups' ranks; group_ranks, when given, must agree
+        cache_ranks = [list(k_latent.ranks), list(v_latent.ranks)]
+        _require(group_ranks is None or [[int(r) for r in x] for x in group_ranks] == cache_ranks,
+                 f"group_ranks {group_ranks} differ from the GroupedLatentCache ranks {cache_ranks}")
+        group_ranks = cache_ranks
     if group_ranks is not None:
         gk, gv = (list(x) for x in group_ranks)
         _require(len(gk) == n_groups and len(gv) == n_groups,
@@ -418,6 +430,11 @@ def paged_update_cache(cache, new_rows: torch.Tensor, update_idxs_tensor: torch.
     [B, G, S, width] bf16 tensor or a LatentCache. With ``page_table`` [B, max_pages] int32 the cache is a
     page pool [n_pages, G, page_size, width] and row b goes to page page_table[b, idx // page_size]."""
     dev = cache.device
+    if isinstance(cache, GroupedLatentCache):
+        _require(page_table is None, "a GroupedLatentCache is contiguous")
+        B, G, S, width = cache.shape
+        decoder_ops.append_from(cache, new_rows.reshape(B, G * width), width, width, update_idxs_tensor)
+        return
     store, (N, G, S, width), layout = _cache_arg(cache, "cache", dev)
     lib = _native.load()
     if page_table is None:
