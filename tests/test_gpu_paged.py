@@ -78,12 +78,13 @@ def _check(out, exp):
     assert torch.isfinite(out).all() and ma <= 2e-2 and cs >= 0.9999, f"max_abs {ma:.3e}, cosine {cs:.6f}"
 
 
-@pytest.mark.parametrize("layout", ["rows", "tiled"])
-@pytest.mark.parametrize("r_k,r_v,page_size", [(64, 64, 64), (32, 128, 64), (128, 64, 64), (64, 32, 32), (96, 96, 128),
-                                               (64, 80, 64), (80, 64, 64), (48, 112, 32)])
+_WIDTHS_32 = [(64, 64, 64), (32, 128, 64), (128, 64, 64), (64, 32, 32), (96, 96, 128)]
+_WIDTHS_16 = [(64, 80, 64), (80, 64, 64), (48, 112, 32)]      # tiled caches only: 16-wide V tiles, K half tiles
+
+
+@pytest.mark.parametrize("layout,r_k,r_v,page_size", [(lay, *w) for lay in ("rows", "tiled") for w in _WIDTHS_32] +
+                         [("tiled", *w) for w in _WIDTHS_16])
 def test_paged_decode_matches_oracle(gpu, layout, r_k, r_v, page_size):
-    if layout == "rows" and (r_k % 32 or r_v % 32):
-        pytest.skip("row-major caches take latent widths in 32s")
     B, S = 4, 2048
     q, k, v, u_k, pos, kp, vp, pt = _case(B, S, r_k, r_v, page_size, seed=r_k + r_v + page_size)
     assert torch.equal(ref.gather_pages(kp, pt), k) and torch.equal(ref.gather_pages(vp, pt), v)
