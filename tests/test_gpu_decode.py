@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import palu_oracle as ref
-from palu_tt import fused
+from palu_tt import decoder_ops, fused
 
 pytestmark = pytest.mark.gpu
 
@@ -409,6 +409,34 @@ def test_tiled_k_widths_in_16s(gpu, B, S, r_k, r_v, out_dtype, det):
     torch.cuda.synchronize()
     assert torch.equal(kc.to_rows().float().cpu(), k_full)
     _check(out.float().cpu(), ref.reference_decode(q, k_full, u_k, v, pos, cos, sin, HD ** -0.5))
+
+
+@pytest.mark.parametrize("B,S,r_k,r_v,det", [(64, 1024, 64, 64, False), (64, 2048, 96, 48, True), (96, 512, 128, 128, False),
+                                            (64, 832, 48, 112, False)])
+def test_two_items_per_workgroup(gpu, B, S, r_k, r_v, det):
+    """Two or more whole items per CU (B * 8 KV heads >= 512, fp32 tables, bf16 output, tiled): one
+    workgroup runs rows b and b + B/2 of a KV head on its two halves of waves, sharing the tables and
+    u_k^T. Rows of different lengths (the halves finish apart), against the oracle, and the same result
+    with the output in the tiled activation layout."""
+    q, k_lat, u_k, v, pos, cos, sin = _inputs(B, S, r_k, r_v, seed=B + r_k)
+    pos[B // 2] = 0                               # the partner of row 0 (length S) holds one position
+    pos[B // 2 + 1] = S // 3
+    w_rot = ref.w_rot_from_u_k(u_k)[None].to(gpu, torch.bfloat16)
+    cs = ref.cs_table(cos, sin, S)[None, None].to(gpu)
+    kc = LatentCache.from_rows(k_lat.to(gpu, torch.bfloat16), "k")
+    vc = LatentCache.from_rows(v.to(gpu, torch.bfloat16), "v")
+    dq, dpos = q.to(gpu, torch.bfloat16), pos.to(gpu, torch.int32)
+    out = fused.palu_sdpa_decode(dq, kc, w_rot, cs, vc, r_v, dpos, scale=HD ** -0.5, out_dtype=torch.bfloat16,
+                                 deterministic=det)
+    torch.cuda.synchronize()
+    rows = [0, 1, B // 2, B // 2 + 1, B - 1]
+    exp = ref.reference_decode(q[:, rows], k_lat[rows], u_k, v[rows], pos[rows], cos, sin, HD ** -0.5)
+    _check(out[:, rows].float().cpu(), exp)
+    if det and B <= 64:
+        t = fused.palu_sdpa_decode(dq, kc, w_rot, cs, vc, r_v, dpos, scale=HD ** -0.5, deterministic=True,
+                                   tiled_rows=True)
+        torch.cuda.synchronize()
+        assert torch.equal(decoder_ops.untile_rows(t, B), out[0].reshape(B, -1))
 
 
 def test_row_major_k_width_in_16s_is_refused(gpu):

@@ -331,7 +331,7 @@ __device__ int plan_chunk_pairs(const DecodeArgs& a) {
 //   th    (cos, sin) of angle 1024*H*f, H < ceil(S / 1024): the high part             [nH][64] float2
 //   kc    staging of cs_tab rows 0..7 and 8, 16, .., 56 ([row][f] float2) while rtab is built, overlaying qx
 // The wave-merge buffer of the epilogue overlays the front.
-template <int RK, int RV, bool KFULL, int NW>
+template <int RK, int RV, bool KFULL, int NW, int IPW = 1>
 struct Smem {
   static constexpr int UKT_STRIDE = RK + 8;
   static constexpr int RTAB_BYTES = KFULL ? 0 : 2 * 2 * 8 * 64 * 8;
@@ -340,7 +340,7 @@ struct Smem {
   static constexpr int QX_WAVE_BYTES = 16 * 4 * 8 * 4 * 2;   // [head 16][g 4][row tile 8][4 dims] fp16
   static constexpr int QX_BYTES = KFULL ? 0 : (NW * QX_WAVE_BYTES > KC_BYTES ? NW * QX_WAVE_BYTES : KC_BYTES);
   static constexpr int TL_BYTES = KFULL ? 0 : 16 * 64 * 8;
-  static constexpr int QS_BYTES = KFULL ? 0 : 16 * HD * 2;
+  static constexpr int QS_BYTES = KFULL ? 0 : IPW * 16 * HD * 2;   // the query rows of each item
   static constexpr int UKT_OFFSET = RTAB_BYTES;
   static constexpr int QX_OFFSET = UKT_OFFSET + UKT_BYTES;
   static constexpr int TL_OFFSET = QX_OFFSET + QX_BYTES;
@@ -363,7 +363,9 @@ __device__ __forceinline__ float4 load4f<__bf16>(const __bf16* p) {
   return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 
-template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, int NW, typename TabT, typename OutT>
+// IPW items per workgroup: 2 runs two items of one KV head (batch rows b and b + B/2) on the two halves
+// of the waves, which share the angle tables and u_k^T staged once.
+template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, int NW, typename TabT, typename OutT, int IPW = 1>
 // At least two waves per SIMD (256 registers) wherever the width pair's default is 8 waves per workgroup,
 // so that its 4-wave variant fits two workgroups per CU.
 __global__ __launch_bounds__(NW * 64, (NW == 8 || pick_nw<RK, RV, KFULL, TILED>() == 8) ? 2 : 1)
@@ -376,7 +378,9 @@ void palu_decode_kernel(const DecodeArgs a) {
   constexpr int KB = KBF + (KH ? 1 : 0);    // register blocks; a half block holds 4 values, zeros above
   constexpr int VB = RV / 32;   // 32-wide blocks of a V row
   constexpr int VT = RV / 16;   // 16-wide V tiles = PV M-tiles
-  using SM = Smem<RK, RV, KFULL, NW>;
+  using SM = Smem<RK, RV, KFULL, NW, IPW>;
+  static_assert(IPW == 1 || (IPW == 2 && !PAGED && !KFULL), "two items per workgroup: contiguous latent caches");
+  constexpr int NWI = NW / IPW;             // waves per item
 
   extern __shared__ __attribute__((aligned(16))) char smem[];
   f16x4* rtab = reinterpret_cast<f16x4*>(smem);
@@ -391,6 +395,8 @@ void palu_decode_kernel(const DecodeArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index, held in a scalar register
+  const int half = IPW == 1 ? 0 : w / NWI;                  // the wave's item slot
+  const int wi = w - half * NWI;                            // wave index within its item
   const int n = lane & 15, g = lane >> 4;
   _Float16* qx = reinterpret_cast<_Float16*>(smem + SM::QX_OFFSET + w * SM::QX_WAVE_BYTES);
 
@@ -418,8 +424,9 @@ void palu_decode_kernel(const DecodeArgs a) {
   // the length-aware plan (computed identically, and uniformly, by every wave).
   int b, kvh, s_lo, s_hi, n_chunks = 1;
   if (!a.balanced) {
-    b = blockIdx.x / a.n_kv;
-    kvh = blockIdx.x - b * a.n_kv;
+    const int item = blockIdx.x + half * a.n_wg;   // two items: n_wg = B * n_kv / 2, so the KV head is shared
+    b = item / a.n_kv;
+    kvh = item - b * a.n_kv;
     s_lo = 0;
     s_hi = row_len(a, b);
   } else {
@@ -543,12 +550,12 @@ void palu_decode_kernel(const DecodeArgs a) {
   // one wave holds when the loop ends (the indices are w < NW, then counter values NW, NW + 1, ...).
   const int nfull = s_hi > s_lo ? (s_hi - s_lo) / BLK : 0;   // an empty split (row shorter than s_lo) has none
   const int npairs = nfull >> 1;
-  if (tid == 0) *ctr = NW;
+  if (tid < IPW) ctr[tid] = NWI;
   bf16x8 kl[2][KB], vl[VT], kln[2][KB], vln[VT];
   auto fence = []() __attribute__((always_inline)) { __builtin_amdgcn_sched_barrier(0); };
   // Block i (0, 1) of the wave's first pair, clamped inside the cache.
   auto load_first = [&](int i, bf16x8 (&kd)[2][KB], bf16x8 (&vd)[VT]) {
-    const int f = min(s_lo + (2 * w + i) * BLK, ((a.S - 1) / BLK) * BLK);
+    const int f = min(s_lo + (2 * wi + i) * BLK, ((a.S - 1) / BLK) * BLK);
     const int pid = page_global(f);
     fence();
     load_blk(f, true, pid, kd, vd);
@@ -572,9 +579,11 @@ void palu_decode_kernel(const DecodeArgs a) {
       e = e < RK * (HD / 8) ? e : 0;
       ukv[i] = *reinterpret_cast<const bf16x8*>(ukp + (long long)(e % RK) * (2 * HD) + (e / RK) * 8);
     }
-    // query rows: 16 heads x 256 B, 16 bytes per thread for the first 256 threads (zero rows past rep)
-    const int qh = tid >> 4, qc = (tid & 15) * 8;
-    const bool qlive = tid < 16 * (HD / 8) && qh < a.rep;
+    // query rows: 16 heads x 256 B, 16 bytes per thread for the first 256 threads of the item's waves
+    // (zero rows past rep)
+    const int qt = tid - half * NWI * 64;
+    const int qh = qt >> 4, qc = (qt & 15) * 8;
+    const bool qlive = qt < 16 * (HD / 8) && qh < a.rep;
     const bf16x8 qrow = *reinterpret_cast<const bf16x8*>(
         a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + (qlive ? qh : 0)) * HD + (qlive ? qc : 0));
     // Every wave's table, u_k and query loads are issued before any wave's first latent block: the CU's
@@ -587,7 +596,7 @@ void palu_decode_kernel(const DecodeArgs a) {
     // then leave this block in flight. The scheduling fences keep that order. The pair's second block
     // follows once the table registers are written out.
     load_first(0, kl, vl);
-    if (tid < 16 * (HD / 8)) *reinterpret_cast<bf16x8*>(qs_lds + qh * HD + qc) = qlive ? qrow : bf16x8{};
+    if (qt < 16 * (HD / 8)) *reinterpret_cast<bf16x8*>(qs_lds + (half * 16 + qh) * HD + qc) = qlive ? qrow : bf16x8{};
     // rows -> [row][f] (cos, sin); lane l < 32 holds cos of f = 2l, 2l+1, lane l >= 32 the sines
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
@@ -717,7 +726,7 @@ void palu_decode_kernel(const DecodeArgs a) {
     for (int k = 0; k < QSLOTS; ++k) {
       const int h = g + 4 * k;
       if (h < a.rep) {
-        const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qs_lds + h * HD + 8 * qf);
+        const bf16x8 qv = *reinterpret_cast<const bf16x8*>(qs_lds + (half * 16 + h) * HD + 8 * qf);
         f16x4 y0, y1;
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -895,13 +904,13 @@ void palu_decode_kernel(const DecodeArgs a) {
   // that still fits the register budget without spilling (full K, r_k <= 64, r_k + r_v <= 192; the
   // rest refill K together with V after the PV product).
   constexpr bool EARLY_K = KFULL || KB * 32 <= 64 || KB * 32 + RV <= 192;
-  int p = w;
+  int p = wi;
   while (p < npairs) {
-    int pn = p + NW;
+    int pn = p + NWI;
     if (!a.deterministic) {
       // readfirstlane keeps the pair index in a scalar register: the loop branches stay uniform.
       int got = 0;
-      if (lane == 0) got = atomicAdd(ctr, 1);
+      if (lane == 0) got = atomicAdd(ctr + half, 1);
       pn = __builtin_amdgcn_readfirstlane(got);
     }
     const int b0 = 2 * p;
@@ -949,23 +958,26 @@ void palu_decode_kernel(const DecodeArgs a) {
       for (int i = 0; i < 4; ++i) row[16 * mt + 4 * g + i] = O[mt][i];
   }
   __syncthreads();
-  for (int e = tid; e < a.rep * RV; e += NW * 64) {
-    const int h = e / RV, r = e - h * RV;
+  for (int e = tid; e < IPW * a.rep * RV; e += NW * 64) {
+    const int slot = IPW == 1 ? 0 : e / (a.rep * RV);     // the item whose waves' partials this merges
+    const int e2 = e - slot * a.rep * RV;
+    const int h = e2 / RV, r = e2 - h * RV;
     float M = NEG_INF;
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mbuf[(ww * 16 + h) * (RV + 2) + RV]);
+    for (int ww = 0; ww < NWI; ++ww) M = fmaxf(M, mbuf[((slot * NWI + ww) * 16 + h) * (RV + 2) + RV]);
     float L = 0.f, acc = 0.f;
     if (M != NEG_INF) {
 #pragma unroll
-      for (int ww = 0; ww < NW; ++ww) {
-        const float* row = mbuf + (ww * 16 + h) * (RV + 2);
+      for (int ww = 0; ww < NWI; ++ww) {
+        const float* row = mbuf + ((slot * NWI + ww) * 16 + h) * (RV + 2);
         const float f = __builtin_amdgcn_exp2f(row[RV] - M);
         L += row[RV + 1] * f;
         acc += row[r] * f;
       }
     }
     if (n_chunks == 1) {
-      OutT* o = static_cast<OutT*>(a.out) + out_index(a, b, ((long long)kvh * a.rep + h) * RV + r, (long long)a.n_q * RV);
+      const int bs = IPW == 1 ? b : (blockIdx.x + slot * a.n_wg) / a.n_kv;
+      OutT* o = static_cast<OutT*>(a.out) + out_index(a, bs, ((long long)kvh * a.rep + h) * RV + r, (long long)a.n_q * RV);
       store_out(o, L > 0.f ? acc / L : 0.f);
     } else {
       float* wrow = a.ws + ((long long)blockIdx.x * 16 + h) * (RV + 2);
@@ -1024,10 +1036,10 @@ __global__ __launch_bounds__(RV) void palu_merge_kernel(const DecodeArgs a) {
 }
 
 
-template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, typename TabT, typename OutT, int NW>
+template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, typename TabT, typename OutT, int NW, int IPW = 1>
 int launch_nw(const DecodeArgs& a, int items, hipStream_t stream) {
-  using SM = Smem<RK, RV, KFULL, NW>;
-  auto kern = palu_decode_kernel<RK, RV, KFULL, TILED, PAGED, NW, TabT, OutT>;
+  using SM = Smem<RK, RV, KFULL, NW, IPW>;
+  auto kern = palu_decode_kernel<RK, RV, KFULL, TILED, PAGED, NW, TabT, OutT, IPW>;
   const int lds = SM::bytes(a.S) + (PAGED ? ((a.S >> 5 >> a.page_shift) + 2) * 4 : 0);
   if (lds > 160 * 1024) return fail(PALU_EUNSUPPORTED, "seq_len %d needs %d bytes of LDS (max 163840)", a.S, lds);
   static int attr_set = 0;
@@ -1062,14 +1074,17 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
   if (need > 0 && (a.ws == nullptr || a.ws_bytes < need))
     return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_decode_workspace_bytes), got %zu", need, a.ws_bytes);
   // Two or more whole items per CU (e.g. batch 64 x 8 KV heads): an 8-wave workgroup fills a CU's
-  // registers, so the CU's second item would start, prologue and all, only when its first ended. Two
-  // 4-wave workgroups fit a CU together (256 registers per wave, LDS for two), and one's prologue then
-  // runs while the other streams. Built for the tiled contiguous caches with fp32 tables and bf16
-  // output, the decoder's configuration.
+  // registers, so the CU's second item would start, prologue and all, only when its first ended. One
+  // 8-wave workgroup runs two items of one KV head instead (rows b and b + B/2, four waves each), so the
+  // CU streams both at once and stages the angle tables and u_k^T once for the two. Built for the
+  // tiled contiguous caches with fp32 tables and bf16 output, the decoder's configuration.
   if constexpr (NW == 8 && TILED && !PAGED && !KFULL && std::is_same<TabT, float>::value &&
                 std::is_same<OutT, __bf16>::value) {
-    if (!a.balanced && items >= 2 * TARGET_WGS && 2 * Smem<RK, RV, KFULL, 4>::bytes(a.S) <= 160 * 1024)
-      return launch_nw<RK, RV, KFULL, TILED, PAGED, TabT, OutT, 4>(a, items, stream);
+    if (!a.balanced && items >= 2 * TARGET_WGS && a.B % 2 == 0 &&
+        Smem<RK, RV, KFULL, 8, 2>::bytes(a.S) <= 160 * 1024) {
+      a.n_wg = items / 2;
+      return launch_nw<RK, RV, KFULL, TILED, PAGED, TabT, OutT, 8, 2>(a, items, stream);
+    }
   }
   return launch_nw<RK, RV, KFULL, TILED, PAGED, TabT, OutT, NW>(a, items, stream);
 }
