@@ -366,9 +366,8 @@ __device__ __forceinline__ float4 load4f<__bf16>(const __bf16* p) {
 // IPW items per workgroup: 2 runs two items of one KV head (batch rows b and b + B/2) on the two halves
 // of the waves, which share the angle tables and u_k^T staged once.
 template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, int NW, typename TabT, typename OutT, int IPW = 1>
-// At least two waves per SIMD (256 registers) wherever the width pair's default is 8 waves per workgroup,
-// so that its 4-wave variant fits two workgroups per CU.
-__global__ __launch_bounds__(NW * 64, (NW == 8 || pick_nw<RK, RV, KFULL, TILED>() == 8) ? 2 : 1)
+// 8 waves: two per SIMD, 256 registers each; 4 waves: one per SIMD with the whole register file.
+__global__ __launch_bounds__(NW * 64, NW == 8 ? 2 : 1)
 void palu_decode_kernel(const DecodeArgs a) {
   static_assert(RK % 16 == 0 && RK <= 128 && (TILED || RK % 32 == 0), "RK: 16-wide half tiles (tiled), 32-wide rows");
   static_assert(RV % 16 == 0 && RV <= 128 && (TILED || RV % 32 == 0), "RV: 16-wide V tiles (tiled), 32-wide rows");
