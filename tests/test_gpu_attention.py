@@ -86,14 +86,16 @@ def test_attention_prefill_then_decode_matches_layer_oracle(gpu, r_k, r_v, gs, l
     _drive(gpu, sd, palu, oracle, dim, nh, nkv, B, S0, steps, layout, fused)
 
 
-def test_attention_grouped_latents_of_unequal_ranks(gpu):
+@pytest.mark.parametrize("fused", [True, False])
+def test_attention_grouped_latents_of_unequal_ranks(gpu, fused):
     """G-LRD with 2 groups of 2 KV heads whose ranks differ (K 96 / 192, V 256 / 64), padded to the
     widest in the factors as load_palu_dir pads them; the layer keeps each group's latents at its own
-    ranks (compact caches) and passes the groups' ranks to the fused op."""
+    ranks (compact caches) and passes the groups' ranks to the fused op; the naive path rebuilds from
+    the same compact caches."""
     dim, nh, nkv, B, S0, steps = 1024, 8, 4, 2, 40, 6
     gr = ([96, 192], [256, 64])
-    sd, palu, oracle = _layer(dim, nh, nkv, 192, 256, 2, seed=7, group_ranks=gr)
-    att = _drive(gpu, sd, palu, oracle, dim, nh, nkv, B, S0, steps, "tiled", True)
+    sd, palu, oracle = _layer(dim, nh, nkv, 192, 256, 2, seed=7, group_ranks=gr, use_fused_k=fused)
+    att = _drive(gpu, sd, palu, oracle, dim, nh, nkv, B, S0, steps, "tiled", fused)
     assert att.group_ranks == ([96, 192], [256, 64])
     assert all(isinstance(c, GroupedLatentCache) for c in att.layer_past)
     assert att.kv_bytes_per_token() == (96 + 192 + 256 + 64) * 2.0
