@@ -314,6 +314,125 @@ def test_qkv_post_equals_rope_and_appends(gpu, layout, gs, r_k, r_v, k_rope):
     assert torch.equal(kt(values), kt(values2))
 
 
+@pytest.mark.parametrize("layout,gs,r_k,r_v,k_rope,rows,x_tiled,rtw",
+                         [("tiled", 1, 64, 96, False, 6, True, 0), ("rows", 1, 32, 128, False, 6, False, 0),
+                          ("tiled", 4, 256, 192, False, 6, True, 3), ("tiled", 1, 128, 64, True, 6, False, 0),
+                          ("tiled", 1, 80, 48, False, 64, True, 0), ("tiled", 1, 112, 64, False, 33, True, 5)])
+def test_linear_qkv_equals_projection_and_qkv_post(gpu, layout, gs, r_k, r_v, k_rope, rows, x_tiled, rtw):
+    """The QKV projection with its epilogue in one launch: q and both caches bit for bit as the one-slice
+    projection's fp32 output through qkv_post (same products, same order, same rotation and rounding)."""
+    g = torch.Generator().manual_seed(r_k + r_v + gs + rows)
+    nh, nkv, hd, S, dim = 8, 4, 128, 256, 1024
+    G = nkv // gs
+    k_w = hd if k_rope else r_k
+    k0, v0 = nh * hd, nh * hd + G * k_w
+    n = v0 + G * r_v
+    x = torch.randn(rows, dim, generator=g).to(gpu, torch.bfloat16)
+    w = (torch.randn(n, dim, generator=g) * 0.03).to(gpu, torch.bfloat16)
+    pos = torch.randint(0, S, (rows,), generator=g).to(gpu, torch.int32)
+    pos[0] = 0
+    pos[-1] = S - 1
+    cos, sin = fused.cos_sin_tables(hd, S, 500000.0, None)
+    cos, sin = cos.to(gpu).contiguous(), sin.to(gpu).contiguous()
+    mk = (lambda wd, role: LatentCache.zeros(rows, G, S, wd, gpu, role)) if layout == "tiled" else \
+        (lambda wd, role: torch.zeros(rows, G, S, wd, dtype=torch.bfloat16, device=gpu))
+    keys, values, keys2, values2 = mk(k_w, "k"), mk(r_v, "v"), mk(k_w, "k"), mk(r_v, "v")
+    rtw = rtw or decoder_ops.linear_plan(rows, n, dim, 1)[0]
+    wt = decoder_ops.tile_weight(w, rtw)
+    xa = decoder_ops.tile_rows(x) if x_tiled else x
+    q = decoder_ops.linear_qkv(xa, wt, rtw, pos, cos, sin, nh, keys, k0, k_w, k_w, values, v0, r_v, r_v,
+                               k_rope=k_rope, x_tiled=x_tiled, rows=rows)
+    part = decoder_ops.linear_tiled(xa, wt, rtw, 1, x_tiled=x_tiled, rows=rows, mode="partials")
+    q2 = decoder_ops.qkv_post(part, pos, cos, sin, nh, keys2, k0, k_w, k_w, values2, v0, r_v, r_v, k_rope=k_rope)
+    torch.cuda.synchronize()
+    kt = (lambda c: c.to_rows()) if layout == "tiled" else (lambda c: c)
+    assert torch.equal(q, q2)
+    assert torch.equal(kt(keys), kt(keys2)) and torch.equal(kt(values), kt(values2))
+    q_ref = fused.apply_rope_meta(_linear_ref(x, w)[:, :k0].view(rows, nh, hd), cos[pos.long()][:, None],
+                                  sin[pos.long()][:, None])
+    _check_linear(q, q_ref)
+
+
+def test_linear_qkv_rejects_overlapping_ranges(gpu):
+    x = torch.zeros(4, 256, dtype=torch.bfloat16, device=gpu)
+    wt = torch.zeros(128 + 2 * 64, 256, dtype=torch.bfloat16, device=gpu)
+    pos = torch.zeros(4, dtype=torch.int32, device=gpu)
+    cos, sin = fused.cos_sin_tables(128, 64, 500000.0, None)
+    cos, sin = cos.to(gpu).contiguous(), sin.to(gpu).contiguous()
+    keys = torch.zeros(4, 1, 64, 64, dtype=torch.bfloat16, device=gpu)
+    values = torch.zeros(4, 1, 64, 64, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError, match="must not overlap"):
+        decoder_ops.linear_qkv(x, wt, 1, pos, cos, sin, 1, keys, 128, 64, 64, values, 160, 64, 64)
+    with pytest.raises(RuntimeError, match="must not overlap"):
+        decoder_ops.linear_qkv(x, wt, 1, pos, cos, sin, 1, keys, 64, 64, 64, values, 192, 64, 64)
+
+
+@pytest.mark.parametrize("rows,n,k,x_tiled,with_tiled", [(64, 4096, 2048, True, True), (64, 4096, 4096, False, True),
+                                                         (23, 4096, 1280, True, True), (5, 400, 1344, False, False)])
+def test_linear_residual_equals_partials_plus_h(gpu, rows, n, k, x_tiled, with_tiled):
+    """h += x w^T in the projection's epilogue: bit for bit bf16(h + the one-slice fp32 product), the tiled
+    copy equal to tile_rows of the new h, rows past the live count of the tiled copy untouched."""
+    g = torch.Generator().manual_seed(n + k + rows)
+    x = torch.randn(rows, k, generator=g).to(gpu, torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(gpu, torch.bfloat16)
+    h = torch.randn(rows, n, generator=g).to(gpu, torch.bfloat16)
+    rtw = decoder_ops.linear_plan(rows, n, k, 1)[0]
+    wt = decoder_ops.tile_weight(w, rtw)
+    xa = decoder_ops.tile_rows(x) if x_tiled else x
+    part = decoder_ops.linear_tiled(xa, wt, rtw, 1, x_tiled=x_tiled, rows=rows, mode="partials")
+    h_ref = (h.float() + part[0]).to(torch.bfloat16)
+    ht = torch.full((64, n), float("nan"), dtype=torch.bfloat16, device=gpu) if with_tiled else None
+    hw = torch.zeros(rows, n + 8, dtype=torch.bfloat16, device=gpu)
+    hv = hw[:, 4:4 + n]
+    hv.copy_(h)
+    decoder_ops.linear_residual(xa, wt, rtw, hv, ht, x_tiled=x_tiled, rows=rows)
+    torch.cuda.synchronize()
+    assert torch.equal(hv, h_ref)
+    assert (hw[:, :4] == 0).all() and (hw[:, 4 + n:] == 0).all()
+    _check_linear(part[0], _linear_ref(x, w))
+    if with_tiled:
+        assert torch.equal(decoder_ops.untile_rows(ht, rows), h_ref)
+        pad = decoder_ops.untile_weight(ht, 4)[rows:]
+        assert torch.isnan(pad.float()).all()
+
+
+@pytest.mark.parametrize("rows,x_tiled", [(64, True), (64, False), (13, True)])
+def test_linear_swiglu_rmsnorm(gpu, rows, x_tiled):
+    """The gate / up launch over RMS-normalised rows (norm weight folded into the gate / up columns) against
+    fp32 torch: silu(g) * u of rmsnorm(x) w^T; and against palu_rmsnorm followed by the SwiGLU projection
+    within their two bf16 roundings. Rows of the tiled input past the live count hold NaN and are ignored."""
+    g = torch.Generator().manual_seed(rows + 7 * x_tiled)
+    k, f, eps = 2048, 1536, 1e-5
+    x = (torch.randn(rows, k, generator=g) * 3).to(gpu, torch.bfloat16)
+    nw = (1 + 0.2 * torch.randn(k, generator=g)).to(gpu, torch.bfloat16)
+    wg = (torch.randn(f, k, generator=g) * 0.05).to(gpu, torch.bfloat16)
+    wu = (torch.randn(f, k, generator=g) * 0.05).to(gpu, torch.bfloat16)
+    lin = decoder_ops.DecodeLinear(None, 64, gate_up=(wg, wu), in_scale=nw)
+    assert lin.tiled and lin.in_scale_folded
+    if x_tiled:
+        pad = torch.full((64, k), float("nan"), dtype=torch.bfloat16, device=gpu)
+        pad[:rows] = x
+        xa = decoder_ops.tile_weight(pad, 4)
+    else:
+        xa = x
+    out = lin.swiglu_rmsnorm(xa, eps, x_tiled=x_tiled, rows=rows)
+    plain = decoder_ops.DecodeLinear(None, 64, gate_up=(wg, wu))
+    y = decoder_ops.rmsnorm(x, nw, eps)
+    two = plain(y)
+    torch.cuda.synchronize()
+    got = decoder_ops.untile_rows(out, rows).float()
+    xf = x.float()
+    xn = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * nw.float()
+    gate, up = xn @ wg.float().T, xn @ wu.float().T
+    ref = gate / (1 + torch.exp(-gate)) * up
+    scale = ref.abs().max().item()
+    # the folded weight and the output each round once to bf16
+    assert (got - ref).abs().max().item() <= scale * 2 ** -6
+    assert F.cosine_similarity(got.flatten(), ref.flatten(), dim=0).item() >= 0.9999
+    two = decoder_ops.untile_rows(two, rows).float()
+    assert (got - two).abs().max().item() <= scale * 2 ** -5
+
+
 @pytest.mark.parametrize("B,S,r_k,r_v,hpg", [(32, 512, 64, 64, 1), (3, 1024, 96, 32, 1), (16, 256, 128, 256, 4)])
 def test_sdpa_decode_tiled_rows_output(gpu, B, S, r_k, r_v, hpg):
     """palu_sdpa_decode with tiled_rows writes tile_rows of its row-major output, bit for bit (fixed

@@ -368,6 +368,31 @@ def test_flash_decode_and_append_envelope_errors(lib):
     assert rc == _native.PALU_EINVAL and "1..16 groups" in lib.palu_last_error().decode()
 
 
+def test_fused_projection_plans_and_envelope_errors(lib):
+    """The one-slice plan the fused epilogues use, and their argument checks (host-side, before any launch)."""
+    rtw, ks = ctypes.c_int(0), ctypes.c_int(0)
+    assert lib.palu_linear_plan_ks(64, 5120, 4096, 1, ctypes.byref(rtw), ctypes.byref(ks)) == _native.PALU_OK
+    assert ks.value == 1 and 1 <= rtw.value <= 8
+    assert lib.palu_linear_plan_ks(64, 4096, 14336, 16, ctypes.byref(rtw), ctypes.byref(ks)) == _native.PALU_OK
+    assert ks.value > 1
+    assert lib.palu_linear_plan_ks(64, 4096, 14336, 0, ctypes.byref(rtw), ctypes.byref(ks)) == _native.PALU_EINVAL
+    F = _FAKE
+    rc = lib.palu_linear_swiglu_rmsnorm(F, 0, 1, 64, F, 4096 + 32, 4096, 7, 1e-5, F, None)
+    assert rc == _native.PALU_EINVAL and "multiple of 64" in lib.palu_last_error().decode()
+    rc = lib.palu_linear_residual(F, 0, 1, 64, F, 4096, 2048, 1, F, 4090, F, None)
+    assert rc == _native.PALU_EINVAL and "ldh" in lib.palu_last_error().decode()
+    rc = lib.palu_linear_residual(F, 0, 1, 65, F, 4096, 2048, 1, F, 4096, F, None)
+    assert rc == _native.PALU_EINVAL and "1..64" in lib.palu_last_error().decode()
+    # q heads 0..1023, K slices from 1024 (2 groups of 64), V slices overlapping the second K slice
+    qkv = lambda v_off, k_gs=64: lib.palu_linear_qkv(F, 0, 1, 8, F, 1024 + 256, 1024, 1, F, F, F, 256, 8, F, F, 1, 1024,
+                                                     k_gs, 64, 0, F, 2, v_off, 64, 64, 2, 256, None)
+    assert qkv(1120) == _native.PALU_EINVAL and "must not overlap" in lib.palu_last_error().decode()
+    assert qkv(1152, k_gs=32) == _native.PALU_EINVAL and "must not overlap" in lib.palu_last_error().decode()
+    rc = lib.palu_linear_qkv(F, 0, 1, 8, F, 1280, 1024, 1, F, F, F, 256, 8, F, F, 2, 1024, 64, 64, 0, F, 2, 1152, 64,
+                             64, 2, 256, None)
+    assert rc == _native.PALU_EINVAL and "K caches are" in lib.palu_last_error().decode()
+
+
 def test_paged_envelope_errors(lib):
     pt = _FAKE
 

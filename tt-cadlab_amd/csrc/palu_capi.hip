@@ -167,25 +167,19 @@ int check_append(void* cache, const void* new_rows, const int32_t* update_idxs, 
 }
 
 // Fused epilogue of the decode step's QKV projection (its fp32 k-slice partials [ks][B][ncols]): per
-// batch row, the q heads (columns h * 128 ..) rotated by Meta RoPE at pos[b] into q_out [B, nh, 128], and
-// each latent group's K slice (columns k_off + g * k_gs, k_w wide; rotated too when k_rope, the stock
-// full-rank K path, one head per group) and V slice (v_off + g * v_gs, v_w wide) appended to the caches
-// at position pos[b], as palu_rope_rows and palu_latent_append_strided do over a bf16 projection output.
-// One thread per 8 consecutive columns; the partials are summed in slice order in fp32 and rounded once.
+// batch row, the q heads rotated at pos[b] into q_out and each latent group's K and V slices appended to
+// the caches at pos[b] (QkvEpi), as palu_rope_rows and palu_latent_append_strided do over a bf16
+// projection output. One thread per 8 consecutive columns; the partials are summed in slice order in
+// fp32 and rounded once.
 constexpr int QP_PK = 4;   // partial slices loaded together
 
-__global__ __launch_bounds__(256) void palu_qkv_post_kernel(const float* part, int ks, int B, int ncols,
-                                                            const int32_t* pos, const float* cos_t, const float* sin_t,
-                                                            int table_rows, int nh, __bf16* q_out, __bf16* kc,
-                                                            int k_layout, int k_off, int k_gs, int k_w, int k_rope,
-                                                            __bf16* vc, int v_layout, int v_off, int v_gs, int v_w,
-                                                            int G, int S) {
-  const int qv = nh * (HD / 8), kv = G * (k_w / 8), vv = G * (v_w / 8);
+__global__ __launch_bounds__(256) void palu_qkv_post_kernel(const float* part, int ks, int B, int ncols, QkvEpi e) {
+  const int qv = e.nh * (HD / 8), kv = e.G * (e.k_w / 8), vv = e.G * (e.v_w / 8);
   const int per = qv + kv + vv;
   const long long total = (long long)B * per;
-  for (long long e = blockIdx.x * 256LL + threadIdx.x; e < total; e += (long long)gridDim.x * 256) {
-    const int b = (int)(e / per), t = (int)(e - (long long)b * per);
-    int kind, gi = 0, c8, col;
+  for (long long i = blockIdx.x * 256LL + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
+    const int b = (int)(i / per), t = (int)(i - (long long)b * per);
+    int kind, gi, c8, col;
     if (t < qv) {
       kind = 0;
       c8 = (t % (HD / 8)) * 8;
@@ -193,18 +187,18 @@ __global__ __launch_bounds__(256) void palu_qkv_post_kernel(const float* part, i
       col = gi * HD + c8;
     } else if (t < qv + kv) {
       kind = 1;
-      gi = (t - qv) / (k_w / 8);
-      c8 = ((t - qv) % (k_w / 8)) * 8;
-      col = k_off + gi * k_gs + c8;
+      gi = (t - qv) / (e.k_w / 8);
+      c8 = ((t - qv) % (e.k_w / 8)) * 8;
+      col = e.k_off + gi * e.k_gs + c8;
     } else {
       kind = 2;
-      gi = (t - qv - kv) / (v_w / 8);
-      c8 = ((t - qv - kv) % (v_w / 8)) * 8;
-      col = v_off + gi * v_gs + c8;
+      gi = (t - qv - kv) / (e.v_w / 8);
+      c8 = ((t - qv - kv) % (e.v_w / 8)) * 8;
+      col = e.v_off + gi * e.v_gs + c8;
     }
     // The row's position and the first QP_PK partial slices are loaded together (the kernel is bound by
     // memory latency); slices past ks re-read the last one and are not added.
-    const int p = pos[b];
+    const int p = e.pos[b];
     const float* pp = part + (long long)b * ncols + col;
     const long long pstride = (long long)B * ncols;
     f32x4 pa[QP_PK][2];
@@ -227,40 +221,10 @@ __global__ __launch_bounds__(256) void palu_qkv_post_kernel(const float* part, i
       s1 += *reinterpret_cast<const f32x4*>(pp + k * pstride + 4);
     }
     float v[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-    if (kind == 0 || (kind == 1 && k_rope)) {
-      const int pr = p < 0 ? 0 : (p >= table_rows ? table_rows - 1 : p);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float c = cos_t[(long long)pr * HD + c8 + 2 * i], sn = sin_t[(long long)pr * HD + c8 + 2 * i];
-        const float x0 = v[2 * i], x1 = v[2 * i + 1];
-        v[2 * i] = x0 * c - x1 * sn;
-        v[2 * i + 1] = x1 * c + x0 * sn;
-      }
-    }
-    bf16x8 o;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = (__bf16)v[j];
-    if (kind == 0) {
-      *reinterpret_cast<bf16x8*>(q_out + ((long long)b * nh + gi) * HD + c8) = o;
-      continue;
-    }
-    if (p < 0 || p >= S) continue;
-    const int layout = kind == 1 ? k_layout : v_layout, width = kind == 1 ? k_w : v_w;
-    __bf16* stream = (kind == 1 ? kc : vc) + ((long long)b * G + gi) * S * width;
-    if (layout == PALU_LAYOUT_ROWS) {
-      *reinterpret_cast<bf16x8*>(stream + (long long)p * width + c8) = o;
-    } else if (layout == PALU_LAYOUT_TILED) {
-      store_k8(stream, p, c8, width, o);
-    } else {
-      const long long off = tiled_v_offset(p, c8, width);   // 8 slots 16 bytes apart
-#pragma unroll
-      for (int j = 0; j < 8; ++j) stream[off + 8 * j] = o[j];
-    }
+    qkv_store<8>(e, b, p, kind, gi, c8, v);
   }
 }
 
-// Validation shared by the contiguous and paged fused decode; fills every field of a except the
-// cache strides and the paging fields.
 int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w_rot, const void* cs_tab,
                const void* v_latent, int head_dim_v, const int32_t* cur_pos, void* out, const float* rot_step,
                const void* trans_mat, const void* u_v, const int32_t* group_ranks, float scale, int heads_per_core,
@@ -473,6 +437,30 @@ int scratch_of_current_device(void** addr) {
 
 }  // namespace
 
+namespace palu {
+
+int check_qkv_epi(const QkvEpi& e, int batch, int ncols, const void* src, const char* who) {
+  if (!src || !e.pos || !e.cos_t || !e.sin_t || !e.q_out) return fail(PALU_EINVAL, "%s: a required pointer is null", who);
+  if (batch < 1 || e.nh < 1 || e.table_rows < 1 || ncols <= 0 || ncols % 8)
+    return fail(PALU_EINVAL, "%s: batch = %d, n_heads = %d, table_rows = %d, ncols = %d (multiple of 8)", who, batch,
+                e.nh, e.table_rows, ncols);
+  if (e.k_layout == PALU_LAYOUT_TILED_V || e.v_layout == PALU_LAYOUT_TILED)
+    return fail(PALU_EINVAL, "%s: K caches are PALU_LAYOUT_ROWS or PALU_LAYOUT_TILED, V caches ROWS or TILED_V", who);
+  if (int rc = check_append(e.kc, src, e.pos, batch, e.G, e.S, e.k_w, e.k_layout, who)) return rc;
+  if (int rc = check_append(e.vc, src, e.pos, batch, e.G, e.S, e.v_w, e.v_layout, who)) return rc;
+  if (!aligned16(e.q_out)) return fail(PALU_EINVAL, "%s: 16-byte alignment required", who);
+  if (e.k_rope && e.k_w != HD) return fail(PALU_EINVAL, "%s: a rotated K slice is one %d-wide head, got %d", who, HD, e.k_w);
+  if ((long long)e.nh * HD > ncols || e.k_off < 0 || e.v_off < 0 || e.k_gs < 0 || e.v_gs < 0 || e.k_off % 8 ||
+      e.v_off % 8 || e.k_gs % 8 || e.v_gs % 8 ||
+      (long long)e.k_off + (long long)(e.G - 1) * e.k_gs + e.k_w > ncols ||
+      (long long)e.v_off + (long long)(e.G - 1) * e.v_gs + e.v_w > ncols)
+    return fail(PALU_EINVAL, "%s: the q, K and V column ranges must lie inside the %d columns, on multiples of 8", who,
+                ncols);
+  return PALU_OK;
+}
+
+}  // namespace palu
+
 extern "C" {
 
 const char* palu_last_error(void) { return palu::g_err; }
@@ -632,31 +620,17 @@ int palu_qkv_post(const float* qkv_part, int ks, int batch, int ncols, const int
                   int v_col_offset, int v_group_stride, int v_width, int n_groups, int seq_len, hipStream_t stream) {
   palu::g_err[0] = 0;
   const char* who = "palu_qkv_post";
-  if (!qkv_part || !pos || !cos_table || !sin_table || !q_out)
-    return fail(PALU_EINVAL, "%s: a required pointer is null", who);
-  if (ks < 1 || ks > 64 || batch < 1 || n_heads < 1 || table_rows < 1 || ncols <= 0 || ncols % 8)
-    return fail(PALU_EINVAL, "%s: ks = %d (1..64), batch = %d, n_heads = %d, table_rows = %d, ncols = %d (multiple of 8)",
-                who, ks, batch, n_heads, table_rows, ncols);
-  if (k_layout == PALU_LAYOUT_TILED_V || v_layout == PALU_LAYOUT_TILED)
-    return fail(PALU_EINVAL, "%s: K caches are PALU_LAYOUT_ROWS or PALU_LAYOUT_TILED, V caches ROWS or TILED_V", who);
-  if (int rc = check_append(k_cache, qkv_part, pos, batch, n_groups, seq_len, k_width, k_layout, who)) return rc;
-  if (int rc = check_append(v_cache, qkv_part, pos, batch, n_groups, seq_len, v_width, v_layout, who)) return rc;
-  if (!aligned16(q_out)) return fail(PALU_EINVAL, "%s: 16-byte alignment required", who);
-  if (k_rope && k_width != HD) return fail(PALU_EINVAL, "%s: a rotated K slice is one %d-wide head, got %d", who, HD, k_width);
-  if ((long long)n_heads * HD > ncols || k_col_offset < 0 || v_col_offset < 0 || k_group_stride < 0 || v_group_stride < 0 ||
-      k_col_offset % 8 || v_col_offset % 8 || k_group_stride % 8 || v_group_stride % 8 ||
-      (long long)k_col_offset + (long long)(n_groups - 1) * k_group_stride + k_width > ncols ||
-      (long long)v_col_offset + (long long)(n_groups - 1) * v_group_stride + v_width > ncols)
-    return fail(PALU_EINVAL, "%s: the q, K and V column ranges must lie inside the %d columns, on multiples of 8", who,
-                ncols);
+  if (!qkv_part) return fail(PALU_EINVAL, "%s: a required pointer is null", who);
+  if (ks < 1 || ks > 64) return fail(PALU_EINVAL, "%s: ks = %d (1..64)", who, ks);
+  const QkvEpi e{pos, cos_table, sin_table, table_rows, n_heads, static_cast<__bf16*>(q_out),
+                 static_cast<__bf16*>(k_cache), k_layout, k_col_offset, k_group_stride, k_width, k_rope ? 1 : 0,
+                 static_cast<__bf16*>(v_cache), v_layout, v_col_offset, v_group_stride, v_width, n_groups, seq_len};
+  if (int rc = check_qkv_epi(e, batch, ncols, qkv_part, who)) return rc;
   const long long vecs = (long long)batch * (n_heads * (HD / 8) + n_groups * (k_width / 8) + n_groups * (v_width / 8));
   const int blocks = (int)std::min<long long>((vecs + 255) / 256, 2048);
-  hipLaunchKernelGGL(palu_qkv_post_kernel, dim3(blocks), dim3(256), 0, stream, qkv_part, ks, batch, ncols, pos, cos_table,
-                     sin_table, table_rows, n_heads, static_cast<__bf16*>(q_out), static_cast<__bf16*>(k_cache),
-                     k_layout, k_col_offset, k_group_stride, k_width, k_rope ? 1 : 0, static_cast<__bf16*>(v_cache),
-                     v_layout, v_col_offset, v_group_stride, v_width, n_groups, seq_len);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(PALU_EHIP, "%s launch: %s", who, hipGetErrorString(e));
+  hipLaunchKernelGGL(palu_qkv_post_kernel, dim3(blocks), dim3(256), 0, stream, qkv_part, ks, batch, ncols, e);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(PALU_EHIP, "%s launch: %s", who, hipGetErrorString(err));
   return PALU_OK;
 }
 

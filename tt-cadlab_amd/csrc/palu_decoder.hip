@@ -9,12 +9,6 @@ namespace {
 
 __device__ __forceinline__ float bf(const __bf16 x) { return (float)x; }
 
-// Element offset of (row, col .. col + 7) in the 64-row tiled activation layout of the decode projection
-// (palu_linear_tiled with x_tiled): tile (col / 32, row / 16) of 1 KB, lane 16 ((col % 32) / 8) + row % 16.
-__device__ __forceinline__ long long tiled_row_offset(int row, int col) {
-  return ((long long)((col >> 5) * 4 + (row >> 4)) * 64 + 16 * ((col & 31) >> 3) + (row & 15)) * 8;
-}
-
 // One workgroup per row: h = x (+ res), stored when h_out is given; y = h * rsqrt(mean(h^2) + eps) * w.
 // Each thread holds up to RMS_VEC vectors of 8 elements in registers between the two passes. The kernel
 // is tiny and bound by memory latency, so every load of the row (x, the residual or the first RMS_PK

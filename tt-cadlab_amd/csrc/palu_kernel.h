@@ -56,6 +56,7 @@ namespace palu {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -111,6 +112,28 @@ struct DecodeArgs {
 // Error reporting (defined in palu_capi.hip): formats the message for palu_last_error, returns code.
 int fail(int code, const char* fmt, ...);
 extern thread_local char g_err[1024];
+
+// The decode step's QKV epilogue (palu_qkv_post over split partials, palu_linear_qkv inside the
+// projection): where each part of a QKV output row goes. q heads are columns h * 128 .. of the row,
+// rotated at pos[b] into q_out [B, nh, 128]; group g's K slice is columns k_off + g * k_gs, k_w wide
+// (rotated too when k_rope: the stock path's full-rank K, one head per group), appended at pos[b] to
+// the K cache (layout k_layout); V the same with v_*. Caches are [B, G, S, width] streams.
+struct QkvEpi {
+  const int32_t* pos;
+  const float* cos_t;
+  const float* sin_t;
+  int table_rows, nh;
+  __bf16* q_out;
+  __bf16* kc;
+  int k_layout, k_off, k_gs, k_w, k_rope;
+  __bf16* vc;
+  int v_layout, v_off, v_gs, v_w;
+  int G, S;
+};
+
+// Checks a QkvEpi for a QKV output of `batch` rows of `ncols` columns read from src (defined in
+// palu_capi.hip; `who` names the entry point in the message).
+int check_qkv_epi(const QkvEpi& e, int batch, int ncols, const void* src, const char* who);
 
 // Waves per workgroup: 8 (two per SIMD) where the kernel fits 256 registers, else 4 (one per SIMD,
 // which lets the compiler use the full 512-entry register file instead of spilling).
@@ -204,6 +227,63 @@ __device__ __forceinline__ void store_k8(__bf16* stream, int p, int k, int R, co
 __device__ __forceinline__ long long tiled_v_offset(int p, int k, int R) {
   const int t = p & 31;
   return (long long)(p >> 5) * (32 * R) + ((k >> 4) * 64 + 16 * (t >> 3) + (k & 15)) * 8 + (t & 7);
+}
+
+// Element offset of (row, col) in the 64-row tiled activation layout of the decode projections
+// (palu_linear_tiled with x_tiled): tile (col / 32, row / 16) of 1 KB, lane 16 ((col % 32) / 8) + row % 16,
+// element col % 8.
+__device__ __forceinline__ long long tiled_row_offset(int row, int col) {
+  return ((long long)((col >> 5) * 4 + (row >> 4)) * 64 + 16 * ((col & 31) >> 3) + (row & 15)) * 8 + (col & 7);
+}
+
+// Meta RoPE of N consecutive fp32 values of one head starting at head column c (even), table row pr:
+// pairs (2i, 2i+1) -> (x0 c - x1 s, x1 c + x0 s). The fused multiply-adds are written out so that every
+// kernel that rotates rounds the same way.
+template <int N>
+__device__ __forceinline__ void rope_meta(float (&v)[N], const float* cos_t, const float* sin_t, int pr, int c) {
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float cs = cos_t[(long long)pr * HD + c + 2 * i], sn = sin_t[(long long)pr * HD + c + 2 * i];
+    const float x0 = v[2 * i], x1 = v[2 * i + 1];
+    v[2 * i] = fmaf(x0, cs, -(x1 * sn));
+    v[2 * i + 1] = fmaf(x1, cs, x0 * sn);
+  }
+}
+
+// N = 4 or 8 consecutive fp32 values of QKV output row b, starting at a multiple of N inside one part
+// of the row: q head gi (kind 0), or group gi's K (kind 1) or V slice (kind 2), at column c of that head
+// or slice. Rotated where the epilogue says, rounded to bf16 once, and stored to q_out or appended to
+// the cache at the row's position p = pos[b] (positions outside the cache are not appended).
+template <int N>
+__device__ __forceinline__ void qkv_store(const QkvEpi& e, int b, int p, int kind, int gi, int c, float (&v)[N]) {
+  typedef __bf16 bfn __attribute__((ext_vector_type(N)));
+  if (kind == 0 || (kind == 1 && e.k_rope)) {
+    const int pr = p < 0 ? 0 : (p >= e.table_rows ? e.table_rows - 1 : p);
+    rope_meta<N>(v, e.cos_t, e.sin_t, pr, c);
+  }
+  bfn o;
+#pragma unroll
+  for (int j = 0; j < N; ++j) o[j] = (__bf16)v[j];
+  if (kind == 0) {
+    *reinterpret_cast<bfn*>(e.q_out + ((long long)b * e.nh + gi) * HD + c) = o;
+    return;
+  }
+  if (p < 0 || p >= e.S) return;
+  const int layout = kind == 1 ? e.k_layout : e.v_layout, width = kind == 1 ? e.k_w : e.v_w;
+  __bf16* stream = (kind == 1 ? e.kc : e.vc) + ((long long)b * e.G + gi) * e.S * width;
+  if (layout == PALU_LAYOUT_ROWS) {
+    *reinterpret_cast<bfn*>(stream + (long long)p * width + c) = o;
+  } else if (layout == PALU_LAYOUT_TILED) {
+    if constexpr (N == 8) {
+      store_k8(stream, p, c, width, o);
+    } else {
+      *reinterpret_cast<bfn*>(stream + tiled_k_offset(p, c, width)) = o;   // 4 width-indices share a slot
+    }
+  } else {
+    const long long off = tiled_v_offset(p, c, width);   // N slots 16 bytes apart
+#pragma unroll
+    for (int j = 0; j < N; ++j) stream[off + 8 * j] = o[j];
+  }
 }
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {

@@ -15,10 +15,15 @@
 // four row tiles ([kt][mt], palu_tt.decoder_ops.tile_rows; one contiguous kilobyte per tile), which
 // the decoder's RMSNorm and SwiGLU kernels write directly.
 //
-// Outputs (y_mode): bf16 y [m][n] (split partials summed by a second launch); the fp32 split partials
-// [KS][m][n] themselves, for a consumer that sums them (palu_rmsnorm's residual input, palu_qkv_post);
-// or, for a gate / up weight interleaved eight rows at a time (tile_weight of
-// palu_tt.decoder_ops.interleave_gate_up), silu(gate) * up in the tiled activation layout.
+// Outputs (the epilogue, EPI): bf16 y [m][n] (split partials summed by a second launch); the fp32 split
+// partials [KS][m][n] themselves, for a consumer that sums them (palu_rmsnorm's residual input,
+// palu_qkv_post); for a gate / up weight interleaved eight rows at a time (tile_weight of
+// palu_tt.decoder_ops.interleave_gate_up), silu(gate) * up in the tiled activation layout, optionally
+// of the RMS-normalised x (the row scale rsqrt(mean(x^2) + eps) applied to the products, the norm's
+// weight folded into the gate / up weight; the loop sums x^2 from the activation tiles it already
+// loads); the residual update h += y, also written tiled for the next projection; or the decode step's
+// QKV epilogue (q RoPE, K / V latent appends), in place of palu_qkv_post's second launch. The last three
+// need KS = 1: the epilogue sees whole dot products.
 //
 // A workgroup owns one group and one of KS slices of the k tiles. Its 4 waves (one per SIMD, so each may
 // use the whole 512-entry register file) take the slice's k tiles in turn (wave w: kt0 + w, kt0 + w + 4,
@@ -35,26 +40,70 @@
 
 namespace {
 
-constexpr int LIN_NW = 4;
 constexpr int LIN_MT = 4;                       // 16-row activation tiles: m <= 64
 constexpr int LIN_MAX_RTW = 8;
 
-template <int RTW>
+// Epilogues.
+constexpr int EPI_OUT = 0;           // bf16 y, or the fp32 split partials
+constexpr int EPI_SWIGLU = 1;        // silu(gate) * up, tiled
+constexpr int EPI_SWIGLU_NORM = 2;   // the same over RMS-normalised x
+constexpr int EPI_RESID = 3;         // h += y (row-major), and h tiled
+constexpr int EPI_QKV = 4;           // q RoPE and latent appends (QkvEpi)
+
+struct LinEpi {
+  float eps, inv_k;                  // EPI_SWIGLU_NORM
+  __bf16* h;                         // EPI_RESID: [m][n] bf16, rows ldh apart
+  long long ldh;
+  __bf16* h_tiled;                   //   and the 64-row tiled copy (or null)
+  QkvEpi q;                          // EPI_QKV
+};
+
+template <int RTW, int NW, int EPI>
 struct LinSmem {
   static constexpr int SLOT = RTW * LIN_MT * 64;          // f32x4 per wave partial
-  static constexpr int BYTES = LIN_NW * SLOT * 16;        // every wave's partial
+  static constexpr int RED = NW * SLOT * 16;              // every wave's partial
+  static constexpr int BYTES = RED + (EPI == EPI_SWIGLU_NORM ? NW * 64 * 4 : 0);   // + per-wave row sums of x^2
 };
+
+// Where the QKV epilogue sends columns col .. col + 3: kind 0 (q head gi), 1 / 2 (group gi's K / V
+// slice) at column c of the head or slice, or -1 (a column no part reads).
+__device__ __forceinline__ int qkv_part_of(const QkvEpi& e, int col, int& gi, int& c) {
+  gi = 0;
+  c = 0;
+  if (col < e.nh * HD) {
+    gi = col / HD;
+    c = col - gi * HD;
+    return 0;
+  }
+  if (col >= e.k_off && col < e.k_off + (e.G - 1) * e.k_gs + e.k_w) {
+    const int d = col - e.k_off;
+    gi = e.G > 1 ? d / e.k_gs : 0;
+    c = d - gi * e.k_gs;
+    return c < e.k_w ? 1 : -1;
+  }
+  if (col >= e.v_off && col < e.v_off + (e.G - 1) * e.v_gs + e.v_w) {
+    const int d = col - e.v_off;
+    gi = e.G > 1 ? d / e.v_gs : 0;
+    c = d - gi * e.v_gs;
+    return c < e.v_w ? 2 : -1;
+  }
+  return -1;
+}
 
 // NB register buffers per wave, so each step's loads are issued NB - 1 steps before its MFMAs. Weight
 // and activation tiles of one step share a buffer: loads return in issue order, so an activation tile
-// loaded later than the weights would make every wait a wait for those weights too.
-template <int RTW, int NB, bool XT, bool SWIGLU>
-__global__ __launch_bounds__(LIN_NW * 64) void palu_linear_kernel(const __bf16* __restrict__ x, long long ldx, int m,
-                                                                  const __bf16* __restrict__ wt, int n16, int kt_total,
-                                                                  int ks_count, int kt_per_split,
-                                                                  __bf16* __restrict__ y, long long ldy,
-                                                                  float* __restrict__ part) {
-  using SM = LinSmem<RTW>;
+// loaded later than the weights would make every wait a wait for those weights too. NW waves per
+// workgroup: 4 (one per SIMD, the whole register file each) or 8 (two per SIMD, twice the loads in flight
+// per CU, for the narrow workgroups of the latency-bound small projections).
+template <int RTW, int NB, int NW, bool XT, int EPI>
+__global__ __launch_bounds__(NW * 64) void palu_linear_kernel(const __bf16* __restrict__ x, long long ldx, int m,
+                                                              const __bf16* __restrict__ wt, int n16, int kt_total,
+                                                              int ks_count, int kt_per_split,
+                                                              __bf16* __restrict__ y, long long ldy,
+                                                              float* __restrict__ part, const LinEpi ep) {
+  using SM = LinSmem<RTW, NW, EPI>;
+  constexpr bool SWIGLU = EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_NORM;
+  constexpr int NT = (RTW * LIN_MT + NW - 1) / NW;       // output tiles each wave stores (at most)
   extern __shared__ __attribute__((aligned(16))) char smem[];
   f32x4* red = reinterpret_cast<f32x4*>(smem);
 
@@ -66,6 +115,24 @@ __global__ __launch_bounds__(LIN_NW * 64) void palu_linear_kernel(const __bf16* 
   const int rt_cnt = min(RTW, n16 - rt0);                 // uniform: the last group may be short
   const int kt_lo = ks * kt_per_split;
   const int kt_hi = min(kt_total, kt_lo + kt_per_split);
+
+  // The epilogue's own global reads (the residual h, the rows' positions) are issued here, ahead of the
+  // weight stream, so the epilogue does not start with a round trip to memory. Wave w stores output
+  // tiles t = w, w + NW, ... (row tile t / 4, activation tile t % 4); lane (g, mm) of tile t holds
+  // columns 16 (rt0 + t / 4) + 4 g .. + 3 of row 16 (t % 4) + mm.
+  bf16x4 hpre[NT];
+  int ppre[NT];
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    const int t = w + i * NW;
+    const int r = t / LIN_MT, row = 16 * (t % LIN_MT) + mm;
+    const bool ok = t < RTW * LIN_MT && r < rt_cnt && row < m;
+    if constexpr (EPI == EPI_RESID) {
+      const int col = 16 * (rt0 + (ok ? r : 0)) + 4 * g;
+      hpre[i] = *reinterpret_cast<const bf16x4*>(ep.h + (ok ? row : 0) * ep.ldh + col);
+    }
+    if constexpr (EPI == EPI_QKV) ppre[i] = ep.q.pos[ok ? row : 0];
+  }
 
   // Activation rows past m are replaced by zeros (row-major: they read row 0); their outputs are not
   // stored.
@@ -84,6 +151,7 @@ __global__ __launch_bounds__(LIN_NW * 64) void palu_linear_kernel(const __bf16* 
   for (int r = 0; r < RTW; ++r)
 #pragma unroll
     for (int mt = 0; mt < LIN_MT; ++mt) acc[r][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ss[LIN_MT] = {0.f, 0.f, 0.f, 0.f};              // EPI_SWIGLU_NORM: this lane's share of sum x^2 per row
 
   // Every load is issued on every path (row tiles past rt_cnt read the last row tile, k tiles past the
   // slice read the matrix's last k tile; their products are never stored), so each wait in the loop is
@@ -106,6 +174,16 @@ __global__ __launch_bounds__(LIN_NW * 64) void palu_linear_kernel(const __bf16* 
     for (int r = 0; r < RTW; ++r)
 #pragma unroll
       for (int mt = 0; mt < LIN_MT; ++mt) acc[r][mt] = mfma16(wa[buf][r], bz[mt], acc[r][mt]);
+    if constexpr (EPI == EPI_SWIGLU_NORM) {
+      // x^2 summed in pairs (v_dot2: the bf16 products are exact in fp32)
+#pragma unroll
+      for (int mt = 0; mt < LIN_MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x2 p2{bz[mt][2 * j], bz[mt][2 * j + 1]};
+          ss[mt] = __builtin_amdgcn_fdot2_f32_bf16(p2, p2, ss[mt], false);
+        }
+    }
   };
 
   // The loop is unrolled by NB so that buffer indices are compile-time, and has no branch: steps past the
@@ -113,36 +191,47 @@ __global__ __launch_bounds__(LIN_NW * 64) void palu_linear_kernel(const __bf16* 
   // The scheduling barriers keep each step's loads ahead of the earlier step's MFMAs (left alone, the
   // compiler sinks every load to its first use and the wave has one tile in flight).
   const int kt0 = kt_lo + w;
-  const int nsteps = kt0 < kt_hi ? (kt_hi - kt0 + LIN_NW - 1) / LIN_NW : 0;   // uniform per wave
+  const int nsteps = kt0 < kt_hi ? (kt_hi - kt0 + NW - 1) / NW : 0;   // uniform per wave
 #pragma unroll
-  for (int j = 0; j < NB - 1; ++j) load(j, kt0 + j * LIN_NW);
+  for (int j = 0; j < NB - 1; ++j) load(j, kt0 + j * NW);
   for (int s = 0; s < nsteps; s += NB) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      load((j + NB - 1) % NB, kt0 + (s + j + NB - 1) * LIN_NW);
+      load((j + NB - 1) % NB, kt0 + (s + j + NB - 1) * NW);
       __builtin_amdgcn_sched_barrier(0);
       compute(j, s + j < nsteps);
     }
   }
 
   // The waves' partials meet in LDS (slot layout [wave][r][mt][lane] of f32x4); each wave then sums
-  // the four slots of every fourth (r, mt) tile and stores that tile, so the epilogue's arithmetic and
-  // stores are spread over the four SIMDs.
+  // the NW slots of every NW-th (r, mt) tile and stores that tile, so the epilogue's arithmetic and
+  // stores are spread over the SIMDs.
 #pragma unroll
   for (int r = 0; r < RTW; ++r)
 #pragma unroll
     for (int mt = 0; mt < LIN_MT; ++mt) red[w * SM::SLOT + (r * LIN_MT + mt) * 64 + lane] = acc[r][mt];
+  float* rss = reinterpret_cast<float*>(smem + SM::RED);   // [wave][row] sums of x^2
+  if constexpr (EPI == EPI_SWIGLU_NORM) {
+    // lanes (g, mm), g = 0..3, hold columns 8 g .. 8 g + 7 of every k tile of row 16 mt + mm
+#pragma unroll
+    for (int mt = 0; mt < LIN_MT; ++mt) {
+      ss[mt] += __shfl_xor(ss[mt], 16, 64);
+      ss[mt] += __shfl_xor(ss[mt], 32, 64);
+      if (g == 0) rss[w * 64 + 16 * mt + mm] = ss[mt];
+    }
+  }
   __syncthreads();
 
-  // Lane (g, mm) of tile (r, mt) holds y^T[16 (rt0 + r) + 4 g + i][16 mt + mm], i < 4: four consecutive
-  // output columns of activation row 16 mt + mm.
 #pragma unroll
-  for (int t = 0; t < RTW * LIN_MT; ++t) {
-    if (t % LIN_NW != w) continue;                         // uniform per wave
+  for (int i = 0; i < NT; ++i) {
+    const int t = w + i * NW;                              // uniform per wave
+    if (t >= RTW * LIN_MT) break;
     const int r = t / LIN_MT, mt = t % LIN_MT;
-    f32x4 v = red[(r * LIN_MT + mt) * 64 + lane];
+    f32x4 v = red[t * 64 + lane];
 #pragma unroll
-    for (int q = 1; q < LIN_NW; ++q) v += red[q * SM::SLOT + (r * LIN_MT + mt) * 64 + lane];
+    for (int q = 1; q < NW; ++q) v += red[q * SM::SLOT + t * 64 + lane];
+    // Lane (g, mm) of tile (r, mt) holds y^T[16 (rt0 + r) + 4 g + i][16 mt + mm], i < 4: four consecutive
+    // output columns of activation row 16 mt + mm.
     const int row = 16 * mt + mm;
     if constexpr (SWIGLU) {
       // Gate / up pairs: rows 0-7 of row tile rt are gate columns 8 rt .. 8 rt + 7 and rows 8-15 the up
@@ -150,17 +239,39 @@ __global__ __launch_bounds__(LIN_NW * 64) void palu_linear_kernel(const __bf16* 
       // holds gate columns 8 rt + 4 g + i and lane (g + 2, mm), 32 lanes on, the matching up values.
       // out = silu(gate) * up, stored in the tiled activation layout (64 rows x n / 2) the next
       // projection reads.
+      if constexpr (EPI == EPI_SWIGLU_NORM) {
+        float tot = 0.f;
+#pragma unroll
+        for (int q = 0; q < NW; ++q) tot += rss[q * 64 + row];
+        v *= rsqrtf(tot * ep.inv_k + ep.eps);
+      }
       f32x4 up;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) up[i] = __shfl_xor(v[i], 32, 64);
+      for (int k = 0; k < 4; ++k) up[k] = __shfl_xor(v[k], 32, 64);
       if (g >= 2 || row >= m || r >= rt_cnt) continue;
       const int col = 8 * (rt0 + r) + 4 * g;
       bf16x4 o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = (__bf16)((v[i] / (1.f + __expf(-v[i]))) * up[i]);
-      const long long off = ((long long)((col >> 5) * 4 + (row >> 4)) * 64 + 16 * ((col & 31) >> 3) + (row & 15)) * 8
-                            + (col & 7);
-      *reinterpret_cast<bf16x4*>(y + off) = o;
+      for (int k = 0; k < 4; ++k) o[k] = (__bf16)((v[k] / (1.f + __expf(-v[k]))) * up[k]);
+      *reinterpret_cast<bf16x4*>(y + tiled_row_offset(row, col)) = o;
+    } else if constexpr (EPI == EPI_RESID) {
+      // h + y rounded to bf16 once (the residual stream), in place and in the tiled layout
+      if (row >= m || r >= rt_cnt) continue;
+      const int col = 16 * (rt0 + r) + 4 * g;
+      bf16x4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o[k] = (__bf16)((float)hpre[i][k] + v[k]);
+      *reinterpret_cast<bf16x4*>(ep.h + row * ep.ldh + col) = o;
+      if (ep.h_tiled) *reinterpret_cast<bf16x4*>(ep.h_tiled + tiled_row_offset(row, col)) = o;
+    } else if constexpr (EPI == EPI_QKV) {
+      // Columns col .. col + 3 of QKV row `row` lie in one q head or one group's K or V slice (the entry
+      // point checks that the three ranges do not overlap and start on multiples of 8).
+      if (row >= m || r >= rt_cnt) continue;
+      int gi, c;
+      const int kind = qkv_part_of(ep.q, 16 * (rt0 + r) + 4 * g, gi, c);
+      if (kind < 0) continue;
+      float vv[4] = {v[0], v[1], v[2], v[3]};
+      qkv_store<4>(ep.q, row, ppre[i], kind, gi, c, vv);
     } else {
       if (row >= m || r >= rt_cnt) continue;
       const long long col = 16LL * (rt0 + r) + 4 * g;
@@ -169,7 +280,7 @@ __global__ __launch_bounds__(LIN_NW * 64) void palu_linear_kernel(const __bf16* 
       } else {
         bf16x4 o;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = (__bf16)v[i];
+        for (int k = 0; k < 4; ++k) o[k] = (__bf16)v[k];
         *reinterpret_cast<bf16x4*>(y + row * ldy + col) = o;
       }
     }
@@ -191,12 +302,19 @@ __global__ __launch_bounds__(256) void palu_linear_reduce_kernel(const float* __
   }
 }
 
-template <int RTW, bool XT, bool SWIGLU>
+// Register buffers per wave: NB = 8 for workgroups of one or two row tiles (latency-bound), 4 for wider
+// ones (about 8 KB of weights in flight per wave either way).
+#ifndef PALU_LIN_NARROW_DEPTH
+#define PALU_LIN_NARROW_DEPTH 8
+#endif
+
+template <int RTW, bool XT, int EPI>
 hipError_t launch_cfg(const __bf16* x, long long ldx, int m, const __bf16* wt, int n16, int kt_total, int ks,
-                      int ktps, __bf16* y, long long ldy, float* part, hipStream_t s) {
-  constexpr int NB = RTW <= 2 ? 8 : 4;                    // about 8 KB of weights in flight per wave
-  auto kern = palu_linear_kernel<RTW, NB, XT, SWIGLU>;
-  constexpr int lds = LinSmem<RTW>::BYTES;
+                      int ktps, __bf16* y, long long ldy, float* part, const LinEpi& ep, hipStream_t s) {
+  constexpr int NB = RTW <= 2 ? PALU_LIN_NARROW_DEPTH : 4;
+  constexpr int NW = 4;                                   // one wave per SIMD (8 measured slower end to end)
+  auto kern = palu_linear_kernel<RTW, NB, NW, XT, EPI>;
+  constexpr int lds = LinSmem<RTW, NW, EPI>::BYTES;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -204,38 +322,46 @@ hipError_t launch_cfg(const __bf16* x, long long ldx, int m, const __bf16* wt, i
     attr_set = true;
   }
   const int groups = (n16 + RTW - 1) / RTW;
-  hipLaunchKernelGGL(kern, dim3(groups * ks), dim3(LIN_NW * 64), lds, s, x, ldx, m, wt, n16, kt_total, ks, ktps, y,
-                     ldy, part);
+  hipLaunchKernelGGL(kern, dim3(groups * ks), dim3(NW * 64), lds, s, x, ldx, m, wt, n16, kt_total, ks, ktps, y,
+                     ldy, part, ep);
   return hipGetLastError();
 }
 
-template <bool XT, bool SWIGLU>
+template <bool XT, int EPI>
 hipError_t launch_rtw(int rtw, const __bf16* x, long long ldx, int m, const __bf16* wt, int n16, int kt_total, int ks,
-                      int ktps, __bf16* y, long long ldy, float* part, hipStream_t s) {
+                      int ktps, __bf16* y, long long ldy, float* part, const LinEpi& ep, hipStream_t s) {
   switch (rtw) {
-    case 1: return launch_cfg<1, XT, SWIGLU>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, s);
-    case 2: return launch_cfg<2, XT, SWIGLU>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, s);
-    case 3: return launch_cfg<3, XT, SWIGLU>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, s);
-    case 4: return launch_cfg<4, XT, SWIGLU>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, s);
-    case 5: return launch_cfg<5, XT, SWIGLU>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, s);
-    case 6: return launch_cfg<6, XT, SWIGLU>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, s);
-    case 7: return launch_cfg<7, XT, SWIGLU>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, s);
-    default: return launch_cfg<8, XT, SWIGLU>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, s);
+    case 1: return launch_cfg<1, XT, EPI>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, ep, s);
+    case 2: return launch_cfg<2, XT, EPI>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, ep, s);
+    case 3: return launch_cfg<3, XT, EPI>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, ep, s);
+    case 4: return launch_cfg<4, XT, EPI>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, ep, s);
+    case 5: return launch_cfg<5, XT, EPI>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, ep, s);
+    case 6: return launch_cfg<6, XT, EPI>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, ep, s);
+    case 7: return launch_cfg<7, XT, EPI>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, ep, s);
+    default: return launch_cfg<8, XT, EPI>(x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, ep, s);
   }
+}
+
+template <int EPI>
+hipError_t launch_epi(int x_tiled, int rtw, const __bf16* x, long long ldx, int m, const __bf16* wt, int n16,
+                      int kt_total, int ks, int ktps, __bf16* y, long long ldy, float* part, const LinEpi& ep,
+                      hipStream_t s) {
+  return x_tiled ? launch_rtw<true, EPI>(rtw, x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, ep, s)
+                 : launch_rtw<false, EPI>(rtw, x, ldx, m, wt, n16, kt_total, ks, ktps, y, ldy, part, ep, s);
 }
 
 // Row tiles per workgroup and k slices: the pair whose busiest CU streams the fewest bytes, counting the
 // activation re-reads (4 KB per k tile and workgroup, from L2, weighted at a quarter of a weight byte)
 // and the split partials (written and read once in fp32, weighted at three weight bytes each: measured,
 // the k-split passes cost more than their bytes).
-void plan(int m, int n16, int kt_total, int* rtw_out, int* ks_out) {
+void plan(int m, int n16, int kt_total, int max_ks, int* rtw_out, int* ks_out) {
   constexpr int CUS = 256;
   double best = 1e300;
   int br = 1, bk = 1;
   for (int rtw = 1; rtw <= LIN_MAX_RTW; ++rtw) {
-    for (int ks = 1; ks <= 16; ks *= 2) {
+    for (int ks = 1; ks <= 16 && ks <= max_ks; ks *= 2) {
       const int ktps = (kt_total + ks - 1) / ks;
-      if (ks > 1 && ktps < 2 * LIN_NW) break;
+      if (ks > 1 && ktps < 8) break;
       const long long units = (long long)((n16 + rtw - 1) / rtw) * ks;
       const long long rounds = (units + CUS - 1) / CUS;
       const double per_unit = rtw * ktps * 1024.0 + 0.25 * ktps * 4096.0;
@@ -250,12 +376,44 @@ void plan(int m, int n16, int kt_total, int* rtw_out, int* ks_out) {
 
 }  // namespace
 
+namespace {
+
+// Checks shared by the decode-projection entry points: rows, shape, x layout and stride, alignment,
+// the weight's row tiles per workgroup.
+int check_operands(const void* x, long long ldx, int x_tiled, int m, const void* w_tiled, int n, int k, int rtw,
+                   const char* who) {
+  if (!x || !w_tiled) return fail(PALU_EINVAL, "%s: a required pointer is null", who);
+  if (m < 1 || m > 64) return fail(PALU_EINVAL, "%s: rows m = %d must be in 1..64", who, m);
+  if (n <= 0 || n % 16) return fail(PALU_EINVAL, "%s: columns n = %d must be a positive multiple of 16", who, n);
+  if (k <= 0 || k % 32) return fail(PALU_EINVAL, "%s: k = %d must be a positive multiple of 32", who, k);
+  if (x_tiled != 0 && x_tiled != 1) return fail(PALU_EINVAL, "%s: x_tiled = %d must be 0 or 1", who, x_tiled);
+  if (!x_tiled && (ldx < k || ldx % 8))
+    return fail(PALU_EINVAL, "%s: row stride ldx = %lld must be >= k and a multiple of 8", who, ldx);
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_tiled)) & 15)
+    return fail(PALU_EINVAL, "%s: x and w_tiled must be 16-byte aligned", who);
+  if (rtw < 1 || rtw > LIN_MAX_RTW)
+    return fail(PALU_EINVAL, "%s: rtw = %d (1..%d, as the weight was tiled)", who, rtw, LIN_MAX_RTW);
+  return PALU_OK;
+}
+
+int launched(hipError_t e, const char* who) {
+  if (e != hipSuccess) return fail(PALU_EHIP, "%s launch: %s", who, hipGetErrorString(e));
+  return PALU_OK;
+}
+
+}  // namespace
+
 extern "C" int palu_linear_plan(int m, int n, int k, int* rtw, int* ks) {
+  return palu_linear_plan_ks(m, n, k, 16, rtw, ks);
+}
+
+extern "C" int palu_linear_plan_ks(int m, int n, int k, int max_ks, int* rtw, int* ks) {
   palu::g_err[0] = 0;
   if (!rtw || !ks) return fail(PALU_EINVAL, "palu_linear_plan: null output pointer");
-  if (m < 1 || m > 64 || n <= 0 || n % 16 || k <= 0 || k % 32)
-    return fail(PALU_EINVAL, "palu_linear_plan: m = %d (1..64), n = %d (multiple of 16), k = %d (multiple of 32)", m, n, k);
-  plan(m, n / 16, k / 32, rtw, ks);
+  if (m < 1 || m > 64 || n <= 0 || n % 16 || k <= 0 || k % 32 || max_ks < 1)
+    return fail(PALU_EINVAL, "palu_linear_plan: m = %d (1..64), n = %d (multiple of 16), k = %d (multiple of 32), max_ks = %d (>= 1)",
+                m, n, k, max_ks);
+  plan(m, n / 16, k / 32, max_ks, rtw, ks);
   return PALU_OK;
 }
 
@@ -268,57 +426,112 @@ extern "C" int palu_linear_tiled(const void* x, long long ldx, int x_tiled, int 
                                  void* y, long long ldy, int y_mode, int rtw, int ks, void* ws, size_t ws_bytes,
                                  hipStream_t stream) {
   palu::g_err[0] = 0;
-  if (!x || !w_tiled || !y) return fail(PALU_EINVAL, "palu_linear_tiled: a required pointer is null");
-  if (m < 1 || m > 64) return fail(PALU_EINVAL, "palu_linear_tiled: rows m = %d must be in 1..64", m);
-  if (n <= 0 || n % 16) return fail(PALU_EINVAL, "palu_linear_tiled: columns n = %d must be a positive multiple of 16", n);
-  if (k <= 0 || k % 32) return fail(PALU_EINVAL, "palu_linear_tiled: k = %d must be a positive multiple of 32", k);
-  if (x_tiled != 0 && x_tiled != 1) return fail(PALU_EINVAL, "palu_linear_tiled: x_tiled = %d must be 0 or 1", x_tiled);
+  const char* who = "palu_linear_tiled";
+  if (!y) return fail(PALU_EINVAL, "%s: a required pointer is null", who);
+  if (int rc = check_operands(x, ldx, x_tiled, m, w_tiled, n, k, rtw, who)) return rc;
   if (y_mode < PALU_LINEAR_BF16 || y_mode > PALU_LINEAR_SWIGLU_TILED)
-    return fail(PALU_EINVAL, "palu_linear_tiled: y_mode = %d is not a PALU_LINEAR_* mode", y_mode);
-  if (!x_tiled && (ldx < k || ldx % 8))
-    return fail(PALU_EINVAL, "palu_linear_tiled: row stride ldx = %lld must be >= k and a multiple of 8", ldx);
+    return fail(PALU_EINVAL, "%s: y_mode = %d is not a PALU_LINEAR_* mode", who, y_mode);
   if (y_mode == PALU_LINEAR_BF16 && (ldy < n || ldy % 4))
-    return fail(PALU_EINVAL, "palu_linear_tiled: row stride ldy = %lld must be >= n and a multiple of 4", ldy);
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_tiled)) & 15)
-    return fail(PALU_EINVAL, "palu_linear_tiled: x and w_tiled must be 16-byte aligned");
+    return fail(PALU_EINVAL, "%s: row stride ldy = %lld must be >= n and a multiple of 4", who, ldy);
   if (reinterpret_cast<uintptr_t>(y) & (y_mode == PALU_LINEAR_F32_PARTIALS ? 15 : 7))
-    return fail(PALU_EINVAL, "palu_linear_tiled: y is misaligned for its mode");
-  if (rtw < 1 || rtw > LIN_MAX_RTW || ks < 1 || ks > 64)
-    return fail(PALU_EINVAL, "palu_linear_tiled: rtw = %d (1..%d, as the weight was tiled) and ks = %d (1..64)", rtw,
-                LIN_MAX_RTW, ks);
+    return fail(PALU_EINVAL, "%s: y is misaligned for its mode", who);
+  if (ks < 1 || ks > 64) return fail(PALU_EINVAL, "%s: ks = %d (1..64)", who, ks);
   if (y_mode == PALU_LINEAR_SWIGLU_TILED && (ks != 1 || n % 64))
-    return fail(PALU_EINVAL, "palu_linear_tiled: the SwiGLU mode needs ks = 1 and n a multiple of 64, got ks = %d, n = %d",
-                ks, n);
+    return fail(PALU_EINVAL, "%s: the SwiGLU mode needs ks = 1 and n a multiple of 64, got ks = %d, n = %d", who, ks, n);
   const int n16 = n / 16, kt_total = k / 32;
   const int ktps = (kt_total + ks - 1) / ks;
-  if ((long long)((n16 + rtw - 1) / rtw) * ks > 2147483647LL) return fail(PALU_EUNSUPPORTED, "palu_linear_tiled: grid too large");
+  if ((long long)((n16 + rtw - 1) / rtw) * ks > 2147483647LL) return fail(PALU_EUNSUPPORTED, "%s: grid too large", who);
   float* part = nullptr;
   if (y_mode == PALU_LINEAR_F32_PARTIALS) {
     part = static_cast<float*>(y);
   } else if (ks > 1) {
     const size_t need = palu_linear_workspace_bytes(m, n, k, ks);
     if (!ws || ws_bytes < need || (reinterpret_cast<uintptr_t>(ws) & 15))
-      return fail(PALU_EINVAL, "palu_linear_tiled: workspace of %zu bytes (16-byte aligned) needed for %d k slices, got %zu",
+      return fail(PALU_EINVAL, "%s: workspace of %zu bytes (16-byte aligned) needed for %d k slices, got %zu", who,
                   need, ks, ws_bytes);
     part = static_cast<float*>(ws);
   }
   const auto* xb = static_cast<const __bf16*>(x);
   const auto* wb = static_cast<const __bf16*>(w_tiled);
   auto* yb = static_cast<__bf16*>(y);
-  hipError_t e;
-  if (y_mode == PALU_LINEAR_SWIGLU_TILED)
-    e = x_tiled ? launch_rtw<true, true>(rtw, xb, ldx, m, wb, n16, kt_total, ks, ktps, yb, ldy, nullptr, stream)
-                : launch_rtw<false, true>(rtw, xb, ldx, m, wb, n16, kt_total, ks, ktps, yb, ldy, nullptr, stream);
-  else
-    e = x_tiled ? launch_rtw<true, false>(rtw, xb, ldx, m, wb, n16, kt_total, ks, ktps, yb, ldy, part, stream)
-                : launch_rtw<false, false>(rtw, xb, ldx, m, wb, n16, kt_total, ks, ktps, yb, ldy, part, stream);
-  if (e != hipSuccess) return fail(PALU_EHIP, "palu_linear_tiled launch: %s", hipGetErrorString(e));
+  const LinEpi ep{};
+  const hipError_t e =
+      y_mode == PALU_LINEAR_SWIGLU_TILED
+          ? launch_epi<EPI_SWIGLU>(x_tiled, rtw, xb, ldx, m, wb, n16, kt_total, ks, ktps, yb, ldy, nullptr, ep, stream)
+          : launch_epi<EPI_OUT>(x_tiled, rtw, xb, ldx, m, wb, n16, kt_total, ks, ktps, yb, ldy, part, ep, stream);
+  if (int rc = launched(e, who)) return rc;
   if (y_mode == PALU_LINEAR_BF16 && ks > 1) {
     const long long quads = (long long)m * (n / 4);
     const int blocks = (int)std::min<long long>((quads + 255) / 256, 1024);
     hipLaunchKernelGGL(palu_linear_reduce_kernel, dim3(blocks), dim3(256), 0, stream, part, ks, m, n, yb, ldy);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(PALU_EHIP, "palu_linear_tiled reduce launch: %s", hipGetErrorString(e));
+    if (int rc = launched(hipGetLastError(), "palu_linear_tiled reduce")) return rc;
   }
   return PALU_OK;
+}
+
+extern "C" int palu_linear_swiglu_rmsnorm(const void* x, long long ldx, int x_tiled, int m, const void* w_tiled, int n,
+                                          int k, int rtw, float eps, void* y_tiled, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  const char* who = "palu_linear_swiglu_rmsnorm";
+  if (!y_tiled) return fail(PALU_EINVAL, "%s: a required pointer is null", who);
+  if (int rc = check_operands(x, ldx, x_tiled, m, w_tiled, n, k, rtw, who)) return rc;
+  if (n % 64) return fail(PALU_EINVAL, "%s: n = %d must be a multiple of 64 (gate and up rows interleaved)", who, n);
+  if (!(eps >= 0.f)) return fail(PALU_EINVAL, "%s: eps must be >= 0", who);
+  if (reinterpret_cast<uintptr_t>(y_tiled) & 15) return fail(PALU_EINVAL, "%s: y_tiled must be 16-byte aligned", who);
+  LinEpi ep{};
+  ep.eps = eps;
+  ep.inv_k = 1.f / (float)k;
+  return launched(launch_epi<EPI_SWIGLU_NORM>(x_tiled, rtw, static_cast<const __bf16*>(x), ldx, m,
+                                              static_cast<const __bf16*>(w_tiled), n / 16, k / 32, 1, k / 32,
+                                              static_cast<__bf16*>(y_tiled), 0, nullptr, ep, stream),
+                  who);
+}
+
+extern "C" int palu_linear_residual(const void* x, long long ldx, int x_tiled, int m, const void* w_tiled, int n, int k,
+                                    int rtw, void* h, long long ldh, void* h_tiled, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  const char* who = "palu_linear_residual";
+  if (!h) return fail(PALU_EINVAL, "%s: a required pointer is null", who);
+  if (int rc = check_operands(x, ldx, x_tiled, m, w_tiled, n, k, rtw, who)) return rc;
+  if (ldh < n || ldh % 4 || (reinterpret_cast<uintptr_t>(h) & 7))
+    return fail(PALU_EINVAL, "%s: h must be 8-byte aligned with a row stride ldh = %lld >= n and a multiple of 4", who,
+                ldh);
+  if (h_tiled && (n % 32 || (reinterpret_cast<uintptr_t>(h_tiled) & 15)))
+    return fail(PALU_EINVAL, "%s: a tiled copy of h needs n = %d a multiple of 32 and 16-byte alignment", who, n);
+  LinEpi ep{};
+  ep.h = static_cast<__bf16*>(h);
+  ep.ldh = ldh;
+  ep.h_tiled = static_cast<__bf16*>(h_tiled);
+  return launched(launch_epi<EPI_RESID>(x_tiled, rtw, static_cast<const __bf16*>(x), ldx, m,
+                                        static_cast<const __bf16*>(w_tiled), n / 16, k / 32, 1, k / 32, nullptr, 0,
+                                        nullptr, ep, stream),
+                  who);
+}
+
+extern "C" int palu_linear_qkv(const void* x, long long ldx, int x_tiled, int m, const void* w_tiled, int n, int k,
+                               int rtw, const int32_t* pos, const float* cos_table, const float* sin_table,
+                               int table_rows, int n_heads, void* q_out, void* k_cache, int k_layout, int k_col_offset,
+                               int k_group_stride, int k_width, int k_rope, void* v_cache, int v_layout,
+                               int v_col_offset, int v_group_stride, int v_width, int n_groups, int seq_len,
+                               hipStream_t stream) {
+  palu::g_err[0] = 0;
+  const char* who = "palu_linear_qkv";
+  if (int rc = check_operands(x, ldx, x_tiled, m, w_tiled, n, k, rtw, who)) return rc;
+  LinEpi ep{};
+  ep.q = QkvEpi{pos, cos_table, sin_table, table_rows, n_heads, static_cast<__bf16*>(q_out),
+                static_cast<__bf16*>(k_cache), k_layout, k_col_offset, k_group_stride, k_width, k_rope ? 1 : 0,
+                static_cast<__bf16*>(v_cache), v_layout, v_col_offset, v_group_stride, v_width, n_groups, seq_len};
+  if (int rc = check_qkv_epi(ep.q, m, n, x, who)) return rc;
+  // Each output column must belong to at most one part of the row: q heads first, then K and V slices
+  // that neither overlap the q heads, each other, nor (with several groups) their neighbours.
+  const long long q_end = (long long)n_heads * HD;
+  const long long k_end = (long long)k_col_offset + (long long)(n_groups - 1) * k_group_stride + k_width;
+  const long long v_end = (long long)v_col_offset + (long long)(n_groups - 1) * v_group_stride + v_width;
+  if (k_col_offset < q_end || v_col_offset < q_end || (k_col_offset < v_end && v_col_offset < k_end) ||
+      (n_groups > 1 && (k_group_stride < k_width || v_group_stride < v_width)))
+    return fail(PALU_EINVAL, "%s: the q, K and V column ranges (and the groups' slices) must not overlap", who);
+  return launched(launch_epi<EPI_QKV>(x_tiled, rtw, static_cast<const __bf16*>(x), ldx, m,
+                                      static_cast<const __bf16*>(w_tiled), n / 16, k / 32, 1, k / 32, nullptr, 0,
+                                      nullptr, ep, stream),
+                  who);
 }

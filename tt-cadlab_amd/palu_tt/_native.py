@@ -15,7 +15,7 @@ from palu_tt._build import library_path
 PALU_OK, PALU_EINVAL, PALU_EUNSUPPORTED, PALU_EHIP = 0, 1, 2, 3
 DTYPE_F32, DTYPE_BF16 = 0, 1
 OUT_TILED_ROWS = 0x100      # PALU_OUT_TILED_ROWS, OR'ed into palu_sdpa_decode's out_dtype
-ABI_VERSION = 12
+ABI_VERSION = 13
 LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_TILED_V, LAYOUT_TILED_GROUPED = 0, 1, 2, 3
 
 _vp, _i, _f, _sz, _ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_longlong
@@ -47,6 +47,11 @@ _SIGNATURES = {
                            _i, _i, _vp]),
     "palu_linear_plan": (_i, [_i, _i, _i, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
     "palu_linear_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "palu_linear_plan_ks": (_i, [_i, _i, _i, _i, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
+    "palu_linear_swiglu_rmsnorm": (_i, [_vp, _ll, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp]),
+    "palu_linear_residual": (_i, [_vp, _ll, _i, _i, _vp, _i, _i, _i, _vp, _ll, _vp, _vp]),
+    "palu_linear_qkv": (_i, [_vp, _ll, _i, _i, _vp, _i, _i, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, _i, _i, _i, _i, _i,
+                             _vp, _i, _i, _i, _i, _i, _i, _vp]),
 }
 EXPORTED = tuple(_SIGNATURES)
 

@@ -95,7 +95,7 @@ class PaluAttention(torch.nn.Module):
         # [nh hd + n_groups (k_width + r_v), dim]: held in the decode projection's tiled order
         # (decoder_ops.DecodeLinear); the prefill multiplies by its nn.Linear-layout copy
         self.wqkv = decoder_ops.DecodeLinear(torch.cat([wq, wk, wv], dim=0).to(dev, bf).contiguous(),
-                                             self.max_batch_size)
+                                             self.max_batch_size, single_slice=True)
         self.wo = state_dict[f"{ln}.wo.weight"].to(dev, bf).contiguous()
         wo_fused = (state_dict[f"{P}.wo_fused"].to(dev, bf) if (self.recon_v and self.gs == 1) else self.wo)
         # decode output width per head: the absorbed-V latent (r_v) or, with u_v / stock V, head_dim; the
@@ -103,7 +103,7 @@ class PaluAttention(torch.nn.Module):
         self.out_width = self.head_dim if (self.gs > 1 or not self.recon_v) else self.r_v
         self.wo_out = decoder_ops.DecodeLinear(wo_fused.view(-1, self.n_heads, self.head_dim)[:, :, :self.out_width]
                                                .reshape(-1, self.n_heads * self.out_width).contiguous(),
-                                               self.max_batch_size)
+                                               self.max_batch_size, single_slice=True)
         self.u_k = state_dict[f"{P}.u_k"].to(dev, bf).contiguous() if self.recon_k else None   # [nkv, r_k, hd]
         self.w_rot = state_dict[f"{P}.w_rot"].to(dev, bf)[None].contiguous() if self.recon_k else None
         self.u_v = state_dict[f"{P}.u_v"].to(dev, bf).contiguous() if self.recon_v else None   # [nkv, r_v, hd]
@@ -157,14 +157,17 @@ class PaluAttention(torch.nn.Module):
 
     # ------------------------------------------------------------------------------------------------
     def forward_decode(self, x, current_pos, rot_mats=None, page_table=None, kv_cache=None, x_tiled=False,
-                       out_partials=False):
+                       out_partials=False, residual=None):
         """One decode step for all max_batch_size rows: QKV projection; RoPE of q (and of K on the K-fast
-        path) and the latent appends from the projection's columns (one fused launch over its split
-        partials when the projection is tiled); the fused op (or the naive path, or the stock decode over
-        rotated K); output projection over the out_width rows per head. With x_tiled, x is the [64, dim]
-        tiled activation buffer (decoder_ops.rmsnorm(..., tiled_out=True)) holding the max_batch_size rows,
-        and the output is [max_batch_size, dim]; with out_partials it is the output projection's fp32 split
-        partials [ks, B, dim] (decoder_ops.rmsnorm's res_part)."""
+        path) and the latent appends from the projection's columns (in the projection's own epilogue when
+        it is tiled in one k slice, else one fused launch over its split partials); the fused op (or the
+        naive path, or the stock decode over rotated K); output projection over the out_width rows per
+        head. With x_tiled, x is the [64, dim] tiled activation buffer (decoder_ops.rmsnorm(...,
+        tiled_out=True)) holding the max_batch_size rows, and the output is [max_batch_size, dim]; with
+        out_partials it is the output projection's fp32 split partials [ks, B, dim] (decoder_ops.rmsnorm's
+        res_part); with residual = (h, h_tiled) the output projection adds into the residual stream h
+        [B, dim] in place and writes the new h to the tiled buffer h_tiled (decoder_ops.linear_residual),
+        and h is returned."""
         assert page_table is None and kv_cache is None
         if x_tiled:
             B = self.max_batch_size
@@ -181,7 +184,10 @@ class PaluAttention(torch.nn.Module):
         keys, values = self.layer_past
         kw, G = self.k_width, self.n_groups
         k0, v0 = nh * hd, nh * hd + G * kw                                  # column offsets of K and V latents
-        if self.wqkv.tiled and not isinstance(keys, GroupedLatentCache):
+        if self.wqkv.tiled and self.wqkv.ks == 1 and not isinstance(keys, GroupedLatentCache):
+            q = self.wqkv.qkv(x2, pos, self.cos, self.sin, nh, keys, k0, kw, kw, values, v0, self.r_v, self.r_v,
+                              k_rope=not self.recon_k, x_tiled=x_tiled, rows=B)
+        elif self.wqkv.tiled and not isinstance(keys, GroupedLatentCache):
             part = self.wqkv(x2, x_tiled=x_tiled, rows=B, mode="partials")  # [ks, B, nh hd + G (kw + r_v)] fp32
             q = decoder_ops.qkv_post(part, pos, self.cos, self.sin, nh, keys, k0, kw, kw, values, v0, self.r_v,
                                      self.r_v, k_rope=not self.recon_k)
@@ -201,6 +207,9 @@ class PaluAttention(torch.nn.Module):
         attn = self.decode_core(q[None], keys, values, pos, tiled_rows=tiled_attn)
         tiled_attn = attn.dim() == 2                                          # a core may answer row-major
         a2 = attn if tiled_attn else attn[0].reshape(B, nh * self.out_width)   # [64 | B, nh * out_width]
+        if residual is not None:
+            h, h_tiled = residual
+            return self.wo_out.residual(a2, h, h_tiled, x_tiled=tiled_attn, rows=B)
         if out_partials:
             return self.wo_out(a2, x_tiled=tiled_attn, rows=B, mode="partials")
         return self.wo_out(a2, x_tiled=tiled_attn, rows=B).reshape(*shape[:-1], self.hidden_size)

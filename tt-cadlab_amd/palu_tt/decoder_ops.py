@@ -192,10 +192,11 @@ def untile_rows(xt: torch.Tensor, rows: int) -> torch.Tensor:
     return untile_weight(xt, 4)[:rows]
 
 
-def linear_plan(rows: int, n: int, k: int):
-    """(row tiles per workgroup, k slices) suggested for this shape: tile the weight with that rtw."""
+def linear_plan(rows: int, n: int, k: int, max_ks: int = 16):
+    """(row tiles per workgroup, k slices) suggested for this shape, with at most max_ks slices (1 for the
+    fused epilogues: linear_swiglu_rmsnorm, linear_residual, linear_qkv): tile the weight with that rtw."""
     rtw, ks = ctypes.c_int(0), ctypes.c_int(0)
-    _native.check(_native.load().palu_linear_plan(rows, n, k, ctypes.byref(rtw), ctypes.byref(ks)))
+    _native.check(_native.load().palu_linear_plan_ks(rows, n, k, max_ks, ctypes.byref(rtw), ctypes.byref(ks)))
     return rtw.value, ks.value
 
 
@@ -258,6 +259,97 @@ def linear_tiled(x: torch.Tensor, w_tiled: torch.Tensor, rtw: int, ks: int, out:
     return out
 
 
+def _operands(x: torch.Tensor, w_tiled: torch.Tensor, x_tiled: bool, rows: Optional[int]):
+    """(rows, n, k) of a decode projection's operands, checked as linear_tiled checks them."""
+    _check(x, "x")
+    _check(w_tiled, "w_tiled")
+    if x.dim() != 2 or x.stride(1) != 1 or w_tiled.dim() != 2 or not w_tiled.is_contiguous():
+        raise RuntimeError("x must be a row-strided [rows, k] view and w_tiled a contiguous [n, k] tensor")
+    if x_tiled:
+        if x.shape[0] != 64 or not x.is_contiguous() or rows is None:
+            raise RuntimeError("a tiled x is a contiguous [64, k] buffer and needs the live row count `rows`")
+    else:
+        rows = x.shape[0]
+    n, k = w_tiled.shape
+    if x.shape[1] != k:
+        raise RuntimeError(f"x has k = {x.shape[1]}, w_tiled has {k}")
+    return rows, n, k
+
+
+def linear_swiglu_rmsnorm(x: torch.Tensor, w_tiled: torch.Tensor, rtw: int, eps: float,
+                          out: Optional[torch.Tensor] = None, x_tiled: bool = False,
+                          rows: Optional[int] = None) -> torch.Tensor:
+    """silu(g) * u with g, u the gate / up products of the RMS-normalised rows of x, in one launch: w_tiled
+    is tile_weight(interleave_gate_up(w1 * norm_w, w3 * norm_w), rtw) (the norm's weight folded into the
+    columns), each row's products scaled by rsqrt(mean(x^2) + eps). Returns (or writes `out`) the
+    [64, n / 2] tiled activations of linear_tiled's "swiglu" mode."""
+    rows, n, k = _operands(x, w_tiled, x_tiled, rows)
+    if out is None:
+        out = torch.empty(64, n // 2, dtype=torch.bfloat16, device=x.device)
+    _check(out, "out")
+    if out.shape != (64, n // 2) or not out.is_contiguous():
+        raise RuntimeError(f"out must be a contiguous [64, {n // 2}] bf16 tensor")
+    _native.check(_native.load().palu_linear_swiglu_rmsnorm(
+        _native.ptr(x), x.stride(0), int(x_tiled), rows, _native.ptr(w_tiled), n, k, rtw, float(eps), _native.ptr(out),
+        _native.stream_handle(x.device)))
+    return out
+
+
+def linear_residual(x: torch.Tensor, w_tiled: torch.Tensor, rtw: int, h: torch.Tensor,
+                    h_tiled: Optional[torch.Tensor] = None, x_tiled: bool = False,
+                    rows: Optional[int] = None) -> torch.Tensor:
+    """h += x @ w.T in one launch (h a row-strided bf16 [rows, n] view, updated in place, each value
+    rounded once), and the new h written to h_tiled ([64, n] tiled activations) when given. Returns h."""
+    rows, n, k = _operands(x, w_tiled, x_tiled, rows)
+    _check(h, "h")
+    if h.dim() != 2 or h.shape != (rows, n) or h.stride(1) != 1:
+        raise RuntimeError(f"h must be a row-strided [{rows}, {n}] view")
+    if h_tiled is not None:
+        _check(h_tiled, "h_tiled")
+        if h_tiled.shape != (64, n) or not h_tiled.is_contiguous():
+            raise RuntimeError(f"h_tiled must be a contiguous [64, {n}] bf16 tensor")
+    _native.check(_native.load().palu_linear_residual(
+        _native.ptr(x), x.stride(0), int(x_tiled), rows, _native.ptr(w_tiled), n, k, rtw, _native.ptr(h), h.stride(0),
+        _native.ptr(h_tiled) if h_tiled is not None else None, _native.stream_handle(x.device)))
+    return h
+
+
+def _cache_args(cache):
+    """(storage, layout, [B, G, S, width]) of a latent cache: LatentCache (tiled) or a row-major tensor."""
+    if isinstance(cache, LatentCache):
+        layout = _native.LAYOUT_TILED if cache.role == "k" else _native.LAYOUT_TILED_V
+        return cache.data, layout, cache.shape
+    return cache, _native.LAYOUT_ROWS, cache.shape
+
+
+def linear_qkv(x: torch.Tensor, w_tiled: torch.Tensor, rtw: int, pos: torch.Tensor, cos: torch.Tensor,
+               sin: torch.Tensor, n_heads: int, keys, k_col_offset: int, k_group_stride: int, k_width: int, values,
+               v_col_offset: int, v_group_stride: int, v_width: int, k_rope: bool = False,
+               q_out: Optional[torch.Tensor] = None, x_tiled: bool = False,
+               rows: Optional[int] = None) -> torch.Tensor:
+    """The decode step's QKV projection and its epilogue in one launch: the columns of x @ w.T go where
+    qkv_post sends the summed partials (q [B, n_heads, 128] rotated at pos, returned; K / V latent slices
+    appended to keys / values at pos), with the same rounding."""
+    rows, n, k = _operands(x, w_tiled, x_tiled, rows)
+    _check(cos, "cos", torch.float32)
+    _check(sin, "sin", torch.float32)
+    p = pos.reshape(-1).to(device=x.device, dtype=torch.int32).contiguous()
+    if p.numel() != rows:
+        raise RuntimeError(f"pos has {p.numel()} entries for {rows} rows")
+    if q_out is None:
+        q_out = torch.empty(rows, n_heads, 128, dtype=torch.bfloat16, device=x.device)
+    kd, kl, (kb, G, S, kw) = _cache_args(keys)
+    vd, vl, (vb, vG, vS, vw) = _cache_args(values)
+    if (kb, G, S, kw) != (rows, G, S, k_width) or (vb, vG, vS, vw) != (rows, G, S, v_width):
+        raise RuntimeError("cache shapes must be [B, G, S, k_width] and [B, G, S, v_width]")
+    _native.check(_native.load().palu_linear_qkv(
+        _native.ptr(x), x.stride(0), int(x_tiled), rows, _native.ptr(w_tiled), n, k, rtw, _native.ptr(p),
+        _native.ptr(cos), _native.ptr(sin), cos.shape[0], n_heads, _native.ptr(q_out), _native.ptr(kd), kl,
+        k_col_offset, k_group_stride, k_width, int(k_rope), _native.ptr(vd), vl, v_col_offset, v_group_stride, v_width,
+        G, S, _native.stream_handle(x.device)))
+    return q_out
+
+
 def interleave_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
     """[2 ffn, k] with gate and up rows interleaved eight at a time (rows 16 j .. 16 j + 7: gate rows
     8 j .. 8 j + 7, then the up rows of the same outputs), the weight linear_tiled's "swiglu" mode takes."""
@@ -295,14 +387,8 @@ def qkv_post(part: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torc
     if q_out is None:
         q_out = torch.empty(B, n_heads, 128, dtype=torch.bfloat16, device=part.device)
 
-    def cache_args(cache, role):
-        if isinstance(cache, LatentCache):
-            layout = _native.LAYOUT_TILED if cache.role == "k" else _native.LAYOUT_TILED_V
-            return cache.data, layout, cache.shape
-        return cache, _native.LAYOUT_ROWS, cache.shape
-
-    kd, kl, (kb, G, S, kw) = cache_args(keys, "k")
-    vd, vl, (vb, vG, vS, vw) = cache_args(values, "v")
+    kd, kl, (kb, G, S, kw) = _cache_args(keys)
+    vd, vl, (vb, vG, vS, vw) = _cache_args(values)
     if (kb, G, S, kw) != (B, G, S, k_width) or (vb, vG, vS, vw) != (B, G, S, v_width):
         raise RuntimeError("cache shapes must be [B, G, S, k_width] and [B, G, S, v_width]")
     _native.check(_native.load().palu_qkv_post(
@@ -316,23 +402,36 @@ class DecodeLinear:
     """One projection of the decode step, y = x @ w.T, for w [n, k] in the nn.Linear layout (for a gate /
     up pair, gate_up=(w_gate, w_up) instead: y = silu(x @ w_gate.T) * (x @ w_up.T)). For up to 64 rows
     (and n % 16 == 0, k % 32 == 0) the weight is held only in the tiled order of linear_tiled, with the
-    work split linear_plan suggests (or rtw / ks) and a workspace for its split partials; otherwise it
-    stays as it is and the call is torch's F.linear. plain() returns the weight in the nn.Linear layout
-    ([gate; up] for a pair; a fresh copy when tiled), for the prefill's many-row products."""
+    work split linear_plan suggests (or rtw / ks; single_slice: one k slice, for the fused residual and
+    QKV epilogues) and a workspace for its split partials; otherwise it stays as it is and the call is
+    torch's F.linear. plain() returns the weight in the nn.Linear layout ([gate; up] for a pair; a fresh
+    copy when tiled), for the prefill's many-row products. in_scale (a gate / up pair only): the weight of
+    the RMSNorm in front of the pair, folded into the tiled weight's columns (w * in_scale) so that
+    norm_eps calls take the normalisation into the same launch (linear_swiglu_rmsnorm); in_scale_folded
+    says whether it was (only a tiled pair folds it), and then plain() holds the folded weight too."""
 
-    def __init__(self, w: Optional[torch.Tensor], rows: int, gate_up=None, rtw: int = 0, ks: int = 0):
+    def __init__(self, w: Optional[torch.Tensor], rows: int, gate_up=None, rtw: int = 0, ks: int = 0,
+                 single_slice: bool = False, in_scale: Optional[torch.Tensor] = None):
         self.gate_up = gate_up is not None
         if self.gate_up:
             w = torch.cat(list(gate_up), 0)
+        elif in_scale is not None:
+            raise RuntimeError("in_scale is folded into a gate / up pair only")
         n, k = w.shape
         self.n, self.k = n, k
         self.tiled = (rows <= 64 and n % (64 if self.gate_up else 16) == 0 and k % 32 == 0 and w.is_cuda
                       and w.dtype == torch.bfloat16)
+        self.in_scale_folded = False
         if self.tiled:
-            self.rtw, self.ks = (rtw, ks) if rtw else linear_plan(rows, n, k)
+            self.rtw, self.ks = (rtw, ks) if rtw else linear_plan(rows, n, k, 1 if single_slice else 16)
             if self.gate_up:
                 self.ks = 1
-                w = interleave_gate_up(*gate_up)
+                g, u = gate_up
+                if in_scale is not None:
+                    sc = in_scale.float().reshape(1, k)
+                    g, u = (g.float() * sc).to(g.dtype), (u.float() * sc).to(u.dtype)
+                    self.in_scale_folded = True
+                w = interleave_gate_up(g, u)
             self.weight = tile_weight(w, self.rtw)
             need = _native.load().palu_linear_workspace_bytes(rows, n, k, self.ks)
             self.workspace = torch.empty(need, dtype=torch.uint8, device=w.device) if need else None
@@ -363,6 +462,31 @@ class DecodeLinear:
             out.copy_(y)
             return out
         return y
+
+    def swiglu_rmsnorm(self, x: torch.Tensor, eps: float, out: Optional[torch.Tensor] = None,
+                       x_tiled: bool = False, rows: Optional[int] = None) -> torch.Tensor:
+        """A folded gate / up pair over the RMS-normalised rows of x (linear_swiglu_rmsnorm): [64, n / 2]
+        tiled activations."""
+        if not (self.gate_up and self.in_scale_folded):
+            raise RuntimeError("swiglu_rmsnorm needs a tiled gate / up pair with the norm weight folded in")
+        return linear_swiglu_rmsnorm(x, self.weight, self.rtw, eps, out=out, x_tiled=x_tiled, rows=rows)
+
+    def residual(self, x: torch.Tensor, h: torch.Tensor, h_tiled: Optional[torch.Tensor] = None,
+                 x_tiled: bool = False, rows: Optional[int] = None) -> torch.Tensor:
+        """h += x @ w.T (linear_residual; a single-slice tiled projection), h_tiled the new h tiled."""
+        if not self.tiled or self.ks != 1 or self.gate_up:
+            raise RuntimeError("residual needs a tiled single-slice projection")
+        return linear_residual(x, self.weight, self.rtw, h, h_tiled, x_tiled=x_tiled, rows=rows)
+
+    def qkv(self, x: torch.Tensor, pos, cos, sin, n_heads, keys, k_col_offset, k_group_stride, k_width, values,
+            v_col_offset, v_group_stride, v_width, k_rope=False, x_tiled: bool = False,
+            rows: Optional[int] = None) -> torch.Tensor:
+        """The QKV projection with its epilogue (linear_qkv; a single-slice tiled projection): returns q."""
+        if not self.tiled or self.ks != 1 or self.gate_up:
+            raise RuntimeError("qkv needs a tiled single-slice projection")
+        return linear_qkv(x, self.weight, self.rtw, pos, cos, sin, n_heads, keys, k_col_offset, k_group_stride,
+                          k_width, values, v_col_offset, v_group_stride, v_width, k_rope=k_rope, x_tiled=x_tiled,
+                          rows=rows)
 
     def plain(self) -> torch.Tensor:
         if not self.tiled:

@@ -72,14 +72,21 @@ class Transformer(torch.nn.Module):
             attn = PaluAttention(dev, None, args, attn_sd, None, i, cache_layout=cache_layout)
             for k in attn_sd:
                 state_dict.pop(k)
-            self.layers.append(dict(
-                attn=attn, attn_norm=t(f"{p}.attention_norm.weight"), ffn_norm=t(f"{p}.ffn_norm.weight"),
-                w13=decoder_ops.DecodeLinear(None, rows, gate_up=(t(f"{p}.feed_forward.w1.weight"),
-                                                                  t(f"{p}.feed_forward.w3.weight"))),
-                w2=decoder_ops.DecodeLinear(t(f"{p}.feed_forward.w2.weight"), rows)))
+            # the FFN norm's weight is folded into a tiled gate / up weight (then the norm in front of it
+            # multiplies by ones, and the decode step normalises inside the gate / up launch)
+            ffn_norm = t(f"{p}.ffn_norm.weight")
+            w13 = decoder_ops.DecodeLinear(None, rows, gate_up=(t(f"{p}.feed_forward.w1.weight"),
+                                                                t(f"{p}.feed_forward.w3.weight")), in_scale=ffn_norm)
+            if w13.in_scale_folded:
+                ffn_norm = torch.ones_like(ffn_norm)
+            self.layers.append(dict(attn=attn, attn_norm=t(f"{p}.attention_norm.weight"), ffn_norm=ffn_norm, w13=w13,
+                                    w2=decoder_ops.DecodeLinear(t(f"{p}.feed_forward.w2.weight"), rows)))
         # tiled activations between the decode step's kernels where every projection that reads them is tiled
         self._tiled_acts = self.output.tiled and all(
             L["w13"].tiled and L["w2"].tiled and L["attn"].wqkv.tiled for L in self.layers)
+        # the fused step: output projections add into the residual stream, the FFN norm runs inside gate / up
+        self._fused_step = self._tiled_acts and all(
+            L["w13"].in_scale_folded and L["attn"].wo_out.tiled and L["attn"].wo_out.ks == 1 for L in self.layers)
         self._graph = None
 
     def set_fused_k(self, use_fused_k: bool, recon_len: Optional[int] = None) -> None:
@@ -115,12 +122,25 @@ class Transformer(torch.nn.Module):
         the bf16 logits (the same ids as argmax of the fp32 ones). The residual stream h is updated in place: each RMSNorm
         kernel first adds the previous sublayer's output to it, as the fp32 split partials of its output
         projection. For up to 64 rows the RMSNorm kernels and the gate / up projection (SwiGLU in its
-        epilogue) write their outputs in the tiled activation layout that the next projections read."""
+        epilogue) write their outputs in the tiled activation layout that the next projections read, and
+        (the fused step) the attention's output projection adds into h itself and writes h tiled, and the
+        gate / up launch normalises its rows (the FFN norm's weight folded into its weight): one RMSNorm
+        launch per layer instead of two."""
         eps = self.args.norm_eps
         B = tokens.shape[0]
         xt = self._tiled_acts
         h = self.tok_embeddings[tokens]                                  # [B, dim]
         f = None                                                         # fp32 split partials [ks, B, dim]
+        if self._fused_step:
+            ht = torch.empty(64, self.args.dim, dtype=h.dtype, device=h.device)   # h, tiled
+            for L in self.layers:
+                y = decoder_ops.rmsnorm(h, L["attn_norm"], eps, res_part=f, h_out=h, tiled_out=True)
+                L["attn"].forward_decode(y, current_pos, x_tiled=True, residual=(h, ht))
+                a = L["w13"].swiglu_rmsnorm(ht, eps, x_tiled=True, rows=B)  # silu(gate) * up of rmsnorm(h)
+                f = L["w2"](a, x_tiled=True, rows=B, mode="partials")
+            y = decoder_ops.rmsnorm(h, self.norm_w, eps, res_part=f, tiled_out=True)
+            logits = self.output(y, x_tiled=True, rows=B)
+            return decoder_ops.argmax_rows(logits) if greedy else logits.float()
         for L in self.layers:
             y = decoder_ops.rmsnorm(h, L["attn_norm"], eps, res_part=f, h_out=h, tiled_out=xt)
             o = L["attn"].forward_decode(y, current_pos, x_tiled=xt, out_partials=True)
