@@ -308,7 +308,8 @@ int palu_linear_plan_ks(int rows, int n, int k, int max_ks, int* rtw, int* ks);
  * weight of palu_linear_tiled's SwiGLU mode whose columns carry the norm's weight (w[c][j] = w_ffn[c][j]
  * * norm_weight[j]), y_tiled [64, n / 2] receives silu(g) * u for g, u = (x w^T) * rsqrt(mean_j(x^2) +
  * eps) per row, i.e. the SwiGLU of the normalised x, the sum of squares taken over the bf16 x the
- * product reads. x, rows, w, n, k, rtw as palu_linear_tiled (one k slice; n a multiple of 64). Replaces
+ * product reads. x, rows, w, n, k, rtw as palu_linear_tiled (one k slice; n a multiple of 64); y_tiled must
+ * not overlap x (every workgroup reads all of x while others write their outputs). Replaces
  * palu_rmsnorm followed by the SwiGLU projection (the reference model's ffn_norm and w1 / w3 of its decode
  * step); no counterpart in the reference's op interface. */
 int palu_linear_swiglu_rmsnorm(const void* x, long long ldx, int x_tiled, int rows, const void* w_tiled, int n, int k,
@@ -317,7 +318,8 @@ int palu_linear_swiglu_rmsnorm(const void* x, long long ldx, int x_tiled, int ro
 /* Residual update by a projection, in one launch: h[r][c] = bf16(h[r][c] + sum_k x[r][k] w[c][k]) for h
  * bf16 [rows, n] with rows ldh apart (>= n, a multiple of 4; h 8-byte aligned), and, when h_tiled is not
  * NULL, the same values in the 64-row tiled activation layout (n a multiple of 32) for the projection
- * that reads h next. x, rows, w, n, k, rtw as palu_linear_tiled (one k slice). Replaces the output
+ * that reads h next. x, rows, w, n, k, rtw as palu_linear_tiled (one k slice); h and h_tiled must not
+ * overlap x. Replaces the output
  * projection plus the residual add of the reference model's decode step; no counterpart in the
  * reference's op interface. */
 int palu_linear_residual(const void* x, long long ldx, int x_tiled, int rows, const void* w_tiled, int n, int k,
@@ -326,7 +328,8 @@ int palu_linear_residual(const void* x, long long ldx, int x_tiled, int rows, co
 /* The decode step's QKV projection with its epilogue in the same launch: the product y = x w^T (one k
  * slice) goes where palu_qkv_post sends its summed partials (q_out, and the K / V latent appends at
  * pos[b], arguments as palu_qkv_post with ncols = n), rounded the same way. The q heads, the K slices and
- * the V slices must not overlap (group strides at least the widths). The reference's counterpart is the
+ * the V slices must not overlap (group strides at least the widths), nor q_out and the caches x. The
+ * reference's counterpart is the
  * fused QKV ttnn.linear, RoPE and paged_update_cache calls of its decode step (attention.py:585-623). */
 int palu_linear_qkv(const void* x, long long ldx, int x_tiled, int rows, const void* w_tiled, int n, int k, int rtw,
                     const int32_t* pos, const float* cos_table, const float* sin_table, int table_rows, int n_heads,
