@@ -328,7 +328,8 @@ int palu_linear_residual(const void* x, long long ldx, int x_tiled, int rows, co
 /* The decode step's QKV projection with its epilogue in the same launch: the product y = x w^T (one k
  * slice) goes where palu_qkv_post sends its summed partials (q_out, and the K / V latent appends at
  * pos[b], arguments as palu_qkv_post with ncols = n), rounded the same way. The q heads, the K slices and
- * the V slices must not overlap (group strides at least the widths), nor q_out and the caches x. The
+ * the V slices must not overlap (group strides at least the widths), and q_out and the caches must not
+ * overlap x. The
  * reference's counterpart is the
  * fused QKV ttnn.linear, RoPE and paged_update_cache calls of its decode step (attention.py:585-623). */
 int palu_linear_qkv(const void* x, long long ldx, int x_tiled, int rows, const void* w_tiled, int n, int k, int rtw,
