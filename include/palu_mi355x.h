@@ -319,9 +319,8 @@ int palu_linear_swiglu_rmsnorm(const void* x, long long ldx, int x_tiled, int ro
  * bf16 [rows, n] with rows ldh apart (>= n, a multiple of 4; h 8-byte aligned), and, when h_tiled is not
  * NULL, the same values in the 64-row tiled activation layout (n a multiple of 32) for the projection
  * that reads h next. x, rows, w, n, k, rtw as palu_linear_tiled (one k slice); h and h_tiled must not
- * overlap x. Replaces the output
- * projection plus the residual add of the reference model's decode step; no counterpart in the
- * reference's op interface. */
+ * overlap x. Replaces the output projection plus the residual add of the reference model's decode step;
+ * no counterpart in the reference's op interface. */
 int palu_linear_residual(const void* x, long long ldx, int x_tiled, int rows, const void* w_tiled, int n, int k,
                          int rtw, void* h, long long ldh, void* h_tiled, palu_stream_t stream);
 
@@ -329,9 +328,8 @@ int palu_linear_residual(const void* x, long long ldx, int x_tiled, int rows, co
  * slice) goes where palu_qkv_post sends its summed partials (q_out, and the K / V latent appends at
  * pos[b], arguments as palu_qkv_post with ncols = n), rounded the same way. The q heads, the K slices and
  * the V slices must not overlap (group strides at least the widths), and q_out and the caches must not
- * overlap x. The
- * reference's counterpart is the
- * fused QKV ttnn.linear, RoPE and paged_update_cache calls of its decode step (attention.py:585-623). */
+ * overlap x. The reference's counterpart is the fused QKV ttnn.linear, RoPE and paged_update_cache calls
+ * of its decode step (attention.py:585-623). */
 int palu_linear_qkv(const void* x, long long ldx, int x_tiled, int rows, const void* w_tiled, int n, int k, int rtw,
                     const int32_t* pos, const float* cos_table, const float* sin_table, int table_rows, int n_heads,
                     void* q_out, void* k_cache, int k_layout, int k_col_offset, int k_group_stride, int k_width,
