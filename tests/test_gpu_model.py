@@ -43,10 +43,14 @@ def _check(out, exp, what):
         assert p >= 0.999 and rel <= 0.03, f"{what} row {b}: pcc {p:.6f}, max-abs / max {rel:.4f}"
 
 
-@pytest.mark.parametrize("layout", ["tiled", "rows"])
-def test_decoder_teacher_forced_matches_lowrank_llama(gpu, layout):
+@pytest.mark.parametrize("layout,vocab", [("tiled", 1024), ("rows", 1024), ("tiled", 1000)])
+def test_decoder_teacher_forced_matches_lowrank_llama(gpu, layout, vocab):
+    """vocab 1024: every decode projection tiled, so the step is the fused one (QKV epilogue in the
+    projection, residual add in the output projection, FFN norm folded into gate / up); vocab 1000: the
+    LM head is not a multiple of 16 columns, so the step runs its separate norms over row-major
+    activations (with the gate / up weight still folded)."""
     pytest.importorskip("transformers")
-    args = pm.ModelArgs(dim=512, n_layers=3, n_heads=4, n_kv_heads=2, vocab_size=1000, ffn_dim=1024,
+    args = pm.ModelArgs(dim=512, n_layers=3, n_heads=4, n_kv_heads=2, vocab_size=vocab, ffn_dim=1024,
                         max_seq_len=128, max_batch_size=2)
     dense = []
     sd = pm.random_palu_state_dict(args, [40, 64, 128], [32, 128, 72], gpu, seed=11, std=0.05, dense_out=dense)
@@ -57,6 +61,7 @@ def test_decoder_teacher_forced_matches_lowrank_llama(gpu, layout):
                rope_theta=args.rope_theta, rope_scaling=args.rope_scaling)
     oracle = ref.lowrank_llama(cfg, hf_w, [ref.Factors(lr.k_VT, lr.k_U, lr.v_VT, lr.v_U) for _, lr in dense])
     model = pm.Transformer(args, sd, gpu, cache_layout=layout)
+    assert model._fused_step == (vocab % 16 == 0)
 
     B, S, steps = 2, 45, 7
     g = torch.Generator().manual_seed(2)
@@ -76,6 +81,33 @@ def test_decoder_teacher_forced_matches_lowrank_llama(gpu, layout):
         # the greedy graph's ids pick a maximal logit of the step (up to the steps' own differences)
         e = eager.cpu()
         assert (e.max(-1).values - e.gather(1, greedy.cpu()[:, None])[:, 0]).abs().max() <= 1e-2 * e.abs().max()
+
+
+def test_decoder_above_64_rows_matches_lowrank_llama(gpu):
+    """Past 64 rows the decode projections are torch's F.linear and the step keeps its separate norms
+    (no tiled activations, no folded FFN norm): the same oracle bar, two teacher-forced steps."""
+    pytest.importorskip("transformers")
+    args = pm.ModelArgs(dim=512, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=700, ffn_dim=1024,
+                        max_seq_len=64, max_batch_size=65)
+    dense = []
+    sd = pm.random_palu_state_dict(args, [64, 48], [32, 96], gpu, seed=13, std=0.05, dense_out=dense)
+    hf_w = _hf_weights(sd, dense, args.n_layers)
+    cfg = dict(dim=args.dim, n_layers=args.n_layers, n_heads=args.n_heads, n_kv_heads=args.n_kv_heads,
+               head_dim=args.head_dim, vocab_size=args.vocab_size, ffn_dim=args.ffn_dim, norm_eps=args.norm_eps,
+               rope_theta=args.rope_theta, rope_scaling=args.rope_scaling)
+    oracle = ref.lowrank_llama(cfg, hf_w, [ref.Factors(lr.k_VT, lr.k_U, lr.v_VT, lr.v_U) for _, lr in dense])
+    model = pm.Transformer(args, sd, gpu)
+    assert not model._fused_step and not any(L["w13"].in_scale_folded for L in model.layers)
+    B, S, steps = 65, 20, 2
+    ids = torch.randint(0, args.vocab_size, (B, S + steps), generator=torch.Generator().manual_seed(4))
+    with torch.no_grad():
+        exp = oracle(ids).logits
+    pm.prefill_all(model, ids[:, :S].to(gpu), users_per_chunk=65)
+    for t in range(steps):
+        pos = torch.full((B,), S + t, dtype=torch.int32, device=gpu)
+        out = model.decode(ids[:, S + t].to(gpu), pos)
+        torch.cuda.synchronize()
+        _check(out, exp[:, S + t], f"decode step {t}")
 
 
 def test_generate_greedy_is_consistent_with_decode(gpu):
