@@ -93,8 +93,8 @@ __device__ __forceinline__ int qkv_part_of(const QkvEpi& e, int col, int& gi, in
 // NB register buffers per wave, so each step's loads are issued NB - 1 steps before its MFMAs. Weight
 // and activation tiles of one step share a buffer: loads return in issue order, so an activation tile
 // loaded later than the weights would make every wait a wait for those weights too. NW waves per
-// workgroup: 4 (one per SIMD, the whole register file each) or 8 (two per SIMD, twice the loads in flight
-// per CU, for the narrow workgroups of the latency-bound small projections).
+// workgroup (the launches use 4: one per SIMD, the whole register file each; 8, two per SIMD, was slower
+// end to end for the one- and two-tile projections).
 template <int RTW, int NB, int NW, bool XT, int EPI>
 __global__ __launch_bounds__(NW * 64) void palu_linear_kernel(const __bf16* __restrict__ x, long long ldx, int m,
                                                               const __bf16* __restrict__ wt, int n16, int kt_total,
