@@ -353,6 +353,39 @@ def test_linear_qkv_equals_projection_and_qkv_post(gpu, layout, gs, r_k, r_v, k_
     _check_linear(q, q_ref)
 
 
+@pytest.mark.parametrize("layout", ["tiled", "rows"])
+def test_linear_qkv_positions_outside_the_cache(gpu, layout):
+    """Rows whose position lies outside the cache (negative, or at or past its length) get q rotated at the
+    position (clamped into the rotation table) and append nothing, as qkv_post does; the other rows
+    append as usual."""
+    g = torch.Generator().manual_seed(77)
+    nh, hd, S, dim, G, r = 4, 128, 64, 256, 2, 32
+    k0, v0 = nh * hd, nh * hd + G * r
+    n = v0 + G * r
+    x = torch.randn(4, dim, generator=g).to(gpu, torch.bfloat16)
+    w = (torch.randn(n, dim, generator=g) * 0.05).to(gpu, torch.bfloat16)
+    pos = torch.tensor([-1, S, 3, S + 5], dtype=torch.int32, device=gpu)
+    cos, sin = fused.cos_sin_tables(hd, S, 500000.0, None)
+    cos, sin = cos.to(gpu).contiguous(), sin.to(gpu).contiguous()
+    mk = (lambda wd, role: LatentCache.zeros(4, G, S, wd, gpu, role)) if layout == "tiled" else \
+        (lambda wd, role: torch.zeros(4, G, S, wd, dtype=torch.bfloat16, device=gpu))
+    keys, values, keys2, values2 = mk(r, "k"), mk(r, "v"), mk(r, "k"), mk(r, "v")
+    rtw = decoder_ops.linear_plan(4, n, dim, 1)[0]
+    wt = decoder_ops.tile_weight(w, rtw)
+    q = decoder_ops.linear_qkv(x, wt, rtw, pos, cos, sin, nh, keys, k0, r, r, values, v0, r, r)
+    part = decoder_ops.linear_tiled(x, wt, rtw, 1, mode="partials")
+    q2 = decoder_ops.qkv_post(part, pos, cos, sin, nh, keys2, k0, r, r, values2, v0, r, r)
+    torch.cuda.synchronize()
+    kt = (lambda c: c.to_rows()) if layout == "tiled" else (lambda c: c)
+    assert torch.equal(q, q2)
+    assert torch.equal(kt(keys), kt(keys2)) and torch.equal(kt(values), kt(values2))
+    rows = kt(keys).float().abs().sum(dim=(1, 3))                     # [B, S]: nonzero where appended
+    assert rows[2, 3] > 0 and rows.count_nonzero() == 1
+    clamp = pos.long().clamp(0, cos.shape[0] - 1)                     # the table's rows, not the cache's
+    q_ref = fused.apply_rope_meta(_linear_ref(x, w)[:, :k0].view(4, nh, hd), cos[clamp][:, None], sin[clamp][:, None])
+    _check_linear(q, q_ref)
+
+
 def test_linear_qkv_rejects_overlapping_ranges(gpu):
     x = torch.zeros(4, 256, dtype=torch.bfloat16, device=gpu)
     wt = torch.zeros(128 + 2 * 64, 256, dtype=torch.bfloat16, device=gpu)
