@@ -1,7 +1,7 @@
 """CPU fp32 oracle for Palu's fused latent flash-decode. TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may import this module, and only
-as the checker (or, in bench.py, as the CPU path being timed beside the GPU). The product
+as the oracle that results are compared with (or, in bench.py, as the CPU path timed beside the GPU). The product
 (tt-cadlab_amd/palu_tt) never imports it and fails loudly when its HIP library is missing.
 
 Everything here is a restatement, written from the mathematics the reference implements, of:
