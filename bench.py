@@ -65,6 +65,11 @@ def parse():
     ap.add_argument("--e2e-tokens", type=int, default=256, help="greedy tokens generated per row")
     ap.add_argument("--e2e-layers", type=int, default=32)
     ap.add_argument("--e2e-no-graph", action="store_true", help="eager decode steps instead of one HIP graph per step")
+    ap.add_argument("--e2e-fidelity-steps", type=int, default=16,
+                    help="teacher-forced decode steps of the fidelity check on the Palu model (fused vs naive vs "
+                         "fp32 attention, palu_tt.decode_check); 0 skips it")
+    ap.add_argument("--e2e-deterministic", action="store_true",
+                    help="fixed block order in the decode kernels during the timed generation (reproducible ids)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="before timing, run 3 plain device copies of MIB MiB (the reference kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -311,6 +316,7 @@ def measure_e2e(a, dev):
     decode greedily; decode tokens/s = batch x timed decode steps / decode wall time (the first generated
     token comes from prefill and is not timed). Then the same model shape with full-rank (128) K and V: the
     stock bf16 full-KV decode through the same engine."""
+    from palu_tt import decode_check
     from palu_tt import model as pm
     B, P, n_new, L = a.e2e_batch, a.e2e_prompt, a.e2e_tokens, a.e2e_layers
     ranks_k, ranks_v = pm.draw_ranks(L, seed=1), pm.draw_ranks(L, seed=2)
@@ -328,6 +334,7 @@ def measure_e2e(a, dev):
         tok = pm.prefill_all(model, prompts).argmax(-1)
         torch.cuda.synchronize()
         t_pre = time.perf_counter() - t0
+        model.set_deterministic(a.e2e_deterministic)
         step = model.decode if a.e2e_no_graph else model.decode_graph
         pos = torch.full((B,), P, dtype=torch.int32, device=dev)
         step(tok, pos, greedy=True)                       # capture / warm-up at position P (rewritten below)
@@ -348,10 +355,29 @@ def measure_e2e(a, dev):
                      "kv_cache_bytes_per_token": int(kv_tok),
                      "ranks_drawn_mean": {"k": sum(rk) / L, "v": sum(rv) / L},
                      "ranks_padded": {"k": args.palu.rank_k, "v": args.palu.rank_v},
-                     # varies from run to run: the fused op's default block order is dynamic (probabilities
-                     # rounded in a different order per call) and random-init logits have near-ties
-                     "generated_ids_checksum": int(torch.stack(toks).sum())}
-        del model, att, step
+                     # with the default dynamic block order it varies from run to run (probabilities rounded
+                     # in a different order per call, and random-init logits have near-ties)
+                     "generated_ids_checksum": int(torch.stack(toks).sum()),
+                     "deterministic": bool(a.e2e_deterministic)}
+        del step
+        if kind == "palu" and a.e2e_fidelity_steps > 0:
+            # decode fidelity (reference palu_tt/decode_check.py:62-134): one prefill, then the same
+            # teacher tokens through the naive path, the fused op and fp32 attention over the same caches;
+            # logit PCC per row and step
+            T = min(a.e2e_fidelity_steps, args.max_seq_len - P)
+            teacher = torch.randint(0, args.vocab_size, (B, T), generator=torch.Generator().manual_seed(8)).to(dev)
+            t0 = time.perf_counter()
+            r = decode_check.fused_vs_naive(model, prompts, teacher, reference_core=decode_check.fp32_attention_core)
+            torch.cuda.synchronize()
+            pick = lambda d: {"pcc_min": round(d["pcc_min"], 6), "pcc_mean": round(d["pcc_mean"], 6),
+                              "argmax_agree": round(d["argmax_agree"], 4)}
+            out[kind]["fidelity"] = {
+                "steps": r["steps"], "rows": r["rows"], "teacher_forced": True,
+                "fused_vs_naive": pick(r), "fused_vs_fp32_attention": pick(r["fused_vs_reference"]),
+                "naive_vs_fp32_attention": pick(r["naive_vs_reference"]),
+                "reference_published_fused_vs_naive_pcc_min": [0.9948, 0.9982, 0.9979],
+                "seconds": round(time.perf_counter() - t0, 1)}
+        del model, att
         torch.cuda.empty_cache()
     out["speedup_vs_stock"] = round(out["palu"]["decode_tokens_per_s"] / out["stock"]["decode_tokens_per_s"], 3)
     return out
@@ -445,7 +471,7 @@ def main():
                    "layer_caches_rotated": a.layers,
                    "rope": "llama3 theta 5e5 factor 8", "deterministic": a.deterministic},
         "kernel_us": round(kern_ms * 1e3, 2),
-        "kernel_us_min": round(min(per) * 1e3, 2),
+        "kernel_us_percall_event_min": round(min(per) * 1e3, 2),
         "kernel_us_percall_events": round(statistics.mean(per) * 1e3, 2),
         "tokens_per_s": round(B / (N_LAYERS_MODEL * wall_ms * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

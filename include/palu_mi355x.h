@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define PALU_ABI_VERSION 13
+#define PALU_ABI_VERSION 14
 
 #define PALU_OK 0
 #define PALU_EINVAL 1       /* arguments outside the op's envelope */
@@ -104,8 +104,11 @@ size_t palu_glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int
  *                                    always rotates block-relative (32 positions) from cs_tab.
  *   u_v      [n_kv, r_v, 128] bf16   optional: in-kernel V rebuild (G-LRD). The output is then
  *                                    softmax(q K^T) (v_latent u_v[h]), 128 wide (head_dim_v == 128);
- *                                    needs PALU_LAYOUT_TILED, r_k and r_v in 32 .. 512 (multiples of
- *                                    32), and is not built for the paged entry point (PALU_EUNSUPPORTED)
+ *                                    r_k and r_v in 32 .. 512 (multiples of 32), caches in
+ *                                    PALU_LAYOUT_ROWS (the reference's [B, n_groups, S, r] call,
+ *                                    tests/test_palu_sdpa_device.py:245-258), PALU_LAYOUT_TILED or
+ *                                    PALU_LAYOUT_TILED_GROUPED; not built for the paged entry point
+ *                                    (PALU_EUNSUPPORTED)
  *   group_ranks [2 * n_groups] int32 (host memory, may be NULL)
  *                                    with u_v: each latent group's own ranks, K ranks then V ranks,
  *                                    multiples of 32 up to r_k / r_v. The caches keep r_k / r_v columns

@@ -241,7 +241,9 @@ class PaluRefAttention:
         self.cache_v_lat = None
 
     @torch.no_grad()
-    def forward(self, x: torch.Tensor, start_pos: int) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, start_pos: int, return_attention: bool = False):
+        """Output [B, S, dim]; with return_attention also the attention output before o_proj, softmax(q K^T /
+        sqrt(hd)) V per head, [B, S, nh * hd] (heads in order, each head's dims in v_proj's row order)."""
         B, S, _ = x.shape
         q = (x @ self.wq.T).view(B, S, self.nh, self.hd).transpose(1, 2)
         k_lat = torch.einsum("bsd,hrd->bhsr", x, self.f.k_VT)
@@ -266,7 +268,7 @@ class PaluRefAttention:
         mask = torch.ones(S, T, dtype=torch.bool).tril(diagonal=start_pos)
         scores = scores.masked_fill(~mask, float("-inf"))
         out = (torch.softmax(scores, dim=-1) @ V).transpose(1, 2).reshape(B, S, self.nh * self.hd)
-        return out @ self.wo.T
+        return (out @ self.wo.T, out) if return_attention else out @ self.wo.T
 
 
 class LowRankProj(torch.nn.Module):

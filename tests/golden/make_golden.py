@@ -13,8 +13,8 @@ with llama3 scaling (factor 8, low 1, high 4, original context 8192); q/k/v/o_pr
 per-head truncated SVD of k_proj / v_proj at rank 64 (Palu's balanced split); batch 1, a 256-token
 prefill of hidden states ~ N(0, 1), then 16 decode steps; seed 0. The inputs are regenerated from the
 seed by config1_inputs() (the draw order is fixed there), so the fixture holds only the outputs -- the
-16 decode outputs and four prefill rows -- and fingerprints of the inputs that detect a change in the
-random stream.
+16 decode outputs, their attention outputs before o_proj (the fused op's result, mapped to head space),
+and four prefill rows -- and fingerprints of the inputs that detect a change in the random stream.
 
 Both outputs come from oracle functions that tests/test_oracle.py pins (transformers' rotary embedding
 and attention, brute-force loops, the reference's own test properties). The fixtures freeze those pinned
@@ -79,19 +79,25 @@ def config1_fingerprint(W, x):
 
 
 def config1_oracle_outputs(W, x):
-    """(prefill output [1, 256, 4096], decode outputs [16, 4096]) of the layer oracle."""
+    """(prefill output [1, 256, 4096], decode outputs [16, 4096], decode attention outputs before o_proj
+    [16, 32 * 128]) of the layer oracle."""
     Uk, VTk = ref.svd_per_head(W["k"], C1_NKV, C1_RANK)
     Uv, VTv = ref.svd_per_head(W["v"], C1_NKV, C1_RANK)
     layer = ref.PaluRefAttention(C1_NQ, C1_NKV, HD, THETA, LLAMA3, W["q"], W["o"], ref.Factors(VTk, Uk, VTv, Uv))
     pre = layer.forward(x[:, :C1_PREFILL], 0)
-    dec = [layer.forward(x[:, C1_PREFILL + t:C1_PREFILL + t + 1], C1_PREFILL + t)[0, 0] for t in range(C1_STEPS)]
-    return pre, torch.stack(dec)
+    dec, attn = [], []
+    for t in range(C1_STEPS):
+        o, a = layer.forward(x[:, C1_PREFILL + t:C1_PREFILL + t + 1], C1_PREFILL + t, return_attention=True)
+        dec.append(o[0, 0])
+        attn.append(a[0, 0])
+    return pre, torch.stack(dec), torch.stack(attn)
 
 
 def make_config1():
     W, x = config1_inputs()
-    pre, dec = config1_oracle_outputs(W, x)
-    return {"decode_out": dec.float().contiguous(), "prefill_rows": pre[0, list(C1_PREFILL_ROWS)].float().contiguous(),
+    pre, dec, attn = config1_oracle_outputs(W, x)
+    return {"decode_out": dec.float().contiguous(), "decode_attn": attn.float().contiguous(),
+            "prefill_rows": pre[0, list(C1_PREFILL_ROWS)].float().contiguous(),
             "prefill_row_index": torch.tensor(C1_PREFILL_ROWS, dtype=torch.int32),
             "input_fingerprint": config1_fingerprint(W, x)}
 
@@ -107,5 +113,6 @@ if __name__ == "__main__":
     save_file(make_config1(), str(path), metadata={
         "layer": "hidden 4096, 32 Q / 8 KV heads, head_dim 128, rank_k = rank_v = 64 (per-head SVD)",
         "rope": "llama3 theta 5e5 factor 8, low 1, high 4, orig 8192", "steps": "256-token prefill, 16 decode",
-        "seed": "0 (draw order Wq, Wk, Wv, Wo, x; see config1_inputs)", "generator": "tests/golden/make_golden.py"})
+        "seed": "0 (draw order Wq, Wk, Wv, Wo, x; see config1_inputs)", "generator": "tests/golden/make_golden.py",
+        "decode_attn": "attention output before o_proj per decode step, [16, 32 heads x 128]"})
     print(f"wrote {path} ({path.stat().st_size} bytes)")

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import palu_oracle as ref
-from palu_tt import convert
+from palu_tt import compress, convert
 from palu_tt.attention import PaluAttention
 from palu_tt.cache import GroupedLatentCache
 
@@ -99,6 +99,34 @@ def test_attention_grouped_latents_of_unequal_ranks(gpu, fused):
     assert att.group_ranks == ([96, 192], [256, 64])
     assert all(isinstance(c, GroupedLatentCache) for c in att.layer_past)
     assert att.kv_bytes_per_token() == (96 + 192 + 256 + 64) * 2.0
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("rank_multiple,expect", [(32, ([128, 160], [192, 96])), (64, ([128, 192], [192, 96]))])
+def test_attention_from_a_dump_with_group_ranks_off_the_kernel_grid(gpu, tmp_path, fused, rank_multiple, expect):
+    """A G-LRD factor directory whose group ranks are not multiples of 32 (K 100 / 140, V 176 / 96, as a
+    real dump's head_wise_ranks may be), written by save_palu_dir and read by load_palu_dir at two rank
+    multiples: the layer rounds each group rank up to 32 (the widest group at the padded width), the
+    factors being zero past each group's rank, and decodes on the fused and the naive path to the layer
+    oracle built from the same loaded factors."""
+    dim, nh, nkv, B, S0, steps = 1024, 8, 4, 2, 40, 4
+    g = torch.Generator().manual_seed(31)
+    W = {"q": torch.randn(nh * HD, dim, generator=g) * 0.02, "k": torch.randn(nkv * HD, dim, generator=g) * 0.02,
+         "v": torch.randn(nkv * HD, dim, generator=g) * 0.02, "o": torch.randn(dim, nh * HD, generator=g) * 0.02}
+    fac = compress.factor_layers({0: {"k": W["k"], "v": W["v"]}}, nkv, [[100, 140]], [[176, 96]])
+    lr = convert.load_palu_dir(convert.save_palu_dir(tmp_path / "dump", fac), 1, nkv, HD, rank_multiple=rank_multiple)[0]
+    assert lr.group_size == 2 and lr.group_ranks_k == [100, 140] and lr.group_ranks_v == [176, 96]
+    sd = {"layers.0.attention.wq.weight": convert.reverse_permute(W["q"], nh, nh * HD, dim),
+          "layers.0.attention.wo.weight": W["o"]}
+    for name, t in convert.palu_layer_tensors(W, lr, nh, nkv, HD).items():
+        sd[f"layers.0.attention.palu.{name}"] = t
+    palu = convert.PaluConfig(rank_k=[lr.r_k], rank_v=[lr.r_v], cache_id="dump", group_size=lr.group_size,
+                              runtime=convert.PaluRuntime(use_fused_k=fused, check=True),
+                              group_ranks=[(lr.group_ranks_k, lr.group_ranks_v)])
+    oracle = ref.PaluRefAttention(nh, nkv, HD, THETA, LLAMA3, W["q"], W["o"],
+                                  ref.Factors(lr.k_VT, lr.k_U, lr.v_VT, lr.v_U))
+    att = _drive(gpu, sd, palu, oracle, dim, nh, nkv, B, S0, steps, "tiled", fused)
+    assert att.group_ranks == expect
 
 
 def _drive(gpu, sd, palu, oracle, dim, nh, nkv, B, S0, steps, layout, fused):

@@ -19,31 +19,13 @@ V layer among its layers) runs the same check through HIP-graph decode steps wit
 import pytest
 import torch
 
-from palu_tt import decode_check, fused
+from palu_tt import decode_check
 from palu_tt import model as pm
 
 pytestmark = pytest.mark.gpu
 
 
-def fp32_attention_core(layer, q4, keys, values, pos):
-    """Plain fp32 torch attention over a PaluAttention layer's caches: the reference pass."""
-    S = layer._recon_len()
-    gs, nkv, nh, hd = layer.gs, layer.n_kv_heads, layer.n_heads, layer.head_dim
-    per_head = (lambda t: t) if gs == 1 else (lambda t: t.repeat_interleave(gs, dim=1))
-    if layer.recon_k:
-        K = per_head(layer._cache_rows(keys, S)).float() @ layer.u_k.float()                 # [B, nkv, S, hd]
-        K = fused.apply_rope_meta(K, layer.cos[:S][None, None], layer.sin[:S][None, None])
-    else:
-        K = layer._cache_rows(keys, S).float()                                                # rotated full K
-    V = layer._cache_rows(values, S).float()
-    if gs > 1:
-        V = per_head(V) @ layer.u_v.float()
-    B = q4.shape[1]
-    q = q4[0].float().view(B, nkv, nh // nkv, hd)
-    sc = (q @ K.transpose(-1, -2)) * layer.scale                                               # [B, nkv, rep, S]
-    masked = torch.arange(S, device=q.device)[None, :] > pos.long()[:, None]
-    sc = sc.masked_fill(masked[:, None, None, :], float("-inf"))
-    return (torch.softmax(sc, dim=-1) @ V).reshape(1, B, nh, -1).to(torch.bfloat16)
+fp32_attention_core = decode_check.fp32_attention_core     # plain fp32 torch attention over the same caches
 
 
 def test_fused_matches_naive_on_the_end_to_end_decoder(gpu):

@@ -2,7 +2,8 @@
 latent, every KV head rebuilds K with its own u_k slice and V with its own u_v slice in-kernel
 (palu_sdpa_decode with u_v; reference interface docs/superpowers/specs/2026-09-12-palu-tt-stage2b-
 design.md:120-142). Oracle: reference_decode with u_v (fp32), on the same bf16-rounded inputs; bar
-max-abs 2e-2 and cosine 0.9999. Group ranks cover the configuration's set {128, 192, 256, 384, 512}.
+max-abs 2e-2 and cosine 0.9999. Group ranks cover the configuration's set {128, 192, 256, 384, 512}; the
+caches are tiled (LatentCache), compact per group (GroupedLatentCache) or the reference's row-major tensors.
 """
 import pytest
 import torch
@@ -46,6 +47,19 @@ def _run(dev, q, k, v, u_k, u_v, pos, S, out_dtype=torch.float32, cs_dtype=torch
         fused.w_rot_from_u_k(u_k).to(dev, torch.bfloat16)[None], fused.cs_table(cos, sin, S)[None, None].to(dev, cs_dtype),
         LatentCache.from_rows(v.to(dev, torch.bfloat16), "v"), HD, pos.to(dev, torch.int32),
         u_v=u_v.to(dev, torch.bfloat16)[None], scale=HD ** -0.5, out_dtype=out_dtype, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu()
+
+
+def _run_rows(dev, q, k, v, u_k, u_v, pos, S, out_dtype=torch.float32, rope=LLAMA3, **kw):
+    """The reference's own call: plain row-major [B, n_groups, S, r] latent tensors
+    (tests/test_palu_sdpa_device.py:245-258), no cache object."""
+    cos, sin = fused.cos_sin_tables(HD, S, THETA, rope)
+    out = fused.palu_sdpa_decode(
+        q.to(dev, torch.bfloat16), k.to(dev, torch.bfloat16).contiguous(),
+        fused.w_rot_from_u_k(u_k).to(dev, torch.bfloat16)[None], fused.cs_table(cos, sin, S)[None, None].to(dev),
+        v.to(dev, torch.bfloat16).contiguous(), HD, pos.to(dev, torch.int32), u_v=u_v.to(dev, torch.bfloat16)[None],
+        scale=HD ** -0.5, out_dtype=out_dtype, **kw)
     torch.cuda.synchronize()
     return out.float().cpu()
 
@@ -217,3 +231,111 @@ def test_pinned_heads_per_core_that_does_not_fit_the_grid_is_rejected(gpu):
     with pytest.raises(RuntimeError, match="only 4 available"):
         _run(gpu, *args, 256, heads_per_core=2, program_config=cfg)
     _check(_run(gpu, *args, 256, heads_per_core=4, program_config=cfg), _oracle(*args, 256))
+
+
+# ---- the reference's own G-LRD call: row-major [B, n_groups, S, r] latents ---------------------------
+
+def _reference_group_case(batch, S, r_k, r_v, gs, seed, nh=16, nkv=4):
+    """Inputs of the reference's _inputs_group (tests/test_palu_sdpa_device.py:219-232): its per-chip
+    16 Q / 4 KV heads, latents and queries N(0, 1), factors N(0, 1/r), positions uniform with row 0 at
+    S - 1 and, from batch 4 on, rows 1-3 at 0, 127 and 128."""
+    g = torch.Generator().manual_seed(seed)
+    ng = nkv // gs
+    q = _bf(torch.randn(1, batch, nh, HD, generator=g))
+    k = _bf(torch.randn(batch, ng, S, r_k, generator=g))
+    u_k = _bf(torch.randn(nkv, r_k, HD, generator=g) / r_k ** 0.5)
+    v = _bf(torch.randn(batch, ng, S, r_v, generator=g))
+    u_v = _bf(torch.randn(nkv, r_v, HD, generator=g) / r_v ** 0.5)
+    pos = torch.randint(0, S, (batch,), generator=g)
+    pos[0] = S - 1
+    if batch >= 4:
+        pos[1], pos[2], pos[3] = 0, 127, 128
+    return q, k, v, u_k, u_v, pos
+
+
+def _oracle_plain(q, k, v, u_k, u_v, pos, S):
+    cos, sin = ref.cos_sin_tables(HD, S, THETA, None)
+    return ref.reference_decode(q, k, u_k, v, pos, cos, sin, HD ** -0.5, u_v=u_v)
+
+
+@pytest.mark.parametrize("batch,S,r_k,r_v,gs", [
+    (1, 1024, 128, 256, 4), (32, 1024, 128, 256, 4),       # test_grouped_latents_with_in_kernel_v (:278-281)
+    (1, 1024, 256, 512, 4), (32, 1024, 256, 512, 4),
+    (1, 1024, 384, 512, 4), (32, 1024, 384, 512, 4),
+    (8, 8192, 64, 512, 4),                                 # test_grouped_latents_long_context_batch8 (:298-299)
+    (32, 1024, 64, 64, 1),                                 # test_in_kernel_v_with_per_head_latents (:302-304)
+    (32, 1024, 512, 512, 4),                               # test_grouped_latents_full_rank_group (:316-318)
+])
+def test_glrd_reference_row_major_call(gpu, batch, S, r_k, r_v, gs):
+    """The reference's G-LRD op cases as it calls them: row-major latents, u_v, head_dim_v 128, its
+    per-chip head shape and input distributions, plain RoPE tables; every row against the oracle at
+    the op's bar (max-abs 2e-2, cosine 0.9999)."""
+    args = _reference_group_case(batch, S, r_k, r_v, gs, seed=batch * 1000 + r_k + r_v + gs)
+    out = _run_rows(gpu, *args, S, rope=None)
+    assert out.shape == (1, batch, 16, HD)
+    _check(out, _oracle_plain(*args, S))
+
+
+@pytest.mark.parametrize("r_k,r_v,B,S", [(128, 192, 4, 2048), (512, 384, 2, 4096), (96, 160, 3, 640)])
+def test_glrd_row_major_equals_tiled(gpu, r_k, r_v, B, S):
+    """Row-major and tiled caches holding the same latents give the same output bit for bit: the same
+    scores arithmetic, and the row-major V pieces are moved into the tiled operand order exactly
+    (identity products), so the PV sums are the same."""
+    args = _case(B, S, r_k, r_v, hpg=4, seed=r_k * 3 + r_v + S)
+    assert torch.equal(_run_rows(gpu, *args, S), _run(gpu, *args, S))
+
+
+@pytest.mark.parametrize("ranks_k,ranks_v,B,S", [([128, 512], [192, 384], 4, 4096), ([96, 32], [64, 160], 3, 1000)])
+def test_glrd_row_major_group_ranks_and_ragged_cache(gpu, ranks_k, ranks_v, B, S):
+    """Row-major caches padded to the widest group, told each group's ranks, with NaN in every padding
+    column and in every cache row past each row's position (never attended): only a group's own
+    columns and the attended rows are read into a result. S = 1000 is not a multiple of the 32-position
+    block, so the last block's rows past the cache end are clamped to its last row and masked."""
+    r_k, r_v = max(ranks_k), max(ranks_v)
+    q, k, v, u_k, u_v, pos = _case(B, S, r_k, r_v, hpg=4, seed=sum(ranks_k) * 7 + S)
+    pos[0] = S - 1
+    for g, (rk, rv) in enumerate(zip(ranks_k, ranks_v)):
+        k[:, g, :, rk:] = 0
+        v[:, g, :, rv:] = 0
+        u_k[4 * g:4 * g + 4, rk:] = 0
+        u_v[4 * g:4 * g + 4, rv:] = 0
+    exp = _oracle(q, k, v, u_k, u_v, pos, S)
+    kn, vn = k.clone(), v.clone()
+    for g, (rk, rv) in enumerate(zip(ranks_k, ranks_v)):
+        kn[:, g, :, rk:] = float("nan")
+        vn[:, g, :, rv:] = float("nan")
+    for b in range(B):
+        kn[b, :, int(pos[b]) + 1:] = float("nan")
+        vn[b, :, int(pos[b]) + 1:] = float("nan")
+    _check(_run_rows(gpu, q, kn, vn, u_k, u_v, pos, S, group_ranks=(ranks_k, ranks_v)), exp)
+
+
+def test_glrd_compact_caches_at_the_benchmark_shape(gpu):
+    """The layer the benchmark times (B=16, ctx 16384, 2 groups of 4 KV heads, K ranks (128, 512), V
+    ranks (192, 384), each group stored at its own ranks in GroupedLatentCaches) against the oracle
+    on three rows, two of them ending mid-cache; the same call on the row-major padded caches (the
+    reference's form) gives the same bits."""
+    ranks_k, ranks_v = [128, 512], [192, 384]
+    B, S = 16, 16384
+    q, k, v, u_k, u_v, pos = _case(B, S, 512, 384, hpg=4, seed=16384, pos=torch.full((16,), S - 1))
+    pos[7], pos[15] = 9000, 16000
+    for g, (rk, rv) in enumerate(zip(ranks_k, ranks_v)):
+        k[:, g, :, rk:] = 0
+        v[:, g, :, rv:] = 0
+        u_k[4 * g:4 * g + 4, rk:] = 0
+        u_v[4 * g:4 * g + 4, rv:] = 0
+    kd, vd = k.to(gpu, torch.bfloat16), v.to(gpu, torch.bfloat16)
+    gk = GroupedLatentCache.from_rows(kd, ranks_k, "k")
+    gv = GroupedLatentCache.from_rows(vd, ranks_v, "v")
+    cos, sin = fused.cos_sin_tables(HD, S, THETA, LLAMA3)
+    compact = fused.palu_sdpa_decode(
+        q.to(gpu, torch.bfloat16), gk, fused.w_rot_from_u_k(u_k).to(gpu, torch.bfloat16)[None],
+        fused.cs_table(cos, sin, S)[None, None].to(gpu), gv, HD, pos.to(gpu, torch.int32),
+        u_v=u_v.to(gpu, torch.bfloat16)[None], scale=HD ** -0.5, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    compact = compact.cpu()
+    del gk, gv
+    rows_out = _run_rows(gpu, q, kd, vd, u_k, u_v, pos, S, group_ranks=(ranks_k, ranks_v))
+    assert torch.equal(compact, rows_out)
+    rows = [0, 7, 15]
+    _check(compact[:, rows], _oracle(q[:, rows], k[rows], v[rows], u_k, u_v, pos[rows], S))

@@ -186,6 +186,18 @@ def test_palu_dir_round_trip_reproduces_the_weights_at_full_rank(tmp_path):
     torch.testing.assert_close(U @ VT, Ur @ VTr, atol=1e-4, rtol=1e-4)
 
 
+def test_group_ranks_off_the_kernel_grid_round_up_to_32():
+    """A dump's group ranks are any positive integers (config.json head_wise_ranks); the layer hands the
+    fused op and its compact caches each rank rounded up to 32, capped at the padded width, with the
+    widest group at exactly that width (load_palu_dir pads r_k / r_v from the widest raw rank)."""
+    from palu_tt.attention import kernel_group_ranks
+    assert kernel_group_ranks([100, 140], [176, 96], 160, 192) == ([128, 160], [192, 96])     # rank_multiple 32
+    assert kernel_group_ranks([100, 140], [176, 96], 192, 192) == ([128, 192], [192, 96])     # rank_multiple 64
+    assert kernel_group_ranks([8, 4], [8, 4], 32, 32) == ([32, 32], [32, 32])
+    assert kernel_group_ranks([128, 512], [192, 384], 512, 384) == ([128, 512], [192, 384])   # already on the grid
+    assert kernel_group_ranks([33, 500, 31], [1, 1, 64], 512, 64) == ([64, 512, 32], [32, 32, 64])
+
+
 def test_palu_dir_cache_id_tracks_content(tmp_path):
     """The id is dirname-<8 hex>, stable across reads and file touches, and changes when one byte of
     config.json changes or the tensors are regenerated with the same shapes."""
@@ -327,7 +339,7 @@ def _sdpa(lib, **kw):
     (dict(rot_mode=5), _native.PALU_EINVAL, "rot_mode must be"),
     (dict(n_groups=3, n_kv=4), _native.PALU_EINVAL, "heads_per_group"),
     (dict(u_v=_FAKE, head_dim_v=64), _native.PALU_EINVAL, "head_dim_v"),
-    (dict(u_v=_FAKE, head_dim_v=128), _native.PALU_EUNSUPPORTED, "u_v"),
+    (dict(u_v=_FAKE, head_dim_v=128), _native.PALU_EINVAL, "palu_glrd_workspace_bytes"),   # rows accepted
     (dict(layout=3), _native.PALU_EINVAL, "needs u_v and group_ranks"),
     (dict(head_dim_v=128), _native.PALU_EINVAL, "head_dim_v"),
     (dict(heads_per_core=4), _native.PALU_EINVAL, "heads_per_core"),
@@ -430,9 +442,11 @@ def test_paged_envelope_errors(lib):
 
 
 def test_glrd_envelope_errors(lib):
-    """Grouped latents with u_v: head_dim_v must be 128, caches tiled, contiguous (not paged)."""
+    """Grouped latents with u_v: head_dim_v must be 128, r_k / r_v up to 512, caches contiguous (not
+    paged). Row-major caches (the reference's call) pass the envelope and stop at the missing
+    workspace, before any launch."""
     rc, msg = _sdpa(lib, u_v=_FAKE, head_dim_v=128, n_kv=4, n_groups=1, n_q=16, layout=0)
-    assert rc == _native.PALU_EUNSUPPORTED and "u_v" in msg and "tiled" in msg
+    assert rc == _native.PALU_EINVAL and "palu_glrd_workspace_bytes" in msg
     rc, msg = _sdpa(lib, u_v=_FAKE, head_dim_v=64, n_kv=4, n_groups=1, n_q=16, layout=1)
     assert rc == _native.PALU_EINVAL and "head_dim_v" in msg
     rc, msg = _sdpa(lib, u_v=_FAKE, head_dim_v=128, r_k=544, layout=1)

@@ -240,9 +240,19 @@ def test_identity_factor_layer_equals_transformers_llama_attention():
     mask = torch.full((S, S), float("-inf")).triu(1)[None, None]
     with torch.no_grad():
         exp, _ = att(x, position_embeddings=pe, attention_mask=mask)
+    seen = {}
+    att.o_proj.register_forward_pre_hook(lambda mod, args: seen.setdefault("attn", args[0].detach().clone()))
+    with torch.no_grad():
+        att(x, position_embeddings=pe, attention_mask=mask)
     layer = ref.PaluRefAttention(nh, nkv, hd, THETA, LLAMA3, W["q"], W["o"], ref.identity_factors(W["k"], W["v"], nkv, hd))
     out = layer.forward(x, 0)
     torch.testing.assert_close(out, exp, atol=1e-4, rtol=1e-4)
+    # the attention output before o_proj (what the fused op computes, in head space) equals transformers'
+    # o_proj input, and o_proj of it is the layer output
+    layer2 = ref.PaluRefAttention(nh, nkv, hd, THETA, LLAMA3, W["q"], W["o"], ref.identity_factors(W["k"], W["v"], nkv, hd))
+    out2, attn = layer2.forward(x, 0, return_attention=True)
+    torch.testing.assert_close(attn, seen["attn"].reshape(attn.shape), atol=1e-5, rtol=1e-4)
+    torch.testing.assert_close(out2, attn @ W["o"].float().T, atol=0, rtol=0)
 
 
 def _tiny_llama_weights(cfg, seed):
@@ -405,3 +415,34 @@ def test_gather_pages_follows_the_page_table_position_by_position():
         for g in range(G):
             for p in range(maxp * ps):
                 assert torch.equal(rows[b, g, p], pool[int(pt[b, p // ps]), g, p % ps])
+
+
+# ------------------------------------------------------------------------------------------------
+# The comparison metrics every parity verdict uses
+
+def test_metric_helpers_match_library_routines():
+    """pcc, cosine and max_abs against torch.corrcoef, F.cosine_similarity and the plain max abs
+    difference on random inputs of several shapes and scales; a constant offset changes the cosine but
+    not the PCC (PCC centres both inputs, cosine does not), and a single changed element moves max_abs
+    by exactly its change."""
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(11)
+    for shape, scale in (((1000,), 1.0), ((7, 33), 1e-3), ((2, 3, 64), 50.0)):
+        a = torch.randn(*shape, generator=g) * scale
+        b = a + 0.3 * scale * torch.randn(*shape, generator=g)
+        exp_pcc = float(torch.corrcoef(torch.stack([a.flatten().double(), b.flatten().double()]))[0, 1])
+        exp_cos = float(F.cosine_similarity(a.flatten().double(), b.flatten().double(), dim=0))
+        assert abs(ref.pcc(a, b) - exp_pcc) < 1e-12
+        assert abs(ref.cosine(a, b) - exp_cos) < 1e-12
+        assert ref.max_abs(a, b) == float((a.double() - b.double()).abs().max())
+        off = b + 5.0 * scale
+        assert abs(ref.pcc(a, off) - ref.pcc(a, b)) < 1e-6       # the fp32 sum b + offset rounds b
+        assert ref.cosine(a, off) < ref.cosine(a, b) - 1e-3
+    x = torch.zeros(50)
+    y = x.clone()
+    y[17] = -0.25
+    assert ref.max_abs(x, y) == 0.25 and ref.max_abs(y, x) == 0.25
+    assert ref.cosine(x, x) == 1.0 and ref.pcc(x, x) == 1.0          # zero inputs: equal -> 1
+    assert ref.cosine(x, y) == 0.0
+    z = torch.randn(64, generator=g)
+    assert ref.pcc(z, -z) == pytest.approx(-1.0, abs=1e-12) and ref.cosine(z, 2 * z) == pytest.approx(1.0, abs=1e-12)

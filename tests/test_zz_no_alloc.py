@@ -12,7 +12,7 @@ import torch
 
 from oracle import palu_oracle as ref
 from palu_tt import _native, fused
-from palu_tt.cache import LatentCache
+from palu_tt.cache import GroupedLatentCache, LatentCache
 
 HD = 128
 THETA = 500000.0
@@ -83,6 +83,67 @@ def test_noalloc_equals_the_workspace_entry_point(gpu, shapes):
         exp = _oracle(c)
         ma, cs = ref.max_abs(no_alloc, exp), ref.cosine(no_alloc, exp)
         assert ma <= 2e-2 and cs >= 0.9999, f"call {i}: max_abs {ma:.3e}, cosine {cs:.6f}"
+
+
+def _layouts_case(dev, kind, B, S, seed, ranks=None):
+    """Inputs for one call of the layout cases: 'grouped' -- compact GroupedLatentCaches of unequal group
+    ranks (PALU_LAYOUT_TILED_GROUPED with the groups' ranks); 'rows_glrd' -- the reference's row-major
+    grouped latents; 'tiled_rows' -- M-LRD with the output in the tiled activation layout
+    (PALU_OUT_TILED_ROWS)."""
+    g = torch.Generator().manual_seed(seed)
+    bf = lambda *s, std=1.0: (torch.randn(*s, generator=g) * std).to(torch.bfloat16)
+    nh, nkv = 32, 8
+    cos, sin = fused.cos_sin_tables(HD, S, THETA, LLAMA3)
+    pos = torch.randint(0, S, (B,), generator=g)
+    pos[0] = S - 1
+    kw = dict(scale=HD ** -0.5, deterministic=True)
+    if kind == "tiled_rows":
+        r = 64
+        k, v = bf(B, nkv, S, r).to(dev), bf(B, nkv, S, r).to(dev)
+        u_k = bf(nkv, r, HD, std=r ** -0.5)
+        args = (bf(1, B, nh, HD).to(dev), LatentCache.from_rows(k, "k"),
+                fused.w_rot_from_u_k(u_k.float()).to(dev, torch.bfloat16)[None],
+                fused.cs_table(cos, sin, S)[None, None].to(dev), LatentCache.from_rows(v, "v"), r,
+                pos.to(dev, torch.int32))
+        return args, dict(kw, tiled_rows=True), lambda: torch.zeros(64, nh * r, dtype=torch.bfloat16, device=dev)
+    rk, rv = ranks
+    ng = 2
+    k, v = bf(B, ng, S, max(rk)), bf(B, ng, S, max(rv))
+    u_k, u_v = bf(nkv, max(rk), HD, std=0.08), bf(nkv, max(rv), HD, std=0.08)
+    for gi in range(ng):
+        k[:, gi, :, rk[gi]:] = 0
+        v[:, gi, :, rv[gi]:] = 0
+        u_k[4 * gi:4 * gi + 4, rk[gi]:] = 0
+        u_v[4 * gi:4 * gi + 4, rv[gi]:] = 0
+    if kind == "grouped":
+        kc, vc = GroupedLatentCache.from_rows(k.to(dev), rk, "k"), GroupedLatentCache.from_rows(v.to(dev), rv, "v")
+    else:
+        kc, vc = k.to(dev), v.to(dev)
+    args = (bf(1, B, nh, HD).to(dev), kc, fused.w_rot_from_u_k(u_k.float()).to(dev, torch.bfloat16)[None],
+            fused.cs_table(cos, sin, S)[None, None].to(dev), vc, HD, pos.to(dev, torch.int32))
+    return args, dict(kw, u_v=u_v.to(dev)[None], group_ranks=(rk, rv), out_dtype=torch.float32), \
+        lambda: torch.zeros(1, B, nh, HD, dtype=torch.float32, device=dev)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,calls", [
+    ("grouped", [(2, 2048, ([96, 192], [256, 64])), (1, 1024, ([64, 128], [128, 32]))]),
+    ("rows_glrd", [(2, 1000, ([128, 256], [192, 96])), (1, 512, ([32, 64], [64, 64]))]),
+    ("tiled_rows", [(16, 1024, None), (8, 512, None)]),
+])
+def test_noalloc_equals_the_workspace_entry_point_on_other_layouts(gpu, kind, calls):
+    """palu_sdpa_decode_noalloc sets its own strides and scratch for every layout: compact grouped caches
+    of unequal group ranks, the reference's row-major grouped latents (S = 1000, not a multiple of the
+    32-position block), and the tiled-rows output the decode step's output projection reads. Each is
+    compared bit for bit with palu_sdpa_decode (workspace) on two calls in a row, the second smaller."""
+    for i, (B, S, ranks) in enumerate(calls):
+        args, kw, fresh = _layouts_case(gpu, kind, B, S, seed=300 + i, ranks=ranks)
+        with_ws = fused.palu_sdpa_decode(*args, out=fresh(), **kw)
+        no_alloc = fused.palu_sdpa_decode(*args, out=fresh(), noalloc=True, **kw)
+        torch.cuda.synchronize()
+        assert torch.isfinite(with_ws.float()).all()
+        assert torch.equal(no_alloc.cpu(), with_ws.cpu()), \
+            f"{kind} call {i}: max diff {(no_alloc.float() - with_ws.float()).abs().max():.3e}"
 
 
 def test_noalloc_rejects_shapes_beyond_the_scratch():

@@ -282,9 +282,6 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
   }
   if (u_v != nullptr) {
     if (head_dim_v != HD) return fail(PALU_EINVAL, "head_dim_v must be %d when u_v rebuilds V in-kernel, got %d", HD, head_dim_v);
-    if (cache_layout != PALU_LAYOUT_TILED)
-      return fail(PALU_EUNSUPPORTED, "u_v: the in-kernel V rebuild reads latent caches in the tiled layout "
-                                     "(PALU_LAYOUT_TILED); row-major caches are not built for it");
     if (!aligned16(u_v)) return fail(PALU_EINVAL, "u_v must be 16-byte aligned");
   } else {
     if (hpg != 1) return fail(PALU_EINVAL, "grouped V latent (heads_per_group %d) needs u_v", hpg);
@@ -349,8 +346,9 @@ int sdpa_dispatch(const DecodeArgs& a, bool paged, int cache_layout, int r_k, in
   const bool tiled = cache_layout == PALU_LAYOUT_TILED;
   if (a.u_v != nullptr) {
     if (paged) return fail(PALU_EUNSUPPORTED, "u_v: the in-kernel V rebuild is not built for paged caches");
-    // Each group's stream: padded caches hold every group at r_k / r_v columns, compact ones at the
-    // group's own ranks, one group after another within a row.
+    // Each group's stream: padded caches (tiled, or the reference's row-major [B, n_groups, S, r]) hold
+    // every group at r_k / r_v columns, compact ones at the group's own ranks, one group after another
+    // within a row.
     DecodeArgs ag = a;
     const int n_groups = a.n_kv / a.hpg;
     long long ok = 0, ov = 0;
@@ -364,7 +362,7 @@ int sdpa_dispatch(const DecodeArgs& a, bool paged, int cache_layout, int r_k, in
     }
     ag.k_sb = ok;
     ag.v_sb = ov;
-    return dispatch_glrd(ag, cs_dtype, out_dtype, stream);
+    return dispatch_glrd(ag, !tiled, cs_dtype, out_dtype, stream);
   }
   if (tiled && r_k % 32 != 0)   // K rows ending in a half tile: their own translation units
     return paged ? dispatch_latent_tiled_paged_k16(a, r_k, r_v, cs_dtype, out_dtype, stream)

@@ -89,7 +89,7 @@ struct G2Smem {
   static_assert(BYTES <= 160 * 1024, "scores kernel LDS");
 };
 
-template <int KBP, typename TabT>
+template <int KBP, typename TabT, bool ROWS>
 __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const DecodeArgs a, float* scores) {
   constexpr int R = (KBP % 4 == 0) ? 4 : 2;       // rank blocks of latent tiles in flight per wave
   using SM = G2Smem<KBP>;
@@ -115,13 +115,14 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   const int b = bg / a.grp_cnt, grp = a.grp_lo + (bg - b * a.grp_cnt);
   const int kvh = grp * a.hpg + hig;
   const int QH = a.hpg * a.rep;
-  const int NB = a.S / BLK;
+  const int NB = (a.S + BLK - 1) / BLK;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int KB = a.gkw[grp] >> 5;                 // rank blocks of the group's stream (tile addressing)
+  const int KW = a.gkw[grp];                      // the group's stream width (row length of a ROWS cache)
+  const int KB = KW >> 5;                         // rank blocks of the group's stream (tile addressing)
   const int KBe = a.rk_eff >> 5;                  // rank blocks of this group (the rest is never read)
 
   int len = a.cur_pos[b] + 1;
@@ -131,6 +132,7 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   const int nblk = s_hi > s_lo ? (s_hi - s_lo + BLK - 1) / BLK : 0;
   const int npairs = (nblk + 1) >> 1;
   const __bf16* kbase = a.k + b * a.k_sb + a.gko[grp];
+  const int lrow = 8 * (n >> 2) + (n & 3);        // the lane's position in half-block 0 of a block
 
   // ---- prologue -----------------------------------------------------------------------------------
   // rot[cc][rt] = fp16 {cos f, sin f, cos f+1, sin f+1} at offset t = 32 hb + 8(n/4) + 4c + n%4 inside a
@@ -208,11 +210,14 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
     __syncthreads();
   }
 
-  // Tile loads of a pair of blocks: tile (kb, hb, c) of pair pp is block 2 pp + hb, K-tile c * KB + kb.
-  // Rank blocks past the group's r_k read the same tile order's kb 0 (the matching u_k^T tiles are zero,
-  // and the cache columns past the group's rank are never touched); blocks past
-  // the split's data read the split's first block. Every path issues the same loads.
-  // The block and tile offsets are uniform (scalar registers), the lane's 16 bytes the only vector part.
+  // Operand loads of a pair of blocks: register t[2 hb + c] of lane (n, g) holds rank indices
+  // 32 kb + 8 g .. +7 of position 8 (n / 4) + 4 c + n % 4 of block 2 pp + hb (the B operand of the
+  // rebuild). TILED: K-tile c * KB + kb of the block, one contiguous kilobyte. ROWS ([S, KW] row-major
+  // stream): 16 bytes of that position's row, rows past the cache end clamped to its last row (their
+  // scores are masked by the PV pass). Rank blocks past the group's r_k read kb 0 (the matching u_k^T
+  // tiles are zero, and the cache columns past the group's rank are never touched); blocks past the
+  // split's data read the split's first block. Every path issues the same loads.
+  // The block and tile offsets are uniform (scalar registers), the lane's part the only vector one.
   auto load_kb = [&](int pp, int kb, bf16x8 (&t)[4]) {
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb) {
@@ -221,9 +226,17 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
       const int kbr = kb < KBe ? kb : 0;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const long long off = __builtin_amdgcn_readfirstlane((int)(((s_lo >> 5) + (live ? blk : 0)) * (32 * KB * 32) +
-                                                                    (c * KB + kbr) * 512));
-        t[2 * hb + c] = *reinterpret_cast<const bf16x8*>(kbase + off + lane * 8);
+        if constexpr (ROWS) {
+          // a 32-bit byte offset from the uniform stream base (a stream holds at most 65536 x 512 values)
+          const int p0 = __builtin_amdgcn_readfirstlane(s_lo + (live ? blk : 0) * BLK);
+          const int p = min(p0 + lrow + 4 * c, a.S - 1);
+          const uint32_t off = (uint32_t)(p * KW + 32 * kbr + 8 * g) * 2u;
+          t[2 * hb + c] = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(kbase) + off);
+        } else {
+          const long long off = __builtin_amdgcn_readfirstlane(
+              (int)(((s_lo >> 5) + (live ? blk : 0)) * (32 * KB * 32) + (c * KB + kbr) * 512));
+          t[2 * hb + c] = *reinterpret_cast<const bf16x8*>(kbase + off + lane * 8);
+        }
       }
     }
   };
@@ -338,13 +351,14 @@ __host__ __device__ inline int glrd_pv_tg(int vt) {
 }
 __host__ __device__ inline int glrd_pv_lds(int tpw) { return G_NW * (16 * tpw * 16 + 2 * 16) * 4; }
 
-template <int TPW>
+template <int TPW, bool ROWS>
 __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArgs a, const float* scores, float* part,
                                                                  int n_ht, int n_splits2, int split_len2) {
+  static_assert(!ROWS || TPW % 2 == 0, "a ROWS wave loads its V tiles in 32-column pieces");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int n_groups = a.n_kv / a.hpg;
   const int QH = a.hpg * a.rep;
-  const int NB = a.S / BLK;
+  const int NB = (a.S + BLK - 1) / BLK;
   int L = blockIdx.x;
   const int split = L % n_splits2;
   L /= n_splits2;
@@ -375,13 +389,18 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
                      (long long)head_c * BLK + 8 * g;
   const long long blk_stride = (long long)QH * BLK;
   const int vw = a.gvw[grp];                              // the group's stream width
-  const __bf16* vbase = a.v + b * a.v_sb + a.gvo[grp] + (long long)(s_lo >> 5) * (32 * vw) + lane * 8;
+  const __bf16* vstream = a.v + b * a.v_sb + a.gvo[grp];
+  const __bf16* vbase = vstream + (long long)(s_lo >> 5) * (32 * vw) + lane * 8;
 
   struct Blk {
     float4 s[2];             // positions 8g .. 8g+7 of this lane's head
     bf16x8 v[TPW];
   };
-  // Loads of block j (past the split's data: its first block, unused; tiles past r_v: tile 0, unused).
+  // Loads of block j (past the split's data: its first block, unused; tiles past r_v: not loaded).
+  // TILED: x.v[i] is V tile tg * TPW + i of the block, the A operand of the PV product as it stands.
+  // ROWS: x.v[2 i2 + c] holds columns 32 (tg * TPW / 2 + i2) + 8 g .. +7 of position 8 (n / 4) + 4 c + n % 4
+  // (rows past the cache end clamped to its last row, masked below); the step regroups each pair into
+  // the two 16-column tiles of that 32-column piece.
   auto load = [&](int j, Blk& x) {
     const int jj = j < nblk ? j : 0;
     const float* p0 = sc0 + jj * blk_stride;
@@ -389,14 +408,40 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
     x.s[1] = *reinterpret_cast<const float4*>(p0 + 4);
     // The V latent is read once per decode step (one workgroup per row, group and split): nontemporal.
     // Tiles past the group's rank are not loaded (their products are skipped below).
+    if constexpr (ROWS) {
+      const int pb = s_lo + jj * BLK;
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      const int mt = tg * TPW + i;
-      if (mt < VT)
-        x.v[i] = __builtin_nontemporal_load(
-            reinterpret_cast<const bf16x8*>(vbase + (long long)jj * (32 * vw) + mt * 512));
+      for (int i2 = 0; i2 < TPW / 2; ++i2) {
+        const int piece = tg * (TPW / 2) + i2;
+        if (2 * piece < VT) {
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const int p = min(pb + 8 * (n >> 2) + 4 * c + (n & 3), a.S - 1);
+            const uint32_t off = (uint32_t)(p * vw + 32 * piece + 8 * g) * 2u;   // 32-bit byte offset
+            x.v[2 * i2 + c] = __builtin_nontemporal_load(
+                reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(vstream) + off));
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        const int mt = tg * TPW + i;
+        if (mt < VT)
+          x.v[i] = __builtin_nontemporal_load(
+              reinterpret_cast<const bf16x8*>(vbase + (long long)jj * (32 * vw) + mt * 512));
+      }
     }
   };
+  // ROWS: identity B operands; mfma16(row piece, idB[par]) moves 16 columns of a 32-column piece of
+  // 16 positions into the accumulator layout, exactly (products with 1 and 0 in fp32).
+  bf16x8 idB[ROWS ? 2 : 1];
+  if constexpr (ROWS) {
+#pragma unroll
+    for (int par = 0; par < 2; ++par)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) idB[par][e] = (8 * g + e == 16 * par + n) ? (__bf16)1.0f : (__bf16)0.0f;
+  }
 
   f32x4 O[TPW];
 #pragma unroll
@@ -434,11 +479,26 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       if (tg * TPW + i >= VT) continue;              // past the group's rank (uniform)
-      bf16x8 vA = x.v[i];
-      if constexpr (partial) {
+      bf16x8 vA;
+      if constexpr (ROWS) {
+        // positions 8 g .. 8 g + 3 (half-block 0) and 8 g + 4 .. + 7 (half-block 1) of column 16 (tg TPW + i) + n
+        f32x4 x0 = mfma16(x.v[2 * (i >> 1)], idB[i & 1], f32x4{0.f, 0.f, 0.f, 0.f});
+        f32x4 x1 = mfma16(x.v[2 * (i >> 1) + 1], idB[i & 1], f32x4{0.f, 0.f, 0.f, 0.f});
+        if constexpr (partial) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (base + 8 * g + e >= s_hi) vA[e] = (__bf16)0.0f;
+          for (int e = 0; e < 4; ++e) {
+            if (base + 8 * g + e >= s_hi) x0[e] = 0.f;
+            if (base + 8 * g + 4 + e >= s_hi) x1[e] = 0.f;
+          }
+        }
+        vA = pack8(x0, x1);
+      } else {
+        vA = x.v[i];
+        if constexpr (partial) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (base + 8 * g + e >= s_hi) vA[e] = (__bf16)0.0f;
+        }
       }
       O[i] = mfma16(vA, pB, O[i]);
     }
@@ -591,9 +651,9 @@ __global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, 
   }
 }
 
-template <int KBP, typename TabT>
+template <int KBP, typename TabT, bool ROWS>
 int launch_scores_full(const DecodeArgs& a, float* scores, int n_wg, hipStream_t stream) {
-  auto kern = palu_glrd_scores_full_kernel<KBP, TabT>;
+  auto kern = palu_glrd_scores_full_kernel<KBP, TabT, ROWS>;
   const int lds = G2Smem<KBP>::BYTES;
   static int attr_set = 0;
   if (attr_set < lds) {
@@ -605,17 +665,17 @@ int launch_scores_full(const DecodeArgs& a, float* scores, int n_wg, hipStream_t
   return PALU_OK;
 }
 
-template <typename TabT>
+template <typename TabT, bool ROWS>
 int scores_full_kb(const DecodeArgs& a, float* scores, int n_wg, hipStream_t s) {
   switch ((a.rk_eff / 32 + 1) / 2) {              // the launch's rank blocks rounded up to even
-    case 1: return launch_scores_full<2, TabT>(a, scores, n_wg, s);
-    case 2: return launch_scores_full<4, TabT>(a, scores, n_wg, s);
-    case 3: return launch_scores_full<6, TabT>(a, scores, n_wg, s);
-    case 4: return launch_scores_full<8, TabT>(a, scores, n_wg, s);
-    case 5: return launch_scores_full<10, TabT>(a, scores, n_wg, s);
-    case 6: return launch_scores_full<12, TabT>(a, scores, n_wg, s);
-    case 7: return launch_scores_full<14, TabT>(a, scores, n_wg, s);
-    case 8: return launch_scores_full<16, TabT>(a, scores, n_wg, s);
+    case 1: return launch_scores_full<2, TabT, ROWS>(a, scores, n_wg, s);
+    case 2: return launch_scores_full<4, TabT, ROWS>(a, scores, n_wg, s);
+    case 3: return launch_scores_full<6, TabT, ROWS>(a, scores, n_wg, s);
+    case 4: return launch_scores_full<8, TabT, ROWS>(a, scores, n_wg, s);
+    case 5: return launch_scores_full<10, TabT, ROWS>(a, scores, n_wg, s);
+    case 6: return launch_scores_full<12, TabT, ROWS>(a, scores, n_wg, s);
+    case 7: return launch_scores_full<14, TabT, ROWS>(a, scores, n_wg, s);
+    case 8: return launch_scores_full<16, TabT, ROWS>(a, scores, n_wg, s);
   }
   return fail(PALU_EUNSUPPORTED, "grouped-latent r_k %d (32 .. 512 in steps of 32)", a.rk_eff);
 }
@@ -631,10 +691,10 @@ int set_out_lds(K kern, int lds) {
   return PALU_OK;
 }
 
-template <int TPW>
+template <int TPW, bool ROWS>
 int launch_pv_t(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, hipStream_t s) {
   const int lds = glrd_pv_lds(TPW);
-  auto kern = palu_glrd_pv_kernel<TPW>;
+  auto kern = palu_glrd_pv_kernel<TPW, ROWS>;
   static int attr_set = 0;
   if (attr_set < lds) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -646,18 +706,33 @@ int launch_pv_t(const DecodeArgs& a, const float* scores, float* part, const Glr
   return PALU_OK;
 }
 
-int launch_pv(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, hipStream_t s) {
-  const int vt = a.rv >> 4;
+// V tiles per wave: the tile groups' share of the cache width's tiles; ROWS rounds it up to even (a
+// wave's tiles are whole 32-column pieces of the rows). The kernel derives the same tile groups.
+inline int glrd_pv_tpw(int rv, bool rows) {
+  const int vt = rv >> 4;
   const int tpw = (vt + glrd_pv_tg(vt) - 1) / glrd_pv_tg(vt);
-  switch (tpw) {
-    case 1: return launch_pv_t<1>(a, scores, part, p, s);
-    case 2: return launch_pv_t<2>(a, scores, part, p, s);
-    case 3: return launch_pv_t<3>(a, scores, part, p, s);
-    case 4: return launch_pv_t<4>(a, scores, part, p, s);
-    case 5: return launch_pv_t<5>(a, scores, part, p, s);
-    case 6: return launch_pv_t<6>(a, scores, part, p, s);
-    case 7: return launch_pv_t<7>(a, scores, part, p, s);
-    case 8: return launch_pv_t<8>(a, scores, part, p, s);
+  return rows ? (tpw + 1) & ~1 : tpw;
+}
+
+int launch_pv(const DecodeArgs& a, const float* scores, float* part, const GlrdPlan& p, bool rows, hipStream_t s) {
+  if (rows) {
+    switch (glrd_pv_tpw(a.rv, true)) {
+      case 2: return launch_pv_t<2, true>(a, scores, part, p, s);
+      case 4: return launch_pv_t<4, true>(a, scores, part, p, s);
+      case 6: return launch_pv_t<6, true>(a, scores, part, p, s);
+      case 8: return launch_pv_t<8, true>(a, scores, part, p, s);
+    }
+  } else {
+    switch (glrd_pv_tpw(a.rv, false)) {
+      case 1: return launch_pv_t<1, false>(a, scores, part, p, s);
+      case 2: return launch_pv_t<2, false>(a, scores, part, p, s);
+      case 3: return launch_pv_t<3, false>(a, scores, part, p, s);
+      case 4: return launch_pv_t<4, false>(a, scores, part, p, s);
+      case 5: return launch_pv_t<5, false>(a, scores, part, p, s);
+      case 6: return launch_pv_t<6, false>(a, scores, part, p, s);
+      case 7: return launch_pv_t<7, false>(a, scores, part, p, s);
+      case 8: return launch_pv_t<8, false>(a, scores, part, p, s);
+    }
   }
   return fail(PALU_EUNSUPPORTED, "grouped-latent r_v %d (32 .. 512 in steps of 32)", a.rv);
 }
@@ -672,7 +747,7 @@ size_t glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int seq_
   return (p.scores_floats + p.part_floats) * sizeof(float) + 256;
 }
 
-int dispatch_glrd(const DecodeArgs& a0, int cs_dtype, int out_dtype, hipStream_t s) {
+int dispatch_glrd(const DecodeArgs& a0, bool rows, int cs_dtype, int out_dtype, hipStream_t s) {
   DecodeArgs a = a0;
   const int n_groups = a.n_kv / a.hpg;
   if (a.hpg * a.rep > 128)
@@ -698,13 +773,15 @@ int dispatch_glrd(const DecodeArgs& a0, int cs_dtype, int out_dtype, hipStream_t
     ag.split_len = pf.split_len;
     ag.n_splits = pf.n_splits;
     const int n_wg = ((a.B * ag.grp_cnt * pf.n_splits + 7) / 8) * 8 * a.hpg;
-    const int rc = cs_dtype == PALU_DTYPE_F32 ? scores_full_kb<float>(ag, scores, n_wg, s)
-                                              : scores_full_kb<__bf16>(ag, scores, n_wg, s);
+    const int rc = rows ? (cs_dtype == PALU_DTYPE_F32 ? scores_full_kb<float, true>(ag, scores, n_wg, s)
+                                                     : scores_full_kb<__bf16, true>(ag, scores, n_wg, s))
+                        : (cs_dtype == PALU_DTYPE_F32 ? scores_full_kb<float, false>(ag, scores, n_wg, s)
+                                                     : scores_full_kb<__bf16, false>(ag, scores, n_wg, s));
     if (rc) return rc;
     e = hipGetLastError();
     if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent scores kernel launch: %s", hipGetErrorString(e));
   }
-  if (int rc2 = launch_pv(a, scores, part, p, s)) return rc2;
+  if (int rc2 = launch_pv(a, scores, part, p, rows, s)) return rc2;
   e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent PV kernel launch: %s", hipGetErrorString(e));
   const int out_lds = glrd_out_lds(a.rep, a.rv);

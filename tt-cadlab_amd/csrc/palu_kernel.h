@@ -188,7 +188,7 @@ int dispatch_latent_tiled_paged(const DecodeArgs& a, int rk, int rv, int cs_dtyp
 int dispatch_latent_tiled_k16(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
 int dispatch_latent_tiled_paged_k16(const DecodeArgs& a, int rk, int rv, int cs_dtype, int out_dtype, hipStream_t s);
 int dispatch_full(const DecodeArgs& a, bool tiled, bool paged, int dv, bool f32_out, hipStream_t s);
-int dispatch_glrd(const DecodeArgs& a, int cs_dtype, int out_dtype, hipStream_t s);
+int dispatch_glrd(const DecodeArgs& a, bool rows, int cs_dtype, int out_dtype, hipStream_t s);
 size_t glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int seq_len, int r_v);
 
 }  // namespace palu

@@ -15,7 +15,7 @@ from palu_tt._build import library_path
 PALU_OK, PALU_EINVAL, PALU_EUNSUPPORTED, PALU_EHIP = 0, 1, 2, 3
 DTYPE_F32, DTYPE_BF16 = 0, 1
 OUT_TILED_ROWS = 0x100      # PALU_OUT_TILED_ROWS, OR'ed into palu_sdpa_decode's out_dtype
-ABI_VERSION = 13
+ABI_VERSION = 14
 LAYOUT_ROWS, LAYOUT_TILED, LAYOUT_TILED_V, LAYOUT_TILED_GROUPED = 0, 1, 2, 3
 
 _vp, _i, _f, _sz, _ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_longlong

@@ -36,6 +36,20 @@ from palu_tt import decoder_ops, fused
 from palu_tt.cache import GroupedLatentCache, LatentCache
 
 
+def kernel_group_ranks(ranks_k, ranks_v, r_k: int, r_v: int):
+    """The per-group ranks a layer hands to the fused op and its compact caches: each group's rank from the
+    factor directory (config.json head_wise_ranks, any positive integer) rounded up to a multiple of 32,
+    capped at the layer's padded r_k / r_v, and the widest group at exactly r_k / r_v (so the compact
+    cache's logical width is the layer's). The factors are zero in the columns added (load_palu_dir pads
+    every group with zeros), so the products are unchanged; the grouped-latent kernels take group ranks
+    in multiples of 32."""
+    def fit(ranks, top):
+        out = [min(-(-int(r) // 32) * 32, top) for r in ranks]
+        out[max(range(len(out)), key=out.__getitem__)] = top
+        return out
+    return fit(ranks_k, int(r_k)), fit(ranks_v, int(r_v))
+
+
 class PaluAttention(torch.nn.Module):
     def __init__(self, mesh_device, tt_ccl, args, state_dict, weight_cache_path, layer_num, dtype=torch.bfloat16,
                  transformation_mats=None, configuration=None, paged_attention_config=None, use_paged_kv_cache=False,
@@ -76,9 +90,10 @@ class PaluAttention(torch.nn.Module):
         # attention.py:151); PaluRuntime() defaults to the naive path, as the reference's does
         self.use_fused_k = self.recon_k and bool(self.palu.runtime.use_fused_k)
         # grouped latents of unequal ranks (padded to rank_k / rank_v): the fused op reads only each
-        # group's own columns when it is given the groups' ranks
+        # group's own columns (rounded up to the kernels' multiple of 32) when it is given the groups' ranks
         gr = self.palu.group_ranks[layer_num] if self.palu.group_ranks else None
-        self.group_ranks = (list(gr[0]), list(gr[1])) if (gr is not None and self.gs > 1) else None
+        self.group_ranks = kernel_group_ranks(gr[0], gr[1], self.r_k, self.r_v) if (gr is not None and self.gs > 1) \
+            else None
         self.cache_layout = cache_layout
         self._naive_pos = {}
 
@@ -219,16 +234,17 @@ class PaluAttention(torch.nn.Module):
         rotated at pos -> [1, B, nh, out_width] bf16. Fused latent op, naive path, or stock decode over the
         cached rotated K, as the layer is configured. With tiled_rows the fused op answers in the tiled
         activation layout, [64, nh * out_width]; the other cores answer row-major regardless."""
+        det = bool(self.palu.runtime.deterministic)
         if self.use_fused_k:
             grouped = self.gs > 1
             return fused.palu_sdpa_decode(q4, keys, self.w_rot, self.cs_tab, values,
                                           self.head_dim if grouped else self.r_v, pos,
                                           u_v=self.u_v[None] if grouped else None, scale=self.scale,
                                           out_dtype=torch.bfloat16, group_ranks=self.group_ranks,
-                                          tiled_rows=tiled_rows)
+                                          tiled_rows=tiled_rows, deterministic=det)
         if self.recon_k:
             return self._naive_attention(q4, keys, values, pos)
-        return fused.flash_multi_latent_attention_decode(q4, keys, values, self.r_v, pos, scale=self.scale)
+        return fused.flash_decode(q4, keys, values, pos, scale=self.scale, head_dim_v=self.r_v, deterministic=det)
 
     def _recon_len(self) -> int:
         """Positions the naive path rebuilds: PaluRuntime.recon_len (the caller's bound on current_pos + 1)
@@ -271,7 +287,8 @@ class PaluAttention(torch.nn.Module):
             v = v_lat.contiguous()                                                         # absorbed V: [B, nkv, S, r_v]
         if v.shape[-1] % 32:   # V widths in 16s exist only as tiled caches (16-wide V tiles): hand both over tiled
             k_rot, v = LatentCache.from_rows(k_rot, "k"), LatentCache.from_rows(v, "v")
-        return fused.flash_multi_latent_attention_decode(q4, k_rot, v, self.out_width, pos, scale=self.scale)
+        return fused.flash_decode(q4, k_rot, v, pos, scale=self.scale, head_dim_v=self.out_width,
+                                  deterministic=bool(self.palu.runtime.deterministic))
 
     def forward_prefill(self, x, rot_mats=None, user_id=0, page_table=None, chunk_page_table=None,
                         chunk_start_idx=None, kv_cache=None):

@@ -46,7 +46,11 @@ class PaluRuntime:
     positions, then the stock flash-decode; reference attention.py:657-710); check makes the naive path
     verify that recon_len covers every row's position. The Tensix work-split switches (cs_recurrence,
     fused_k_chunk, group_heads_per_core, rot_mode, table_mcast) and latent_quant_in_prefill are accepted
-    and recorded: the MI355X kernels have one schedule and bf16 caches."""
+    and recorded: the MI355X kernels have one schedule and bf16 caches. deterministic (no counterpart in the
+    reference, whose op always sums in one order) fixes which wave of a decode workgroup sums which
+    32-position block, so repeated decodes are bit-identical; the default hands blocks out from a counter
+    (faster where rows differ in length; results differ between calls at the bf16 rounding of the
+    softmax probabilities)."""
     recon_len: Optional[int] = None
     check: bool = False
     use_fused_k: bool = False
@@ -56,6 +60,7 @@ class PaluRuntime:
     rot_mode: str = "dst"
     table_mcast: bool = True
     latent_quant_in_prefill: bool = True
+    deterministic: bool = False
 
 
 @dataclass

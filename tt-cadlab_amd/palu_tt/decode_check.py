@@ -11,15 +11,41 @@ wrote and reads nothing stale. Reported per step: the minimum over rows of the l
 the argmax agrees.
 
 A caller may add a third pass through its own attention core (``reference_core(layer, q4, keys, values,
-pos) -> [1, B, nh, out_width]``, e.g. fp32 attention over the same latent caches): both paths are then
-also compared with it, which separates a path's own error from the run-to-run spread of the model.
+pos) -> [1, B, nh, out_width]``; ``fp32_attention_core`` below is plain fp32 attention over the same
+latent caches): both paths are then also compared with it, which separates a path's own error from the
+run-to-run spread of the model.
 """
 import types
 from typing import Callable, Dict, Optional
 
 import torch
 
+from palu_tt import fused
 from palu_tt import model as pm
+
+
+def fp32_attention_core(layer, q4, keys, values, pos):
+    """A reference attention core for fused_vs_naive: plain fp32 torch attention over a PaluAttention
+    layer's own caches (K = latent @ u_k for the first recon_len positions, Meta RoPE, masked softmax, V
+    rebuilt with u_v for grouped latents or attended in latent space), rounded to bf16 like the cores it
+    stands beside. [1, B, nh, out_width]."""
+    S = layer._recon_len()
+    gs, nkv, nh, hd = layer.gs, layer.n_kv_heads, layer.n_heads, layer.head_dim
+    per_head = (lambda t: t) if gs == 1 else (lambda t: t.repeat_interleave(gs, dim=1))
+    if layer.recon_k:
+        K = per_head(layer._cache_rows(keys, S)).float() @ layer.u_k.float()                 # [B, nkv, S, hd]
+        K = fused.apply_rope_meta(K, layer.cos[:S][None, None], layer.sin[:S][None, None])
+    else:
+        K = layer._cache_rows(keys, S).float()                                                # rotated full K
+    V = layer._cache_rows(values, S).float()
+    if gs > 1:
+        V = per_head(V) @ layer.u_v.float()
+    B = q4.shape[1]
+    q = q4[0].float().view(B, nkv, nh // nkv, hd)
+    sc = (q @ K.transpose(-1, -2)) * layer.scale                                               # [B, nkv, rep, S]
+    masked = torch.arange(S, device=q.device)[None, :] > pos.long()[:, None]
+    sc = sc.masked_fill(masked[:, None, None, :], float("-inf"))
+    return (torch.softmax(sc, dim=-1) @ V).reshape(1, B, nh, -1).to(torch.bfloat16)
 
 
 def _pcc_rows(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:

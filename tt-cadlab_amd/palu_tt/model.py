@@ -89,6 +89,12 @@ class Transformer(torch.nn.Module):
             L["w13"].in_scale_folded and L["attn"].wo_out.tiled and L["attn"].wo_out.ks == 1 for L in self.layers)
         self._graph = None
 
+    def set_deterministic(self, deterministic: bool) -> None:
+        """PaluRuntime.deterministic for every layer (a fixed block order in the decode kernels, so repeated
+        decodes are bit-identical); a captured decode graph is dropped."""
+        self.args.palu.runtime.deterministic = bool(deterministic)
+        self._graph = None
+
     def set_fused_k(self, use_fused_k: bool, recon_len: Optional[int] = None) -> None:
         """Switches every layer between the fused latent decode and the naive path (PaluRuntime.use_fused_k,
         recon_len), as the reference selects per built model; a captured decode graph is dropped."""
@@ -246,11 +252,17 @@ def prefill_all(model: Transformer, prompts: torch.Tensor, users_per_chunk: int 
 
 
 @torch.no_grad()
-def generate(model: Transformer, prompts: torch.Tensor, n_new: int, use_graph: bool = True):
+def generate(model: Transformer, prompts: torch.Tensor, n_new: int, use_graph: bool = True,
+             deterministic: Optional[bool] = None):
     """Greedy decode (reference generate.py:53-62): prefill every row's prompt, then n_new steps of
-    argmax sampling. prompts [B, S] with B == max_batch_size. Returns the generated ids [B, n_new]."""
+    argmax sampling. prompts [B, S] with B == max_batch_size. Returns the generated ids [B, n_new].
+    deterministic (PaluRuntime.deterministic when given) fixes the decode kernels' block order so that
+    the same prompts give the same ids on every run; by default the order is dynamic and a random-init
+    model's near-tied logits can pick different ids from run to run."""
     B, S = prompts.shape
     assert B == model.args.max_batch_size and S + n_new <= model.args.max_seq_len
+    if deterministic is not None:
+        model.set_deterministic(deterministic)
     tok = prefill_all(model, prompts).argmax(-1)
     out = [tok]
     pos = torch.full((B,), S, dtype=torch.int32, device=model.device)
