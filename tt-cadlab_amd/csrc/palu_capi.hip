@@ -343,7 +343,8 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
 
 int sdpa_dispatch(const DecodeArgs& a, bool paged, int cache_layout, int r_k, int r_v, int cs_dtype, int out_dtype,
                   hipStream_t stream) {
-  const bool tiled = cache_layout == PALU_LAYOUT_TILED;
+  // compact grouped caches use the tiled orders (sdpa_setup records them as grouped_streams)
+  const bool tiled = cache_layout == PALU_LAYOUT_TILED || cache_layout == PALU_LAYOUT_TILED_GROUPED;
   if (a.u_v != nullptr) {
     if (paged) return fail(PALU_EUNSUPPORTED, "u_v: the in-kernel V rebuild is not built for paged caches");
     // Each group's stream: padded caches (tiled, or the reference's row-major [B, n_groups, S, r]) hold
