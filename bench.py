@@ -246,7 +246,8 @@ def measure_glrd(dev, steps, warmup):
     q = (torch.randn(1, B, NQ, HD, generator=g) * 1.3).to(dev, torch.bfloat16)
     cur = torch.full((B,), S - 1, dtype=torch.int32, device=dev)
     res = []
-    for r_k, r_v, note in ((max(drawn_k), max(drawn_v), "drawn"), (512, 512, "widest")):
+    for r_k, r_v, note in ((max(drawn_k), max(drawn_v), "drawn"), (512, 512, "widest"),
+                           (max(drawn_k), max(drawn_v), "drawn_rows")):
         n_layers = 2
         gd = torch.Generator(device=dev).manual_seed(r_k + r_v)
         layers = []
@@ -254,17 +255,23 @@ def measure_glrd(dev, steps, warmup):
             if note == "drawn":
                 k = GroupedLatentCache.zeros(B, drawn_k, S, dev, "k")
                 v = GroupedLatentCache.zeros(B, drawn_v, S, dev, "v")
+                k.data.normal_(generator=gd)
+                v.data.normal_(generator=gd)
+            elif note == "drawn_rows":
+                # the reference's layout: row-major [B, n_groups, S, r] padded to the widest group
+                k = torch.randn(B, ng, S, r_k, device=dev, generator=gd).to(torch.bfloat16)
+                v = torch.randn(B, ng, S, r_v, device=dev, generator=gd).to(torch.bfloat16)
             else:
                 k = LatentCache.zeros(B, ng, S, r_k, dev, "k")
                 v = LatentCache.zeros(B, ng, S, r_v, dev, "v")
-            k.data.normal_(generator=gd)
-            v.data.normal_(generator=gd)
+                k.data.normal_(generator=gd)
+                v.data.normal_(generator=gd)
             layers.append((k, v))
         u_k = torch.randn(NKV, r_k, HD, generator=g) / r_k ** 0.5
         u_v = torch.randn(NKV, r_v, HD, generator=g) / r_v ** 0.5
         # the drawn layer: each group's latents at its own ranks (compact caches), the narrower group
         # zero-padded in the factors (as load_palu_dir pads it); the op reads only each group's columns
-        group_ranks = (drawn_k, drawn_v) if note == "drawn" else None
+        group_ranks = (drawn_k, drawn_v) if note != "widest" else None
         if group_ranks is not None:
             for gi in range(ng):
                 u_k[hpg * gi:hpg * (gi + 1), drawn_k[gi]:] = 0
@@ -283,13 +290,17 @@ def measure_glrd(dev, steps, warmup):
         wall, kern, _ = time_calls(step, n_layers, steps, warmup)
         # algorithmic work counts each group at its own ranks (the drawn layer's narrower group is
         # zero-padded to the layer width in the cache; those padding bytes are not algorithmic)
-        gk, gv = (drawn_k, drawn_v) if note == "drawn" else ([r_k] * ng, [r_v] * ng)
+        gk, gv = (drawn_k, drawn_v) if note != "widest" else ([r_k] * ng, [r_v] * ng)
+        cache_bytes = sum(x.nbytes() if hasattr(x, "nbytes") and callable(x.nbytes) else x.numel() * x.element_size()
+                          for x in layers[0])
         nbytes = B * S * (sum(gk) + sum(gv)) * 2
         flops = sum(2 * B * hpg * S * rk_g * HD + 2 * B * hpg * NQ // NKV * S * (HD + rv_g) +
                     2 * B * hpg * NQ // NKV * rv_g * HD for rk_g, rv_g in zip(gk, gv))
         res.append({"ranks": note, "rank_k": r_k, "rank_v": r_v, "group_ranks": {"k": gk, "v": gv},
                     "us_per_layer": round(wall * 1e3, 2), "kernel_us": round(kern * 1e3, 2),
-                    "cache_bytes": layers[0][0].nbytes() + layers[0][1].nbytes(), **_roof(nbytes, flops, kern)})
+                    "cache_layout": {"drawn": "compact tiled groups", "widest": "tiled",
+                                     "drawn_rows": "row-major, padded to the widest group"}[note],
+                    "cache_bytes": cache_bytes, **_roof(nbytes, flops, kern)})
         del layers
         torch.cuda.empty_cache()
     kv = [(LatentCache.zeros(B, NKV, S, HD, dev, "k"), LatentCache.zeros(B, NKV, S, HD, dev, "v")) for _ in range(2)]
@@ -303,8 +314,8 @@ def measure_glrd(dev, steps, warmup):
                                                                 workspace=ws_s), 2, steps, warmup)
     del kv
     torch.cuda.empty_cache()
-    return {"workload": "G-LRD group size 4 (2 groups x 4 KV heads), batch 16, ctx 16384, tiled bf16, V rebuilt "
-                        "per head in-kernel", "drawn_group_ranks": {"k": drawn_k, "v": drawn_v}, "layers": res,
+    return {"workload": "G-LRD group size 4 (2 groups x 4 KV heads), batch 16, ctx 16384, bf16, V rebuilt per head "
+                        "in-kernel", "drawn_group_ranks": {"k": drawn_k, "v": drawn_v}, "layers": res,
             "stock_full_kv": {"us_per_layer": round(s_wall * 1e3, 2), "kernel_us": round(s_kern * 1e3, 2)}}
 
 
@@ -515,8 +526,11 @@ def main():
         if wl.get("layers") is not None:
             wl["layers"] = None
             torch.cuda.empty_cache()
-        res["paged_mixed_ranks"] = measure_paged(dev, max(a.steps // 4, 10), max(a.warmup // 4, 5))
-        res["glrd"] = measure_glrd(dev, max(a.steps // 8, 10), max(a.warmup // 8, 3))
+        # the extra lines take their own minimum counts (about 20-60 ms of GPU time each): a handful of
+        # calls after 3-5 warm-ups reads the clocks and caches still ramping (the G-LRD widest layer timed
+        # 402 us at 10 calls after 3 warm-ups against 366 us at steady state on one box)
+        res["paged_mixed_ranks"] = measure_paged(dev, max(a.steps // 4, 100), max(a.warmup // 4, 30))
+        res["glrd"] = measure_glrd(dev, max(a.steps // 8, 60), max(a.warmup // 8, 20))
     if not a.no_e2e:
         if wl.get("layers") is not None:
             wl["layers"] = None
