@@ -16,7 +16,7 @@
 //      split the V tiles and the blocks of the split, run the online softmax (exp2 domain, lazy
 //      rescale) and accumulate O_lat^T = V_lat^T P^T for their V tiles, streamed from HBM two blocks
 //      ahead. Partials (O_lat, m, l) per head and split go to the workspace.
-//   3. Merge and V rebuild. One workgroup per (row, KV head): log-sum-exp merge of the splits, then
+//   3. Merge and V rebuild. One workgroup per (row, KV head, query head): log-sum-exp merge of the splits, then
 //      out = O_lat u_v[h] / l in fp32 -- the same sum as softmax(q K^T) (V_lat u_v[h]), V never built.
 // The K latent of a group is read by heads_per_group scores workgroups; they are numbered so they land
 // on one XCD (the dispatcher deals consecutive workgroup ids round-robin over the 8 XCDs) and meet in
@@ -417,9 +417,10 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
             const int p = min(pb + 8 * (n >> 2) + 4 * c + (n & 3), a.S - 1);
+            // cached: the 64-byte piece is half a 128-byte line whose other half another tile group
+            // reads (a nontemporal read would fetch the line twice)
             const uint32_t off = (uint32_t)(p * vw + 32 * piece + 8 * g) * 2u;   // 32-bit byte offset
-            x.v[2 * i2 + c] = __builtin_nontemporal_load(
-                reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(vstream) + off));
+            x.v[2 * i2 + c] = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(vstream) + off);
           }
         }
       }
@@ -557,97 +558,80 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
 }
 
 // ---------------------------------------------------------------------------------------------------
-// Pass 3: merge the splits of every query head of one (row, KV head) and apply u_v. The split weights
-// 2^(m_s - M) are computed once per head, each latent column of O_lat is merged once (a dot product over
-// independent loads), and the projection reads u_v in 16-byte pieces: thread (head group of 4, rank
-// slice, 8 output dims) accumulates 4 x 8 outputs over its slice; the slices are summed through LDS.
+// Pass 3: merge the splits of one query head of one (row, KV head) and apply u_v; one workgroup per
+// (row, KV head, query head), so the launch has B * n_kv * rep workgroups (512 at the benchmark's
+// shapes) instead of one per (row, KV head). The split weights 2^(m_s - M) are computed once, each latent
+// column of O_lat is merged once (a dot product over independent loads), and the projection reads u_v
+// in 16-byte pieces: thread (rank slice, 8 output dims) accumulates 8 outputs over its slice; the 16
+// slices are summed through LDS.
 constexpr int G_MAX_SPLITS2 = 128;      // split partials per head the merge workgroup stages
 
-// Dynamic LDS: red [16 rank slices][4 heads][HD], olat [rep][rv], wsplit [rep][G_MAX_SPLITS2], lsum [16].
-__host__ __device__ inline int glrd_out_lds(int rep, int rv) { return (16 * 4 * HD + rep * rv + rep * G_MAX_SPLITS2 + 16) * 4; }
+// Dynamic LDS: red [16 rank slices][HD], olat [rv], wsplit [G_MAX_SPLITS2], lsum.
+__host__ __device__ inline int glrd_out_lds(int rv) { return (16 * HD + rv + G_MAX_SPLITS2 + 4) * 4; }
 
 template <typename OutT>
 __global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, const float* part, int n_splits2) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int rep = a.rep;
-  const int item = blockIdx.x;
+  const int item = blockIdx.x, h = blockIdx.y;        // query head h of the item's KV head
   const int b = item / a.n_kv, kvh = item - b * a.n_kv;
   const int rv = a.grv[kvh / a.hpg];                  // the group's rank: partial columns past it are unset
   float* red = reinterpret_cast<float*>(smem);
-  float* olat = red + 16 * 4 * HD;
-  float* wsplit = olat + rep * a.rv;
-  float* lsum = wsplit + rep * G_MAX_SPLITS2;
+  float* olat = red + 16 * HD;
+  float* wsplit = olat + a.rv;
+  float* lsum = wsplit + G_MAX_SPLITS2;
   const int stride = a.rv + G_PSTRIDE_PAD;
   const int tid = threadIdx.x;
-  const float* p0 = part + (long long)(b * a.n_q + kvh * rep) * n_splits2 * stride;
-  // split weights: wsplit[h][s] = 2^(m_s - M_h); lsum[h] = sum_s l_s 2^(m_s - M_h). Wave w handles heads
-  // w, w + 4, ...; its lanes take the splits in turn.
-  {
-    const int w = tid >> 6, lane = tid & 63;
-    for (int h = w; h < rep; h += 4) {
-      const float* ph = p0 + (long long)h * n_splits2 * stride;
-      float M = NEG_INF;
-      for (int s = lane; s < n_splits2; s += 64) M = fmaxf(M, ph[(long long)s * stride + a.rv]);
+  const float* ph = part + (long long)(b * a.n_q + kvh * a.rep + h) * n_splits2 * stride;
+  // split weights: wsplit[s] = 2^(m_s - M); lsum = sum_s l_s 2^(m_s - M). The first wave's lanes take
+  // the splits in turn.
+  if (tid < 64) {
+    const int lane = tid;
+    float M = NEG_INF;
+    for (int s = lane; s < n_splits2; s += 64) M = fmaxf(M, ph[(long long)s * stride + a.rv]);
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-      float Ls = 0.f;
-      for (int s = lane; s < n_splits2; s += 64) {
-        const float f = (M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(ph[(long long)s * stride + a.rv] - M);
-        wsplit[h * G_MAX_SPLITS2 + s] = f;
-        Ls += ph[(long long)s * stride + a.rv + 1] * f;
-      }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) Ls += __shfl_xor(Ls, o, 64);
-      if (lane == 0) lsum[h] = Ls;
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    float Ls = 0.f;
+    for (int s = lane; s < n_splits2; s += 64) {
+      const float f = (M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(ph[(long long)s * stride + a.rv] - M);
+      wsplit[s] = f;
+      Ls += ph[(long long)s * stride + a.rv + 1] * f;
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) Ls += __shfl_xor(Ls, o, 64);
+    if (lane == 0) lsum[0] = Ls;
   }
   __syncthreads();
-  for (int e = tid; e < rep * rv; e += 256) {
-    const int h = e / rv, r = e - h * rv;
-    const float* pr = p0 + (long long)h * n_splits2 * stride + r;
-    const float* wh = wsplit + h * G_MAX_SPLITS2;
+  for (int r = tid; r < rv; r += 256) {
+    const float* pr = ph + r;
     float acc = 0.f;
 #pragma unroll 8
-    for (int s = 0; s < n_splits2; ++s) acc += pr[(long long)s * stride] * wh[s];
-    olat[h * rv + r] = acc;
+    for (int s = 0; s < n_splits2; ++s) acc += pr[(long long)s * stride] * wsplit[s];
+    olat[r] = acc;
   }
   __syncthreads();
   const int dg = tid & 15, rs = tid >> 4;             // 8 output dims, one of 16 rank slices
   const int per = rv / 16;                              // rv is a multiple of 32
   const __bf16* uv = a.u_v + (long long)kvh * a.rv * HD + 8 * dg;
-  for (int hg = 0; hg < rep; hg += 4) {                 // heads hg .. hg + 3 of this KV head
-    float acc[4][8];
+  float acc[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+#pragma unroll 8                                        // 8 u_v rows in flight
+  for (int r = rs * per; r < rs * per + per; ++r) {
+    const bf16x8 u = *reinterpret_cast<const bf16x8*>(uv + (long long)r * HD);
+    const float o = olat[r];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
-#pragma unroll 8                                      // 8 u_v rows in flight (unroll 4: 14.5 us, 16: 13.8)
-    for (int r = rs * per; r < rs * per + per; ++r) {
-      const bf16x8 u = *reinterpret_cast<const bf16x8*>(uv + (long long)r * HD);
+    for (int j = 0; j < 8; ++j) acc[j] += o * (float)u[j];
+  }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float o = (hg + i < rep) ? olat[(hg + i) * rv + r] : 0.f;
+  for (int j = 0; j < 8; ++j) red[rs * HD + 8 * dg + j] = acc[j];
+  __syncthreads();
+  if (tid < HD) {
+    float sum = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] += o * (float)u[j];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) red[(rs * 4 + i) * HD + 8 * dg + j] = acc[i][j];
-    __syncthreads();
-    for (int e = tid; e < 4 * HD; e += 256) {
-      const int i = e / HD, d = e - i * HD, h = hg + i;
-      if (h < rep) {
-        float sum = 0.f;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) sum += red[(q * 4 + i) * HD + d];
-        const float Ls = lsum[h];
-        OutT* o = static_cast<OutT*>(a.out) + out_index(a, b, ((long long)kvh * rep + h) * HD + d, (long long)a.n_q * HD);
-        store_out(o, Ls > 0.f ? sum / Ls : 0.f);
-      }
-    }
-    __syncthreads();
+    for (int q = 0; q < 16; ++q) sum += red[q * HD + tid];
+    const float Ls = lsum[0];
+    OutT* o = static_cast<OutT*>(a.out) + out_index(a, b, ((long long)kvh * a.rep + h) * HD + tid, (long long)a.n_q * HD);
+    store_out(o, Ls > 0.f ? sum / Ls : 0.f);
   }
 }
 
@@ -784,13 +768,14 @@ int dispatch_glrd(const DecodeArgs& a0, bool rows, int cs_dtype, int out_dtype, 
   if (int rc2 = launch_pv(a, scores, part, p, rows, s)) return rc2;
   e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent PV kernel launch: %s", hipGetErrorString(e));
-  const int out_lds = glrd_out_lds(a.rep, a.rv);
+  const int out_lds = glrd_out_lds(a.rv);
+  const dim3 out_grid((unsigned)(a.B * a.n_kv), (unsigned)a.rep);
   if (out_dtype == PALU_DTYPE_F32) {
     if (int rc3 = set_out_lds(palu_glrd_out_kernel<float>, out_lds)) return rc3;
-    hipLaunchKernelGGL(palu_glrd_out_kernel<float>, dim3(a.B * a.n_kv), dim3(256), out_lds, s, a, part, p.n_splits2);
+    hipLaunchKernelGGL(palu_glrd_out_kernel<float>, out_grid, dim3(256), out_lds, s, a, part, p.n_splits2);
   } else {
     if (int rc3 = set_out_lds(palu_glrd_out_kernel<__bf16>, out_lds)) return rc3;
-    hipLaunchKernelGGL(palu_glrd_out_kernel<__bf16>, dim3(a.B * a.n_kv), dim3(256), out_lds, s, a, part, p.n_splits2);
+    hipLaunchKernelGGL(palu_glrd_out_kernel<__bf16>, out_grid, dim3(256), out_lds, s, a, part, p.n_splits2);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent output kernel launch: %s", hipGetErrorString(e));
