@@ -131,3 +131,25 @@ def test_generate_greedy_is_consistent_with_decode(gpu):
         assert torch.all((logits.argmax(-1) == out[:, t]) | close), f"step {t}"
         if t < 5:
             logits = m2.decode(out[:, t], torch.full((3,), 33 + t, dtype=torch.int32, device=gpu))
+
+
+def test_deterministic_decode_is_bit_reproducible(gpu):
+    """PaluRuntime.deterministic (Transformer.set_deterministic, generate(..., deterministic=True)) fixes the
+    decode kernels' block order: the same decode step repeated from the same state gives the same logits
+    bit for bit, eager and from the HIP graph, and greedy generation gives the same ids on every run."""
+    args = pm.ModelArgs(dim=512, n_layers=2, n_heads=8, n_kv_heads=2, vocab_size=640, ffn_dim=1024,
+                        max_seq_len=640, max_batch_size=4)
+    model = pm.Transformer(args, pm.random_palu_state_dict(args, [64, 96], [48, 64], gpu, seed=21, std=0.1), gpu)
+    model.set_deterministic(True)
+    prompts = torch.randint(0, args.vocab_size, (4, 500), generator=torch.Generator().manual_seed(22)).to(gpu)
+    first = pm.prefill_all(model, prompts).argmax(-1)
+    pos = torch.full((4,), 500, dtype=torch.int32, device=gpu)
+    a = model.decode(first, pos).clone()          # the step rewrites the same cache position each time
+    b = model.decode(first, pos).clone()
+    c = model.decode_graph(first, pos).clone()
+    d = model.decode_graph(first, pos).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(c, d) and torch.equal(a, c)
+    g1 = pm.generate(model, prompts, n_new=8, deterministic=True)
+    g2 = pm.generate(model, prompts, n_new=8, deterministic=True)
+    assert torch.equal(g1, g2)
