@@ -77,7 +77,7 @@ def _close(out, exp, what):
 @pytest.mark.parametrize("r_k,r_v,gs,layout,fused,recon_len", [
     (64, 64, 1, "tiled", True, None), (64, 64, 1, "rows", True, None), (32, 96, 1, "tiled", True, None),
     (HD, 64, 1, "tiled", True, None), (32, HD, 1, "tiled", True, None), (HD, HD, 1, "rows", True, None),
-    (192, 256, 2, "tiled", True, None),
+    (192, 256, 2, "tiled", True, None), (192, 256, 2, "rows", True, None),
     (64, 64, 1, "tiled", False, None), (32, 96, 1, "rows", False, 50), (192, 256, 2, "tiled", False, None),
     (32, HD, 1, "tiled", False, 64)])
 def test_attention_prefill_then_decode_matches_layer_oracle(gpu, r_k, r_v, gs, layout, fused, recon_len):

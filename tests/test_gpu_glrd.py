@@ -106,6 +106,21 @@ def test_glrd_bf16_output_and_table(gpu):
     _check(_run(gpu, *args, 512, cs_dtype=torch.bfloat16), exp, max_abs=5e-2, cos=0.999)
 
 
+def test_glrd_row_major_bf16_output_and_table(gpu):
+    """The reference's row-major call with a bf16 output and a bf16 [cos | sin] table."""
+    args = _case(4, 512, 192, 192, hpg=4, seed=98)
+    exp = _oracle(*args, 512)
+    _check(_run_rows(gpu, *args, 512, out_dtype=torch.bfloat16), exp)
+    cos, sin = fused.cos_sin_tables(HD, 512, THETA, LLAMA3)
+    q, k, v, u_k, u_v, pos = args
+    out = fused.palu_sdpa_decode(
+        q.to(gpu, torch.bfloat16), k.to(gpu, torch.bfloat16), fused.w_rot_from_u_k(u_k).to(gpu, torch.bfloat16)[None],
+        fused.cs_table(cos, sin, 512)[None, None].to(gpu, torch.bfloat16), v.to(gpu, torch.bfloat16), HD,
+        pos.to(gpu, torch.int32), u_v=u_v.to(gpu, torch.bfloat16)[None], scale=HD ** -0.5, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _check(out.cpu(), exp, max_abs=5e-2, cos=0.999)
+
+
 def test_glrd_reference_head_shape(gpu):
     """The reference op tests' per-chip shape: 16 Q / 4 KV heads, one group of 4."""
     args = _case(8, 1024, 256, 384, hpg=4, seed=5, nh=16, nkv=4)
