@@ -107,8 +107,8 @@ size_t palu_glrd_workspace_bytes(int batch, int n_q, int n_kv, int n_groups, int
  *                                    r_k and r_v in 32 .. 512 (multiples of 32), caches in
  *                                    PALU_LAYOUT_ROWS (the reference's [B, n_groups, S, r] call,
  *                                    tests/test_palu_sdpa_device.py:245-258), PALU_LAYOUT_TILED or
- *                                    PALU_LAYOUT_TILED_GROUPED; not built for the paged entry point
- *                                    (PALU_EUNSUPPORTED)
+ *                                    PALU_LAYOUT_TILED_GROUPED; at most 32 latent groups; not built
+ *                                    for the paged entry point (PALU_EUNSUPPORTED)
  *   group_ranks [2 * n_groups] int32 (host memory, may be NULL)
  *                                    with u_v: each latent group's own ranks, K ranks then V ranks,
  *                                    multiples of 32 up to r_k / r_v. The caches keep r_k / r_v columns
@@ -228,7 +228,7 @@ int palu_latent_append_strided(void* cache, const void* src, long long src_batch
  * row b (offsets as that layout says, widths[g] wide: host memory, multiples of 16 up to 512) gets at
  * position update_idxs[b] the first widths[g] values of src[b * src_batch_stride + g * src_group_stride
  * ..], in K-tile (order = PALU_LAYOUT_TILED) or V-tile order (PALU_LAYOUT_TILED_V). seq_len a multiple of
- * 32, at most 16 groups. No counterpart in the reference (its caches are padded to the widest group). */
+ * 32, at most 32 groups. No counterpart in the reference (its caches are padded to the widest group). */
 int palu_latent_append_grouped(void* cache, const void* src, long long src_batch_stride, long long src_group_stride,
                                const int32_t* update_idxs, int batch, int n_groups, int seq_len, const int32_t* widths,
                                int order, palu_stream_t stream);

@@ -354,3 +354,33 @@ def test_glrd_compact_caches_at_the_benchmark_shape(gpu):
     assert torch.equal(compact, rows_out)
     rows = [0, 7, 15]
     _check(compact[:, rows], _oracle(q[:, rows], k[rows], v[rows], u_k, u_v, pos[rows], S))
+
+
+def test_glrd_32_groups_of_unequal_ranks(gpu):
+    """Per-head latents with u_v at 32 KV heads (32 latent groups, the most the grouped-latent kernels
+    take), each group at its own drawn K and V ranks in compact caches: the PV pass deals its splits over
+    32 groups of different widths and the group tables are full. Against the oracle, and bit for bit
+    against row-major caches padded to the widest group."""
+    B, S, nkv = 3, 768, 32
+    g = torch.Generator().manual_seed(3232)
+    ranks_k = [int(x) * 32 for x in torch.randint(1, 5, (nkv,), generator=g)]
+    ranks_v = [int(x) * 32 for x in torch.randint(1, 5, (nkv,), generator=g)]
+    ranks_k[0], ranks_v[1] = 128, 128
+    q, k, v, u_k, u_v, pos = _case(B, S, max(ranks_k), max(ranks_v), hpg=1, seed=3233, nh=32, nkv=nkv)
+    for gi, (rk, rv) in enumerate(zip(ranks_k, ranks_v)):
+        k[:, gi, :, rk:] = 0
+        v[:, gi, :, rv:] = 0
+        u_k[gi, rk:] = 0
+        u_v[gi, rv:] = 0
+    gk = GroupedLatentCache.from_rows(k.to(gpu, torch.bfloat16), ranks_k, "k")
+    gv = GroupedLatentCache.from_rows(v.to(gpu, torch.bfloat16), ranks_v, "v")
+    cos, sin = fused.cos_sin_tables(HD, S, THETA, LLAMA3)
+    compact = fused.palu_sdpa_decode(
+        q.to(gpu, torch.bfloat16), gk, fused.w_rot_from_u_k(u_k).to(gpu, torch.bfloat16)[None],
+        fused.cs_table(cos, sin, S)[None, None].to(gpu), gv, HD, pos.to(gpu, torch.int32),
+        u_v=u_v.to(gpu, torch.bfloat16)[None], scale=HD ** -0.5, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    compact = compact.float().cpu()
+    rows = _run_rows(gpu, q, k, v, u_k, u_v, pos, S, group_ranks=(ranks_k, ranks_v))
+    assert torch.equal(compact, rows)
+    _check(compact, _oracle(q, k, v, u_k, u_v, pos, S))

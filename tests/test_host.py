@@ -376,8 +376,8 @@ def test_flash_decode_and_append_envelope_errors(lib):
     widths = (ctypes.c_int32 * 2)(64, 32)
     rc = lib.palu_latent_append_grouped(_FAKE, _FAKE, 256, 128, _FAKE, 2, 2, 256, widths, 0, None)
     assert rc == _native.PALU_EINVAL and "order must be" in lib.palu_last_error().decode()
-    rc = lib.palu_latent_append_grouped(_FAKE, _FAKE, 256, 128, _FAKE, 2, 17, 256, widths, 1, None)
-    assert rc == _native.PALU_EINVAL and "1..16 groups" in lib.palu_last_error().decode()
+    rc = lib.palu_latent_append_grouped(_FAKE, _FAKE, 256, 128, _FAKE, 2, 33, 256, widths, 1, None)
+    assert rc == _native.PALU_EINVAL and "1..32 groups" in lib.palu_last_error().decode()
 
 
 def test_fused_projection_plans_and_envelope_errors(lib):
@@ -451,6 +451,11 @@ def test_glrd_envelope_errors(lib):
     assert rc == _native.PALU_EINVAL and "head_dim_v" in msg
     rc, msg = _sdpa(lib, u_v=_FAKE, head_dim_v=128, r_k=544, layout=1)
     assert rc == _native.PALU_EINVAL and "r_k" in msg
+    # per-head latents with u_v: 32 groups are taken (they stop at the workspace), 64 are not
+    rc, msg = _sdpa(lib, u_v=_FAKE, head_dim_v=128, n_q=64, n_kv=32, n_groups=32, layout=1)
+    assert rc == _native.PALU_EINVAL and "palu_glrd_workspace_bytes" in msg
+    rc, msg = _sdpa(lib, u_v=_FAKE, head_dim_v=128, n_q=64, n_kv=64, n_groups=64, layout=1)
+    assert rc == _native.PALU_EUNSUPPORTED and "64 latent groups" in msg
     rc = lib.palu_sdpa_decode_paged(_FAKE, _FAKE, _FAKE, _FAKE, _FAKE, 128, _FAKE, _FAKE, _FAKE, None, None, _FAKE,
                                     0.088, 0, 2, 1, 0, 2, 16, 4, 1, 16, 64, 4, 256, 256, 256, 256, 256, 0, 1, 1, 0,
                                     None, 0, None)

@@ -282,6 +282,9 @@ int sdpa_setup(DecodeArgs& a, const void* q, const void* k_latent, const void* w
   }
   if (u_v != nullptr) {
     if (head_dim_v != HD) return fail(PALU_EINVAL, "head_dim_v must be %d when u_v rebuilds V in-kernel, got %d", HD, head_dim_v);
+    if (n_groups > MAX_GROUPS)
+      return fail(PALU_EUNSUPPORTED, "u_v: %d latent groups (the grouped-latent kernels take up to %d)", n_groups,
+                  MAX_GROUPS);
     if (!aligned16(u_v)) return fail(PALU_EINVAL, "u_v must be 16-byte aligned");
   } else {
     if (hpg != 1) return fail(PALU_EINVAL, "grouped V latent (heads_per_group %d) needs u_v", hpg);

@@ -25,9 +25,26 @@
 
 namespace {
 
+// Lane K of the caller's row of 16 lanes, for every lane of the row (DPP row_newbcast:K).
+template <int K>
+__device__ __forceinline__ float row_bcast(float v) {
+  static_assert(K >= 0 && K < 16, "row lane");
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + K, 0xF, 0xF, false));
+}
+
+// f(std::integral_constant<int, I>) for I = B .. E - 1, unrolled at compile time.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 constexpr int G_NW = 8;                 // waves per workgroup (PV kernel)
-constexpr int G_QS = HD + 8;            // padded query row (bf16), spreads the 16 rows over the banks
+constexpr int G_QS = HD + 4;            // padded query row (fp32) of the scores kernel's LDS copy
 constexpr int G_PSTRIDE_PAD = 4;        // partial row: r_v values, m, l, 2 pad (16-byte rows)
+constexpr int G_MAX_SPLITS2 = 128;      // PV splits per group (the merge workgroup stages their weights)
 
 inline int glrd_pv_splits(int items2, int nb) {
   // About 256 PV workgroups, at least 4 blocks each, at most 128 splits.
@@ -42,6 +59,8 @@ struct GlrdPlan {
   size_t scores_floats, part_floats;
 };
 
+// Workspace sizing: the PV pass's split partials are counted as if every group had n_splits2 splits
+// (the per-group plan below hands out the same total).
 inline GlrdPlan glrd_plan(int B, int n_q, int n_kv, int n_groups, int S, int rv) {
   GlrdPlan p;
   (void)n_kv;
@@ -57,6 +76,51 @@ inline GlrdPlan glrd_plan(int B, int n_q, int n_kv, int n_groups, int S, int rv)
   return p;
 }
 
+__host__ __device__ inline int glrd_pv_tg_group(int vt_g, int tpw);
+
+// The PV pass's splits per group. A group of lower V rank covers its tiles with fewer tile groups and
+// walks its blocks with more position groups, so it finishes a split sooner: the n_groups * n_splits2
+// splits of the uniform plan are dealt out in proportion to each group's time per position (tile groups
+// x (V tiles of its busiest wave + 2 for the scores and the softmax)), largest remaining share first, so
+// one chip-fill of workgroups ends together. Equal ranks keep the uniform plan. Fills a.gns2 / gsl2 /
+// gwg2 / gprow; returns the workgroup count. tpw: V tiles per wave of the launch.
+inline int glrd_group_plan(DecodeArgs& a, const GlrdPlan& p, int tpw) {
+  const int n_groups = a.n_kv / a.hpg;
+  const int QH = a.hpg * a.rep;
+  const int nb = (a.S + BLK - 1) / BLK;
+  const int cap = (nb + 3) / 4 < G_MAX_SPLITS2 ? ((nb + 3) / 4 < 1 ? 1 : (nb + 3) / 4) : G_MAX_SPLITS2;
+  int s[MAX_GROUPS], wt[MAX_GROUPS];
+  bool uniform = true;
+  for (int g = 0; g < n_groups; ++g) {
+    s[g] = 1;
+    uniform = uniform && a.grv[g] == a.grv[0];
+    const int vt = a.grv[g] >> 4;
+    wt[g] = glrd_pv_tg_group(vt, tpw) * ((vt < tpw ? vt : tpw) + 2);
+  }
+  if (uniform)
+    for (int g = 0; g < n_groups; ++g) s[g] = p.n_splits2;
+  for (int k = uniform ? n_groups * p.n_splits2 : n_groups; k < n_groups * p.n_splits2; ++k) {
+    int best = -1;
+    for (int g = 0; g < n_groups; ++g)      // largest weight / splits, compared without division
+      if (s[g] < cap && (best < 0 || (long long)wt[g] * s[best] > (long long)wt[best] * s[g])) best = g;
+    if (best < 0) break;
+    ++s[best];
+  }
+  int wg = 0, row = 0;
+  for (int g = 0; g < n_groups; ++g) {
+    const int len = ((nb + s[g] - 1) / s[g]) * BLK;
+    const int ns = (nb * BLK + len - 1) / len;      // <= s[g]
+    a.gsl2[g] = len;
+    a.gns2[g] = (short)ns;
+    a.gwg2[g] = wg;
+    a.gprow[g] = row;
+    wg += a.B * p.n_ht * ns;
+    row += a.B * QH * ns;
+  }
+  a.gwg2[n_groups] = wg;
+  return wg;
+}
+
 // ---------------------------------------------------------------------------------------------------
 // Pass 1: scores. One workgroup per (row, KV head, sequence split), 4 waves, one per SIMD, so each wave
 // may hold up to 512 registers. The KV head's whole u_k^T (128 dims x r_k) sits in LDS as A tiles; each
@@ -66,14 +130,14 @@ inline GlrdPlan glrd_plan(int B, int n_q, int n_kv, int n_groups, int S, int rv)
 // rotation is the same for every pair, so it lives in registers as fp16 (cos, sin) pairs. Each query
 // head's score is complete here; the PV pass reads one score per (head, position).
 //
-// LDS map (KBP = rank blocks rounded up to even), at most 150.3 KB (r_k 512) at every length:
+// LDS map (KBP = rank blocks rounded up to even), at most 154.3 KB (r_k 512) at every length:
 //   ukt   u_k^T as A tiles [row tile 8][rank block KBP][lane] bf16x8 (zero past the group's r_k); at
 //         least 32 KB,
 //         because the prologue stages cs_tab rows 0..63 ([t][f] float2) in the same place
 //   tl    (cos, sin) of angle 64*Lo*f, Lo < 16                                              8 KB
 //   tm    (cos, sin) of angle 1024*Mi*f, Mi < 16                                            8 KB
 //   tt    (cos, sin) of angle 16384*T*f, T < 4                                              2 KB
-//   qs    the KV head's query rows, padded to G_QS                                    16 x G_QS bf16
+//   qs    the KV head's query rows times scale * log2 e, padded to G_QS               16 x G_QS fp32
 // A pair base 64 J (J = 256 T + 16 Mi + Lo) takes its angle by two angle additions of these rows.
 constexpr int G2_NW = 4;                // waves per workgroup of the scores kernel
 
@@ -85,7 +149,7 @@ struct G2Smem {
   static constexpr int TM = TL + 16 * 64 * 8;
   static constexpr int TT = TM + 16 * 64 * 8;
   static constexpr int QS = TT + 4 * 64 * 8;
-  static constexpr int BYTES = QS + 16 * G_QS * 2;
+  static constexpr int BYTES = QS + 16 * G_QS * 4;
   static_assert(BYTES <= 160 * 1024, "scores kernel LDS");
 };
 
@@ -99,7 +163,7 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   float2* tl = reinterpret_cast<float2*>(smem + SM::TL);
   float2* tm = reinterpret_cast<float2*>(smem + SM::TM);
   float2* tt = reinterpret_cast<float2*>(smem + SM::TT);
-  __bf16* qs_lds = reinterpret_cast<__bf16*>(smem + SM::QS);
+  float* qs_lds = reinterpret_cast<float*>(smem + SM::QS);
 
   // Workgroup id -> (latent stream, KV head in group): ids 8*q + x with the same x share an XCD, and the
   // hpg workgroups of one stream (same row, group and split) get consecutive q, so they meet in one L2.
@@ -157,7 +221,11 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
       bf16x8 qrow = bf16x8{};
       if (qh < a.rep)
         qrow = *reinterpret_cast<const bf16x8*>(a.q + ((long long)b * a.n_q + (long long)kvh * a.rep + qh) * HD + qc);
-      *reinterpret_cast<bf16x8*>(qs_lds + qh * G_QS + qc) = qrow;
+      float4* qd = reinterpret_cast<float4*>(qs_lds + qh * G_QS + qc);
+      qd[0] = make_float4((float)qrow[0] * a.qscale, (float)qrow[1] * a.qscale, (float)qrow[2] * a.qscale,
+                          (float)qrow[3] * a.qscale);
+      qd[1] = make_float4((float)qrow[4] * a.qscale, (float)qrow[5] * a.qscale, (float)qrow[6] * a.qscale,
+                          (float)qrow[7] * a.qscale);
     }
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
@@ -242,34 +310,31 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
   };
 
   // Query rotated back by the pair base, scaled by scale * log2 e, in fp16: qB[kq] is the B operand of the
-  // QK MFMA over dims 32 kq + {4g .. 4g+3, 16+4g .. 16+4g+3} (the order of the packed K^T slices).
+  // QK MFMA over dims 32 kq + {4g .. 4g+3, 16+4g .. 16+4g+3} (the order of the packed K^T slices). The
+  // angle of a frequency is the same for every head, so lane (n, g) composes only frequency
+  // fi = 16 (n / 4) + 8 ((n / 2) % 2) + 2 g + n % 2 -- the 16 lanes of a DPP row (one g) hold the 16
+  // frequencies that row's lanes use -- and takes the others' (cos, sin) by row broadcast.
   auto make_q = [&](int base, f16x8 (&qB)[4]) {
     const int J = base >> 6;
-    const float2* lo = tl + (J & 15) * 64;
-    const float2* mi = tm + ((J >> 4) & 15) * 64;
-    const float2* hi = tt + (J >> 8) * 64;
+    const int fi = 16 * (n >> 2) + 8 * ((n >> 1) & 1) + 2 * g + (n & 1);
+    const float2 l2 = tl[(J & 15) * 64 + fi];
+    const float2 m2 = tm[((J >> 4) & 15) * 64 + fi];
+    const float2 h2 = tt[(J >> 8) * 64 + fi];
+    const float hc = h2.x * m2.x - h2.y * m2.y, hs = h2.y * m2.x + h2.x * m2.y;
+    const float cf = hc * l2.x - hs * l2.y, sf = hs * l2.x + hc * l2.y;
+    float4 qv[8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int d0 = 32 * t + 16 * half + 4 * g;     // 4 dims = 2 frequency pairs
-        const bf16x4 qv = *reinterpret_cast<const bf16x4*>(qs_lds + n * G_QS + d0);
-        const float4 l4 = *reinterpret_cast<const float4*>(lo + (d0 >> 1));
-        const float4 m4 = *reinterpret_cast<const float4*>(mi + (d0 >> 1));
-        const float4 h4 = *reinterpret_cast<const float4*>(hi + (d0 >> 1));
-        const float lc[2] = {l4.x, l4.z}, ls[2] = {l4.y, l4.w}, mc[2] = {m4.x, m4.z}, ms[2] = {m4.y, m4.w};
-        const float tc[2] = {h4.x, h4.z}, ts[2] = {h4.y, h4.w};
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const float hc = tc[p] * mc[p] - ts[p] * ms[p], hs = ts[p] * mc[p] + tc[p] * ms[p];
-          const float cf = (hc * lc[p] - hs * ls[p]) * a.qscale;
-          const float sf = (hs * lc[p] + hc * ls[p]) * a.qscale;
-          const float x0 = (float)qv[2 * p], x1 = (float)qv[2 * p + 1];
-          qB[t][4 * half + 2 * p] = (_Float16)(x0 * cf + x1 * sf);      // R_{-base}
-          qB[t][4 * half + 2 * p + 1] = (_Float16)(x1 * cf - x0 * sf);
-        }
-      }
-    }
+    for (int i = 0; i < 8; ++i)                       // dims 32 (i / 2) + 16 (i % 2) + 4 g .. +3 of head n
+      qv[i] = *reinterpret_cast<const float4*>(qs_lds + n * G_QS + 32 * (i >> 1) + 16 * (i & 1) + 4 * g);
+    static_for<0, 16>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;          // frequency of row lane k: t = k / 4, half = (k / 2) % 2, p = k % 2
+      constexpr int t = k >> 2, half = (k >> 1) & 1, p = k & 1;
+      const float c = row_bcast<k>(cf), sn = row_bcast<k>(sf);
+      const float4 q4 = qv[2 * t + half];
+      const float x0 = p ? q4.z : q4.x, x1 = p ? q4.w : q4.y;
+      qB[t][4 * half + 2 * p] = (_Float16)(x0 * c + x1 * sn);      // R_{-base}
+      qB[t][4 * half + 2 * p + 1] = (_Float16)(x1 * c - x0 * sn);
+    });
   };
 
   float* srow = scores + ((long long)(b * n_groups + grp) * NB + (s_lo >> 5)) * QH * BLK;
@@ -339,40 +404,51 @@ __global__ __launch_bounds__(G2_NW * 64) void palu_glrd_scores_full_kernel(const
 }
 
 // ---------------------------------------------------------------------------------------------------
-// Pass 2: latent PV. The 8 waves form TG tile groups x PG position groups (TG * PG = 8, TG the smallest
-// power of two with TG * 8 >= r_v / 16): wave (tg, pg) owns V tiles tg * TPW .. tg * TPW + TPW - 1 and
-// the blocks j = pg, pg + PG, ... of the split, with its own online softmax; the PG partials of a tile
-// group are merged through LDS at the end. A block's scores are thus loaded and exponentiated by TG
-// waves, not by all 8.
+// Pass 2: latent PV. The 8 waves form TG tile groups x PG position groups (TG * PG = 8): wave (tg, pg)
+// owns V tiles tg * TPW .. tg * TPW + TPW - 1 and the blocks j = pg, pg + PG, ... of the split, with its
+// own online softmax; the PG partials of a tile group are merged through LDS at the end. A block's
+// scores are thus loaded and exponentiated by TG waves, not by all 8. TPW comes from the cache width (TG
+// the smallest power of two with TG * 8 >= r_v / 16); a group of lower V rank takes the fewest tile
+// groups that cover its own tiles, so its spare waves take more position groups instead of idling.
 __host__ __device__ inline int glrd_pv_tg(int vt) {
   int tg = 1;
   while (tg * 8 < vt) tg *= 2;
+  return tg;
+}
+// Tile groups of a group with vt_g V tiles when a wave holds tpw tiles.
+__host__ __device__ inline int glrd_pv_tg_group(int vt_g, int tpw) {
+  int tg = 1;
+  while (tg * tpw < vt_g && tg < G_NW) tg *= 2;
   return tg;
 }
 __host__ __device__ inline int glrd_pv_lds(int tpw) { return G_NW * (16 * tpw * 16 + 2 * 16) * 4; }
 
 template <int TPW, bool ROWS>
 __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArgs a, const float* scores, float* part,
-                                                                 int n_ht, int n_splits2, int split_len2) {
+                                                                 int n_ht) {
   static_assert(!ROWS || TPW % 2 == 0, "a ROWS wave loads its V tiles in 32-column pieces");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int n_groups = a.n_kv / a.hpg;
   const int QH = a.hpg * a.rep;
   const int NB = (a.S + BLK - 1) / BLK;
+  // workgroup -> (group, row, head tile, split): each group's workgroups form one range (per-group plan)
   int L = blockIdx.x;
+  int grp = 0;
+  while (grp + 1 < n_groups && L >= a.gwg2[grp + 1]) ++grp;
+  L -= a.gwg2[grp];
+  const int n_splits2 = a.gns2[grp], split_len2 = a.gsl2[grp];
   const int split = L % n_splits2;
   L /= n_splits2;
   const int ht = L % n_ht;
-  L /= n_ht;
-  const int grp = L % n_groups, b = L / n_groups;
+  const int b = L / n_ht;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int TG = glrd_pv_tg(a.rv >> 4), PG = G_NW / TG;   // tile groups from the cache width (TPW's basis)
   const int rv_g = a.grv[grp];                            // this group's rank: V tiles past it are never read
   const int VT = rv_g >> 4;
+  const int TG = glrd_pv_tg_group(VT, TPW), PG = G_NW / TG;
   const int tg = w % TG, pg = w / TG;
   const int head = ht * 16 + n;                       // head of this lane column inside the group
   const bool head_live = head < QH;
@@ -550,8 +626,8 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
         Ls += oq[16 * TPW * 16 + 16 + hh] * f;
       }
     }
-    const int qh = (b * n_groups + grp) * QH + ht * 16 + hh;    // == b * n_q + global query head
-    float* prow = part + ((long long)qh * n_splits2 + split) * (a.rv + G_PSTRIDE_PAD);
+    const int row = a.gprow[grp] + (b * QH + ht * 16 + hh) * n_splits2 + split;
+    float* prow = part + (long long)row * (a.rv + G_PSTRIDE_PAD);
     prow[col] = acc;
     if (col == 0) { prow[a.rv] = M; prow[a.rv + 1] = Ls; }
   }
@@ -564,24 +640,26 @@ __global__ __launch_bounds__(G_NW * 64) void palu_glrd_pv_kernel(const DecodeArg
 // column of O_lat is merged once (a dot product over independent loads), and the projection reads u_v
 // in 16-byte pieces: thread (rank slice, 8 output dims) accumulates 8 outputs over its slice; the 16
 // slices are summed through LDS.
-constexpr int G_MAX_SPLITS2 = 128;      // split partials per head the merge workgroup stages
 
 // Dynamic LDS: red [16 rank slices][HD], olat [rv], wsplit [G_MAX_SPLITS2], lsum.
 __host__ __device__ inline int glrd_out_lds(int rv) { return (16 * HD + rv + G_MAX_SPLITS2 + 4) * 4; }
 
 template <typename OutT>
-__global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, const float* part, int n_splits2) {
+__global__ __launch_bounds__(256) void palu_glrd_out_kernel(const DecodeArgs a, const float* part) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int item = blockIdx.x, h = blockIdx.y;        // query head h of the item's KV head
   const int b = item / a.n_kv, kvh = item - b * a.n_kv;
-  const int rv = a.grv[kvh / a.hpg];                  // the group's rank: partial columns past it are unset
+  const int grp = kvh / a.hpg;
+  const int rv = a.grv[grp];                          // the group's rank: partial columns past it are unset
+  const int n_splits2 = a.gns2[grp];
   float* red = reinterpret_cast<float*>(smem);
   float* olat = red + 16 * HD;
   float* wsplit = olat + a.rv;
   float* lsum = wsplit + G_MAX_SPLITS2;
   const int stride = a.rv + G_PSTRIDE_PAD;
   const int tid = threadIdx.x;
-  const float* ph = part + (long long)(b * a.n_q + kvh * a.rep + h) * n_splits2 * stride;
+  const int hh = (kvh - grp * a.hpg) * a.rep + h;     // query head within the group
+  const float* ph = part + (long long)(a.gprow[grp] + (b * a.hpg * a.rep + hh) * n_splits2) * stride;
   // split weights: wsplit[s] = 2^(m_s - M); lsum = sum_s l_s 2^(m_s - M). The first wave's lanes take
   // the splits in turn.
   if (tid < 64) {
@@ -685,8 +763,7 @@ int launch_pv_t(const DecodeArgs& a, const float* scores, float* part, const Glr
     if (e != hipSuccess) return fail(PALU_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
     attr_set = lds;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)p.n_wg2), dim3(G_NW * 64), lds, s, a, scores, part, p.n_ht, p.n_splits2,
-                     p.split_len2);
+  hipLaunchKernelGGL(kern, dim3((unsigned)a.gwg2[a.n_kv / a.hpg]), dim3(G_NW * 64), lds, s, a, scores, part, p.n_ht);
   return PALU_OK;
 }
 
@@ -765,6 +842,7 @@ int dispatch_glrd(const DecodeArgs& a0, bool rows, int cs_dtype, int out_dtype, 
     e = hipGetLastError();
     if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent scores kernel launch: %s", hipGetErrorString(e));
   }
+  glrd_group_plan(a, p, glrd_pv_tpw(a.rv, rows));
   if (int rc2 = launch_pv(a, scores, part, p, rows, s)) return rc2;
   e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent PV kernel launch: %s", hipGetErrorString(e));
@@ -772,10 +850,10 @@ int dispatch_glrd(const DecodeArgs& a0, bool rows, int cs_dtype, int out_dtype, 
   const dim3 out_grid((unsigned)(a.B * a.n_kv), (unsigned)a.rep);
   if (out_dtype == PALU_DTYPE_F32) {
     if (int rc3 = set_out_lds(palu_glrd_out_kernel<float>, out_lds)) return rc3;
-    hipLaunchKernelGGL(palu_glrd_out_kernel<float>, out_grid, dim3(256), out_lds, s, a, part, p.n_splits2);
+    hipLaunchKernelGGL(palu_glrd_out_kernel<float>, out_grid, dim3(256), out_lds, s, a, part);
   } else {
     if (int rc3 = set_out_lds(palu_glrd_out_kernel<__bf16>, out_lds)) return rc3;
-    hipLaunchKernelGGL(palu_glrd_out_kernel<__bf16>, out_grid, dim3(256), out_lds, s, a, part, p.n_splits2);
+    hipLaunchKernelGGL(palu_glrd_out_kernel<__bf16>, out_grid, dim3(256), out_lds, s, a, part);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent output kernel launch: %s", hipGetErrorString(e));

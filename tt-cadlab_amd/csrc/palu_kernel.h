@@ -63,7 +63,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int HD = 128;     // head dim
-constexpr int MAX_GROUPS = 16;  // latent groups per layer with per-group ranks
+constexpr int MAX_GROUPS = 32;  // latent groups per layer of the grouped-latent (u_v) kernels
 constexpr int BLK = 32;     // positions per block: two 16-position MFMA tiles, also the rotation chunk
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LAZY_RESCALE_LOG2 = 8.0f;  // running max is refreshed when a score exceeds it by > 2^8
@@ -107,6 +107,10 @@ struct DecodeArgs {
   // the group's own rank). Same for V.
   long long gko[MAX_GROUPS], gvo[MAX_GROUPS];
   short gkw[MAX_GROUPS], gvw[MAX_GROUPS];
+  // Grouped-latent PV plan, per group: gns2 splits of gsl2 positions; its workgroups are gwg2[g] ..
+  // gwg2[g + 1] - 1 and its partial rows start at gprow[g] ([row][head of the group][split] order).
+  short gns2[MAX_GROUPS];
+  int gsl2[MAX_GROUPS], gwg2[MAX_GROUPS + 1], gprow[MAX_GROUPS];
 };
 
 // Error reporting (defined in palu_capi.hip): formats the message for palu_last_error, returns code.
