@@ -119,6 +119,11 @@ def build_workload(a, dev):
     return dict(q=q, w_rot=w_rot, cs=cs, layers=layers, cur=cur, u_k=u_k, cos=cos, sin=sin)
 
 
+def progress(msg):
+    """One progress line on stderr (stdout carries only the JSON result line)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def time_calls(fn, n_layers, steps, warmup):
     """Warm up, then time exactly `steps` back-to-back calls bracketed by synchronize, with one pair of
     HIP events around the same region on the launch stream (torch's current stream, where the library
@@ -345,6 +350,7 @@ def measure_e2e(a, dev):
         tok = pm.prefill_all(model, prompts).argmax(-1)
         torch.cuda.synchronize()
         t_pre = time.perf_counter() - t0
+        progress(f"decoder ({kind}): built in {t_build:.1f} s, prefilled in {t_pre:.1f} s; {n_new} greedy tokens")
         model.set_deterministic(a.e2e_deterministic)
         step = model.decode if a.e2e_no_graph else model.decode_graph
         pos = torch.full((B,), P, dtype=torch.int32, device=dev)
@@ -378,6 +384,7 @@ def measure_e2e(a, dev):
             T = min(a.e2e_fidelity_steps, args.max_seq_len - P)
             teacher = torch.randint(0, args.vocab_size, (B, T), generator=torch.Generator().manual_seed(8)).to(dev)
             t0 = time.perf_counter()
+            progress(f"decoder ({kind}): fidelity check, {T} teacher-forced steps")
             r = decode_check.fused_vs_naive(model, prompts, teacher, reference_core=decode_check.fp32_attention_core)
             torch.cuda.synchronize()
             pick = lambda d: {"pcc_min": round(d["pcc_min"], 6), "pcc_mean": round(d["pcc_mean"], 6),
@@ -457,7 +464,9 @@ def main():
         fused.palu_sdpa_decode(wl["q"], k, wl["w_rot"], wl["cs"], v, rv, wl["cur"], scale=HD ** -0.5, out=out,
                                workspace=ws, deterministic=a.deterministic)
 
+    progress(f"fused decode: {a.steps} timed calls after {a.warmup} warm-ups")
     wall_ms, kern_ms, per = time_calls(fused_step, a.layers, a.steps, a.warmup)
+    progress(f"fused decode: {wall_ms * 1e3:.2f} us per call")
     lat_bytes = B * NKV * S * (rk + rv) * 2
     flops = 2 * B * NKV * S * rk * HD + 2 * B * NQ * S * HD + 2 * B * NQ * S * rv
     achieved = lat_bytes / (kern_ms * 1e-3) / 1e9
@@ -514,6 +523,7 @@ def main():
                                deterministic=a.deterministic)
 
         # the same timed calls and warm-ups as the fused line, so the ratio compares like with like
+        progress("stock full-KV decode")
         s_wall, s_kern, _ = time_calls(stock_step, n_stock, a.steps, a.warmup)
         s_bytes = B * NKV * S * HD * 2 * 2
         res["stock_full_kv"] = {"us_per_layer": round(s_wall * 1e3, 2), "kernel_us": round(s_kern * 1e3, 2),
@@ -530,17 +540,21 @@ def main():
         # the extra lines take their own minimum counts (about 20-60 ms of GPU time each): a handful of
         # calls after 3-5 warm-ups reads the clocks and caches still ramping (the G-LRD widest layer timed
         # 402 us at 10 calls after 3 warm-ups against 366 us at steady state on one box)
+        progress("paged mixed ranks")
         res["paged_mixed_ranks"] = measure_paged(dev, max(a.steps // 4, 100), max(a.warmup // 4, 30))
+        progress("grouped latents (G-LRD)")
         res["glrd"] = measure_glrd(dev, max(a.steps // 8, 60), max(a.warmup // 8, 20))
     if not a.no_e2e:
         if wl.get("layers") is not None:
             wl["layers"] = None
             torch.cuda.empty_cache()
+        progress("32-layer decoder")
         res["e2e_decoder"] = measure_e2e(a, dev)
     if not a.no_cpu:
         if wl.get("layers") is None:
             gd = torch.Generator(device=dev).manual_seed(1)
             wl["layers"] = build_workload(argparse.Namespace(**{**vars(a), "layers": 1}), dev)["layers"]
+        progress("CPU baseline")
         res["cpu_baseline"] = cpu_baseline(a, wl)
     print(json.dumps(res), flush=True)
 
