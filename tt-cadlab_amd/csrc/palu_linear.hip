@@ -157,8 +157,18 @@ __global__ __launch_bounds__(NW * 64) void palu_linear_kernel(const __bf16* __re
   // slice read the matrix's last k tile; their products are never stored), so each wait in the loop is
   // for exactly the loads of the buffer about to be used.
   bf16x8 wa[NB][RTW], xb[NB][LIN_MT];
+  // Every workgroup reads the same activation tiles. Walked in the same order, all workgroups would
+  // request the same few kilobytes at once; instead each group starts its slice at its own offset and
+  // wraps around (32-layer decode step 5.21 -> 5.16 ms in a same-box A/B). i -> (i + krot) mod klen is
+  // a permutation of the slice, so the waves together still cover each k tile once; the sums are the
+  // same up to the order of the fp32 additions.
+  const int klen = kt_hi - kt_lo;
+  const int kper = klen / NW > 0 ? klen / NW : 1;
+  const int krot = ((blockIdx.x / ks_count) * 37 % kper) * NW % (klen > 0 ? klen : 1);
   auto load = [&](int buf, int kt) {
-    kt = min(kt, kt_total - 1);
+    int i = kt - kt_lo;                                   // steps past the slice read its last tile
+    i = i < klen ? (i + krot >= klen ? i + krot - klen : i + krot) : klen - 1;
+    kt = klen > 0 ? min(kt_lo + i, kt_total - 1) : kt_total - 1;   // an empty slice reads the last tile
 #pragma unroll
     for (int r = 0; r < RTW; ++r)
       wa[buf][r] = __builtin_nontemporal_load(wp + ((long long)kt * rt_cnt + min(r, rt_cnt - 1)) * 64);
@@ -190,10 +200,17 @@ __global__ __launch_bounds__(NW * 64) void palu_linear_kernel(const __bf16* __re
   // wave's count (the rest of the last round) load clamped tiles and multiply them by zero activations.
   // The scheduling barriers keep each step's loads ahead of the earlier step's MFMAs (left alone, the
   // compiler sinks every load to its first use and the wave has one tile in flight).
+  // The prologue's loads keep their order (a scheduling barrier after each buffer): the loop-top wait
+  // is computed from the load order on both paths into the loop, and a prologue reordered by the
+  // scheduler made the compiler wait there for all but the newest loads, a drain every NB steps
+  // (32-layer decode step 5.27 -> 5.23 ms in a same-box A/B).
   const int kt0 = kt_lo + w;
   const int nsteps = kt0 < kt_hi ? (kt_hi - kt0 + NW - 1) / NW : 0;   // uniform per wave
 #pragma unroll
-  for (int j = 0; j < NB - 1; ++j) load(j, kt0 + j * NW);
+  for (int j = 0; j < NB - 1; ++j) {
+    load(j, kt0 + j * NW);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   for (int s = 0; s < nsteps; s += NB) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
