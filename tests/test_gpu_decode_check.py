@@ -56,3 +56,15 @@ def test_fused_matches_naive_with_graph_steps(gpu):
     r = decode_check.fused_vs_naive(model, prompts, teacher, use_graph=True, reference_core=fp32_attention_core)
     print("decode_check small, graph steps:", r, flush=True)
     assert r["pcc_min"] >= 0.999 and r["fused_vs_reference"]["pcc_min"] >= 0.999, r
+
+
+def test_command_line_writes_the_result_row(gpu, tmp_path):
+    """The reference's harness is a command that writes one JSON per run (decode_check.py:62-134): the
+    same here, on a 2-layer model of the full vocabulary."""
+    import json
+    r = decode_check.main(["--row", "t2", "--layers", "2", "--prompt", "64", "--steps", "5", "--batch", "2",
+                           "--out", str(tmp_path)])
+    saved = json.loads((tmp_path / "decode_check_t2.json").read_text())
+    assert saved["row"] == "t2" and saved["steps"] == 5 and saved["rows"] == 2
+    assert saved == json.loads(json.dumps(r))
+    assert saved["pcc_min"] >= 0.99 and 0.0 <= saved["argmax_agree"] <= 1.0

@@ -83,7 +83,7 @@ __host__ __device__ inline int glrd_pv_tg_group(int vt_g, int tpw);
 // splits of the uniform plan are dealt out in proportion to each group's time per position (tile groups
 // x (V tiles of its busiest wave + 2 for the scores and the softmax)), largest remaining share first, so
 // one chip-fill of workgroups ends together. Equal ranks keep the uniform plan. Fills a.gns2 / gsl2 /
-// gwg2 / gprow; returns the workgroup count. tpw: V tiles per wave of the launch.
+// gwg2 / gprow; returns the partial rows written. tpw: V tiles per wave of the launch.
 inline int glrd_group_plan(DecodeArgs& a, const GlrdPlan& p, int tpw) {
   const int n_groups = a.n_kv / a.hpg;
   const int QH = a.hpg * a.rep;
@@ -118,7 +118,7 @@ inline int glrd_group_plan(DecodeArgs& a, const GlrdPlan& p, int tpw) {
     row += a.B * QH * ns;
   }
   a.gwg2[n_groups] = wg;
-  return wg;
+  return row;                                       // partial rows the plan writes
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -842,7 +842,9 @@ int dispatch_glrd(const DecodeArgs& a0, bool rows, int cs_dtype, int out_dtype, 
     e = hipGetLastError();
     if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent scores kernel launch: %s", hipGetErrorString(e));
   }
-  glrd_group_plan(a, p, glrd_pv_tpw(a.rv, rows));
+  // the plan deals out the uniform plan's splits, so its partial rows fit the workspace's
+  if ((size_t)glrd_group_plan(a, p, glrd_pv_tpw(a.rv, rows)) * (a.rv + G_PSTRIDE_PAD) > p.part_floats)
+    return fail(PALU_EUNSUPPORTED, "grouped-latent PV plan exceeds its workspace");
   if (int rc2 = launch_pv(a, scores, part, p, rows, s)) return rc2;
   e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "grouped-latent PV kernel launch: %s", hipGetErrorString(e));

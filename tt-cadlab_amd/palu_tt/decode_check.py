@@ -15,7 +15,10 @@ pos) -> [1, B, nh, out_width]``; ``fp32_attention_core`` below is plain fp32 att
 latent caches): both paths are then also compared with it, which separates a path's own error from the
 run-to-run spread of the model.
 """
+import argparse
+import json
 import types
+from pathlib import Path
 from typing import Callable, Dict, Optional
 
 import torch
@@ -100,3 +103,49 @@ def fused_vs_naive(model: "pm.Transformer", prompts: torch.Tensor, teacher: torc
         out["naive_vs_reference"] = _compare(naive, ref)
     model.set_fused_k(True)
     return out
+
+
+def main(argv=None) -> Dict[str, object]:
+    """Command line: ``python -m palu_tt.decode_check --row NAME [--steps 64] [--out DIR]``, the
+    reference's harness (palu_tt/decode_check.py:62-134) on a Llama-3.1-8B-shaped Palu model. There are
+    no checkpoints or datasets here, so the weights are seeded random-init with per-layer SVD factors
+    (ranks drawn as the benchmark draws them) and the prompt and teacher tokens are seeded random ids.
+    --steps counts the decode steps compared (the reference's counts the prefill step too and reports
+    one less). Prints one JSON line; with --out also writes it to DIR/decode_check_<row>.json."""
+    p = argparse.ArgumentParser(description=main.__doc__.splitlines()[0])
+    p.add_argument("--row", required=True, help="name of the result row")
+    p.add_argument("--steps", type=int, default=63, help="teacher-forced decode steps compared")
+    p.add_argument("--batch", type=int, default=1)
+    p.add_argument("--prompt", type=int, default=512, help="prompt tokens prefilled before the decode steps")
+    p.add_argument("--layers", type=int, default=32)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--graph", action="store_true", help="decode steps as HIP graphs")
+    p.add_argument("--fp32-core", action="store_true",
+                   help="also compare both paths with plain fp32 attention over the same caches")
+    p.add_argument("--out", default=None, help="directory for decode_check_<row>.json")
+    a = p.parse_args(argv)
+    dev = torch.device("cuda:0")
+    L, B, P, T = a.layers, a.batch, a.prompt, a.steps
+    args = pm.ModelArgs(n_layers=L, max_batch_size=B, max_seq_len=(P + T + 32) // 32 * 32)
+    ranks_k, ranks_v = pm.draw_ranks(L, seed=1), pm.draw_ranks(L, seed=2)
+    sd = pm.random_palu_state_dict(args, ranks_k, ranks_v, dev, seed=a.seed, rank_multiple=16)
+    model = pm.Transformer(args, sd, dev)
+    del sd
+    g = torch.Generator().manual_seed(a.seed + 7)
+    prompts = torch.randint(0, args.vocab_size, (B, P), generator=g).to(dev)
+    teacher = torch.randint(0, args.vocab_size, (B, T), generator=g).to(dev)
+    r = fused_vs_naive(model, prompts, teacher, use_graph=a.graph,
+                       reference_core=fp32_attention_core if a.fp32_core else None)
+    out = {"row": a.row, "weights": "random-init, seeded", "layers": L, "batch": B, "prompt": P,
+           "ranks_k": ranks_k, "ranks_v": ranks_v, "graph": bool(a.graph), **r}
+    line = json.dumps(out)
+    print(line, flush=True)
+    if a.out:
+        d = Path(a.out)
+        d.mkdir(parents=True, exist_ok=True)
+        (d / f"decode_check_{a.row}.json").write_text(json.dumps(out, indent=1))
+    return out
+
+
+if __name__ == "__main__":
+    main()
