@@ -127,8 +127,8 @@ def progress(msg):
 def time_calls(fn, n_layers, steps, warmup):
     """Warm up, then time exactly `steps` back-to-back calls bracketed by synchronize, with one pair of
     HIP events around the same region on the launch stream (torch's current stream, where the library
-    enqueues its kernels): wall ms/step, and the device's average duration of one call (its kernel, plus
-    the merge kernel where the op splits items), with the queue never idle between calls. A second pass
+    enqueues its kernels): wall ms/step, and the device's average duration of one call (its kernels and
+    the boundaries between them), with the queue never idle between calls. A second pass
     of the same length brackets each call by its own events for the per-call spread; those events add
     about 3 us per call, so the mean comes from the first pass.
     Returns (wall ms/step, average kernel ms per call, per-call kernel ms of the second pass)."""

@@ -67,8 +67,11 @@ const char* palu_last_error(void);
 /* PALU_ABI_VERSION of the loaded library. */
 int palu_abi_version(void);
 
-/* Bytes of fp32 workspace palu_sdpa_decode / palu_flash_decode need for these shapes (0 when the
- * sequence is not split across workgroups). head_dim_v is the output width of the call. */
+/* Bytes of workspace palu_sdpa_decode / palu_flash_decode need for these shapes (0 when the
+ * sequence is not split across workgroups). head_dim_v is the output width of the call. It holds the
+ * split items' fp32 partials and one 8-byte chunk counter per (row, KV head); the launch merges the
+ * partials itself and needs no particular contents on entry (counters of other calls count as zero).
+ * Calls that share a workspace must be ordered on one stream. */
 size_t palu_decode_workspace_bytes(int batch, int n_kv, int seq_len, int head_dim_v);
 
 /* Bytes of workspace palu_sdpa_decode needs with u_v (grouped latents, in-kernel V rebuild): the fp32

@@ -91,7 +91,7 @@ def test_glrd_other_group_sizes_and_ranks(gpu, hpg, r_k, r_v):
 
 @pytest.mark.parametrize("B,S", [(1, 4096), (2, 300), (5, 33)])
 def test_glrd_splits_and_ragged_lengths(gpu, B, S):
-    """Batch 1 splits every sequence across workgroups (merged by the merge kernel); lengths that are
+    """Batch 1 splits every sequence across workgroups (merged by the out kernel); lengths that are
     not a multiple of the 32-position block and caches shorter than one block group."""
     S_pad = (S + 31) // 32 * 32
     args = list(_case(B, S_pad, 256, 256, hpg=4, seed=B * 7 + S))

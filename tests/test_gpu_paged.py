@@ -194,3 +194,35 @@ def test_paged_stock_decode_matches_full_kv_oracle(gpu, layout):
                              out_dtype=torch.float32, page_table_tensor=pt.to(gpu))
     torch.cuda.synchronize()
     _check(out.cpu(), exp)
+
+
+def test_split_items_repeat_exactly_on_one_shared_workspace(gpu):
+    """Split items (8 rows x 8 KV heads on a 256-workgroup plan) merge inside the decode launch: each
+    chunk counts itself into an 8-byte counter of its item in the workspace, and the chunk that completes
+    the count merges the item. Two inputs alternate on one workspace that first holds stale counter words
+    (the fixed tag with an old call number and a nonzero count), with a call of other widths in between
+    whose partial slots overlay these calls' counters: every output must equal its input's first output
+    bit for bit, and match the oracle."""
+    S, ps = 8192, 64
+    cases = []
+    for seed, r_k, r_v in ((1, 64, 64), (2, 64, 64), (3, 32, 128)):
+        g = torch.Generator().manual_seed(100 + seed)
+        lengths = torch.randint(1, S + 1, (8,), generator=g).tolist()
+        lengths[0] = S
+        cases.append(_case(8, S, r_k, r_v, ps, seed=seed, lengths=lengths))
+    from palu_tt import _native
+    need = max(_native.load().palu_decode_workspace_bytes(8, 8, S, c[2].shape[-1]) for c in cases)
+    assert need > 0, "the plan must split items for this test"
+    ws = torch.empty(need // 8 + 1, dtype=torch.int64, device=gpu)
+    stale = (0xA5C3 << 48) | (1 << 16) | 5                             # call number 1, five chunks counted
+    ws.fill_(stale - (1 << 64))
+    cos, sin = ref.cos_sin_tables(HD, S, THETA, LLAMA3)
+    first = {}
+    for it, i in enumerate([0, 1, 0, 2, 1, 0, 2, 1, 1, 0, 0]):
+        q, k, v, u_k, pos, kp, vp, pt = cases[i]
+        out = _decode(gpu, q, kp, vp, u_k, pos, pt, S, "tiled", workspace=ws)
+        if i not in first:
+            first[i] = out
+            _check(out, ref.reference_decode(q, k, u_k, v, pos, cos, sin, HD ** -0.5))
+        else:
+            assert torch.equal(out, first[i]), f"call {it} (input {i}) differs from that input's first call"

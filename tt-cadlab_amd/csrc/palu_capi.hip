@@ -18,6 +18,11 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+unsigned long long next_epoch() {
+  static std::atomic<unsigned long long> calls{0};
+  return CHUNK_TAG | (((calls.fetch_add(1) + 1) & 0xFFFFFFFFull) << 16);
+}
+
 }  // namespace palu
 
 namespace {

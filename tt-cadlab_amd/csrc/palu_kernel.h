@@ -85,6 +85,7 @@ struct DecodeArgs {
   int n_splits;
   int n_wg;               // M-LRD / stock decode: workgroups launched; n_wg > B * n_kv splits items by length
   int balanced;           // 1 when n_wg > B * n_kv (length-aware chunks, merged through ws)
+  unsigned long long epoch;  // balanced: this call's tag for the items' chunk counters (CHUNK_TAG | call number)
   int deterministic;      // 1: wave w takes blocks w, w + NW, ... (reproducible); 0: blocks from a counter
   int out_tiled;          // 1: out in the 64-row tiled activation layout of the next projection (B <= 64)
   int grouped_streams;    // grouped latents stored compactly, each group at its own ranks (PALU_LAYOUT_TILED_GROUPED)
@@ -116,6 +117,11 @@ struct DecodeArgs {
 // Error reporting (defined in palu_capi.hip): formats the message for palu_last_error, returns code.
 int fail(int code, const char* fmt, ...);
 extern thread_local char g_err[1024];
+
+// Chunk counters of split items (see decode_ws_bytes): bits 63..48 a fixed tag, 47..16 the call number
+// (next_epoch, one per decode launch in the process), 15..0 the count of the item's chunks done.
+constexpr unsigned long long CHUNK_TAG = 0xA5C3ull << 48;
+unsigned long long next_epoch();   // defined in palu_capi.hip
 
 // The decode step's QKV epilogue (palu_qkv_post over split partials, palu_linear_qkv inside the
 // projection): where each part of a QKV output row goes. q heads are columns h * 128 .. of the row,
@@ -178,8 +184,8 @@ inline size_t ws_bytes(int items, int n_splits, int rv) {
 inline int decode_workgroups(int items) { return ((items + TARGET_WGS - 1) / TARGET_WGS) * TARGET_WGS; }
 inline size_t decode_ws_bytes(int items, int rv) {
   const int wg = decode_workgroups(items);
-  // partial slots [wg][16][rv + 2] floats, then one (first slot, chunk count) int pair per item
-  return wg == items ? 0 : (size_t)wg * 16 * (rv + 2) * sizeof(float) + (size_t)items * 2 * sizeof(int);
+  // partial slots [wg][16][rv + 2] floats, then one 8-byte chunk counter per item
+  return wg == items ? 0 : (size_t)wg * 16 * (rv + 2) * sizeof(float) + (size_t)items * sizeof(unsigned long long);
 }
 
 
@@ -447,6 +453,73 @@ __device__ __forceinline__ float4 load4f<__bf16>(const __bf16* p) {
   return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 
+// A split item's chunks merge inside the decode launch (no second launch). Each chunk's workgroup has
+// written its partial (O, m, l) with system-scope stores, which write through to memory; once they have
+// completed it counts itself into the item's 8-byte counter (a system-scope compare-and-swap), and the
+// workgroup whose count completes the item reads every chunk's partial with system-scope loads (past
+// the XCDs' L2s, so no cache write-back or invalidate is needed) and writes
+// out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), chunks in order: the result does not depend on
+// which workgroup finishes last. That workgroup also leaves the counter at zero. A counter word whose
+// upper 48 bits are not this call's tag (another call's, or memory never written) counts as zero.
+// smem: any LDS word no wave reads any more.
+template <int RV, int NW, typename OutT>
+__device__ __forceinline__ void merge_split_item(const DecodeArgs& a, char* smem, int first, int nc, int b, int kvh) {
+  __builtin_amdgcn_s_waitcnt(0);            // this thread's partial stores have completed
+  __syncthreads();
+  int* last = reinterpret_cast<int*>(smem);
+  if (threadIdx.x == 0) {
+    unsigned long long* ctr =
+        reinterpret_cast<unsigned long long*>(a.ws + (long long)a.n_wg * 16 * (RV + 2)) + (b * a.n_kv + kvh);
+    const unsigned long long tag = a.epoch;  // low 16 bits zero
+    unsigned long long old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM), nw;
+    int done;
+    do {
+      done = (((old & ~0xFFFFull) == tag) ? (int)(old & 0xFFFF) : 0) + 1;
+      nw = tag | (unsigned long long)(done == nc ? 0 : done);
+    } while (!__hip_atomic_compare_exchange_strong(ctr, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_SYSTEM));
+    last[0] = done == nc;
+  }
+  __syncthreads();
+  if (!last[0]) return;                     // uniform
+  constexpr int MC = 8;                     // chunk partials loaded together per round trip
+  constexpr long long SLOT = 16 * (RV + 2);
+  for (int e = threadIdx.x; e < a.rep * RV; e += NW * 64) {
+    const int h = e / RV, r = e - h * RV;
+    const float* ws = a.ws + ((long long)first * 16 + h) * (RV + 2);
+    float M = NEG_INF, L = 0.f, acc = 0.f;
+    for (int s0 = 0; s0 < nc; s0 += MC) {
+      float mv[MC], lv[MC], ov[MC];
+#pragma unroll
+      for (int i = 0; i < MC; ++i) {
+        const float* row = ws + min(s0 + i, nc - 1) * SLOT;   // clamped into the item's slots
+        mv[i] = __hip_atomic_load(row + RV, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        lv[i] = __hip_atomic_load(row + RV + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        ov[i] = __hip_atomic_load(row + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+      float Mn = M;
+#pragma unroll
+      for (int i = 0; i < MC; ++i)
+        if (s0 + i < nc) Mn = fmaxf(Mn, mv[i]);
+      if (Mn == NEG_INF) continue;          // every chunk so far empty
+      const float c = __builtin_amdgcn_exp2f(M - Mn);   // 0 while M is -inf
+      L *= c;
+      acc *= c;
+#pragma unroll
+      for (int i = 0; i < MC; ++i) {
+        if (s0 + i < nc) {
+          const float f = __builtin_amdgcn_exp2f(mv[i] - Mn);
+          L += lv[i] * f;
+          acc += ov[i] * f;
+        }
+      }
+      M = Mn;
+    }
+    OutT* o = static_cast<OutT*>(a.out) + out_index(a, b, ((long long)kvh * a.rep + h) * RV + r, (long long)a.n_q * RV);
+    store_out(o, L > 0.f ? acc / L : 0.f);
+  }
+}
+
 // IPW items per workgroup: 2 runs two items of one KV head (batch rows b and b + B/2) on the two halves
 // of the waves, which share the angle tables and u_k^T staged once.
 template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, int NW, typename TabT, typename OutT, int IPW = 1>
@@ -505,7 +578,7 @@ void palu_decode_kernel(const DecodeArgs a) {
 
   // This workgroup's item and position range: the whole sequence of item blockIdx.x, or one chunk of
   // the length-aware plan (computed identically, and uniformly, by every wave).
-  int b, kvh, s_lo, s_hi, n_chunks = 1;
+  int b, kvh, s_lo, s_hi, n_chunks = 1, first_chunk = 0;
   if (!a.balanced) {
     const int item = blockIdx.x + half * a.n_wg;   // two items: n_wg = B * n_kv / 2, so the KV head is shared
     b = item / a.n_kv;
@@ -527,11 +600,7 @@ void palu_decode_kernel(const DecodeArgs a) {
     b = rb;
     kvh = fdiv(gid - base, fn);
     const int j = gid - base - kvh * n_chunks;
-    if (j == 0 && threadIdx.x == 0) {       // the item's entry for the merge kernel
-      int* ent = reinterpret_cast<int*>(a.ws + (long long)a.n_wg * 16 * (RV + 2)) + 2 * (b * a.n_kv + kvh);
-      ent[0] = gid;
-      ent[1] = n_chunks;
-    }
+    first_chunk = gid - j;                  // the item's chunks are workgroups first_chunk .. + n_chunks - 1
     s_lo = 64 * fdiv(j * np, fn);
     s_hi = min(row_len(a, b), 64 * fdiv((j + 1) * np, fn));
   }
@@ -540,6 +609,7 @@ void palu_decode_kernel(const DecodeArgs a) {
   s_lo = __builtin_amdgcn_readfirstlane(s_lo);
   s_hi = __builtin_amdgcn_readfirstlane(s_hi);
   n_chunks = __builtin_amdgcn_readfirstlane(n_chunks);
+  first_chunk = __builtin_amdgcn_readfirstlane(first_chunk);
   const int grp = KFULL ? kvh : kvh / a.hpg;
   const int nblk = s_hi > s_lo ? (s_hi - s_lo + BLK - 1) / BLK : 0;
 
@@ -1063,64 +1133,21 @@ void palu_decode_kernel(const DecodeArgs a) {
       OutT* o = static_cast<OutT*>(a.out) + out_index(a, bs, ((long long)kvh * a.rep + h) * RV + r, (long long)a.n_q * RV);
       store_out(o, L > 0.f ? acc / L : 0.f);
     } else {
+      // the chunk's partial, written through to memory (system-scope stores bypass the XCD's L2, so the
+      // workgroup that merges it reads it from any XCD without a cache write-back)
       float* wrow = a.ws + ((long long)blockIdx.x * 16 + h) * (RV + 2);
-      wrow[r] = acc;
-      if (r == 0) { wrow[RV] = M; wrow[RV + 1] = L; }
-    }
-  }
-}
-
-// Merge the chunk partials of every split item: out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)
-// over the item's chunks. One workgroup per (item, query head), one thread per output column; the
-// item's first chunk left (first slot, chunk count) after the partial slots. Items in one chunk were
-// written by the decode kernel itself. The partials of MC chunks are loaded together (one round trip
-// to memory per MC chunks, not one per load); the chunks past MC are folded in with a running rescale.
-template <int RV, typename OutT>
-__global__ __launch_bounds__(RV) void palu_merge_kernel(const DecodeArgs a) {
-  constexpr int MC = 8;
-  const int item = blockIdx.x / a.rep, h = blockIdx.x - item * a.rep;
-  const int b = item / a.n_kv, kvh = item - b * a.n_kv;
-  const int* ent = reinterpret_cast<const int*>(a.ws + (long long)a.n_wg * 16 * (RV + 2)) + 2 * item;
-  const int first = ent[0], nc = ent[1];
-  if (nc <= 1) return;
-  const int r = threadIdx.x;
-  const float* ws = a.ws + ((long long)first * 16 + h) * (RV + 2);
-  constexpr long long SLOT = 16 * (RV + 2);
-  float M = NEG_INF, L = 0.f, acc = 0.f;
-  for (int s0 = 0; s0 < nc; s0 += MC) {
-    float mv[MC], lv[MC], ov[MC];
-#pragma unroll
-    for (int i = 0; i < MC; ++i) {
-      const float* row = ws + min(s0 + i, nc - 1) * SLOT;   // clamped into the item's slots
-      mv[i] = row[RV];
-      lv[i] = row[RV + 1];
-      ov[i] = row[r];
-    }
-    float Mn = M;
-#pragma unroll
-    for (int i = 0; i < MC; ++i)
-      if (s0 + i < nc) Mn = fmaxf(Mn, mv[i]);
-    if (Mn == NEG_INF) continue;            // every chunk so far empty
-    const float c = __builtin_amdgcn_exp2f(M - Mn);   // 0 while M is -inf
-    L *= c;
-    acc *= c;
-#pragma unroll
-    for (int i = 0; i < MC; ++i) {
-      if (s0 + i < nc) {
-        const float f = __builtin_amdgcn_exp2f(mv[i] - Mn);
-        L += lv[i] * f;
-        acc += ov[i] * f;
+      __hip_atomic_store(wrow + r, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      if (r == 0) {
+        __hip_atomic_store(wrow + RV, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(wrow + RV + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       }
     }
-    M = Mn;
   }
-  OutT* o = static_cast<OutT*>(a.out) + out_index(a, b, ((long long)kvh * a.rep + h) * RV + r, (long long)a.n_q * RV);
-  store_out(o, L > 0.f ? acc / L : 0.f);
+  if (n_chunks > 1) merge_split_item<RV, NW, OutT>(a, smem, first_chunk, n_chunks, b, kvh);
 }
 
-
 template <int RK, int RV, bool KFULL, bool TILED, bool PAGED, typename TabT, typename OutT, int NW, int IPW = 1>
-int launch_nw(const DecodeArgs& a, int items, hipStream_t stream) {
+int launch_nw(const DecodeArgs& a, hipStream_t stream) {
   using SM = Smem<RK, RV, KFULL, NW, IPW>;
   auto kern = palu_decode_kernel<RK, RV, KFULL, TILED, PAGED, NW, TabT, OutT, IPW>;
   const int lds = SM::bytes(a.S) + (PAGED ? ((a.S >> 5 >> a.page_shift) + 2) * 4 : 0);
@@ -1134,11 +1161,6 @@ int launch_nw(const DecodeArgs& a, int items, hipStream_t stream) {
   hipLaunchKernelGGL(kern, dim3(a.n_wg), dim3(NW * 64), lds, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(PALU_EHIP, "decode kernel launch: %s", hipGetErrorString(e));
-  if (a.balanced) {
-    hipLaunchKernelGGL((palu_merge_kernel<RV, OutT>), dim3(items * a.rep), dim3(RV), 0, stream, a);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(PALU_EHIP, "merge kernel launch: %s", hipGetErrorString(e));
-  }
   return PALU_OK;
 }
 
@@ -1153,6 +1175,7 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
   // Chunks of the length-aware plan are short: there the fixed block order (no round trip to the
   // shared counter per pair) is the faster one, and it is reproducible as well.
   if (a.balanced) a.deterministic = 1;
+  a.epoch = a.balanced ? next_epoch() : 0;
   const size_t need = decode_ws_bytes(items, RV);
   if (need > 0 && (a.ws == nullptr || a.ws_bytes < need))
     return fail(PALU_EINVAL, "workspace of %zu bytes needed (palu_decode_workspace_bytes), got %zu", need, a.ws_bytes);
@@ -1166,10 +1189,10 @@ int launch(const DecodeArgs& a0, hipStream_t stream) {
     if (!a.balanced && items >= 2 * TARGET_WGS && a.B % 2 == 0 &&
         Smem<RK, RV, KFULL, 8, 2>::bytes(a.S) <= 160 * 1024) {
       a.n_wg = items / 2;
-      return launch_nw<RK, RV, KFULL, TILED, PAGED, TabT, OutT, 8, 2>(a, items, stream);
+      return launch_nw<RK, RV, KFULL, TILED, PAGED, TabT, OutT, 8, 2>(a, stream);
     }
   }
-  return launch_nw<RK, RV, KFULL, TILED, PAGED, TabT, OutT, NW>(a, items, stream);
+  return launch_nw<RK, RV, KFULL, TILED, PAGED, TabT, OutT, NW>(a, stream);
 }
 
 template <int RK, bool KFULL, bool TILED, bool PAGED, typename TabT, typename OutT>
