@@ -48,12 +48,16 @@ def test_decoder_teacher_forced_matches_lowrank_llama(gpu, layout, vocab):
     """vocab 1024: every decode projection tiled, so the step is the fused one (QKV epilogue in the
     projection, residual add in the output projection, FFN norm folded into gate / up); vocab 1000: the
     LM head is not a multiple of 16 columns, so the step runs its separate norms over row-major
-    activations (with the gate / up weight still folded)."""
+    activations (with the gate / up weight still folded). The norms' weights are drawn around 1, so the
+    folding is exercised."""
     pytest.importorskip("transformers")
     args = pm.ModelArgs(dim=512, n_layers=3, n_heads=4, n_kv_heads=2, vocab_size=vocab, ffn_dim=1024,
                         max_seq_len=128, max_batch_size=2)
     dense = []
     sd = pm.random_palu_state_dict(args, [40, 64, 128], [32, 128, 72], gpu, seed=11, std=0.05, dense_out=dense)
+    gn = torch.Generator().manual_seed(12)
+    for key in [k for k in sd if k.endswith("_norm.weight") or k == "norm.weight"]:
+        sd[key] = (1 + 0.2 * torch.randn(args.dim, generator=gn)).to(sd[key].device, sd[key].dtype)
     assert args.palu.rank_k == [64, 64, 128] and args.palu.rank_v == [32, 128, 96]
     hf_w = _hf_weights(sd, dense, args.n_layers)
     cfg = dict(dim=args.dim, n_layers=args.n_layers, n_heads=args.n_heads, n_kv_heads=args.n_kv_heads,
@@ -62,6 +66,7 @@ def test_decoder_teacher_forced_matches_lowrank_llama(gpu, layout, vocab):
     oracle = ref.lowrank_llama(cfg, hf_w, [ref.Factors(lr.k_VT, lr.k_U, lr.v_VT, lr.v_U) for _, lr in dense])
     model = pm.Transformer(args, sd, gpu, cache_layout=layout)
     assert model._fused_step == (vocab % 16 == 0)
+    assert all(L["w13"].in_scale_folded for L in model.layers)
 
     B, S, steps = 2, 45, 7
     g = torch.Generator().manual_seed(2)

@@ -200,7 +200,7 @@ def test_split_items_repeat_exactly_on_one_shared_workspace(gpu):
     """Split items (8 rows x 8 KV heads on a 256-workgroup plan) merge inside the decode launch: each
     chunk counts itself into an 8-byte counter of its item in the workspace, and the chunk that completes
     the count merges the item. Two inputs alternate on one workspace that first holds stale counter words
-    (the fixed tag with an old call number and a nonzero count), with a call of other widths in between
+    (the fixed tag with a call number no launch carries and a nonzero count), with a call of other widths in between
     whose partial slots overlay these calls' counters: every output must equal its input's first output
     bit for bit, and match the oracle."""
     S, ps = 8192, 64
@@ -214,7 +214,7 @@ def test_split_items_repeat_exactly_on_one_shared_workspace(gpu):
     need = max(_native.load().palu_decode_workspace_bytes(8, 8, S, c[2].shape[-1]) for c in cases)
     assert need > 0, "the plan must split items for this test"
     ws = torch.empty(need // 8 + 1, dtype=torch.int64, device=gpu)
-    stale = (0xA5C3 << 48) | (1 << 16) | 5                             # call number 1, five chunks counted
+    stale = (0xA5C3 << 48) | (0 << 16) | 5                 # call number 0 (no launch's), five chunks counted
     ws.fill_(stale - (1 << 64))
     cos, sin = ref.cos_sin_tables(HD, S, THETA, LLAMA3)
     first = {}

@@ -118,8 +118,8 @@ struct DecodeArgs {
 int fail(int code, const char* fmt, ...);
 extern thread_local char g_err[1024];
 
-// Chunk counters of split items (see decode_ws_bytes): bits 63..48 a fixed tag, 47..16 the call number
-// (next_epoch, one per decode launch in the process), 15..0 the count of the item's chunks done.
+// Last-finisher counters (count_done; the chunks of split decode items): bits 63..48 a fixed tag,
+// 47..16 the call number (next_epoch, one per launch that counts), 15..0 the count so far.
 constexpr unsigned long long CHUNK_TAG = 0xA5C3ull << 48;
 unsigned long long next_epoch();   // defined in palu_capi.hip
 
@@ -453,35 +453,46 @@ __device__ __forceinline__ float4 load4f<__bf16>(const __bf16* p) {
   return make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
 }
 
-// A split item's chunks merge inside the decode launch (no second launch). Each chunk's workgroup has
-// written its partial (O, m, l) with system-scope stores, which write through to memory; once they have
-// completed it counts itself into the item's 8-byte counter (a system-scope compare-and-swap), and the
-// workgroup whose count completes the item reads every chunk's partial with system-scope loads (past
-// the XCDs' L2s, so no cache write-back or invalidate is needed) and writes
-// out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), chunks in order: the result does not depend on
-// which workgroup finishes last. That workgroup also leaves the counter at zero. A counter word whose
-// upper 48 bits are not this call's tag (another call's, or memory never written) counts as zero.
-// smem: any LDS word no wave reads any more.
+// Last-finisher counting across the workgroups of one launch. Each of nc workgroups that produce parts
+// of one result has written its part with system-scope stores (global stores that write through past
+// the XCD's L2 to memory) and waited for them to complete; then one thread calls count_done, which adds
+// the workgroup to the result's 8-byte counter with a system-scope compare-and-swap and returns true for
+// the workgroup whose count completes the result. That workgroup reads the parts with system-scope loads
+// (from memory, whichever XCD wrote them: no L2 write-back or invalidate, no fence) and leaves the
+// counter at zero. A counter word carries a fixed tag and the call number in its upper 48 bits (tag,
+// from next_epoch; its low 16 bits zero) and the count below; a word with other upper bits (another
+// call's, memory never written) counts as zero, so counters need no clearing between calls.
+__device__ __forceinline__ bool count_done(unsigned long long* ctr, unsigned long long tag, int nc) {
+  unsigned long long old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM), nw;
+  int done;
+  do {
+    done = (((old & ~0xFFFFull) == tag) ? (int)(old & 0xFFFF) : 0) + 1;
+    nw = tag | (unsigned long long)(done == nc ? 0 : done);
+  } while (!__hip_atomic_compare_exchange_strong(ctr, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_SYSTEM));
+  return done == nc;
+}
+
+// The workgroup-wide step before and around count_done: every thread's system-scope stores complete,
+// thread 0 counts, and the answer (uniform) comes back through the LDS word *flag.
+__device__ __forceinline__ bool workgroup_count_done(unsigned long long* ctr, unsigned long long tag, int nc, int* flag) {
+  __builtin_amdgcn_s_waitcnt(0);            // this thread's part stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) flag[0] = count_done(ctr, tag, nc) ? 1 : 0;
+  __syncthreads();
+  return flag[0] != 0;
+}
+
+// A split item's chunks merge inside the decode launch (no second launch): each chunk's workgroup has
+// written its partial (O, m, l) with system-scope stores, counts itself into the item's counter, and the
+// workgroup that completes the item writes out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), chunks in
+// order: the result does not depend on which workgroup finishes last. smem: any LDS word no wave reads
+// any more.
 template <int RV, int NW, typename OutT>
 __device__ __forceinline__ void merge_split_item(const DecodeArgs& a, char* smem, int first, int nc, int b, int kvh) {
-  __builtin_amdgcn_s_waitcnt(0);            // this thread's partial stores have completed
-  __syncthreads();
-  int* last = reinterpret_cast<int*>(smem);
-  if (threadIdx.x == 0) {
-    unsigned long long* ctr =
-        reinterpret_cast<unsigned long long*>(a.ws + (long long)a.n_wg * 16 * (RV + 2)) + (b * a.n_kv + kvh);
-    const unsigned long long tag = a.epoch;  // low 16 bits zero
-    unsigned long long old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM), nw;
-    int done;
-    do {
-      done = (((old & ~0xFFFFull) == tag) ? (int)(old & 0xFFFF) : 0) + 1;
-      nw = tag | (unsigned long long)(done == nc ? 0 : done);
-    } while (!__hip_atomic_compare_exchange_strong(ctr, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_SYSTEM));
-    last[0] = done == nc;
-  }
-  __syncthreads();
-  if (!last[0]) return;                     // uniform
+  unsigned long long* ctr =
+      reinterpret_cast<unsigned long long*>(a.ws + (long long)a.n_wg * 16 * (RV + 2)) + (b * a.n_kv + kvh);
+  if (!workgroup_count_done(ctr, a.epoch, nc, reinterpret_cast<int*>(smem))) return;   // uniform
   constexpr int MC = 8;                     // chunk partials loaded together per round trip
   constexpr long long SLOT = 16 * (RV + 2);
   for (int e = threadIdx.x; e < a.rep * RV; e += NW * 64) {
