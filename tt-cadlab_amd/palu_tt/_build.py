@@ -20,8 +20,10 @@ LIB_DIR = PKG_DIR / "_lib"
 LIB_NAME = "libpalu_mi355x.so"
 SOURCES = ["palu_capi.hip", "palu_decode_rows.hip", "palu_decode_tiled.hip", "palu_decode_rows_paged.hip",
            "palu_decode_tiled_paged.hip", "palu_decode_tiled_k16.hip", "palu_decode_tiled_paged_k16.hip",
-           "palu_decode_full.hip", "palu_glrd.hip", "palu_decoder.hip", "palu_linear.hip"]
-HEADERS = ["palu_kernel.h"]
+           "palu_decode_full.hip", "palu_glrd.hip", "palu_glrd_narrow.hip", "palu_decoder.hip", "palu_linear.hip"]
+HEADERS = ["palu_kernel.h", "palu_glrd_scores.h"]
+# Per-file flags: the narrow-rank grouped-latent scores kernels keep their MFMA results in VGPRs.
+SOURCE_FLAGS = {"palu_glrd_narrow.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -62,7 +64,8 @@ def build_native(verbose: bool = False, extra_flags=(), jobs: int = 0) -> Path:
     jobs = jobs or min(len(SOURCES), max(1, min(16, os.cpu_count() or 1)))
     with tempfile.TemporaryDirectory(prefix="palu_build_") as td:
         objs = [Path(td) / (Path(s).stem + ".o") for s in SOURCES]
-        cmds = [[hipcc(), *HIPCC_FLAGS, *extra_flags, f"-I{INCLUDE}", "-c", str(CSRC / s), "-o", str(o)]
+        cmds = [[hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(s, []), *extra_flags, f"-I{INCLUDE}", "-c", str(CSRC / s),
+                 "-o", str(o)]
                 for s, o in zip(SOURCES, objs)]
         if verbose:
             for c in cmds:
