@@ -230,17 +230,20 @@ def test_linear_partials_mode(gpu, rtw, ks):
     _check_linear(s, _linear_ref(x, w))
 
 
-@pytest.mark.parametrize("rows,x_tiled", [(64, True), (64, False), (13, True)])
-def test_linear_swiglu_mode(gpu, rows, x_tiled):
+@pytest.mark.parametrize("rows,x_tiled,rtw", [(64, True, 0), (64, False, 0), (13, True, 0), (64, True, 7), (29, True, 8),
+                                              (64, True, 1), (64, True, 3)])
+def test_linear_swiglu_mode(gpu, rows, x_tiled, rtw):
     """The gate / up projection with SwiGLU in its epilogue (interleave_gate_up weight, tiled output)
-    equals silu(x w_gate^T) * (x w_up^T) from fp32 products, one bf16 rounding at the end."""
-    g = torch.Generator().manual_seed(rows + x_tiled)
+    equals silu(x w_gate^T) * (x w_up^T) from fp32 products, one bf16 rounding at the end. Explicit row
+    tiles per workgroup: each wave's tiles are stored in pairs, so 7 and 3 (an odd count per wave, 192
+    row tiles leaving a short last group for 7) and 1 (one unpaired tile) cover the unpaired ends."""
+    g = torch.Generator().manual_seed(rows + x_tiled + 100 * rtw)
     k, f = 1024, 1536
     x = torch.randn(rows, k, generator=g).to(gpu, torch.bfloat16)
     wg = (torch.randn(f, k, generator=g) * 0.05).to(gpu, torch.bfloat16)
     wu = (torch.randn(f, k, generator=g) * 0.05).to(gpu, torch.bfloat16)
-    lin = decoder_ops.DecodeLinear(None, 64, gate_up=(wg, wu))
-    assert lin.tiled and lin.ks == 1
+    lin = decoder_ops.DecodeLinear(None, 64, gate_up=(wg, wu), rtw=rtw, ks=1 if rtw else 0)
+    assert lin.tiled and lin.ks == 1 and (not rtw or lin.rtw == rtw)
     xa = decoder_ops.tile_rows(x) if x_tiled else x
     out = lin(xa, x_tiled=x_tiled, rows=rows)
     torch.cuda.synchronize()
@@ -429,19 +432,21 @@ def test_linear_residual_equals_partials_plus_h(gpu, rows, n, k, x_tiled, with_t
         assert torch.isnan(pad.float()).all()
 
 
-@pytest.mark.parametrize("rows,x_tiled", [(64, True), (64, False), (13, True)])
-def test_linear_swiglu_rmsnorm(gpu, rows, x_tiled):
+@pytest.mark.parametrize("rows,x_tiled,rtw", [(64, True, 0), (64, False, 0), (13, True, 0), (64, True, 7), (21, True, 5),
+                                              (64, True, 2)])
+def test_linear_swiglu_rmsnorm(gpu, rows, x_tiled, rtw):
     """The gate / up launch over RMS-normalised rows (norm weight folded into the gate / up columns) against
     fp32 torch: silu(g) * u of rmsnorm(x) w^T; and against palu_rmsnorm followed by the SwiGLU projection
-    within their two bf16 roundings. Rows of the tiled input past the live count hold NaN and are ignored."""
-    g = torch.Generator().manual_seed(rows + 7 * x_tiled)
+    within their two bf16 roundings. Rows of the tiled input past the live count hold NaN and are ignored.
+    rtw 7 (the decoder's gate / up split) and 5 leave an odd tile per wave and a short last group."""
+    g = torch.Generator().manual_seed(rows + 7 * x_tiled + 100 * rtw)
     k, f, eps = 2048, 1536, 1e-5
     x = (torch.randn(rows, k, generator=g) * 3).to(gpu, torch.bfloat16)
     nw = (1 + 0.2 * torch.randn(k, generator=g)).to(gpu, torch.bfloat16)
     wg = (torch.randn(f, k, generator=g) * 0.05).to(gpu, torch.bfloat16)
     wu = (torch.randn(f, k, generator=g) * 0.05).to(gpu, torch.bfloat16)
-    lin = decoder_ops.DecodeLinear(None, 64, gate_up=(wg, wu), in_scale=nw)
-    assert lin.tiled and lin.in_scale_folded
+    lin = decoder_ops.DecodeLinear(None, 64, gate_up=(wg, wu), in_scale=nw, rtw=rtw, ks=1 if rtw else 0)
+    assert lin.tiled and lin.in_scale_folded and (not rtw or lin.rtw == rtw)
     if x_tiled:
         pad = torch.full((64, k), float("nan"), dtype=torch.bfloat16, device=gpu)
         pad[:rows] = x

@@ -222,7 +222,10 @@ __global__ __launch_bounds__(NW * 64) void palu_linear_kernel(const __bf16* __re
 
   // The waves' partials meet in LDS (slot layout [wave][r][mt][lane] of f32x4); each wave then sums
   // the NW slots of every NW-th (r, mt) tile and stores that tile, so the epilogue's arithmetic and
-  // stores are spread over the SIMDs.
+  // stores are spread over the SIMDs. Every LDS read of the sums is issued before the first is used and
+  // the tiles are stored under a predicate rather than a branch per tile: the epilogue sits between the
+  // last weight load and the end of the launch, and one round trip to LDS per tile (its reads, then the
+  // next tile's) made it 1.2 us longer for the gate / up shape.
 #pragma unroll
   for (int r = 0; r < RTW; ++r)
 #pragma unroll
@@ -230,75 +233,105 @@ __global__ __launch_bounds__(NW * 64) void palu_linear_kernel(const __bf16* __re
   float* rss = reinterpret_cast<float*>(smem + SM::RED);   // [wave][row] sums of x^2
   if constexpr (EPI == EPI_SWIGLU_NORM) {
     // lanes (g, mm), g = 0..3, hold columns 8 g .. 8 g + 7 of every k tile of row 16 mt + mm
+    float s16[LIN_MT];
 #pragma unroll
-    for (int mt = 0; mt < LIN_MT; ++mt) {
-      ss[mt] += __shfl_xor(ss[mt], 16, 64);
-      ss[mt] += __shfl_xor(ss[mt], 32, 64);
-      if (g == 0) rss[w * 64 + 16 * mt + mm] = ss[mt];
+    for (int mt = 0; mt < LIN_MT; ++mt) s16[mt] = ss[mt] + __shfl_xor(ss[mt], 16, 64);
+#pragma unroll
+    for (int mt = 0; mt < LIN_MT; ++mt) ss[mt] = s16[mt] + __shfl_xor(s16[mt], 32, 64);
+    if (g == 0) {
+#pragma unroll
+      for (int mt = 0; mt < LIN_MT; ++mt) rss[w * 64 + 16 * mt + mm] = ss[mt];
     }
   }
   __syncthreads();
 
+  // Wave w's tiles t = w + i NW, i < NT (clamped to the last tile for the loads; tiles past it are not
+  // stored). Lane (g, mm) of tile (r, mt) holds y^T[16 (rt0 + r) + 4 g + i][16 mt + mm], i < 4: four
+  // consecutive output columns of activation row 16 mt + mm.
+  f32x4 v[NT];
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
-    const int t = w + i * NW;                              // uniform per wave
-    if (t >= RTW * LIN_MT) break;
-    const int r = t / LIN_MT, mt = t % LIN_MT;
-    f32x4 v = red[t * 64 + lane];
+    const int t = min(w + i * NW, RTW * LIN_MT - 1);
+    v[i] = red[t * 64 + lane];
 #pragma unroll
-    for (int q = 1; q < NW; ++q) v += red[q * SM::SLOT + t * 64 + lane];
-    // Lane (g, mm) of tile (r, mt) holds y^T[16 (rt0 + r) + 4 g + i][16 mt + mm], i < 4: four consecutive
-    // output columns of activation row 16 mt + mm.
-    const int row = 16 * mt + mm;
-    if constexpr (SWIGLU) {
-      // Gate / up pairs: rows 0-7 of row tile rt are gate columns 8 rt .. 8 rt + 7 and rows 8-15 the up
-      // columns of the same outputs (tile_weight of the interleaved weight), so lane (g, mm) with g < 2
-      // holds gate columns 8 rt + 4 g + i and lane (g + 2, mm), 32 lanes on, the matching up values.
-      // out = silu(gate) * up, stored in the tiled activation layout (64 rows x n / 2) the next
-      // projection reads.
-      if constexpr (EPI == EPI_SWIGLU_NORM) {
-        float tot = 0.f;
+    for (int q = 1; q < NW; ++q) v[i] += red[q * SM::SLOT + t * 64 + lane];
+  }
+  if constexpr (EPI == EPI_SWIGLU_NORM) {
+    // the row scale rsqrt(mean x^2 + eps): with NW a multiple of LIN_MT (asserted below) every tile of
+    // wave w lies in activation tile w % LIN_MT, one row per lane
+    const int row = 16 * (w % LIN_MT) + mm;
+    float tot = 0.f;
 #pragma unroll
-        for (int q = 0; q < NW; ++q) tot += rss[q * 64 + row];
-        v *= rsqrtf(tot * ep.inv_k + ep.eps);
+    for (int q = 0; q < NW; ++q) tot += rss[q * 64 + row];
+    const float sc = rsqrtf(tot * ep.inv_k + ep.eps);
+#pragma unroll
+    for (int i = 0; i < NT; ++i) v[i] *= sc;
+  }
+  if constexpr (SWIGLU) {
+    static_assert(NW % LIN_MT == 0, "the SwiGLU epilogue pairs tiles of one activation tile");
+    // Gate / up pairs: rows 0-7 of row tile rt are gate columns 8 rt .. 8 rt + 7 and rows 8-15 the up
+    // columns of the same outputs (tile_weight of the interleaved weight), so lanes g < 2 of a tile hold
+    // gate values and lanes g + 2, 32 lanes on, the matching up values. Tiles i and i + 1 of a wave
+    // share their activation rows; one v_permlane32_swap of the upper half of tile i with the lower half
+    // of tile i + 1 puts the gates of both in one register and the ups in the other, so that every lane
+    // computes and stores one output of one of the two tiles (lanes 32-63: tile i + 1, output columns
+    // 8 rt + 4 (g - 2) .. + 3). out = silu(gate) * up, stored in the tiled activation layout (64 rows x
+    // n / 2) the next projection reads.
+    const int row = 16 * (w % LIN_MT) + mm;
+#pragma unroll
+    for (int i = 0; i < NT; i += 2) {
+      const int j = i + 1 < NT ? i + 1 : i;
+      f32x4 gv, uv;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i][k]), __float_as_uint(v[j][k]), false, false);
+        gv[k] = __uint_as_float(sw[0]);
+        uv[k] = __uint_as_float(sw[1]);
       }
-      f32x4 up;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) up[k] = __shfl_xor(v[k], 32, 64);
-      if (g >= 2 || row >= m || r >= rt_cnt) continue;
-      const int col = 8 * (rt0 + r) + 4 * g;
       bf16x4 o;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = (__bf16)((v[k] / (1.f + __expf(-v[k]))) * up[k]);
-      *reinterpret_cast<bf16x4*>(y + tiled_row_offset(row, col)) = o;
-    } else if constexpr (EPI == EPI_RESID) {
-      // h + y rounded to bf16 once (the residual stream), in place and in the tiled layout
-      if (row >= m || r >= rt_cnt) continue;
-      const int col = 16 * (rt0 + r) + 4 * g;
-      bf16x4 o;
+      for (int k = 0; k < 4; ++k) o[k] = (__bf16)((gv[k] / (1.f + __expf(-gv[k]))) * uv[k]);
+      const int t = w + (g < 2 ? i : j) * NW, r = t / LIN_MT;
+      if (t < RTW * LIN_MT && r < rt_cnt && row < m && (g < 2 || j != i))
+        *reinterpret_cast<bf16x4*>(y + tiled_row_offset(row, 8 * (rt0 + r) + 4 * (g & 1))) = o;
+    }
+  } else {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = (__bf16)((float)hpre[i][k] + v[k]);
-      *reinterpret_cast<bf16x4*>(ep.h + row * ep.ldh + col) = o;
-      if (ep.h_tiled) *reinterpret_cast<bf16x4*>(ep.h_tiled + tiled_row_offset(row, col)) = o;
-    } else if constexpr (EPI == EPI_QKV) {
-      // Columns col .. col + 3 of QKV row `row` lie in one q head or one group's K or V slice (the entry
-      // point checks that the three ranges do not overlap and start on multiples of 8).
-      if (row >= m || r >= rt_cnt) continue;
-      int gi, c;
-      const int kind = qkv_part_of(ep.q, 16 * (rt0 + r) + 4 * g, gi, c);
-      if (kind < 0) continue;
-      float vv[4] = {v[0], v[1], v[2], v[3]};
-      qkv_store<4>(ep.q, row, ppre[i], kind, gi, c, vv);
-    } else {
-      if (row >= m || r >= rt_cnt) continue;
-      const long long col = 16LL * (rt0 + r) + 4 * g;
-      if (part) {
-        *reinterpret_cast<f32x4*>(part + ((long long)ks * m + row) * (16LL * n16) + col) = v;
+    for (int i = 0; i < NT; ++i) {
+      const int t = w + i * NW;
+      const int r = t / LIN_MT, row = 16 * (t % LIN_MT) + mm;
+      const bool ok = t < RTW * LIN_MT && r < rt_cnt && row < m;
+      if constexpr (EPI == EPI_RESID) {
+        // h + y rounded to bf16 once (the residual stream), in place and in the tiled layout
+        if (ok) {
+          const int col = 16 * (rt0 + r) + 4 * g;
+          bf16x4 o;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) o[k] = (__bf16)((float)hpre[i][k] + v[i][k]);
+          *reinterpret_cast<bf16x4*>(ep.h + row * ep.ldh + col) = o;
+          if (ep.h_tiled) *reinterpret_cast<bf16x4*>(ep.h_tiled + tiled_row_offset(row, col)) = o;
+        }
+      } else if constexpr (EPI == EPI_QKV) {
+        // Columns col .. col + 3 of QKV row `row` lie in one q head or one group's K or V slice (the
+        // entry point checks that the three ranges do not overlap and start on multiples of 8).
+        int gi, c;
+        const int kind = ok ? qkv_part_of(ep.q, 16 * (rt0 + r) + 4 * g, gi, c) : -1;
+        if (kind >= 0) {
+          float vv[4] = {v[i][0], v[i][1], v[i][2], v[i][3]};
+          qkv_store<4>(ep.q, row, ppre[i], kind, gi, c, vv);
+        }
       } else {
-        bf16x4 o;
+        if (ok) {
+          const long long col = 16LL * (rt0 + r) + 4 * g;
+          if (part) {
+            *reinterpret_cast<f32x4*>(part + ((long long)ks * m + row) * (16LL * n16) + col) = v[i];
+          } else {
+            bf16x4 o;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) o[k] = (__bf16)v[k];
-        *reinterpret_cast<bf16x4*>(y + row * ldy + col) = o;
+            for (int k = 0; k < 4; ++k) o[k] = (__bf16)v[i][k];
+            *reinterpret_cast<bf16x4*>(y + row * ldy + col) = o;
+          }
+        }
       }
     }
   }
