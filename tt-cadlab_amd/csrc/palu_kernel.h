@@ -384,13 +384,17 @@ __device__ __forceinline__ int load_uniform(const int32_t* p, long long i) {
   return reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(reinterpret_cast<uintptr_t>(p))[i];
 }
 
-__device__ __forceinline__ int row_len(const DecodeArgs& a, int b) {
-  const int len = load_uniform(a.cur_pos, b) + 1;
+__device__ __forceinline__ int clamp_len(const DecodeArgs& a, int pos) {
+  const int len = pos + 1;
   return len < 0 ? 0 : (len > a.S ? a.S : len);
 }
+__device__ __forceinline__ int row_len(const DecodeArgs& a, int b) { return clamp_len(a, load_uniform(a.cur_pos, b)); }
+
 __device__ __forceinline__ int row_pairs(const DecodeArgs& a, int b) { return (row_len(a, b) + 63) >> 6; }
 
-// The plan's chunk length T in pairs (the same value in every lane of every wave that calls it).
+// The plan's chunk length T in pairs (the same value in every lane of every wave that calls it). The
+// rows' positions are read through the scalar cache: one line holds 16 rows, so B rows cost a miss per
+// 16 rows and hits for the rest.
 __device__ int plan_chunk_pairs(const DecodeArgs& a) {
   const int lane = threadIdx.x & 63;
   const int G = a.n_wg, items = a.B * a.n_kv;
@@ -568,8 +572,8 @@ void palu_decode_kernel(const DecodeArgs a) {
   _Float16* qx = reinterpret_cast<_Float16*>(smem + SM::QX_OFFSET + w * SM::QX_WAVE_BYTES);
 
   // Latent mode: the angle-table rows are the same for every workgroup and depend on nothing below, so
-  // their loads are issued first, ahead of the plan's scalar reads of cur_pos. Rows t < 64 serve the K
-  // rotation, 64*Lo (Lo < 16) and 1024*H the query's pair base; one coalesced row per wave load.
+  // their loads are issued first, ahead of the plan. Rows t < 64 serve the K rotation, 64*Lo (Lo < 16)
+  // and 1024*H the query's pair base; one coalesced row per wave load.
   // Rows: t0 < 8 and 8 t1 (t1 = 1..7) for the K rotation (t = 8 t1 + t0 by angle addition), 64 Lo
   // (Lo < 16) and 1024 H (H < ceil(S / 1024)) for the query's pair base.
   const int n_rows = KFULL ? 0 : 31 + (a.S + 1023) / 1024;
@@ -578,24 +582,30 @@ void palu_decode_kernel(const DecodeArgs a) {
   float4 rowv[KFULL ? 1 : RPW];
   if constexpr (!KFULL) {
     const TabT* cs = static_cast<const TabT*>(a.cs);
+    // Only the rows the sequence length needs are loaded (the branch is uniform): each row load is 16
+    // cache lines for the CU's vector memory pipeline, and RPW rows per wave for every wave held the
+    // second wave of each SIMD about 1.4 us behind the first before its loads went out.
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
       const int r = w + i * NW;
-      int t = row_t(r);
-      t = (r < n_rows && t < a.cs_rows) ? t : 0;
-      rowv[i] = load4f(cs + (long long)t * (2 * HD) + 4 * lane);   // lane < 32: cos, else sin
+      if (r < n_rows) {
+        int t = row_t(r);
+        t = t < a.cs_rows ? t : 0;
+        rowv[i] = load4f(cs + (long long)t * (2 * HD) + 4 * lane);   // lane < 32: cos, else sin
+      }
     }
   }
 
   // This workgroup's item and position range: the whole sequence of item blockIdx.x, or one chunk of
   // the length-aware plan (computed identically, and uniformly, by every wave).
-  int b, kvh, s_lo, s_hi, n_chunks = 1, first_chunk = 0;
+  // A whole item's end (its row length) is read after the first latent blocks are issued, in the
+  // prologue: those loads do not depend on it.
+  int b, kvh, s_lo, s_hi = 0, n_chunks = 1, first_chunk = 0;
   if (!a.balanced) {
     const int item = blockIdx.x + half * a.n_wg;   // two items: n_wg = B * n_kv / 2, so the KV head is shared
     b = item / a.n_kv;
     kvh = item - b * a.n_kv;
     s_lo = 0;
-    s_hi = row_len(a, b);
   } else {
     const FDiv fT = make_fdiv(plan_chunk_pairs(a));
     int base = 0, rb = -1, np = 0;
@@ -618,11 +628,9 @@ void palu_decode_kernel(const DecodeArgs a) {
   b = __builtin_amdgcn_readfirstlane(b);
   kvh = __builtin_amdgcn_readfirstlane(kvh);
   s_lo = __builtin_amdgcn_readfirstlane(s_lo);
-  s_hi = __builtin_amdgcn_readfirstlane(s_hi);
   n_chunks = __builtin_amdgcn_readfirstlane(n_chunks);
   first_chunk = __builtin_amdgcn_readfirstlane(first_chunk);
   const int grp = KFULL ? kvh : kvh / a.hpg;
-  const int nblk = s_hi > s_lo ? (s_hi - s_lo + BLK - 1) / BLK : 0;
 
   const __bf16* kbase = a.k + (PAGED ? 0 : b * a.k_sb) + grp * a.k_sg;
   const __bf16* vbase = a.v + (PAGED ? 0 : b * a.v_sb) + grp * a.v_sg;
@@ -712,8 +720,7 @@ void palu_decode_kernel(const DecodeArgs a) {
   // every NW-th pair. The loop runs complete pairs only; the one or two blocks left after them (an odd
   // full block, a partial last block) go to the wave whose next pair index is npairs, which exactly
   // one wave holds when the loop ends (the indices are w < NW, then counter values NW, NW + 1, ...).
-  const int nfull = s_hi > s_lo ? (s_hi - s_lo) / BLK : 0;   // an empty split (row shorter than s_lo) has none
-  const int npairs = nfull >> 1;
+  // (nfull and npairs follow the prologue, where a whole item's end is read.)
   if (tid < IPW) ctr[tid] = NWI;
   bf16x8 kl[2][KB], vl[VT], kln[2][KB], vln[VT];
   auto fence = []() __attribute__((always_inline)) { __builtin_amdgcn_sched_barrier(0); };
@@ -754,12 +761,14 @@ void palu_decode_kernel(const DecodeArgs a) {
     // vector-memory pipeline serves them in order, so the (L2-hit) table loads of later waves do not
     // queue behind earlier waves' HBM latent loads.
     __syncthreads();
-    // The wave's first block, issued before the row length is known (a wave whose first pair lies past
-    // the row's data loads a block inside the cache instead and never uses it) and after every table
-    // load: loads complete in issue order for the wait counter, so the prologue's waits on the tables
-    // then leave this block in flight. The scheduling fences keep that order. The pair's second block
-    // follows once the table registers are written out.
+    // The wave's first pair of blocks, issued before the row length is known (a wave whose first pair
+    // lies past the row's data loads blocks inside the cache instead and never uses them) and after
+    // every table load: loads complete in issue order for the wait counter, so the prologue's waits on
+    // the tables leave these blocks in flight. The scheduling fences keep that order. Both blocks go
+    // out before the staging below, so that the stream from memory starts at the barrier.
     load_first(0, kl, vl);
+    load_first(1, kln, vln);
+    if (!a.balanced) s_hi = row_len(a, b);
     if (qt < 16 * (HD / 8)) *reinterpret_cast<bf16x8*>(qs_lds + (half * 16 + qh) * HD + qc) = qlive ? qrow : bf16x8{};
     // rows -> [row][f] (cos, sin); lane l < 32 holds cos of f = 2l, 2l+1, lane l >= 32 the sines
 #pragma unroll
@@ -784,7 +793,6 @@ void palu_decode_kernel(const DecodeArgs a) {
         for (int j = 0; j < 8; ++j) ukT[(d0 + j) * SM::UKT_STRIDE + r] = ukv[i][j];
       }
     }
-    load_first(1, kln, vln);
     __syncthreads();
     // K rotation table in lane order: (cos, sin) of t f for t = 8 t1 + t0 < 64 by angle addition of the
     // staged rows t0 and 8 t1 in fp32 (within fp32 rounding of the table's own values, far below the
@@ -806,7 +814,12 @@ void palu_decode_kernel(const DecodeArgs a) {
   } else {
     load_first(0, kl, vl);
     load_first(1, kln, vln);
+    if (!a.balanced) s_hi = row_len(a, b);
   }
+  s_hi = __builtin_amdgcn_readfirstlane(s_hi);
+  const int nblk = s_hi > s_lo ? (s_hi - s_lo + BLK - 1) / BLK : 0;
+  const int nfull = s_hi > s_lo ? (s_hi - s_lo) / BLK : 0;   // an empty split (row shorter than s_lo) has none
+  const int npairs = nfull >> 1;
   if constexpr (PAGED) {
     const int pg_hi = nblk > 0 ? (((s_hi - 1) >> 5) >> a.page_shift) : pg_lo - 1;
     for (int e = tid; e <= pg_hi - pg_lo; e += NW * 64)
