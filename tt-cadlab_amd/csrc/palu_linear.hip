@@ -352,16 +352,16 @@ __global__ __launch_bounds__(256) void palu_linear_reduce_kernel(const float* __
   }
 }
 
-// Register buffers per wave: NB = 8 for workgroups of one or two row tiles (latency-bound), 4 for wider
-// ones (about 8 KB of weights in flight per wave either way).
-#ifndef PALU_LIN_NARROW_DEPTH
-#define PALU_LIN_NARROW_DEPTH 8
-#endif
+// Register buffers per wave: NB = 4 for every width. Workgroups of one or two row tiles load more
+// activation than weight bytes per k tile (4 KB against 1-2 KB), and deeper rings only queue more of
+// those L2 reads ahead of the weights: in graph-captured probes the QKV shape (two row tiles) took 16.4 us
+// at NB 4 against 17.0 at 8 and 18.2 at 12, the output projection's (one row tile) 7.9 against 8.2 us at 8,
+// and the 32-layer decode step 5.02 against 5.06 ms (same-box A/B, three runs each).
 
 template <int RTW, bool XT, int EPI>
 hipError_t launch_cfg(const __bf16* x, long long ldx, int m, const __bf16* wt, int n16, int kt_total, int ks,
                       int ktps, __bf16* y, long long ldy, float* part, const LinEpi& ep, hipStream_t s) {
-  constexpr int NB = RTW <= 2 ? PALU_LIN_NARROW_DEPTH : 4;
+  constexpr int NB = 4;
   constexpr int NW = 4;                                   // one wave per SIMD (8 measured slower end to end)
   auto kern = palu_linear_kernel<RTW, NB, NW, XT, EPI>;
   constexpr int lds = LinSmem<RTW, NW, EPI>::BYTES;
