@@ -1082,6 +1082,10 @@ void palu_decode_kernel(const DecodeArgs a) {
   // that still fits the register budget without spilling (full K, r_k <= 64, r_k + r_v <= 192; the
   // rest refill K together with V after the PV product).
   constexpr bool EARLY_K = KFULL || KB * 32 <= 64 || KB * 32 + RV <= 192;
+  // The blocks left after the full pairs are loaded by the loop like a next pair (below) where both
+  // stay in registers past the loop without spilling: every width but r_k <= 64 (u_k^T in registers)
+  // with r_v >= 112 tiled or >= 96 row-major, whose waves take them one at a time after the loop.
+  constexpr bool TAIL_REGS = KFULL || UK_LDS || RV + (TILED ? 0 : 16) < 112;
   int p = wi;
   while (p < npairs) {
     int pn = p + NWI;
@@ -1093,33 +1097,50 @@ void palu_decode_kernel(const DecodeArgs a) {
     }
     const int b0 = 2 * p;
     const bool hasn = pn < npairs;
-    const int nb0 = s_lo + (hasn ? 2 * pn : b0) * BLK, nb1 = nb0 + BLK;
+    // Index npairs stands for the blocks left after the full pairs (an odd full block and / or the
+    // partial last block): the wave that draws it loads them like a pair here, so they are in its
+    // registers when the loop ends instead of loaded one at a time after it. A missing second one reads
+    // the current pair's second block (in the cache; never used).
+    const bool tailn = TAIL_REGS && pn == npairs && 2 * npairs < nblk;
+    const bool ln0 = hasn || tailn, ln1 = hasn || (tailn && 2 * npairs + 1 < nblk);
+    const int nb0 = s_lo + (ln0 ? 2 * pn : b0) * BLK, nb1 = ln1 ? nb0 + BLK : s_lo + (b0 + 1) * BLK;
     const int pid0 = page_lds(nb0), pid1 = page_lds(nb1);
     if constexpr (!KFULL) make_q(s_lo + b0 * BLK);   // one query rotation serves both blocks of the pair
     compute(full_blk, b0, kl, vl, [&] {
-      if constexpr (EARLY_K) { fence(); load_k(nb0, hasn, pid0, kl); fence(); }
+      if constexpr (EARLY_K) { fence(); load_k(nb0, ln0, pid0, kl); fence(); }
     });
     fence();
-    if constexpr (!EARLY_K) load_k(nb0, hasn, pid0, kl);
-    load_v(nb0, hasn, pid0, vl);
+    if constexpr (!EARLY_K) load_k(nb0, ln0, pid0, kl);
+    load_v(nb0, ln0, pid0, vl);
     fence();
     compute(full_blk, b0 + 1, kln, vln, [&] {
-      if constexpr (EARLY_K) { fence(); load_k(nb1, hasn, pid1, kln); fence(); }
+      if constexpr (EARLY_K) { fence(); load_k(nb1, ln1, pid1, kln); fence(); }
     });
     fence();
-    if constexpr (!EARLY_K) load_k(nb1, hasn, pid1, kln);
-    load_v(nb1, hasn, pid1, vln);
+    if constexpr (!EARLY_K) load_k(nb1, ln1, pid1, kln);
+    load_v(nb1, ln1, pid1, vln);
     fence();
     p = pn;
   }
-  if (p == npairs) {   // an odd full block and / or the partial last block, one at a time
+  if (p == npairs && 2 * npairs < nblk) {
     auto none = [] {};
-    for (int e = 2 * npairs; e < nblk; ++e) {
-      const int base = s_lo + e * BLK;
-      load_blk(base, true, page_lds(base), kl, vl);
-      if constexpr (!KFULL) make_q(s_lo + (e & ~1) * BLK);
-      if (e < nfull) compute(full_blk, e, kl, vl, none);
-      else compute(partial_blk, e, kl, vl, none);
+    const int e0 = 2 * npairs;
+    if constexpr (!KFULL) make_q(s_lo + e0 * BLK);
+    if constexpr (TAIL_REGS) {
+      // The blocks left after the full pairs, already in (kl, vl) and (kln, vln): loaded in this wave's
+      // last loop step, or as its first pair in the prologue when it drew no full pair. The second,
+      // when there is one, is the partial last block.
+      if (e0 < nfull) compute(full_blk, e0, kl, vl, none);
+      else compute(partial_blk, e0, kl, vl, none);
+      if (e0 + 1 < nblk) compute(partial_blk, e0 + 1, kln, vln, none);
+    } else {
+      // one at a time (both held in registers would not fit this width's register budget)
+      for (int e = e0; e < nblk; ++e) {
+        const int base = s_lo + e * BLK;
+        load_blk(base, true, page_lds(base), kl, vl);
+        if (e < nfull) compute(full_blk, e, kl, vl, none);
+        else compute(partial_blk, e, kl, vl, none);
+      }
     }
   }
 
