@@ -306,6 +306,21 @@ int palu_linear_plan(int rows, int n, int k, int* rtw, int* ks);
 /* Workspace bytes of palu_linear_tiled with ks k slices (0 for ks == 1 or invalid shapes). */
 size_t palu_linear_workspace_bytes(int rows, int n, int k, int ks);
 
+/* Greedy pick fused into the LM head: ids[r] (r < rows) = the index of the largest value of row r of
+ * the bf16 result palu_linear_tiled gives with PALU_LINEAR_BF16 and ks = 1 (the same sums in the same
+ * order, rounded the same way), the first one among equal maxima and NaN above every number: what
+ * palu_argmax_rows returns for those logits, which are not written. x, w_tiled, n, k and rtw as in
+ * palu_linear_tiled; a caller workspace of palu_linear_argmax_workspace_bytes(rows, n) bytes (16-byte
+ * aligned) holds one key per row and group of rtw row tiles. Two launches. No counterpart in the
+ * reference's op interface: its generation loop takes the argmax of the host-side logits
+ * (generate.py:53-62); this keeps the greedy pick in the decode step's graph without writing the 64 x
+ * vocab logits and reading them back. */
+int palu_linear_argmax(const void* x, long long ldx, int x_tiled, int rows, const void* w_tiled, int n, int k, int rtw,
+                       int64_t* ids, void* workspace, size_t workspace_bytes, palu_stream_t stream);
+
+/* Workspace bytes of palu_linear_argmax (0 for invalid shapes). */
+size_t palu_linear_argmax_workspace_bytes(int rows, int n);
+
 /* palu_linear_plan with at most max_ks k slices (max_ks = 1: the split for the fused epilogues below,
  * which see whole dot products). */
 int palu_linear_plan_ks(int rows, int n, int k, int max_ks, int* rtw, int* ks);

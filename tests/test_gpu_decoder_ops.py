@@ -172,6 +172,97 @@ def test_linear_tiled_activations(gpu, rows, n, k, rtw, ks):
     _check_linear(a, _linear_ref(x, w))
 
 
+def _argmax_case(gpu, rows, n, k, rtw, x_tiled, seed, plant=None):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, k, generator=g)
+    w = torch.randn(n, k, generator=g) * 0.05
+    if plant:
+        plant(x, w)
+    x, w = x.to(gpu, torch.bfloat16), w.to(gpu, torch.bfloat16)
+    wt = decoder_ops.tile_weight(w, rtw)
+    if x_tiled:
+        padded = torch.zeros(64, k, dtype=torch.bfloat16, device=gpu)
+        padded[:rows] = x
+        xa, kw = decoder_ops.tile_weight(padded, 4), dict(x_tiled=True, rows=rows)
+    else:
+        xa, kw = x, {}
+    ids = decoder_ops.linear_argmax(xa, wt, rtw, **kw)
+    logits = decoder_ops.linear_tiled(xa, wt, rtw, 1, **kw)
+    want = decoder_ops.argmax_rows(logits)
+    torch.cuda.synchronize()
+    return ids, want, logits
+
+
+@pytest.mark.parametrize("rows,n,k,rtw,x_tiled", [(64, 128256, 256, 8, True), (9, 128256, 256, 8, False),
+                                                   (64, 4800, 1344, 1, True), (33, 16016, 96, 3, False),
+                                                   (64, 16 * 2053, 160, 8, True), (1, 256, 1024, 2, False),
+                                                   (64, 4096, 4096, 8, True)])
+def test_linear_argmax_matches_argmax_of_the_logits(gpu, rows, n, k, rtw, x_tiled):
+    """The fused LM-head pick equals argmax_rows of linear_tiled's bf16 logits (ks = 1) id for id, and
+    torch.argmax of those logits: the LM head's 1,002 groups of 8 row tiles and fewer groups than
+    workgroups, ragged last groups, short rows, k tiles fewer than the waves, row-major and tiled x."""
+    ids, want, logits = _argmax_case(gpu, rows, n, k, rtw, x_tiled, seed=n + rows + rtw)
+    assert ids.dtype == torch.int64 and ids.shape == (rows,)
+    assert torch.equal(ids, want)
+    assert torch.equal(ids.cpu(), torch.argmax(logits.float().cpu(), dim=-1))
+
+
+def test_linear_argmax_ties_nan_and_zeros(gpu):
+    """Equal maxima pick the first column, within a group of row tiles and across groups (duplicated
+    weight rows give bit-identical logits); a NaN column wins over every number, the first of two; an
+    all-zero activation row gives all-zero logits and id 0; torch.argmax agrees on every row."""
+    n, k = 16 * 700, 256
+
+    def plant(x, w):
+        w[3000] = w[100] * 4                                  # row 0's maximum, twice: 100 first
+        w[2000] = w[100] * 4
+        w[100] = w[100] * 4
+        w[17] = w[9]                                          # the same group of 8 row tiles
+        x[0] = w[100] / w[100].norm()
+        x[1] = w[9] / w[9].norm()
+        x[2].zero_()
+        w[5000, 7] = float("nan")                            # NaN columns 5000 and 9000: 5000 wins
+        w[9000, 3] = float("nan")
+
+    ids, want, logits = _argmax_case(gpu, 16, n, k, 8, True, seed=5, plant=plant)
+    assert torch.equal(ids, want)
+    assert torch.equal(ids.cpu(), torch.argmax(logits.float().cpu(), dim=-1))
+    assert ids[0].item() == 5000 and ids[2].item() == 5000          # NaN above every number
+    lg = logits.float().cpu()
+    lg[:, 5000] = lg[:, 9000] = float("-inf")
+    assert torch.argmax(lg[0]).item() == 100 and torch.argmax(lg[1]).item() == 9
+
+
+def test_linear_argmax_without_nan_ties(gpu):
+    """The same planted ties without NaN columns: row 0 picks column 100 of three equal maxima (the
+    others 1,900 and 2,900 columns later, other groups), row 1 column 9 of two (9 and 17, one group),
+    the all-zero row column 0."""
+    n, k = 16 * 700, 256
+
+    def plant(x, w):
+        w[100] = w[100] * 4
+        w[2000] = w[100]
+        w[3000] = w[100]
+        w[17] = w[9]
+        x[0] = w[100] / w[100].norm()
+        x[1] = w[9] / w[9].norm()
+        x[2].zero_()
+
+    ids, want, logits = _argmax_case(gpu, 16, n, k, 8, False, seed=6, plant=plant)
+    assert torch.equal(ids, want)
+    assert ids[0].item() == 100 and ids[1].item() == 9 and ids[2].item() == 0
+    assert torch.equal(ids.cpu(), torch.argmax(logits.float().cpu(), dim=-1))
+
+
+def test_linear_argmax_rejects_bad_arguments(gpu):
+    x = torch.zeros(8, 64, dtype=torch.bfloat16, device=gpu)
+    wt = torch.zeros(32, 64, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError, match="workspace"):
+        decoder_ops.linear_argmax(x, wt, 1, workspace=torch.empty(16, dtype=torch.uint8, device=gpu))
+    with pytest.raises(RuntimeError, match="rtw"):
+        decoder_ops.linear_argmax(x, wt, 9)
+
+
 @pytest.mark.parametrize("rows,n,stride", [(64, 128256, 128256), (3, 1000, 1008), (1, 7, 8), (5, 4099, 4104)])
 def test_argmax_rows_matches_torch(gpu, rows, n, stride):
     """First index among equal maxima (planted ties, a row of equal values), NaN above every number."""

@@ -337,6 +337,208 @@ __global__ __launch_bounds__(NW * 64) void palu_linear_kernel(const __bf16* __re
   }
 }
 
+// Greedy pick fused into the LM head: for y = x w^T (one k slice, the sums and their order those of
+// palu_linear_kernel, rounded to bf16 as its plain output would be), key[r][group] = the largest
+// (value, -column) of row r over the group's columns, packed so that one unsigned 64-bit max picks the
+// largest value and, among equal ones, the first column: bits 63-32 the bf16 value made order-preserving
+// (NaN above +inf, -0 taken as +0), bits 31-0 ~column. palu_argmax_keys_kernel then reduces a row's
+// group keys. The logits are never written: at the LM head's shape (64 x 128256) the 16 MB of bf16
+// stores cost the projection 30 us of its 191 (a probe with the same loop and one 8-byte store per
+// lane and group: 175-183 us), and the argmax launch that read them back 11.5 us.
+// A fixed grid of at most PERSIST_WGS workgroups takes groups blockIdx.x, blockIdx.x + gridDim.x, ...;
+// the next group's first NB - 1 k steps are issued before the current group's LDS reduce and key
+// stores, so the weight stream runs on through them.
+constexpr int PERSIST_WGS = 256;
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int col) {
+  unsigned u = __builtin_bit_cast(unsigned short, (__bf16)v);
+  if ((u & 0x7fffu) > 0x7f80u) u = 0xffffu;                   // NaN: above every number
+  else if ((u & 0x7fffu) == 0) u = 0x8000u;                   // -0 and +0 compare equal
+  else u = (u & 0x8000u) ? (~u & 0xffffu) : (u | 0x8000u);
+  return ((unsigned long long)u << 32) | (0xffffffffu - (unsigned)col);
+}
+
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int mask) {
+  const unsigned lo = __shfl_xor((unsigned)v, mask, 64), hi = __shfl_xor((unsigned)(v >> 32), mask, 64);
+  return ((unsigned long long)hi << 32) | lo;
+}
+
+template <int RTW, int NB, int NW, bool XT>
+__global__ __launch_bounds__(NW * 64) void palu_linear_argmax_kernel(const __bf16* __restrict__ x, long long ldx,
+                                                                     int m, const __bf16* __restrict__ wt, int n16,
+                                                                     int kt_total,
+                                                                     unsigned long long* __restrict__ keys) {
+  using SM = LinSmem<RTW, NW, EPI_OUT>;
+  static_assert(NW == LIN_MT, "wave w reduces activation rows 16 w .. 16 w + 15");
+  constexpr int NT = (RTW * LIN_MT + NW - 1) / NW;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  f32x4* red = reinterpret_cast<f32x4*>(smem);
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int mm = lane & 15, g = lane >> 4;
+  const int groups = (n16 + RTW - 1) / RTW;
+
+  const __bf16* xp[LIN_MT];
+  bool xv[LIN_MT];
+#pragma unroll
+  for (int mt = 0; mt < LIN_MT; ++mt) {
+    const int r = 16 * mt + mm;
+    xv[mt] = r < m;
+    xp[mt] = XT ? x + ((long long)mt * 64 + lane) * 8 : x + (long long)(xv[mt] ? r : 0) * ldx + 8 * g;
+  }
+  // The group a workgroup streams: its row tiles and its k offset (palu_linear_kernel's, one slice).
+  const int klen = kt_total;
+  const int kper = klen / NW > 0 ? klen / NW : 1;
+  int grp = blockIdx.x;
+  int rt0 = 0, rt_cnt = 0, krot = 0;
+  const bf16x8* wp = nullptr;
+  auto setup = [&](int gi) {
+    gi = gi < groups ? gi : groups - 1;                  // past the last group: reload it (never reduced)
+    rt0 = gi * RTW;
+    rt_cnt = min(RTW, n16 - rt0);
+    krot = (gi * 37 % kper) * NW % klen;
+    wp = reinterpret_cast<const bf16x8*>(wt) + (long long)rt0 * kt_total * 64 + lane;
+  };
+  setup(grp);
+
+  bf16x8 wa[NB][RTW], xb[NB][LIN_MT];
+  auto load = [&](int buf, int kt) {
+    int i = kt < klen ? (kt + krot >= klen ? kt + krot - klen : kt + krot) : klen - 1;
+#pragma unroll
+    for (int r = 0; r < RTW; ++r) wa[buf][r] = __builtin_nontemporal_load(wp + ((long long)i * rt_cnt + min(r, rt_cnt - 1)) * 64);
+#pragma unroll
+    for (int mt = 0; mt < LIN_MT; ++mt)
+      xb[buf][mt] = *reinterpret_cast<const bf16x8*>(xp[mt] + (XT ? (long long)i * (LIN_MT * 512) : 32LL * i));
+  };
+  const int kt0 = w;
+  const int nsteps = kt0 < klen ? (klen - kt0 + NW - 1) / NW : 0;
+#pragma unroll
+  for (int j = 0; j < NB - 1; ++j) {
+    load(j, kt0 + j * NW);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  while (true) {
+    f32x4 acc[RTW][LIN_MT];
+#pragma unroll
+    for (int r = 0; r < RTW; ++r)
+#pragma unroll
+      for (int mt = 0; mt < LIN_MT; ++mt) acc[r][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < nsteps; s += NB) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        load((j + NB - 1) % NB, kt0 + (s + j + NB - 1) * NW);
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8 bz[LIN_MT];
+#pragma unroll
+        for (int mt = 0; mt < LIN_MT; ++mt) bz[mt] = (xv[mt] && s + j < nsteps) ? xb[j][mt] : bf16x8{};
+#pragma unroll
+        for (int r = 0; r < RTW; ++r)
+#pragma unroll
+          for (int mt = 0; mt < LIN_MT; ++mt) acc[r][mt] = mfma16(wa[j][r], bz[mt], acc[r][mt]);
+      }
+    }
+    // This group's sums to LDS (after every wave has read the previous group's), then the next group's
+    // first k steps go out before the reads and the key stores of this one.
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RTW; ++r)
+#pragma unroll
+      for (int mt = 0; mt < LIN_MT; ++mt) red[w * SM::SLOT + (r * LIN_MT + mt) * 64 + lane] = acc[r][mt];
+    const int cur = grp, cur_rt0 = rt0, cur_rt_cnt = rt_cnt;
+    const int next = grp + (int)gridDim.x;                 // uniform
+    setup(next);
+#pragma unroll
+    for (int j = 0; j < NB - 1; ++j) {
+      load(j, kt0 + j * NW);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+    // Wave w's tiles t = w + i NW are row tiles r = i of activation rows 16 w + mm; lane (g, mm) holds
+    // columns 16 (rt0 + i) + 4 g .. + 3 of row 16 w + mm.
+    unsigned long long best = 0;                            // below every key (no value maps to 0)
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      const int t = min(w + i * NW, RTW * LIN_MT - 1);
+      f32x4 v = red[t * 64 + lane];
+#pragma unroll
+      for (int q = 1; q < NW; ++q) v += red[q * SM::SLOT + t * 64 + lane];
+      if (w + i * NW < RTW * LIN_MT && i < cur_rt_cnt) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const unsigned long long key = argmax_key(v[k], 16 * (cur_rt0 + i) + 4 * g + k);
+          best = key > best ? key : best;
+        }
+      }
+    }
+    unsigned long long o = shfl_xor_u64(best, 16);
+    best = o > best ? o : best;
+    o = shfl_xor_u64(best, 32);
+    best = o > best ? o : best;
+    const int row = 16 * w + mm;
+    if (g == 0 && row < m) keys[(long long)row * groups + cur] = best;
+    if (next >= groups) break;
+    grp = next;
+  }
+}
+
+// ids[r] = the column of the largest of row r's group keys (one workgroup per row).
+__global__ __launch_bounds__(256) void palu_argmax_keys_kernel(const unsigned long long* __restrict__ keys, int groups,
+                                                               long long* __restrict__ ids) {
+  __shared__ unsigned long long part[4];
+  const int row = blockIdx.x;
+  unsigned long long best = 0;
+  for (int gi = threadIdx.x; gi < groups; gi += 256) {
+    const unsigned long long k = keys[(long long)row * groups + gi];
+    best = k > best ? k : best;
+  }
+#pragma unroll
+  for (int mask = 32; mask >= 1; mask >>= 1) {
+    const unsigned long long o = shfl_xor_u64(best, mask);
+    best = o > best ? o : best;
+  }
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int q = 1; q < 4; ++q) best = part[q] > best ? part[q] : best;
+    ids[row] = (long long)(0xffffffffu - (unsigned)(best & 0xffffffffu));
+  }
+}
+
+template <int RTW, bool XT>
+hipError_t launch_argmax_cfg(const __bf16* x, long long ldx, int m, const __bf16* wt, int n16, int kt_total,
+                             unsigned long long* keys, long long* ids, hipStream_t s) {
+  constexpr int NB = 4;
+  constexpr int NW = 4;
+  auto kern = palu_linear_argmax_kernel<RTW, NB, NW, XT>;
+  constexpr int lds = LinSmem<RTW, NW, EPI_OUT>::BYTES;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int groups = (n16 + RTW - 1) / RTW;
+  hipLaunchKernelGGL(kern, dim3(std::min(groups, PERSIST_WGS)), dim3(NW * 64), lds, s, x, ldx, m, wt, n16, kt_total, keys);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  hipLaunchKernelGGL(palu_argmax_keys_kernel, dim3(m), dim3(256), 0, s, keys, groups, ids);
+  return hipGetLastError();
+}
+
+template <bool XT>
+hipError_t launch_argmax(int rtw, const __bf16* x, long long ldx, int m, const __bf16* wt, int n16, int kt_total,
+                         unsigned long long* keys, long long* ids, hipStream_t s) {
+  switch (rtw) {
+    case 1: return launch_argmax_cfg<1, XT>(x, ldx, m, wt, n16, kt_total, keys, ids, s);
+    case 2: return launch_argmax_cfg<2, XT>(x, ldx, m, wt, n16, kt_total, keys, ids, s);
+    case 3: return launch_argmax_cfg<3, XT>(x, ldx, m, wt, n16, kt_total, keys, ids, s);
+    case 4: return launch_argmax_cfg<4, XT>(x, ldx, m, wt, n16, kt_total, keys, ids, s);
+    case 5: return launch_argmax_cfg<5, XT>(x, ldx, m, wt, n16, kt_total, keys, ids, s);
+    case 6: return launch_argmax_cfg<6, XT>(x, ldx, m, wt, n16, kt_total, keys, ids, s);
+    case 7: return launch_argmax_cfg<7, XT>(x, ldx, m, wt, n16, kt_total, keys, ids, s);
+    default: return launch_argmax_cfg<8, XT>(x, ldx, m, wt, n16, kt_total, keys, ids, s);
+  }
+}
+
 // y[r][c] = bf16(sum over ks of part[ks][r][c]); 4 columns per thread.
 __global__ __launch_bounds__(256) void palu_linear_reduce_kernel(const float* __restrict__ part, int ks_count, int m,
                                                                  int n, __bf16* __restrict__ y, long long ldy) {
@@ -517,6 +719,30 @@ extern "C" int palu_linear_tiled(const void* x, long long ldx, int x_tiled, int 
     if (int rc = launched(hipGetLastError(), "palu_linear_tiled reduce")) return rc;
   }
   return PALU_OK;
+}
+
+extern "C" size_t palu_linear_argmax_workspace_bytes(int m, int n) {
+  if (m < 1 || m > 64 || n <= 0 || n % 16) return 0;
+  return (size_t)m * (n / 16) * sizeof(unsigned long long);
+}
+
+extern "C" int palu_linear_argmax(const void* x, long long ldx, int x_tiled, int m, const void* w_tiled, int n, int k,
+                                  int rtw, int64_t* ids, void* ws, size_t ws_bytes, hipStream_t stream) {
+  palu::g_err[0] = 0;
+  const char* who = "palu_linear_argmax";
+  if (!ids) return fail(PALU_EINVAL, "%s: a required pointer is null", who);
+  if (int rc = check_operands(x, ldx, x_tiled, m, w_tiled, n, k, rtw, who)) return rc;
+  if (reinterpret_cast<uintptr_t>(ids) & 7) return fail(PALU_EINVAL, "%s: ids must be 8-byte aligned", who);
+  const size_t need = palu_linear_argmax_workspace_bytes(m, n);
+  if (!ws || ws_bytes < need || (reinterpret_cast<uintptr_t>(ws) & 15))
+    return fail(PALU_EINVAL, "%s: workspace of %zu bytes (16-byte aligned) needed, got %zu", who, need, ws_bytes);
+  const auto* xb = static_cast<const __bf16*>(x);
+  const auto* wb = static_cast<const __bf16*>(w_tiled);
+  auto* keys = static_cast<unsigned long long*>(ws);
+  auto* out = reinterpret_cast<long long*>(ids);
+  return launched(x_tiled ? launch_argmax<true>(rtw, xb, ldx, m, wb, n / 16, k / 32, keys, out, stream)
+                          : launch_argmax<false>(rtw, xb, ldx, m, wb, n / 16, k / 32, keys, out, stream),
+                  who);
 }
 
 extern "C" int palu_linear_swiglu_rmsnorm(const void* x, long long ldx, int x_tiled, int m, const void* w_tiled, int n,

@@ -47,6 +47,8 @@ _SIGNATURES = {
                            _i, _i, _vp]),
     "palu_linear_plan": (_i, [_i, _i, _i, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
     "palu_linear_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "palu_linear_argmax": (_i, [_vp, _ll, _i, _i, _vp, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "palu_linear_argmax_workspace_bytes": (_sz, [_i, _i]),
     "palu_linear_plan_ks": (_i, [_i, _i, _i, _i, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
     "palu_linear_swiglu_rmsnorm": (_i, [_vp, _ll, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp]),
     "palu_linear_residual": (_i, [_vp, _ll, _i, _i, _vp, _i, _i, _i, _vp, _ll, _vp, _vp]),

@@ -398,6 +398,40 @@ def qkv_post(part: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torc
     return q_out
 
 
+def linear_argmax(x: torch.Tensor, w_tiled: torch.Tensor, rtw: int, workspace: Optional[torch.Tensor] = None,
+                  x_tiled: bool = False, rows: Optional[int] = None,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """argmax_rows(linear_tiled(x, w_tiled, rtw, 1)) as int64 [rows] without writing the logits: the
+    projection's epilogue keeps each row's largest (value, first column) per group of row tiles and a
+    second launch picks among the groups. x as for linear_tiled; workspace: a uint8 GPU tensor of at
+    least palu_linear_argmax_workspace_bytes(rows, n) bytes (else a fresh one)."""
+    _check(x, "x")
+    _check(w_tiled, "w_tiled")
+    k = x.shape[1]
+    if x_tiled:
+        if x.shape[0] != 64 or not x.is_contiguous() or rows is None:
+            raise RuntimeError("a tiled x is a contiguous [64, k] buffer and needs the live row count `rows`")
+    else:
+        rows = x.shape[0]
+        if x.dim() != 2 or x.stride(1) != 1:
+            raise RuntimeError("x must be a row-strided [rows, k] view")
+    n = w_tiled.shape[0]
+    if w_tiled.shape[1] != k:
+        raise RuntimeError(f"x has k = {k}, w_tiled has {w_tiled.shape[1]}")
+    lib = _native.load()
+    need = lib.palu_linear_argmax_workspace_bytes(rows, n)
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=x.device)
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=x.device)
+    if out.dtype != torch.int64 or out.shape != (rows,) or not out.is_contiguous() or out.device != x.device:
+        raise RuntimeError(f"out must be a contiguous int64 [{rows}] tensor on {x.device}")
+    _native.check(lib.palu_linear_argmax(_native.ptr(x), 64 if x_tiled else x.stride(0), int(x_tiled), rows,
+                                         _native.ptr(w_tiled), n, k, rtw, _native.ptr(out), _native.ptr(workspace),
+                                         workspace.numel(), _native.stream_handle(x.device)))
+    return out
+
+
 class DecodeLinear:
     """One projection of the decode step, y = x @ w.T, for w [n, k] in the nn.Linear layout (for a gate /
     up pair, gate_up=(w_gate, w_up) instead: y = silu(x @ w_gate.T) * (x @ w_up.T)). For up to 64 rows
@@ -422,6 +456,7 @@ class DecodeLinear:
         self.tiled = (rows <= 64 and n % (64 if self.gate_up else 16) == 0 and k % 32 == 0 and w.is_cuda
                       and w.dtype == torch.bfloat16)
         self.in_scale_folded = False
+        self.argmax_ws = None
         if self.tiled:
             self.rtw, self.ks = (rtw, ks) if rtw else linear_plan(rows, n, k, 1 if single_slice else 16)
             if self.gate_up:
@@ -462,6 +497,16 @@ class DecodeLinear:
             out.copy_(y)
             return out
         return y
+
+    def argmax(self, x: torch.Tensor, x_tiled: bool = False, rows: Optional[int] = None) -> torch.Tensor:
+        """argmax_rows(self(x)) as int64 [rows]: linear_argmax for a tiled projection (the logits are not
+        written), else torch's projection and argmax_rows."""
+        if self.tiled and not self.gate_up:
+            if self.argmax_ws is None:
+                need = _native.load().palu_linear_argmax_workspace_bytes(64, self.n)
+                self.argmax_ws = torch.empty(need, dtype=torch.uint8, device=self.weight.device)
+            return linear_argmax(x, self.weight, self.rtw, self.argmax_ws, x_tiled=x_tiled, rows=rows)
+        return argmax_rows(self(x, x_tiled=x_tiled, rows=rows))
 
     def swiglu_rmsnorm(self, x: torch.Tensor, eps: float, out: Optional[torch.Tensor] = None,
                        x_tiled: bool = False, rows: Optional[int] = None) -> torch.Tensor:

@@ -145,8 +145,9 @@ class Transformer(torch.nn.Module):
                 a = L["w13"].swiglu_rmsnorm(ht, eps, x_tiled=True, rows=B)  # silu(gate) * up of rmsnorm(h)
                 f = L["w2"](a, x_tiled=True, rows=B, mode="partials")
             y = decoder_ops.rmsnorm(h, self.norm_w, eps, res_part=f, tiled_out=True)
-            logits = self.output(y, x_tiled=True, rows=B)
-            return decoder_ops.argmax_rows(logits) if greedy else logits.float()
+            if greedy:
+                return self.output.argmax(y, x_tiled=True, rows=B)              # the logits are not written
+            return self.output(y, x_tiled=True, rows=B).float()
         for L in self.layers:
             y = decoder_ops.rmsnorm(h, L["attn_norm"], eps, res_part=f, h_out=h, tiled_out=xt)
             o = L["attn"].forward_decode(y, current_pos, x_tiled=xt, out_partials=True)
