@@ -311,7 +311,8 @@ size_t palu_linear_workspace_bytes(int rows, int n, int k, int ks);
  * order, rounded the same way), the first one among equal maxima and NaN above every number: what
  * palu_argmax_rows returns for those logits, which are not written. x, w_tiled, n, k and rtw as in
  * palu_linear_tiled; a caller workspace of palu_linear_argmax_workspace_bytes(rows, n) bytes (16-byte
- * aligned) holds one key per row and group of rtw row tiles. Two launches. No counterpart in the
+ * aligned) holds one key per row and workgroup (at most 256 workgroups, each running groups of rtw row
+ * tiles). Two launches. No counterpart in the
  * reference's op interface: its generation loop takes the argmax of the host-side logits
  * (generate.py:53-62); this keeps the greedy pick in the decode step's graph without writing the 64 x
  * vocab logits and reading them back. */

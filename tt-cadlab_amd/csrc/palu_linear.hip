@@ -338,11 +338,13 @@ __global__ __launch_bounds__(NW * 64) void palu_linear_kernel(const __bf16* __re
 }
 
 // Greedy pick fused into the LM head: for y = x w^T (one k slice, the sums and their order those of
-// palu_linear_kernel, rounded to bf16 as its plain output would be), key[r][group] = the largest
-// (value, -column) of row r over the group's columns, packed so that one unsigned 64-bit max picks the
-// largest value and, among equal ones, the first column: bits 63-32 the bf16 value made order-preserving
-// (NaN above +inf, -0 taken as +0), bits 31-0 ~column. palu_argmax_keys_kernel then reduces a row's
-// group keys. The logits are never written: at the LM head's shape (64 x 128256) the 16 MB of bf16
+// palu_linear_kernel, rounded to bf16 as its plain output would be), key[r][wg] = the largest
+// (value, -column) of row r over the columns of every group workgroup wg ran, packed so that one
+// unsigned 64-bit max picks the largest value and, among equal ones, the first column: bits 63-32 the
+// bf16 value made order-preserving (NaN above +inf, -0 taken as +0), bits 31-0 ~column. The max is
+// associative, so a workgroup keeps one running key per row over its groups and stores it once, at the
+// end (stores inside the group loop would hold the next group's loads behind them: the loop's waits
+// count stores too). palu_argmax_keys_kernel then reduces a row's workgroup keys. The logits are never written: at the LM head's shape (64 x 128256) the 16 MB of bf16
 // stores cost the projection 30 us of its 191 (a probe with the same loop and one 8-byte store per
 // lane and group: 175-183 us), and the argmax launch that read them back 11.5 us.
 // A fixed grid of at most PERSIST_WGS workgroups takes groups blockIdx.x, blockIdx.x + gridDim.x, ...;
@@ -400,6 +402,7 @@ __global__ __launch_bounds__(NW * 64) void palu_linear_argmax_kernel(const __bf1
     wp = reinterpret_cast<const bf16x8*>(wt) + (long long)rt0 * kt_total * 64 + lane;
   };
   setup(grp);
+  unsigned long long best = 0;                              // below every key (no value maps to 0)
 
   bf16x8 wa[NB][RTW], xb[NB][LIN_MT];
   auto load = [&](int buf, int kt) {
@@ -444,7 +447,7 @@ __global__ __launch_bounds__(NW * 64) void palu_linear_argmax_kernel(const __bf1
     for (int r = 0; r < RTW; ++r)
 #pragma unroll
       for (int mt = 0; mt < LIN_MT; ++mt) red[w * SM::SLOT + (r * LIN_MT + mt) * 64 + lane] = acc[r][mt];
-    const int cur = grp, cur_rt0 = rt0, cur_rt_cnt = rt_cnt;
+    const int cur_rt0 = rt0, cur_rt_cnt = rt_cnt;
     const int next = grp + (int)gridDim.x;                 // uniform
     setup(next);
 #pragma unroll
@@ -455,7 +458,6 @@ __global__ __launch_bounds__(NW * 64) void palu_linear_argmax_kernel(const __bf1
     __syncthreads();
     // Wave w's tiles t = w + i NW are row tiles r = i of activation rows 16 w + mm; lane (g, mm) holds
     // columns 16 (rt0 + i) + 4 g .. + 3 of row 16 w + mm.
-    unsigned long long best = 0;                            // below every key (no value maps to 0)
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
       const int t = min(w + i * NW, RTW * LIN_MT - 1);
@@ -470,25 +472,25 @@ __global__ __launch_bounds__(NW * 64) void palu_linear_argmax_kernel(const __bf1
         }
       }
     }
-    unsigned long long o = shfl_xor_u64(best, 16);
-    best = o > best ? o : best;
-    o = shfl_xor_u64(best, 32);
-    best = o > best ? o : best;
-    const int row = 16 * w + mm;
-    if (g == 0 && row < m) keys[(long long)row * groups + cur] = best;
     if (next >= groups) break;
     grp = next;
   }
+  unsigned long long o = shfl_xor_u64(best, 16);
+  best = o > best ? o : best;
+  o = shfl_xor_u64(best, 32);
+  best = o > best ? o : best;
+  const int row = 16 * w + mm;
+  if (g == 0 && row < m) keys[(long long)row * gridDim.x + blockIdx.x] = best;
 }
 
-// ids[r] = the column of the largest of row r's group keys (one workgroup per row).
-__global__ __launch_bounds__(256) void palu_argmax_keys_kernel(const unsigned long long* __restrict__ keys, int groups,
+// ids[r] = the column of the largest of row r's n_keys keys (one workgroup per row).
+__global__ __launch_bounds__(256) void palu_argmax_keys_kernel(const unsigned long long* __restrict__ keys, int n_keys,
                                                                long long* __restrict__ ids) {
   __shared__ unsigned long long part[4];
   const int row = blockIdx.x;
   unsigned long long best = 0;
-  for (int gi = threadIdx.x; gi < groups; gi += 256) {
-    const unsigned long long k = keys[(long long)row * groups + gi];
+  for (int gi = threadIdx.x; gi < n_keys; gi += 256) {
+    const unsigned long long k = keys[(long long)row * n_keys + gi];
     best = k > best ? k : best;
   }
 #pragma unroll
@@ -518,9 +520,10 @@ hipError_t launch_argmax_cfg(const __bf16* x, long long ldx, int m, const __bf16
     attr_set = true;
   }
   const int groups = (n16 + RTW - 1) / RTW;
-  hipLaunchKernelGGL(kern, dim3(std::min(groups, PERSIST_WGS)), dim3(NW * 64), lds, s, x, ldx, m, wt, n16, kt_total, keys);
+  const int n_wg = std::min(groups, PERSIST_WGS);          // one key per row and workgroup
+  hipLaunchKernelGGL(kern, dim3(n_wg), dim3(NW * 64), lds, s, x, ldx, m, wt, n16, kt_total, keys);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-  hipLaunchKernelGGL(palu_argmax_keys_kernel, dim3(m), dim3(256), 0, s, keys, groups, ids);
+  hipLaunchKernelGGL(palu_argmax_keys_kernel, dim3(m), dim3(256), 0, s, keys, n_wg, ids);
   return hipGetLastError();
 }
 
