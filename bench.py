@@ -230,7 +230,7 @@ def measure_paged(dev, steps, warmup):
         del layers
         torch.cuda.empty_cache()
     return {"workload": "paged M-LRD, batch 8, context lengths U[1024, 32768], 64-token pages, tiled bf16",
-            "lengths": [int(x) for x in lens], "ranks": res}
+            "lengths": [int(x) for x in lens], "steps": steps, "warmup": warmup, "ranks": res}
 
 
 def measure_glrd(dev, steps, warmup):
@@ -320,7 +320,8 @@ def measure_glrd(dev, steps, warmup):
     del kv
     torch.cuda.empty_cache()
     return {"workload": "G-LRD group size 4 (2 groups x 4 KV heads), batch 16, ctx 16384, bf16, V rebuilt per head "
-                        "in-kernel", "drawn_group_ranks": {"k": drawn_k, "v": drawn_v}, "layers": res,
+                        "in-kernel", "drawn_group_ranks": {"k": drawn_k, "v": drawn_v}, "steps": steps,
+            "warmup": warmup, "layers": res,
             "stock_full_kv": {"us_per_layer": round(s_wall * 1e3, 2), "kernel_us": round(s_kern * 1e3, 2)}}
 
 
