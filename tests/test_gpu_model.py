@@ -141,7 +141,8 @@ def test_generate_greedy_is_consistent_with_decode(gpu):
 def test_deterministic_decode_is_bit_reproducible(gpu):
     """PaluRuntime.deterministic (Transformer.set_deterministic, generate(..., deterministic=True)) fixes the
     decode kernels' block order: the same decode step repeated from the same state gives the same logits
-    bit for bit, eager and from the HIP graph, and greedy generation gives the same ids on every run."""
+    bit for bit, eager and from the HIP graph, the greedy step's ids (picked inside the LM head) are the
+    argmax of those logits, and greedy generation gives the same ids on every run."""
     args = pm.ModelArgs(dim=512, n_layers=2, n_heads=8, n_kv_heads=2, vocab_size=640, ffn_dim=1024,
                         max_seq_len=640, max_batch_size=4)
     model = pm.Transformer(args, pm.random_palu_state_dict(args, [64, 96], [48, 64], gpu, seed=21, std=0.1), gpu)
@@ -153,8 +154,13 @@ def test_deterministic_decode_is_bit_reproducible(gpu):
     b = model.decode(first, pos).clone()
     c = model.decode_graph(first, pos).clone()
     d = model.decode_graph(first, pos).clone()
+    ge = model.decode(first, pos, greedy=True).clone()      # the pick fused into the LM head
+    gg = model.decode_graph(first, pos, greedy=True).clone()
     torch.cuda.synchronize()
     assert torch.equal(a, b) and torch.equal(c, d) and torch.equal(a, c)
+    assert model._fused_step and model.output.tiled
+    want = torch.argmax(a.cpu(), dim=-1)                   # argmax of the same step's bf16 logits
+    assert torch.equal(ge.cpu(), want) and torch.equal(gg.cpu(), want)
     g1 = pm.generate(model, prompts, n_new=8, deterministic=True)
     g2 = pm.generate(model, prompts, n_new=8, deterministic=True)
     assert torch.equal(g1, g2)
