@@ -541,9 +541,9 @@ def main():
         # the extra lines take their own minimum counts (about 20-60 ms of GPU time each): a handful of
         # calls after 3-5 warm-ups reads the clocks and caches still ramping (the G-LRD widest layer timed
         # 402 us at 10 calls after 3 warm-ups against 366 us at steady state on one box), and the paged
-        # layers' first 130 calls after their page pools are built run 4-6 % slower than the 400 after
-        # them (one box: 72.5 and 86.6 us against 68.3 and 83.3), hence 160 warm-ups and the headline's
-        # count of timed calls there (about 0.1 s of GPU time)
+        # layers' first 130 calls after their page pools are built run slower (the (32, 128) pair 72.5-74.1
+        # us per call against 68.3-69.6 for later ones on two boxes), hence 160 warm-ups and the
+        # headline's count of timed calls there (about 0.1 s of GPU time; 600 warm-ups read the same)
         progress("paged mixed ranks")
         res["paged_mixed_ranks"] = measure_paged(dev, max(a.steps, 100), max(a.warmup * 4, 160))
         progress("grouped latents (G-LRD)")
